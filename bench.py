@@ -1,0 +1,337 @@
+#!/usr/bin/env python3
+"""bench.py — the RAC rotation-accumulate hot path on one MI355X.
+
+Metric: rac_matmul equiv-GFLOP/s at 4096^3 with 16 CORDIC
+iterations; RoPE / softmax / RMSNorm HBM GB/s.  A "step" is one 4096^3
+CORDIC-16 matmul (rotate-project-accumulate: 16 micro-rotations per MAC)
+over synthetic U[-1,1] operands resident in HBM.  value = 2*4096^3 / t.
+
+Also measured in the same run (fields "ops" and "cpu_baseline"):
+  * the matmul at n = 8 and 24;
+  * softmax 4096x4096 N(0, std 2) at n = 8/16/24, RoPE on Q and K
+    [8,32,4096,128], RMSNorm 16384x4096, SiLU 16384x11008 (n=16): HBM GB/s
+    of 1 read + 1 write per element, buffers rotated past the 256 MB MALL;
+  * the reference lib/c on the host cores (oracle/_ref, compiled from the
+    reference sources): rac_hal_matmul 4096^3 and the row ops, timed in a
+    child process.
+
+Roofline of the dominant kernel (the matmul): VALU-bound; algorithmic work
+per MAC is W(n) = 2n+1 FP32 FMA lane-ops (n micro-rotations on the (x, y)
+pair plus the projecting FMA), i.e. 2*(2n+1) FLOP; achieved = that over the
+kernel's average launch time (HIP events on the launch stream); peak =
+MI355X FP32 vector 157.3 TFLOP/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--iters 16]
+                       [--no-cpu-baseline] [--matmul-only]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+
+
+def _events_time(fn, reps, torch):
+    """Average time of fn() per call from HIP events on the current stream."""
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps / 1e3
+
+
+def bench_gpu(args):
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from rac_amd import ext
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    M = N = K = 4096
+    A = torch.rand((M, K), device=dev, generator=g) * 2 - 1
+    B = torch.rand((K, N), device=dev, generator=g) * 2 - 1
+    C = torch.empty((M, N), device=dev)
+    lib = ext._lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def mm(n):
+        rc = lib.rac_gemm_dev(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 0, 0, 1.0, 0.0,
+                              n, ext.MODE_CORDIC, stream)
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    n = args.iters
+    for _ in range(args.warmup):
+        mm(n)
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` steps, synchronised on both sides
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        mm(n)
+        b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_s = sum(a.elapsed_time(b) for a, b in ev) / len(ev) / 1e3
+    ms_per_step = wall / args.steps * 1e3
+    print(f"# matmul 4096^3 CORDIC n={n}: {launch_s * 1e3:.2f} ms/launch, wall {ms_per_step:.2f} ms/step",
+          file=sys.stderr, flush=True)
+
+    ops = {"matmul_4096_cordic": {}}
+    for nn in (8, 16, 24):
+        if nn == n:
+            t = launch_s
+        else:
+            mm(nn)
+            torch.cuda.synchronize()
+            t = _events_time(lambda: mm(nn), max(3, args.steps // 4), torch)
+        w = 2 * nn + 1
+        ops["matmul_4096_cordic"][f"n{nn}"] = {
+            "ms": round(t * 1e3, 3),
+            "equiv_GFLOPs": round(2 * M * N * K / t / 1e9, 1),
+            "valu_TFLOPs": round(M * N * K * 2 * w / t / 1e12, 2),
+            "frac_of_fp32_peak": round(M * N * K * 2 * w / t / 1e12 / PEAK_FP32_TFLOPS, 4),
+        }
+        print(f"# matmul n={nn}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    del A, B, C
+
+    if not args.matmul_only:
+        ops.update(bench_hbm_ops(torch, ext, dev, g))
+
+    w = 2 * n + 1
+    achieved = M * N * K * 2 * w / launch_s / 1e12
+    return {
+        "value": round(2 * M * N * K / (ms_per_step / 1e3) / 1e9, 1),
+        "ms_per_step": round(ms_per_step, 3),
+        "roofline": {"bound": "valu", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                     "traffic": None,
+                     "kernel": f"gemm_kernel<CORDIC,{n},NN> 64x64 tile, 4x4 per lane",
+                     "avg_launch_ms": round(launch_s * 1e3, 3),
+                     "work_per_mac": f"{w} FMA lane-ops (2n+1)"},
+        "ops": ops,
+    }
+
+
+def bench_hbm_ops(torch, ext, dev, g):
+    lib = ext._lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+
+    def chk(rc):
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    def record(name, nbytes, t):
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4)}
+        print(f"# {name}: {t * 1e6:.1f} us, {nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+
+    reps = 20
+    # softmax 4096 x 4096, N(0, std 2); 4 buffer sets (512 MiB) rotate past MALL
+    R, Cn = 4096, 4096
+    xs = [torch.randn((R, Cn), device=dev, generator=g) * 2.0 for _ in range(4)]
+    ys = [torch.empty_like(xs[0]) for _ in range(4)]
+    for n in (8, 16, 24):
+        state = {"i": 0}
+
+        def sm():
+            i = state["i"] = (state["i"] + 1) % 4
+            chk(lib.rac_softmax_dev(xs[i].data_ptr(), ys[i].data_ptr(), R, Cn, n, stream))
+
+        sm()
+        torch.cuda.synchronize()
+        record(f"softmax_4096x4096_n{n}", 2 * 4 * R * Cn, _events_time(sm, reps, torch))
+    del xs, ys
+
+    # RoPE: Q and K [8,32,4096,128] in place (2 GiB moved per step)
+    shape = (8, 32, 4096, 128)
+    q = torch.randn(shape, device=dev, generator=g)
+    k = torch.randn(shape, device=dev, generator=g)
+    cos, sin = ext.rope_cache(4096, 128, 10000.0, device=dev)
+    Bq, Hq, Tq, Dq = shape
+
+    def rope():
+        for t in (q, k):
+            chk(lib.rac_rope_apply_dev(t.data_ptr(), cos.data_ptr(), sin.data_ptr(), Bq, Hq, Tq, Dq,
+                                       Hq * Tq * Dq, Tq * Dq, Dq, stream))
+
+    rope()
+    torch.cuda.synchronize()
+    record("rope_qk_8x32x4096x128", 2 * 2 * 4 * q.numel(), _events_time(rope, reps, torch))
+    del q, k
+
+    # RMSNorm 16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6; 2 sets (1 GiB)
+    R, D = 16384, 4096
+    xr = [torch.randn((R, D), device=dev, generator=g) for _ in range(2)]
+    yr = [torch.empty_like(xr[0]) for _ in range(2)]
+    gam = torch.randn(D, device=dev, generator=g) * 0.02 + 1.0
+    st = {"i": 0}
+
+    def rms():
+        i = st["i"] = (st["i"] + 1) % 2
+        chk(lib.rac_rmsnorm_dev(xr[i].data_ptr(), yr[i].data_ptr(), gam.data_ptr(), 1e-6, R, D, stream))
+
+    rms()
+    torch.cuda.synchronize()
+    record("rmsnorm_16384x4096", 2 * 4 * R * D + 4 * D, _events_time(rms, reps, torch))
+    del xr, yr
+
+    # SiLU 16384 x 11008 (n = 16)
+    xsilu = torch.randn((16384, 11008), device=dev, generator=g)
+    ysilu = torch.empty_like(xsilu)
+
+    def silu():
+        chk(lib.rac_silu_dev(xsilu.data_ptr(), ysilu.data_ptr(), xsilu.numel(), 16, stream))
+
+    silu()
+    torch.cuda.synchronize()
+    record("silu_16384x11008_n16", 2 * 4 * xsilu.numel(), _events_time(silu, 10, torch))
+    del xsilu, ysilu
+    return out
+
+
+# ── CPU baseline: the compiled reference lib/c, in a child process ─────────
+
+def cpu_baseline_child():
+    """Runs without torch: times oracle/_ref (reference lib/c) on host cores."""
+    import ctypes
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import raclib as rl
+
+    if not rl.have_ref():
+        print(json.dumps({"error": "oracle/_ref/librac_ref.so not present"}))
+        return
+    r = rl.ref()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    res = {"threads": threads}
+    M = N = K = 4096
+    A = rl.gen_uniform((M, K), 0)
+    B = rl.gen_uniform((K, N), 1)
+    Cm = np.zeros((M, N), np.float32)
+    r.rac_hal_matmul(rl.p(A), rl.p(B), rl.p(Cm), M, N, K)   # warm-up (HAL init, page-in)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        r.rac_hal_matmul(rl.p(A), rl.p(B), rl.p(Cm), M, N, K)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 40:
+            break
+    t = (time.perf_counter() - t0) / reps
+    res["matmul"] = {"seconds": t, "reps": reps, "GFLOPs": 2 * M * N * K / t / 1e9}
+    del A, B, Cm
+
+    def timeit(fn, n):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return (time.perf_counter() - t0) / n
+
+    x = rl.gen_normal((4096, 4096), 0, std=2.0)
+    y = np.empty_like(x)
+    t = timeit(lambda: r.rac_softmax_batch(rl.p(x), rl.p(y), 4096, 4096), 3)
+    res["softmax"] = {"seconds": t, "GBps": 2 * x.nbytes / t / 1e9}
+    q = np.random.default_rng(0).standard_normal((8, 32, 4096, 128), dtype=np.float32)
+    c = np.zeros((4096, 64), np.float32)
+    s = np.zeros((4096, 64), np.float32)
+    r.rac_rope_cache(rl.p(c), rl.p(s), 4096, 128, 10000.0)
+    t = timeit(lambda: r.rac_rope_apply(rl.p(q), rl.p(c), rl.p(s), 8, 32, 4096, 128, None), 2)
+    res["rope_per_tensor"] = {"seconds": t, "GBps": 2 * q.nbytes / t / 1e9}
+    del q
+    x = np.random.default_rng(1).standard_normal((16384, 4096), dtype=np.float32)
+    y = np.empty_like(x)
+    gam = np.ones(4096, np.float32)
+    t = timeit(lambda: r.rac_rmsnorm(rl.p(x), rl.p(y), rl.p(gam), 1e-6, 16384, 4096, None), 2)
+    res["rmsnorm"] = {"seconds": t, "GBps": 2 * x.nbytes / t / 1e9}
+    print(json.dumps(res))
+
+
+def run_cpu_baseline():
+    env = dict(os.environ)
+    env.setdefault("OMP_PROC_BIND", "close")
+    env.setdefault("OMP_PLACES", "cores")
+    try:
+        out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-child"],
+                             capture_output=True, text=True, env=env, timeout=240)
+        line = [ln for ln in out.stdout.splitlines() if ln.startswith("{")][-1]
+        return json.loads(line)
+    except Exception as e:  # noqa: BLE001
+        return {"error": f"cpu baseline failed: {e}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--iters", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--matmul-only", action="store_true")
+    ap.add_argument("--cpu-baseline-child", action="store_true", help=argparse.SUPPRESS)
+    args = ap.parse_args()
+
+    if args.cpu_baseline_child:
+        cpu_baseline_child()
+        return
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): this "
+              "build's hot path is single-GPU; see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    gpu = bench_gpu(args)
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline()
+    line = {
+        "metric": "rac_matmul equiv-GFLOP/s at 4096³ (16 iters); RoPE/softmax/RMSNorm HBM GB/s",
+        "value": gpu["value"],
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": gpu["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (U[-1,1] operands, torch generator seed 0, resident in HBM)",
+        "config": {"workload": f"rac_matmul 4096x4096x4096 fp32 CORDIC mode n={args.iters} (NN, row-major)",
+                   "M": 4096, "N": 4096, "K": 4096, "cordic_iters": args.iters, "mode": "cordic"},
+        "roofline": gpu["roofline"],
+        "ops": gpu["ops"],
+    }
+    if cpu is not None and "matmul" in cpu:
+        line["cpu_baseline"] = {
+            "value": round(cpu["matmul"]["GFLOPs"], 1), "unit": "GFLOP/s", "cores": cpu["threads"],
+            "kind": "reference",
+            "sample": f"reference lib/c rac_hal_matmul (AVX2 GotoBLAS, FMA; ignores n) 4096^3 x "
+                      f"{cpu['matmul']['reps']} reps, {cpu['threads']} OpenMP threads",
+            "ops": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in cpu.items()
+                    if isinstance(v, dict) and k != "matmul"},
+        }
+    elif cpu is not None:
+        line["cpu_baseline"] = {"value": None, "unit": "GFLOP/s", "cores": 0, "kind": "reference",
+                                "sample": cpu.get("error", "unavailable")}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+/*
+ * rac_ext.h — device-pointer, stream-ordered entry points of librac_amd.so,
+ * the process knobs, and the reference kernel-library launcher ABI.
+ *
+ * Device API (rac_*_dev): every buffer is device memory; the work is
+ * enqueued on `stream` (a hipStream_t, 0 = null stream) and the call
+ * returns without synchronising.  Return value: 0 on success, or
+ *   -1 RAC_ERR_NULL_PTR, -2 RAC_ERR_INVALID_DIM, -3 RAC_ERR_ALLOC
+ *   (same codes as the reference rac_cpu.h:54-59), -4 HIP error;
+ * the message is in rac_last_error().  Arguments are validated before any
+ * HIP call.  These are the calls the Python layer makes (with torch's
+ * current stream); they have no counterpart in rac.h, whose entry points
+ * are synchronous.
+ */
+#ifndef RAC_EXT_H
+#define RAC_EXT_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RAC_MODE_FAST 0     /* rac_kernels.hip:23-25 */
+#define RAC_MODE_CORDIC 1
+#define RAC_MODE_SHIFTADD 2
+
+/* ── errors, knobs, info ─────────────────────────────────────────────────── */
+
+const char *rac_last_error(void);   /* thread-local message of the last failure */
+void rac_clear_error(void);
+/* Process knobs of the synchronous rac.h API, seeded from RAC_CORDIC_ITERS
+ * (default 16) and RAC_CORDIC_MODE (fast|cordic|shiftadd, default cordic).
+ * Clamping follows rac_torch_bind.cpp:205-219 (iters <= 0 -> default,
+ * clamp to [1, 24]; an unknown mode selects FAST). */
+void rac_set_cordic_iters(int iters);
+int rac_get_cordic_iters(void);
+void rac_set_cordic_mode(int mode);
+int rac_get_cordic_mode(void);
+/* Stream used by the synchronous rac.h calls (default 0). */
+void rac_set_stream(void *stream);
+void *rac_get_stream(void);
+int rac_version(void);
+/* Host-side queries of the constants the kernels use (no GPU needed):
+ * the circular direction sequence of CORDIC-mode matmul (d[i] = +1/-1 for
+ * i < iters; returns the clamped count), 1/K_h of the n-step exp, and 1/K_h
+ * of the 16-step rsqrt. */
+int rac_cordic_direction_bits(int iters, int *d);
+float rac_exp_gain_inverse(int iters);
+float rac_rsqrt_gain_inverse(void);
+
+/* ── device API ──────────────────────────────────────────────────────────── */
+
+/* C[M,N] = alpha * op(A) op(B) (+ beta * C); op(A) = A [M,K] or, with
+ * trans_a, A stored [K,M]; op(B) = B [K,N] or, with trans_b, B stored [N,K].
+ * mode 0 FAST / 1 CORDIC / 2 SHIFTADD, iters clamped to [1, 24].
+ * Replaces rac_kernels.hip:822-883 (same semantics, explicit status). */
+int rac_gemm_dev(const float *A, const float *B, float *C, int M, int N, int K,
+                 int trans_a, int trans_b, float alpha, float beta, int iters, int mode,
+                 void *stream);
+/* Softmax of each of `rows` rows of n floats (rac_cpu.c:258-271 with the
+ * n-step CORDIC exp). */
+int rac_softmax_dev(const float *x, float *y, long rows, long n, int iters, void *stream);
+/* Elementwise: CORDIC e^x, SiLU x/(1+e^-x), sigmoid 1/(1+e^-x), tanh;
+ * GELU x/2(1+erf(x/sqrt2)) and ReLU (rac_cpu.c:441-457). */
+int rac_exp_dev(const float *x, float *y, long count, int iters, void *stream);
+int rac_silu_dev(const float *x, float *y, long count, int iters, void *stream);
+int rac_sigmoid_dev(const float *x, float *y, long count, int iters, void *stream);
+int rac_tanh_dev(const float *x, float *y, long count, int iters, void *stream);
+int rac_gelu_dev(const float *x, float *y, long count, void *stream);
+int rac_relu_dev(const float *x, float *y, long count, void *stream);
+/* Batch CORDIC rsqrt and circular sin/cos (the scalar rac.h calls use these). */
+int rac_rsqrt_dev(const float *x, float *y, long count, void *stream);
+int rac_sincos_dev(const float *theta, float *s, float *c, long count, void *stream);
+/* RMSNorm / LayerNorm over rows of d floats; gamma/beta may be NULL
+ * (rac_cpu.c:507-574 with the CORDIC rsqrt). */
+int rac_rmsnorm_dev(const float *x, float *y, const float *gamma, float eps, long rows, long d,
+                    void *stream);
+int rac_layernorm_dev(const float *x, float *y, const float *gamma, const float *beta, float eps,
+                      long rows, long d, void *stream);
+/* RoPE table on the device.  inv_freq_dev holds head_dim/2 floats produced
+ * by rac_rope_inv_freq (host) and copied by the caller, so the call itself
+ * allocates nothing.  `base` is informational (inv_freq carries it). */
+int rac_rope_inv_freq(float *inv_freq_host, int head_dim, float base);
+int rac_rope_cache_dev(float *cos_out, float *sin_out, int max_seq, int head_dim, float base,
+                       const float *inv_freq_dev, void *stream);
+/* In-place RoPE on rows (b, h, t) at x + b*stride_b + h*stride_h + t*stride_t
+ * (element strides; head_dim contiguous).  Contiguous [B,H,T,D]:
+ * stride_b = H*T*D, stride_h = T*D, stride_t = D; the [B,T,H,D] storage of
+ * attention projections: stride_b = T*H*D, stride_h = D, stride_t = H*D. */
+int rac_rope_apply_dev(float *x, const float *cos_tab, const float *sin_tab, int batch,
+                       int n_heads, int seq, int head_dim, long stride_b, long stride_h,
+                       long stride_t, void *stream);
+
+/* ── reference launcher ABI (rac_kernels.hip:822-909; bound by
+ *    rac_torch_bind.cpp:16-45 with the stream as void*) ──────────────────── */
+
+void rac_launch_nn_iters(const float *A, const float *B, float *C, int M, int N, int K,
+                         float alpha, float beta, int iters, int mode, void *stream);
+void rac_launch_nt_iters(const float *A, const float *B, float *C, int M, int N, int K,
+                         float alpha, float beta, int iters, int mode, void *stream);
+void rac_launch_tn_iters(const float *A, const float *B, float *C, int M, int N, int K,
+                         float alpha, float beta, int iters, int mode, void *stream);
+void rac_launch_nn(const float *A, const float *B, float *C, int M, int N, int K, float alpha,
+                   float beta, void *stream);
+void rac_launch_nt(const float *A, const float *B, float *C, int M, int N, int K, float alpha,
+                   float beta, void *stream);
+void rac_launch_tn(const float *A, const float *B, float *C, int M, int N, int K, float alpha,
+                   float beta, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAC_EXT_H */

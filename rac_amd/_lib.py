@@ -1,0 +1,129 @@
+"""ctypes binding of librac_amd.so, the gfx950 kernel library.
+
+The library is loaded after torch so that it shares torch's HIP runtime
+(same soname, libamdhip64.so.7): device pointers and streams are then
+interchangeable between the two.  There is no fallback: if the library is
+missing or the device is not usable, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librac_amd.so")
+
+_lock = threading.Lock()
+_lib = None
+
+c_float_p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_l = ctypes.c_long
+_f = ctypes.c_float
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    # rac_ext.h — device pointers, explicit stream
+    "rac_gemm_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rac_softmax_dev": (_i, [_vp, _vp, _l, _l, _i, _vp]),
+    "rac_exp_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_silu_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_sigmoid_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_tanh_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_gelu_dev": (_i, [_vp, _vp, _l, _vp]),
+    "rac_relu_dev": (_i, [_vp, _vp, _l, _vp]),
+    "rac_rsqrt_dev": (_i, [_vp, _vp, _l, _vp]),
+    "rac_sincos_dev": (_i, [_vp, _vp, _vp, _l, _vp]),
+    "rac_rmsnorm_dev": (_i, [_vp, _vp, _vp, _f, _l, _l, _vp]),
+    "rac_layernorm_dev": (_i, [_vp, _vp, _vp, _vp, _f, _l, _l, _vp]),
+    "rac_rope_cache_dev": (_i, [_vp, _vp, _i, _i, _f, _vp, _vp]),
+    "rac_rope_inv_freq": (_i, [_vp, _i, _f]),
+    "rac_rope_apply_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l, _vp]),
+    "rac_last_error": (ctypes.c_char_p, []),
+    "rac_clear_error": (None, []),
+    "rac_set_cordic_iters": (None, [_i]),
+    "rac_get_cordic_iters": (_i, []),
+    "rac_set_cordic_mode": (None, [_i]),
+    "rac_get_cordic_mode": (_i, []),
+    "rac_set_stream": (None, [_vp]),
+    "rac_get_stream": (_vp, []),
+    "rac_version": (_i, []),
+    "rac_cordic_direction_bits": (_i, [_i, _vp]),
+    "rac_exp_gain_inverse": (_f, [_i]),
+    "rac_rsqrt_gain_inverse": (_f, []),
+    # rac.h — synchronous, pointer-agnostic
+    "rac_matmul": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "rac_softmax": (None, [_vp, _vp, _i]),
+    "rac_softmax_batch": (None, [_vp, _vp, _i, _i]),
+    "rac_exp": (_f, [_f]),
+    "rac_tanh": (_f, [_f]),
+    "rac_sigmoid": (_f, [_f]),
+    "rac_rsqrt": (_f, [_f]),
+    "rac_sincos": (None, [_f, c_float_p, c_float_p]),
+    "rac_rmsnorm": (None, [_vp, _vp, _vp, _f, _i, _i]),
+    "rac_layernorm": (None, [_vp, _vp, _vp, _vp, _f, _i, _i]),
+    "rac_rope_cache": (None, [_vp, _vp, _i, _i, _f]),
+    "rac_rope_apply": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "rac_relu": (None, [_vp, _vp, _i]),
+    "rac_gelu": (None, [_vp, _vp, _i]),
+    "rac_silu": (None, [_vp, _vp, _i]),
+    "rac_create_context": (_vp, [_i]),
+    "rac_destroy_context": (None, [_vp]),
+    "rac_query_capability": (_i, [_vp, _i]),
+    "rac_execute": (_i, [_vp, _i, _vp]),
+    # reference launcher ABI (rac_kernels.hip:822-909)
+    "rac_launch_nn_iters": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rac_launch_nt_iters": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rac_launch_tn_iters": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rac_launch_nn": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
+    "rac_launch_nt": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
+    "rac_launch_tn": (None, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
+}
+
+
+class RACError(RuntimeError):
+    """A librac_amd call failed (bad arguments, or a HIP error)."""
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load librac_amd.so (once) and declare every exported signature."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RACError(
+                f"{p} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C rac_amd/csrc` (hipcc, gfx950)")
+        lib = ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().rac_last_error()
+        raise RACError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()

@@ -1,0 +1,548 @@
+// rac_capi.hip — the C ABI of librac_amd.so.
+//
+// Three surfaces, all extern "C", plain pointers and sizes:
+//  1. rac.h (reference rac.h:85-346): synchronous, void, pointer-agnostic.
+//     Each pointer is classified per call; host buffers are staged through
+//     device memory, device buffers are used in place; the call returns once
+//     the result is in the caller's buffer.  Errors leave the output
+//     untouched and are reported through rac_last_error().
+//  2. rac_ext.h: device pointers, an explicit HIP stream, asynchronous,
+//     returning a status (0 = ok, <0 = rac_status-style error).  This is
+//     what the Python layer and hot loops call.
+//  3. The kernel-library launcher ABI of rac_kernels.hip:822-909
+//     (rac_launch_{nn,nt,tn}[_iters]), which rac_torch_bind.cpp binds.
+// Process-wide knobs: RAC_CORDIC_ITERS (default RAC_ITERS = 16, rac.h:41)
+// and RAC_CORDIC_MODE (default "cordic") seed rac_{set,get}_cordic_{iters,mode}.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <atomic>
+#include <mutex>
+#include <string>
+#include "rac_internal.hpp"
+#include "rac_tables.hpp"
+
+#define RAC_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace rac {
+
+// ── constants computed once on the host ──────────────────────────────────
+
+static double hyp_gain(int steps) {
+    double k = 1.0;
+    for (int j = 0; j < steps; j++) k *= sqrt(1.0 - ldexp(1.0, -2 * hyp_shift(j)));
+    return k;
+}
+
+const HostConsts& host_consts() {
+    static const HostConsts c = [] {
+        HostConsts h{};
+        h.exp_khinv[0] = 1.0f;
+        for (int n = 1; n <= 24; n++) h.exp_khinv[n] = (float)(1.0 / hyp_gain(n));
+        h.rsqrt_khinv = (float)(1.0 / hyp_gain(kRsqrtSteps));
+        return h;
+    }();
+    return c;
+}
+
+}  // namespace rac
+
+using namespace rac;
+
+enum {
+    RAC_OK = 0,
+    RAC_ERR_NULL_PTR = -1,     // rac_cpu.h:54-59
+    RAC_ERR_INVALID_DIM = -2,
+    RAC_ERR_ALLOC = -3,
+    RAC_ERR_DEVICE = -4,
+};
+
+// ── error channel ────────────────────────────────────────────────────────
+
+static thread_local char g_last_error[512] = "";
+
+static int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+static int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return RAC_OK;
+    (void)hipGetLastError();
+    return fail(RAC_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+RAC_EXPORT const char* rac_last_error(void) { return g_last_error; }
+RAC_EXPORT void rac_clear_error(void) { g_last_error[0] = '\0'; }
+
+// ── process knobs ────────────────────────────────────────────────────────
+
+static std::atomic<int> g_iters{0};     // 0 = not yet read from the environment
+static std::atomic<int> g_mode{-1};
+
+static int mode_from_string(const char* s) {
+    if (!s) return -1;
+    if (!strcmp(s, "fast") || !strcmp(s, "0")) return kModeFast;
+    if (!strcmp(s, "cordic") || !strcmp(s, "1")) return kModeCordic;
+    if (!strcmp(s, "shiftadd") || !strcmp(s, "2")) return kModeShiftAdd;
+    return -1;
+}
+
+RAC_EXPORT void rac_set_cordic_iters(int iters) {
+    // rac_torch_bind.cpp:205-210: <= 0 means the default, clamp to [1, 24]
+    g_iters.store(iters <= 0 ? 16 : clamp_iters(iters));
+}
+
+RAC_EXPORT int rac_get_cordic_iters(void) {
+    int v = g_iters.load();
+    if (v == 0) {
+        const char* e = getenv("RAC_CORDIC_ITERS");
+        v = e ? clamp_iters(atoi(e)) : 16;
+        if (e && atoi(e) <= 0) v = 16;
+        int expected = 0;
+        g_iters.compare_exchange_strong(expected, v);
+        v = g_iters.load();
+    }
+    return v;
+}
+
+RAC_EXPORT void rac_set_cordic_mode(int mode) {
+    // rac_torch_bind.cpp:216-219: out-of-range modes select FAST
+    g_mode.store((mode < 0 || mode > 2) ? kModeFast : mode);
+}
+
+RAC_EXPORT int rac_get_cordic_mode(void) {
+    int v = g_mode.load();
+    if (v < 0) {
+        int m = mode_from_string(getenv("RAC_CORDIC_MODE"));
+        if (m < 0) m = kModeCordic;
+        int expected = -1;
+        g_mode.compare_exchange_strong(expected, m);
+        v = g_mode.load();
+    }
+    return v;
+}
+
+// Stream used by the synchronous rac.h entry points (default: null stream).
+static std::atomic<hipStream_t> g_stream{nullptr};
+RAC_EXPORT void rac_set_stream(void* stream) { g_stream.store((hipStream_t)stream); }
+RAC_EXPORT void* rac_get_stream(void) { return (void*)g_stream.load(); }
+
+RAC_EXPORT int rac_version(void) { return 10000; }   // 1.0.0
+
+RAC_EXPORT int rac_cordic_direction_bits(int iters, int* d) {
+    if (!d) return fail(RAC_ERR_NULL_PTR, "rac_cordic_direction_bits: null output");
+    const int n = clamp_iters(iters);
+    for (int i = 0; i < n; i++) d[i] = cordic_dir(i);
+    return n;
+}
+
+RAC_EXPORT float rac_exp_gain_inverse(int iters) { return host_consts().exp_khinv[clamp_iters(iters)]; }
+RAC_EXPORT float rac_rsqrt_gain_inverse(void) { return host_consts().rsqrt_khinv; }
+
+// ── pointer staging for the synchronous API ──────────────────────────────
+
+static bool is_device_pointer(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+struct Staged {
+    void* host = nullptr;     // caller's host pointer (null when device)
+    void* dev = nullptr;      // pointer the kernel uses
+    size_t bytes = 0;
+    bool owned = false;
+    Staged() = default;
+    Staged(const Staged&) = delete;
+    Staged& operator=(const Staged&) = delete;
+    ~Staged() {
+        if (owned && dev) (void)hipFree(dev);
+    }
+    // Make `p` (bytes long) visible to the device; copy host contents in when
+    // `copy_in`.
+    int bind(const void* p, size_t nbytes, bool copy_in, hipStream_t s) {
+        bytes = nbytes;
+        if (!p) return RAC_OK;
+        if (is_device_pointer(p)) {
+            dev = const_cast<void*>(p);
+            return RAC_OK;
+        }
+        host = const_cast<void*>(p);
+        if (nbytes == 0) return RAC_OK;
+        if (hipMalloc(&dev, nbytes) != hipSuccess) {
+            (void)hipGetLastError();
+            dev = nullptr;
+            return fail(RAC_ERR_ALLOC, "device staging allocation of %zu bytes failed", nbytes);
+        }
+        owned = true;
+        if (copy_in)
+            return check_hip(hipMemcpyAsync(dev, p, nbytes, hipMemcpyHostToDevice, s), "staging copy in");
+        return RAC_OK;
+    }
+    int copy_out(hipStream_t s) {
+        if (!owned || !host || bytes == 0) return RAC_OK;
+        return check_hip(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, s), "staging copy out");
+    }
+    float* f() const { return static_cast<float*>(dev); }
+};
+
+static int finish_sync(hipStream_t s, int rc) {
+    const int rc2 = check_hip(hipStreamSynchronize(s), "stream synchronize");
+    return rc != RAC_OK ? rc : rc2;
+}
+
+// ── argument checks shared by both API styles ────────────────────────────
+
+static int check_gemm(const void* A, const void* B, const void* C, long M, long N, long K) {
+    if (!A || !B || !C) return fail(RAC_ERR_NULL_PTR, "rac_matmul: null operand");
+    if (M <= 0 || N <= 0 || K <= 0) return fail(RAC_ERR_INVALID_DIM, "rac_matmul: M, N, K must be > 0 (got %ld, %ld, %ld)", M, N, K);
+    if ((N + 15) / 16 > 2147483647L || (M + 15) / 16 > 65535L * 64)
+        return fail(RAC_ERR_INVALID_DIM, "rac_matmul: shape too large for one launch");
+    return RAC_OK;
+}
+
+static int check_rows(const char* who, const void* x, const void* y, long rows, long n) {
+    if (!x || !y) return fail(RAC_ERR_NULL_PTR, "%s: null buffer", who);
+    if (rows <= 0 || n <= 0) return fail(RAC_ERR_INVALID_DIM, "%s: rows and row length must be > 0", who);
+    if (rows > 16777215L) return fail(RAC_ERR_INVALID_DIM, "%s: at most 16777215 rows per call", who);
+    return RAC_OK;
+}
+
+static int check_rope(const void* x, const void* c, const void* s, long b, long h, long t, long d) {
+    if (!x || !c || !s) return fail(RAC_ERR_NULL_PTR, "rac_rope_apply: null buffer");
+    if (b <= 0 || h <= 0 || t <= 0 || d <= 0 || (d & 1))
+        return fail(RAC_ERR_INVALID_DIM, "rac_rope_apply: dims must be > 0 and head_dim even");
+    if ((b * h + 15) / 16 > 65535L) return fail(RAC_ERR_INVALID_DIM, "rac_rope_apply: batch*heads too large");
+    return RAC_OK;
+}
+
+// ═════════════════════════ rac_ext.h: device API ══════════════════════════
+
+RAC_EXPORT int rac_gemm_dev(const float* A, const float* B, float* C, int M, int N, int K,
+                            int trans_a, int trans_b, float alpha, float beta, int iters,
+                            int mode, void* stream) {
+    int rc = check_gemm(A, B, C, M, N, K);
+    if (rc) return rc;
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_gemm_dev: mode must be 0, 1 or 2");
+    return check_hip(gemm_launch(trans_a != 0, trans_b != 0, A, B, C, M, N, K, alpha, beta,
+                                 clamp_iters(iters), mode, (hipStream_t)stream),
+                     "rac_gemm_dev launch");
+}
+
+RAC_EXPORT int rac_softmax_dev(const float* x, float* y, long rows, long n, int iters, void* stream) {
+    int rc = check_rows("rac_softmax_dev", x, y, rows, n);
+    if (rc) return rc;
+    return check_hip(softmax_launch(x, y, rows, n, iters, (hipStream_t)stream), "rac_softmax_dev launch");
+}
+
+static int elt_dev(const char* who, int op, const float* x, float* y, long count, int iters, void* stream) {
+    if (!x || !y) return fail(RAC_ERR_NULL_PTR, "%s: null buffer", who);
+    if (count < 0) return fail(RAC_ERR_INVALID_DIM, "%s: negative count", who);
+    if (count == 0) return RAC_OK;
+    return check_hip(eltwise_launch(op, x, y, count, iters, (hipStream_t)stream), who);
+}
+
+RAC_EXPORT int rac_exp_dev(const float* x, float* y, long count, int iters, void* stream) {
+    return elt_dev("rac_exp_dev", kEltExp, x, y, count, iters, stream);
+}
+RAC_EXPORT int rac_silu_dev(const float* x, float* y, long count, int iters, void* stream) {
+    return elt_dev("rac_silu_dev", kEltSilu, x, y, count, iters, stream);
+}
+RAC_EXPORT int rac_sigmoid_dev(const float* x, float* y, long count, int iters, void* stream) {
+    return elt_dev("rac_sigmoid_dev", kEltSigmoid, x, y, count, iters, stream);
+}
+RAC_EXPORT int rac_tanh_dev(const float* x, float* y, long count, int iters, void* stream) {
+    return elt_dev("rac_tanh_dev", kEltTanh, x, y, count, iters, stream);
+}
+RAC_EXPORT int rac_gelu_dev(const float* x, float* y, long count, void* stream) {
+    return elt_dev("rac_gelu_dev", kEltGelu, x, y, count, 0, stream);
+}
+RAC_EXPORT int rac_relu_dev(const float* x, float* y, long count, void* stream) {
+    return elt_dev("rac_relu_dev", kEltRelu, x, y, count, 0, stream);
+}
+
+RAC_EXPORT int rac_rsqrt_dev(const float* x, float* y, long count, void* stream) {
+    if (!x || !y) return fail(RAC_ERR_NULL_PTR, "rac_rsqrt_dev: null buffer");
+    if (count < 0) return fail(RAC_ERR_INVALID_DIM, "rac_rsqrt_dev: negative count");
+    if (count == 0) return RAC_OK;
+    return check_hip(rsqrt_launch(x, y, count, (hipStream_t)stream), "rac_rsqrt_dev launch");
+}
+
+RAC_EXPORT int rac_sincos_dev(const float* theta, float* s, float* c, long count, void* stream) {
+    if (!theta || !s || !c) return fail(RAC_ERR_NULL_PTR, "rac_sincos_dev: null buffer");
+    if (count < 0) return fail(RAC_ERR_INVALID_DIM, "rac_sincos_dev: negative count");
+    if (count == 0) return RAC_OK;
+    return check_hip(sincos_launch(theta, s, c, count, (hipStream_t)stream), "rac_sincos_dev launch");
+}
+
+RAC_EXPORT int rac_rmsnorm_dev(const float* x, float* y, const float* gamma, float eps, long rows,
+                               long d, void* stream) {
+    int rc = check_rows("rac_rmsnorm_dev", x, y, rows, d);
+    if (rc) return rc;
+    return check_hip(rmsnorm_launch(x, y, gamma, eps, rows, d, (hipStream_t)stream), "rac_rmsnorm_dev launch");
+}
+
+RAC_EXPORT int rac_layernorm_dev(const float* x, float* y, const float* gamma, const float* beta,
+                                 float eps, long rows, long d, void* stream) {
+    int rc = check_rows("rac_layernorm_dev", x, y, rows, d);
+    if (rc) return rc;
+    return check_hip(layernorm_launch(x, y, gamma, beta, eps, rows, d, (hipStream_t)stream),
+                     "rac_layernorm_dev launch");
+}
+
+// inv_freq[i] = 1.0f / powf(base, (2.0f*i)/head_dim) on the host, as
+// rac_cpu.c:588-589 computes it (glibc powf; the angle p*inv_freq and the
+// CORDIC rotation run on the device).
+static void rope_inv_freq(float* inv, int head_dim, float base) {
+    const int half = head_dim / 2;
+    for (int i = 0; i < half; i++) {
+        const float exponent = (2.0f * (float)i) / (float)head_dim;
+        inv[i] = 1.0f / powf(base, exponent);
+    }
+}
+
+RAC_EXPORT int rac_rope_cache_dev(float* cos_out, float* sin_out, int max_seq, int head_dim,
+                                  float base, const float* inv_freq_dev, void* stream) {
+    // inv_freq_dev: device buffer of head_dim/2 floats filled by
+    // rac_rope_inv_freq (the caller owns it, so no allocation happens here).
+    if (!cos_out || !sin_out || !inv_freq_dev) return fail(RAC_ERR_NULL_PTR, "rac_rope_cache_dev: null buffer");
+    if (max_seq <= 0 || head_dim <= 0 || (head_dim & 1))
+        return fail(RAC_ERR_INVALID_DIM, "rac_rope_cache_dev: max_seq > 0 and even head_dim > 0 required");
+    (void)base;
+    return check_hip(rope_cache_launch(cos_out, sin_out, inv_freq_dev, max_seq, head_dim / 2,
+                                       (hipStream_t)stream),
+                     "rac_rope_cache_dev launch");
+}
+
+RAC_EXPORT int rac_rope_inv_freq(float* inv_freq_host, int head_dim, float base) {
+    if (!inv_freq_host) return fail(RAC_ERR_NULL_PTR, "rac_rope_inv_freq: null buffer");
+    if (head_dim <= 0 || (head_dim & 1)) return fail(RAC_ERR_INVALID_DIM, "rac_rope_inv_freq: even head_dim > 0 required");
+    rope_inv_freq(inv_freq_host, head_dim, base);
+    return RAC_OK;
+}
+
+RAC_EXPORT int rac_rope_apply_dev(float* x, const float* cos_tab, const float* sin_tab, int batch,
+                                  int n_heads, int seq, int head_dim, long stride_b, long stride_h,
+                                  long stride_t, void* stream) {
+    int rc = check_rope(x, cos_tab, sin_tab, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    return check_hip(rope_apply_launch(x, cos_tab, sin_tab, batch, n_heads, seq, head_dim, stride_b,
+                                       stride_h, stride_t, (hipStream_t)stream),
+                     "rac_rope_apply_dev launch");
+}
+
+// ═════════════════ reference launcher ABI (rac_kernels.hip) ═══════════════
+
+RAC_EXPORT void rac_launch_nn_iters(const float* A, const float* B, float* C, int M, int N, int K,
+                                    float alpha, float beta, int iters, int mode, void* stream) {
+    (void)rac_gemm_dev(A, B, C, M, N, K, 0, 0, alpha, beta, iters, mode, stream);
+}
+RAC_EXPORT void rac_launch_nt_iters(const float* A, const float* B, float* C, int M, int N, int K,
+                                    float alpha, float beta, int iters, int mode, void* stream) {
+    (void)rac_gemm_dev(A, B, C, M, N, K, 0, 1, alpha, beta, iters, mode, stream);
+}
+RAC_EXPORT void rac_launch_tn_iters(const float* A, const float* B, float* C, int M, int N, int K,
+                                    float alpha, float beta, int iters, int mode, void* stream) {
+    (void)rac_gemm_dev(A, B, C, M, N, K, 1, 0, alpha, beta, iters, mode, stream);
+}
+RAC_EXPORT void rac_launch_nn(const float* A, const float* B, float* C, int M, int N, int K,
+                              float alpha, float beta, void* stream) {
+    rac_launch_nn_iters(A, B, C, M, N, K, alpha, beta, 24, kModeFast, stream);
+}
+RAC_EXPORT void rac_launch_nt(const float* A, const float* B, float* C, int M, int N, int K,
+                              float alpha, float beta, void* stream) {
+    rac_launch_nt_iters(A, B, C, M, N, K, alpha, beta, 24, kModeFast, stream);
+}
+RAC_EXPORT void rac_launch_tn(const float* A, const float* B, float* C, int M, int N, int K,
+                              float alpha, float beta, void* stream) {
+    rac_launch_tn_iters(A, B, C, M, N, K, alpha, beta, 24, kModeFast, stream);
+}
+
+// ══════════════════════ rac.h: synchronous API ════════════════════════════
+
+RAC_EXPORT void rac_matmul(float* A, float* B, float* C, int M, int N, int K) {
+    if (check_gemm(A, B, C, M, N, K)) return;
+    hipStream_t s = g_stream.load();
+    Staged a, b, c;
+    int rc = a.bind(A, sizeof(float) * (size_t)M * K, true, s);
+    if (!rc) rc = b.bind(B, sizeof(float) * (size_t)K * N, true, s);
+    if (!rc) rc = c.bind(C, sizeof(float) * (size_t)M * N, false, s);
+    if (!rc) rc = check_hip(gemm_launch(0, 0, a.f(), b.f(), c.f(), M, N, K, 1.0f, 0.0f,
+                                        rac_get_cordic_iters(), rac_get_cordic_mode(), s),
+                            "rac_matmul launch");
+    if (!rc) rc = c.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+static void softmax_sync(const float* x, float* out, long rows, long n) {
+    if (check_rows("rac_softmax", x, out, rows, n)) return;
+    hipStream_t s = g_stream.load();
+    const size_t bytes = sizeof(float) * (size_t)rows * n;
+    Staged a, b;
+    int rc = a.bind(x, bytes, true, s);
+    if (!rc) rc = b.bind(out, bytes, false, s);
+    if (!rc) rc = check_hip(softmax_launch(a.f(), b.f(), rows, n, rac_get_cordic_iters(), s), "rac_softmax launch");
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_softmax(float* x, float* out, int n) { softmax_sync(x, out, 1, n); }
+
+// rac_cpu.h:172 signature
+RAC_EXPORT void rac_softmax_batch(const float* x, float* out, int batch, int n) {
+    softmax_sync(x, out, batch, n);
+}
+
+static void elt_sync(const char* who, int op, const float* x, float* out, long n, int iters) {
+    if (!x || !out) { fail(RAC_ERR_NULL_PTR, "%s: null buffer", who); return; }
+    if (n <= 0) return;
+    hipStream_t s = g_stream.load();
+    Staged a, b;
+    int rc = a.bind(x, sizeof(float) * (size_t)n, true, s);
+    if (!rc) rc = b.bind(out, sizeof(float) * (size_t)n, false, s);
+    if (!rc) rc = check_hip(eltwise_launch(op, a.f(), b.f(), n, iters, s), who);
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+// rac_cpu.h:169-171 batch activations
+RAC_EXPORT void rac_relu(const float* x, float* out, int n) { elt_sync("rac_relu", kEltRelu, x, out, n, 0); }
+RAC_EXPORT void rac_gelu(const float* x, float* out, int n) { elt_sync("rac_gelu", kEltGelu, x, out, n, 0); }
+RAC_EXPORT void rac_silu(const float* x, float* out, int n) {
+    elt_sync("rac_silu", kEltSilu, x, out, n, rac_get_cordic_iters());
+}
+
+static float scalar_elt(int op, float x) {
+    float y = 0.0f;
+    elt_sync("rac scalar op", op, &x, &y, 1, rac_get_cordic_iters());
+    return y;
+}
+
+RAC_EXPORT float rac_exp(float x) { return scalar_elt(kEltExp, x); }
+RAC_EXPORT float rac_tanh(float x) { return scalar_elt(kEltTanh, x); }
+RAC_EXPORT float rac_sigmoid(float x) { return scalar_elt(kEltSigmoid, x); }
+
+RAC_EXPORT float rac_rsqrt(float x) {
+    hipStream_t s = g_stream.load();
+    Staged a, b;
+    float y = 0.0f;
+    int rc = a.bind(&x, sizeof(float), true, s);
+    if (!rc) rc = b.bind(&y, sizeof(float), false, s);
+    if (!rc) rc = check_hip(rsqrt_launch(a.f(), b.f(), 1, s), "rac_rsqrt launch");
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+    return y;
+}
+
+RAC_EXPORT void rac_sincos(float theta, float* sp, float* cp) {
+    if (!sp || !cp) { fail(RAC_ERR_NULL_PTR, "rac_sincos: null output"); return; }
+    hipStream_t s = g_stream.load();
+    float sv = 0.0f, cv = 0.0f;
+    Staged a, b, c;
+    int rc = a.bind(&theta, sizeof(float), true, s);
+    if (!rc) rc = b.bind(&sv, sizeof(float), false, s);
+    if (!rc) rc = c.bind(&cv, sizeof(float), false, s);
+    if (!rc) rc = check_hip(sincos_launch(a.f(), b.f(), c.f(), 1, s), "rac_sincos launch");
+    if (!rc) rc = b.copy_out(s);
+    if (!rc) rc = c.copy_out(s);
+    if (finish_sync(s, rc) == RAC_OK) { *sp = sv; *cp = cv; }
+}
+
+RAC_EXPORT void rac_rmsnorm(const float* x, float* y, const float* gamma, float eps, int rows, int d) {
+    if (check_rows("rac_rmsnorm", x, y, rows, d)) return;
+    hipStream_t s = g_stream.load();
+    const size_t bytes = sizeof(float) * (size_t)rows * d;
+    Staged a, b, g;
+    int rc = a.bind(x, bytes, true, s);
+    if (!rc) rc = b.bind(y, bytes, false, s);
+    if (!rc) rc = g.bind(gamma, sizeof(float) * (size_t)d, true, s);
+    if (!rc) rc = check_hip(rmsnorm_launch(a.f(), b.f(), g.f(), eps, rows, d, s), "rac_rmsnorm launch");
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_layernorm(const float* x, float* y, const float* gamma, const float* beta,
+                              float eps, int rows, int d) {
+    if (check_rows("rac_layernorm", x, y, rows, d)) return;
+    hipStream_t s = g_stream.load();
+    const size_t bytes = sizeof(float) * (size_t)rows * d;
+    Staged a, b, g, bt;
+    int rc = a.bind(x, bytes, true, s);
+    if (!rc) rc = b.bind(y, bytes, false, s);
+    if (!rc) rc = g.bind(gamma, sizeof(float) * (size_t)d, true, s);
+    if (!rc) rc = bt.bind(beta, sizeof(float) * (size_t)d, true, s);
+    if (!rc) rc = check_hip(layernorm_launch(a.f(), b.f(), g.f(), bt.f(), eps, rows, d, s), "rac_layernorm launch");
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_rope_cache(float* cos_out, float* sin_out, int max_seq, int head_dim, float base) {
+    if (!cos_out || !sin_out) { fail(RAC_ERR_NULL_PTR, "rac_rope_cache: null buffer"); return; }
+    if (max_seq <= 0 || head_dim <= 0 || (head_dim & 1)) {
+        fail(RAC_ERR_INVALID_DIM, "rac_rope_cache: max_seq > 0 and even head_dim > 0 required");
+        return;
+    }
+    hipStream_t s = g_stream.load();
+    const int half = head_dim / 2;
+    const size_t bytes = sizeof(float) * (size_t)max_seq * half;
+    std::string inv_host(sizeof(float) * (size_t)half, '\0');
+    rope_inv_freq(reinterpret_cast<float*>(&inv_host[0]), head_dim, base);
+    Staged c, sn, inv;
+    int rc = c.bind(cos_out, bytes, false, s);
+    if (!rc) rc = sn.bind(sin_out, bytes, false, s);
+    if (!rc) rc = inv.bind(&inv_host[0], inv_host.size(), true, s);
+    if (!rc) rc = check_hip(rope_cache_launch(c.f(), sn.f(), inv.f(), max_seq, half, s), "rac_rope_cache launch");
+    if (!rc) rc = c.copy_out(s);
+    if (!rc) rc = sn.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_rope_apply(float* x, const float* cos_tab, const float* sin_tab, int batch,
+                               int n_heads, int seq, int head_dim) {
+    if (check_rope(x, cos_tab, sin_tab, batch, n_heads, seq, head_dim)) return;
+    hipStream_t s = g_stream.load();
+    const size_t xbytes = sizeof(float) * (size_t)batch * n_heads * seq * head_dim;
+    const size_t tbytes = sizeof(float) * (size_t)seq * (head_dim / 2);
+    Staged a, c, sn;
+    int rc = a.bind(x, xbytes, true, s);
+    if (!rc) rc = c.bind(cos_tab, tbytes, true, s);
+    if (!rc) rc = sn.bind(sin_tab, tbytes, true, s);
+    const long st = head_dim, sh = (long)seq * head_dim, sb = (long)n_heads * sh;
+    if (!rc) rc = check_hip(rope_apply_launch(a.f(), c.f(), sn.f(), batch, n_heads, seq, head_dim, sb, sh, st, s),
+                            "rac_rope_apply launch");
+    if (!rc) rc = a.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+// ── context (rac.h:85-88; the reference's HIP backend is a stub,
+//    rac_hip.cpp:416-435: every op but RAC_OP_EXTENDED is "supported") ────
+
+struct rac_context_t {
+    int backend;
+};
+
+RAC_EXPORT rac_context_t* rac_create_context(int backend) {
+    rac_context_t* c = (rac_context_t*)malloc(sizeof(rac_context_t));
+    if (c) c->backend = backend;
+    return c;
+}
+RAC_EXPORT void rac_destroy_context(rac_context_t* ctx) { free(ctx); }
+RAC_EXPORT int rac_query_capability(rac_context_t* ctx, int op) {
+    (void)ctx;
+    return op == 0xFF ? 0 : 1;
+}
+RAC_EXPORT int rac_execute(rac_context_t* ctx, int op, void* desc) {
+    (void)ctx; (void)op; (void)desc;
+    return 0;
+}

@@ -1,0 +1,208 @@
+// rac_gemm.hip — rotate-project-accumulate GEMM for gfx950 (VALU, no MFMA).
+//
+// C[M,N] = alpha * op(A) @ op(B) (+ beta * C), row-major, with the MAC of
+// rac_fma_iters (rac_kernels.hip:204-219):
+//   FAST     fmaf(a ^ sign(b), |b|, acc)                  == fmaf(a, b, acc)
+//   CORDIC   n circular micro-rotations of (a ^ sign(b), 0), x * 1/K-hat(n),
+//            projected on |b| and accumulated               (rac_math.hpp)
+//   SHIFTADD acc + integer shift-add product of the top n mantissa bits of b
+// op(A) = A or A^T (A stored [K,M], the TN launcher); op(B) = B or B^T
+// (B stored [N,K], the NT launcher).  Each output keeps ONE accumulator over
+// k = 0..K-1 in order, like every reference tile shape, so results do not
+// depend on the tiling; out-of-range operands are zero-padded (a zero MAC
+// leaves acc unchanged).
+//
+// Design: CORDIC mode costs ~2n VALU lane-ops per MAC, so the kernel is
+// VALU-bound by two orders of magnitude over LDS and HBM traffic.  A 64x64
+// block tile (4x4 outputs per lane, 256 lanes = 4 wave64) staged through LDS
+// with BK = 16 keeps 16 independent MAC chains per lane for latency hiding
+// and reads only 2 ds_read_b128 per 16 MACs.  FAST mode (1 FMA per MAC)
+// uses a 128x128 tile with 8x8 per lane so LDS traffic stays below the VALU
+// rate.  The next K-tile is prefetched into registers while the current one
+// is computed.
+#include <hip/hip_runtime.h>
+#include "rac_math.hpp"
+#include "rac_internal.hpp"
+
+namespace rac {
+
+template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
+struct GemmCfg {
+    static constexpr int kThreads = 256;
+    static constexpr int kBM = 16 * TM;
+    static constexpr int kBN = 16 * TN;
+    static constexpr int kBK = 16;
+    static constexpr int kPad = 4;
+    static constexpr int kALoads = kBM * kBK / kThreads;
+    static constexpr int kBLoads = kBN * kBK / kThreads;
+};
+
+template <int MODE, int NITER>
+__device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc,
+                                     int iters, float kinv) {
+    if constexpr (MODE == kModeFast) {
+        return __builtin_fmaf(a, b, acc);
+    } else if constexpr (MODE == kModeCordic) {
+        if constexpr (NITER > 0) {
+            return mac_cordic<NITER>(a, b, bsign, acc);
+        } else {
+            const float x0 = as_f(as_u(a) ^ bsign);
+            const float xr = cordic_rot_x_rt(x0, iters);
+            return __builtin_fmaf(xr * kinv, __builtin_fabsf(b), acc);
+        }
+    } else {
+        return acc + shiftadd_mul(a, b, iters);
+    }
+}
+
+template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
+__global__ __launch_bounds__(256) void gemm_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+    int M, int N, int K, float alpha, float beta, int iters, float kinv)
+{
+    using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
+    constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
+    __shared__ __attribute__((aligned(16))) float sA[BK][BM + PAD];
+    __shared__ __attribute__((aligned(16))) float sB[BK][BN + PAD];
+
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+    const long m0 = (long)blockIdx.y * BM, n0 = (long)blockIdx.x * BN;
+
+    float acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+
+    float ra[Cfg::kALoads], rb[Cfg::kBLoads];
+
+    // Global -> register staging of one K-tile; element (m, k) of op(A) and
+    // (k, n) of op(B), zero outside the matrix.  Index order is chosen so
+    // consecutive lanes read consecutive addresses.
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int r = 0; r < Cfg::kALoads; r++) {
+            const int idx = tid + r * 256;
+            int mm, kk;
+            if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
+            else { mm = idx / BK; kk = idx % BK; }
+            const long gm = m0 + mm, gk = (long)k0 + kk;
+            float v = 0.0f;
+            if (gm < M && gk < K) v = TA ? A[gk * M + gm] : A[gm * K + gk];
+            ra[r] = v;
+        }
+#pragma unroll
+        for (int r = 0; r < Cfg::kBLoads; r++) {
+            const int idx = tid + r * 256;
+            int nn, kk;
+            if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
+            else { kk = idx / BN; nn = idx % BN; }
+            const long gn = n0 + nn, gk = (long)k0 + kk;
+            float v = 0.0f;
+            if (gn < N && gk < K) v = TB ? B[gn * K + gk] : B[gk * N + gn];
+            rb[r] = v;
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int r = 0; r < Cfg::kALoads; r++) {
+            const int idx = tid + r * 256;
+            int mm, kk;
+            if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
+            else { mm = idx / BK; kk = idx % BK; }
+            sA[kk][mm] = ra[r];
+        }
+#pragma unroll
+        for (int r = 0; r < Cfg::kBLoads; r++) {
+            const int idx = tid + r * 256;
+            int nn, kk;
+            if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
+            else { kk = idx / BN; nn = idx % BN; }
+            sB[kk][nn] = rb[r];
+        }
+    };
+
+    load_tile(0);
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        __syncthreads();            // previous tile fully consumed
+        store_tile();
+        __syncthreads();
+        if (k0 + BK < K) load_tile(k0 + BK);   // prefetch overlaps the MACs
+#pragma unroll 1
+        for (int kk = 0; kk < BK; kk++) {
+            float a[TM], b[TN];
+            uint32_t bs[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
+                a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
+                b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) bs[j] = as_u(b[j]) & 0x80000000u;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const long gm = m0 + ty * TM + i;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const long gn = n0 + tx * TN + j;
+            if (gn >= N) continue;
+            float* cp = C + gm * N + gn;
+            // rac_kernels.hip:267-272
+            *cp = (beta != 0.0f) ? __builtin_fmaf(alpha, acc[i][j], beta * *cp)
+                                 : alpha * acc[i][j];
+        }
+    }
+}
+
+template <int MODE, int NITER, bool TA, bool TB>
+static hipError_t launch_cfg(const float* A, const float* B, float* C, int M, int N, int K,
+                             float alpha, float beta, int iters, hipStream_t stream) {
+    constexpr int TM = (MODE == kModeFast) ? 8 : 4;
+    constexpr int TN = TM;
+    using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
+    const float kinv = cordic_kinv(iters);
+    dim3 grid((unsigned)((N + Cfg::kBN - 1) / Cfg::kBN), (unsigned)((M + Cfg::kBM - 1) / Cfg::kBM));
+    hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN>), grid, dim3(256), 0, stream,
+                       A, B, C, M, N, K, alpha, beta, iters, kinv);
+    return hipGetLastError();
+}
+
+template <int MODE, int NITER>
+static hipError_t launch_layout(int ta, int tb, const float* A, const float* B, float* C,
+                                int M, int N, int K, float alpha, float beta, int iters,
+                                hipStream_t s) {
+    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false>(A, B, C, M, N, K, alpha, beta, iters, s);
+    if (!ta && tb) return launch_cfg<MODE, NITER, false, true>(A, B, C, M, N, K, alpha, beta, iters, s);
+    if (ta && !tb) return launch_cfg<MODE, NITER, true, false>(A, B, C, M, N, K, alpha, beta, iters, s);
+    return launch_cfg<MODE, NITER, true, true>(A, B, C, M, N, K, alpha, beta, iters, s);
+}
+
+hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
+                       int M, int N, int K, float alpha, float beta, int iters, int mode,
+                       hipStream_t s) {
+    if (mode == kModeFast) return launch_layout<kModeFast, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+    if (mode == kModeShiftAdd) return launch_layout<kModeShiftAdd, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+    switch (iters) {
+        case 8: return launch_layout<kModeCordic, 8>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+        case 16: return launch_layout<kModeCordic, 16>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+        case 24: return launch_layout<kModeCordic, 24>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+        default: return launch_layout<kModeCordic, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+    }
+}
+
+}  // namespace rac

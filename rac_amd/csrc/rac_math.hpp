@@ -1,0 +1,243 @@
+// rac_math.hpp — per-element CORDIC arithmetic of the gfx950 kernels.
+//
+// Every function here is written so that each IEEE rounding is explicit
+// (sources are compiled with -ffp-contract=off; fused steps are spelled
+// __builtin_fmaf).  The CPU checker in oracle/rac_oracle.c evaluates the
+// same roundings, so results agree bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include "rac_tables.hpp"
+
+namespace rac {
+
+__device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
+
+// 16-byte streaming (non-temporal) global load/store: data touched once.
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld4_stream(const float4* p) {
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st4_stream(float4* p, float4 v) {
+    const v4f w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(p));
+}
+
+// ── CORDIC-mode MAC (rac_kernels.hip:140-185) ────────────────────────────
+//
+// R_n(x0): x output of n circular micro-rotations of (x0, 0) starting at
+// angle 0 (directions cordic_dir(i)).  Micro-rotation 0 maps (x0, 0) to
+// (x0, x0); micro-rotation 1 gives (fl(1.5 x0), x0/2), the latter exact, so
+// y is carried doubled (yh = x0); each later micro-rotation is two FMAs with
+// power-of-two constants; the final y update is never needed.  Bit-identical
+// to the literal chain for all finite x0 whose products stay normal.
+template <int N>
+__device__ __forceinline__ float cordic_rot_x(float x0) {
+    static_assert(N >= 1 && N <= kMaxIters, "iteration count");
+    if constexpr (N == 1) {
+        return x0;
+    } else {
+        float x = x0 * 1.5f;
+        float yh = x0;
+#pragma unroll
+        for (int i = 2; i < N; i++) {
+            const float xn = __builtin_fmaf(chain_cx(i), yh, x);
+            if (i + 1 < N) yh = __builtin_fmaf(chain_cy(i), x, yh);
+            x = xn;
+        }
+        return x;
+    }
+}
+
+// Constant tables for the run-time iteration count paths (wave-uniform
+// indices -> scalar loads).  Built from the same constexpr definitions.
+struct StepTables {
+    float cx[kMaxIters];
+    float cy[kMaxIters];
+    float hS[kMaxIters];
+    float hC[kMaxIters];
+};
+constexpr StepTables make_step_tables() {
+    StepTables t{};
+    for (int i = 0; i < kMaxIters; i++) {
+        t.cx[i] = chain_cx(i);
+        t.cy[i] = chain_cy(i);
+        t.hS[i] = hyp_S(i);
+        t.hC[i] = hyp_C(i);
+    }
+    return t;
+}
+static __constant__ StepTables g_steps = make_step_tables();
+
+// The same chain with a run-time iteration count; used for n outside the
+// specialised set.
+__device__ __forceinline__ float cordic_rot_x_rt(float x0, int n) {
+    if (n == 1) return x0;
+    float x = x0 * 1.5f;
+    float yh = x0;
+    for (int i = 2; i < n; i++) {
+        const float xn = __builtin_fmaf(g_steps.cx[i], yh, x);
+        yh = __builtin_fmaf(g_steps.cy[i], x, yh);
+        x = xn;
+    }
+    return x;
+}
+
+// One CORDIC-mode multiply-accumulate: b is the angle index (sign -> 0 or pi,
+// applied as a negation of (a, 0)) and magnitude |b|; the rotated x, gain
+// compensated by kinv, is projected on |b| and accumulated by one FMA.
+// `bsign` is b's sign bit, extracted once per B element by the caller.
+template <int N>
+__device__ __forceinline__ float mac_cordic(float a, float b, uint32_t bsign, float acc) {
+    const float x0 = as_f(as_u(a) ^ bsign);
+    const float xr = cordic_rot_x<N>(x0);
+    return __builtin_fmaf(xr * cordic_kinv(N), __builtin_fabsf(b), acc);
+}
+
+// ── SHIFTADD-mode product (rac_kernels.hip:85-122) ───────────────────────
+__device__ __forceinline__ float shiftadd_mul(float a, float b, int iters) {
+    if (a == 0.0f || b == 0.0f) return 0.0f;
+    const uint32_t ai = as_u(a), bi = as_u(b);
+    const uint32_t sign = (ai ^ bi) & 0x80000000u;
+    const int exp_a = (int)((ai >> 23) & 0xFFu) - 127;
+    const int exp_b = (int)((bi >> 23) & 0xFFu) - 127;
+    const uint64_t ma = 0x00800000u | (ai & 0x007FFFFFu);
+    const uint32_t mb = 0x00800000u | (bi & 0x007FFFFFu);
+    // top `lim` bits of mb, each adding ma at its weight: the bit-serial sum
+    // equals ma * (mb with the low 24-lim bits cleared); written as a loop of
+    // shifts and masked adds (no multiplier), as the reference does.
+    uint64_t prod = 0;
+    const int lim = iters < 1 ? 1 : (iters > 24 ? 24 : iters);
+    for (int i = 0; i < lim; i++) {
+        const uint64_t bit = (mb >> (23 - i)) & 1u;
+        prod += (ma << (23 - i)) & (0ull - bit);
+    }
+    if (prod == 0) return 0.0f;
+    const int top = 63 - __clzll((long long)prod);
+    const int shift_r = top - 23;
+    uint32_t mantissa;
+    if (shift_r > 0) mantissa = (uint32_t)(prod >> shift_r) & 0x007FFFFFu;
+    else if (shift_r < 0) mantissa = (uint32_t)(prod << -shift_r) & 0x007FFFFFu;
+    else mantissa = (uint32_t)prod & 0x007FFFFFu;
+    const int rexp = exp_a + exp_b + (top - 46) + 127;
+    if (rexp <= 0 || rexp >= 0xFF) return 0.0f;
+    return as_f(sign | ((uint32_t)(rexp & 0xFF) << 23) | mantissa);
+}
+
+// ── Hyperbolic CORDIC e^x (product-register form) ────────────────────────
+//
+// Range reduction k = trunc(fma(x, 1/ln2, +-0.5)), r = fma(-k, ln2, x)
+// (rac_alu.c:560-561 as its build contracts them); then n Walther steps on
+// the sum register p = x + y of the hyperbolic rotation of (1, 0) by r:
+// p <- p (1 + d 2^-s) as one FMA, z <- z - d atanh(2^-s) as one FMA with
+// the constant atanh(2^-s) 2^s, d = copysign(1, z) (rac_alu.c:246).  Output
+// (p / K_h(n)) 2^k through the exponent field (rac_alu.c:572-581).
+__device__ __forceinline__ void exp_reduce(float x, int& k, float& r) {
+    float t = __builtin_fmaf(x, kInvLn2, (x >= 0.0f) ? 0.5f : -0.5f);
+    t = fminf(fmaxf(t, -1073741824.0f), 1073741824.0f);
+    k = (int)t;
+    r = __builtin_fmaf(-(float)k, kLn2, x);
+}
+
+__device__ __forceinline__ float exp_scale(float er, int k) {
+    const int bias_k = k + 127;
+    const float scaled = er * as_f((uint32_t)(bias_k & 0xFF) << 23);
+    float res = (bias_k > 254) ? er * __builtin_inff() : scaled;
+    return (bias_k < 0) ? 0.0f : res;
+}
+
+template <int N>
+__device__ __forceinline__ float exp_cordic(float x, float khinv) {
+    int k;
+    float r;
+    exp_reduce(x, k, r);
+    float p = 1.0f, z = r;
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        const float ds = __builtin_copysignf(hyp_S(j), z);
+        p = __builtin_fmaf(ds, p, p);
+        if (j + 1 < N) z = __builtin_fmaf(-ds, hyp_C(j), z);
+    }
+    const float res = exp_scale(p * khinv, k);
+    return (x != x) ? x : res;
+}
+
+__device__ __forceinline__ float exp_cordic_rt(float x, int n, float khinv) {
+    int k;
+    float r;
+    exp_reduce(x, k, r);
+    float p = 1.0f, z = r;
+    for (int j = 0; j < n; j++) {
+        const float ds = __builtin_copysignf(g_steps.hS[j], z);
+        p = __builtin_fmaf(ds, p, p);
+        z = __builtin_fmaf(-ds, g_steps.hC[j], z);
+    }
+    const float res = exp_scale(p * khinv, k);
+    return (x != x) ? x : res;
+}
+
+// ── rsqrt by hyperbolic vectoring ────────────────────────────────────────
+//
+// rac_rsqrt's contract (rac_cpu.c:330-335): v <= 0 -> 0, NaN -> NaN,
+// +inf -> 0.  v = m 4^e, m in [0.5, 2); vectoring (m + 1/4, m - 1/4) to
+// y = 0 leaves x = K_h sqrt(m); 1/sqrt(v) = (1 / (x / K_h)) 2^-e.
+// khinv16 = 1/K_h over the 16-step schedule (host computed).
+__device__ __forceinline__ float rsqrt_cordic(float v, float khinv16) {
+    if (v != v) return v;
+    if (!(v > 0.0f) || v == __builtin_inff()) return 0.0f;
+    int ex = __builtin_amdgcn_frexp_expf(v);
+    float mant = __builtin_amdgcn_frexp_mantf(v);   // v = mant 2^ex, mant in [0.5, 1)
+    float m;
+    int e;
+    if (ex & 1) { m = mant * 2.0f; e = (ex - 1) / 2; }
+    else { m = mant; e = ex / 2; }
+    float X = m + 0.25f, Y = m - 0.25f;
+#pragma unroll
+    for (int j = 0; j < kRsqrtSteps; j++) {
+        const float ds = __builtin_copysignf(hyp_S(j), Y);
+        const float Xn = __builtin_fmaf(-ds, Y, X);
+        const float Yn = __builtin_fmaf(-ds, X, Y);
+        X = Xn;
+        Y = Yn;
+    }
+    const float root = X * khinv16;
+    const float r = 1.0f / root;
+    return __builtin_ldexpf(r, -e);
+}
+
+// ── Circular CORDIC sin/cos (rac_cpu.c:90-118, 322-328) ──────────────────
+// One 16-step rotation of (K_INV, 0) by theta, with the reference's
+// sequential float wrap of theta into (-pi, pi] (a loop, not a remainder:
+// its rounding drift at large angles is part of the table's values).
+// The reference's wrap loop never terminates for |theta| >= 2^27 or +-inf
+// (theta - 2pi rounds back to theta); such angles return NaN here instead.
+// Below 2^27 every subtraction makes progress, so the loop is bounded.
+constexpr float kWrapLimit = 134217728.0f;   // 2^27
+
+__device__ __forceinline__ void sincos_cordic(float theta, float& s, float& c) {
+    if (!(__builtin_fabsf(theta) < kWrapLimit)) {
+        s = c = __builtin_nanf("");
+        return;
+    }
+    while (theta > kPi) theta -= kTau;
+    while (theta <= -kPi) theta += kTau;
+    float x = kKInv, y = 0.0f;
+    if (theta > kPi * 0.5f) { x = -x; y = -y; theta -= kPi; }
+    else if (theta < -kPi * 0.5f) { x = -x; y = -y; theta += kPi; }
+    float angle = theta, scale = 1.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float d = (angle >= 0.0f) ? 1.0f : -1.0f;
+        const float xn = x - d * y * scale;
+        const float yn = y + d * x * scale;
+        angle -= d * kAtan[i];
+        x = xn;
+        y = yn;
+        scale *= 0.5f;
+    }
+    c = x;
+    s = y;
+}
+
+}  // namespace rac

@@ -1,0 +1,354 @@
+// rac_rowops.hip — row-wise softmax (hyperbolic-CORDIC exp), RMSNorm and
+// LayerNorm (CORDIC-vectoring rsqrt) for gfx950.
+//
+// One 256-lane workgroup (4 wave64) per row.  When the row length is a
+// multiple of 4 and the row fits in registers (<= 16 float4 per lane), the
+// row is read from HBM exactly once into registers with 16-byte loads, the
+// reductions run as wave64 butterflies (ds_swizzle/DPP via __shfl_xor) plus a
+// 4-entry LDS exchange, and the result is written once: 1 read + 1 write per
+// element, the HBM minimum.  Other shapes take a strided loop that re-reads
+// the row (from L2 for rows up to a few MB).
+//
+// Arithmetic follows rac_cpu.c:258-271 (softmax), :548-574 (RMSNorm) and
+// :507-546 (LayerNorm) rounding for rounding, except that row sums are
+// reduced as a tree instead of left to right (differences are O(1e-7)
+// relative; every per-element stage is bit-exact with the CPU checker).
+#include <hip/hip_runtime.h>
+#include "rac_math.hpp"
+#include "rac_internal.hpp"
+
+namespace rac {
+
+constexpr int kRowThreads = 256;
+constexpr int kRowWaves = kRowThreads / 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Block-wide reductions; `red` holds kRowWaves floats.  The result is the
+// same value in every lane (fixed combination order).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; i++) r += red[i];
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; i++) r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+template <int NITER>
+__device__ __forceinline__ float exp_n(float x, int iters, float khinv) {
+    if constexpr (NITER > 0) return exp_cordic<NITER>(x, khinv);
+    else return exp_cordic_rt(x, iters, khinv);
+}
+
+// ── softmax ──────────────────────────────────────────────────────────────
+
+template <int VPT, int NITER>
+__global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
+    const float* __restrict__ x, float* __restrict__ y, long n, int iters, float khinv)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * n);
+    float4* yr = reinterpret_cast<float4*>(y + row * n);
+    const long n4 = n / 4;
+    float4 v[VPT];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < n4) v[i] = ld4_stream(&xr[idx]);
+        else v[i] = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; i++) m = fmaxf(fmaxf(fmaxf(m, v[i].x), fmaxf(v[i].y, v[i].z)), v[i].w);
+    m = block_max(m, red);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < n4) {
+            v[i].x = exp_n<NITER>(v[i].x - m, iters, khinv);
+            v[i].y = exp_n<NITER>(v[i].y - m, iters, khinv);
+            v[i].z = exp_n<NITER>(v[i].z - m, iters, khinv);
+            v[i].w = exp_n<NITER>(v[i].w - m, iters, khinv);
+            s += v[i].x;
+            s += v[i].y;
+            s += v[i].z;
+            s += v[i].w;
+        }
+    }
+    s = block_sum(s, red);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < n4) {
+            float4 o;
+            o.x = v[i].x * inv; o.y = v[i].y * inv; o.z = v[i].z * inv; o.w = v[i].w * inv;
+            st4_stream(&yr[idx], o);
+        }
+    }
+}
+
+template <int NITER>
+__global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
+    const float* __restrict__ x, float* __restrict__ y, long n, int iters, float khinv)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float* xr = x + row * n;
+    float* yr = y + row * n;
+    float m = -__builtin_inff();
+    for (long i = threadIdx.x; i < n; i += kRowThreads) m = fmaxf(m, xr[i]);
+    m = block_max(m, red);
+    float s = 0.0f;
+    for (long i = threadIdx.x; i < n; i += kRowThreads) {
+        const float e = exp_n<NITER>(xr[i] - m, iters, khinv);
+        yr[i] = e;
+        s += e;
+    }
+    s = block_sum(s, red);
+    const float inv = 1.0f / s;
+    for (long i = threadIdx.x; i < n; i += kRowThreads) yr[i] = yr[i] * inv;
+}
+
+template <int NITER>
+static hipError_t softmax_dispatch(const float* x, float* y, long rows, long n, int iters,
+                                   float khinv, hipStream_t s) {
+    const bool vec_ok = (n % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+                        ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
+    const long n4 = n / 4;
+    dim3 grid((unsigned)rows), block(kRowThreads);
+    if (vec_ok && n4 <= 1 * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<1, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    else if (vec_ok && n4 <= 2 * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<2, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    else if (vec_ok && n4 <= 4 * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<4, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    else if (vec_ok && n4 <= 8 * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<8, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    else if (vec_ok && n4 <= 16 * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<16, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    else
+        hipLaunchKernelGGL((softmax_loop_kernel<NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+    return hipGetLastError();
+}
+
+hipError_t softmax_launch(const float* x, float* y, long rows, long n, int iters, hipStream_t s) {
+    iters = clamp_iters(iters);
+    const float khinv = host_consts().exp_khinv[iters];
+    switch (iters) {
+        case 8: return softmax_dispatch<8>(x, y, rows, n, iters, khinv, s);
+        case 16: return softmax_dispatch<16>(x, y, rows, n, iters, khinv, s);
+        case 24: return softmax_dispatch<24>(x, y, rows, n, iters, khinv, s);
+        default: return softmax_dispatch<0>(x, y, rows, n, iters, khinv, s);
+    }
+}
+
+// ── RMSNorm / LayerNorm ──────────────────────────────────────────────────
+
+template <int VPT>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_reg_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const float* __restrict__ gamma,
+    float eps, long d, float khinv16)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * d);
+    float4* yr = reinterpret_cast<float4*>(y + row * d);
+    const float4* g4 = reinterpret_cast<const float4*>(gamma);
+    const long d4 = d / 4;
+    float4 v[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        v[i] = (idx < d4) ? ld4_stream(&xr[idx]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        ss = __builtin_fmaf(v[i].x, v[i].x, ss);
+        ss = __builtin_fmaf(v[i].y, v[i].y, ss);
+        ss = __builtin_fmaf(v[i].z, v[i].z, ss);
+        ss = __builtin_fmaf(v[i].w, v[i].w, ss);
+    }
+    const float ms = block_sum(ss, red) / (float)d;
+    const float inv = rsqrt_cordic(ms + eps, khinv16);
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < d4) {
+            const float4 g = gamma ? g4[idx] : make_float4(1.f, 1.f, 1.f, 1.f);
+            float4 o;
+            o.x = v[i].x * inv * g.x; o.y = v[i].y * inv * g.y;
+            o.z = v[i].z * inv * g.z; o.w = v[i].w * inv * g.w;
+            st4_stream(&yr[idx], o);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_loop_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const float* __restrict__ gamma,
+    float eps, long d, float khinv16)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float* xr = x + row * d;
+    float* yr = y + row * d;
+    float ss = 0.0f;
+    for (long i = threadIdx.x; i < d; i += kRowThreads) ss = __builtin_fmaf(xr[i], xr[i], ss);
+    const float ms = block_sum(ss, red) / (float)d;
+    const float inv = rsqrt_cordic(ms + eps, khinv16);
+    for (long i = threadIdx.x; i < d; i += kRowThreads) {
+        const float g = gamma ? gamma[i] : 1.0f;
+        yr[i] = xr[i] * inv * g;
+    }
+}
+
+template <int VPT>
+__global__ __launch_bounds__(kRowThreads) void layernorm_reg_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, long d, float khinv16)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * d);
+    float4* yr = reinterpret_cast<float4*>(y + row * d);
+    const float4* g4 = reinterpret_cast<const float4*>(gamma);
+    const float4* b4 = reinterpret_cast<const float4*>(beta);
+    const long d4 = d / 4;
+    float4 v[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        v[i] = (idx < d4) ? ld4_stream(&xr[idx]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float sm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) { sm += v[i].x; sm += v[i].y; sm += v[i].z; sm += v[i].w; }
+    const float mean = block_sum(sm, red) / (float)d;
+    float sv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < d4) {
+            float z;
+            z = v[i].x - mean; sv = __builtin_fmaf(z, z, sv);
+            z = v[i].y - mean; sv = __builtin_fmaf(z, z, sv);
+            z = v[i].z - mean; sv = __builtin_fmaf(z, z, sv);
+            z = v[i].w - mean; sv = __builtin_fmaf(z, z, sv);
+        }
+    }
+    const float var = block_sum(sv, red) / (float)d;
+    const float inv = rsqrt_cordic(var + eps, khinv16);
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (idx < d4) {
+            const float4 g = gamma ? g4[idx] : make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 b = beta ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 o;
+            o.x = __builtin_fmaf(g.x, (v[i].x - mean) * inv, b.x);
+            o.y = __builtin_fmaf(g.y, (v[i].y - mean) * inv, b.y);
+            o.z = __builtin_fmaf(g.z, (v[i].z - mean) * inv, b.z);
+            o.w = __builtin_fmaf(g.w, (v[i].w - mean) * inv, b.w);
+            st4_stream(&yr[idx], o);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kRowThreads) void layernorm_loop_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, long d, float khinv16)
+{
+    __shared__ float red[kRowWaves];
+    const long row = blockIdx.x;
+    const float* xr = x + row * d;
+    float* yr = y + row * d;
+    float sm = 0.0f;
+    for (long i = threadIdx.x; i < d; i += kRowThreads) sm += xr[i];
+    const float mean = block_sum(sm, red) / (float)d;
+    float sv = 0.0f;
+    for (long i = threadIdx.x; i < d; i += kRowThreads) {
+        const float z = xr[i] - mean;
+        sv = __builtin_fmaf(z, z, sv);
+    }
+    const float var = block_sum(sv, red) / (float)d;
+    const float inv = rsqrt_cordic(var + eps, khinv16);
+    for (long i = threadIdx.x; i < d; i += kRowThreads) {
+        const float g = gamma ? gamma[i] : 1.0f;
+        const float b = beta ? beta[i] : 0.0f;
+        yr[i] = __builtin_fmaf(g, (xr[i] - mean) * inv, b);
+    }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+hipError_t rmsnorm_launch(const float* x, float* y, const float* gamma, float eps,
+                          long rows, long d, hipStream_t s) {
+    const float k = host_consts().rsqrt_khinv;
+    const bool vec_ok = (d % 4 == 0) && aligned16(x) && aligned16(y) && (!gamma || aligned16(gamma));
+    const long d4 = d / 4;
+    dim3 grid((unsigned)rows), block(kRowThreads);
+    if (vec_ok && d4 <= kRowThreads)
+        hipLaunchKernelGGL((rmsnorm_reg_kernel<1>), grid, block, 0, s, x, y, gamma, eps, d, k);
+    else if (vec_ok && d4 <= 2 * kRowThreads)
+        hipLaunchKernelGGL((rmsnorm_reg_kernel<2>), grid, block, 0, s, x, y, gamma, eps, d, k);
+    else if (vec_ok && d4 <= 4 * kRowThreads)
+        hipLaunchKernelGGL((rmsnorm_reg_kernel<4>), grid, block, 0, s, x, y, gamma, eps, d, k);
+    else if (vec_ok && d4 <= 8 * kRowThreads)
+        hipLaunchKernelGGL((rmsnorm_reg_kernel<8>), grid, block, 0, s, x, y, gamma, eps, d, k);
+    else if (vec_ok && d4 <= 16 * kRowThreads)
+        hipLaunchKernelGGL((rmsnorm_reg_kernel<16>), grid, block, 0, s, x, y, gamma, eps, d, k);
+    else
+        hipLaunchKernelGGL(rmsnorm_loop_kernel, grid, block, 0, s, x, y, gamma, eps, d, k);
+    return hipGetLastError();
+}
+
+hipError_t layernorm_launch(const float* x, float* y, const float* gamma, const float* beta,
+                            float eps, long rows, long d, hipStream_t s) {
+    const float k = host_consts().rsqrt_khinv;
+    const bool vec_ok = (d % 4 == 0) && aligned16(x) && aligned16(y) &&
+                        (!gamma || aligned16(gamma)) && (!beta || aligned16(beta));
+    const long d4 = d / 4;
+    dim3 grid((unsigned)rows), block(kRowThreads);
+    if (vec_ok && d4 <= kRowThreads)
+        hipLaunchKernelGGL((layernorm_reg_kernel<1>), grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    else if (vec_ok && d4 <= 2 * kRowThreads)
+        hipLaunchKernelGGL((layernorm_reg_kernel<2>), grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    else if (vec_ok && d4 <= 4 * kRowThreads)
+        hipLaunchKernelGGL((layernorm_reg_kernel<4>), grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    else if (vec_ok && d4 <= 8 * kRowThreads)
+        hipLaunchKernelGGL((layernorm_reg_kernel<8>), grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    else if (vec_ok && d4 <= 16 * kRowThreads)
+        hipLaunchKernelGGL((layernorm_reg_kernel<16>), grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    else
+        hipLaunchKernelGGL(layernorm_loop_kernel, grid, block, 0, s, x, y, gamma, beta, eps, d, k);
+    return hipGetLastError();
+}
+
+}  // namespace rac

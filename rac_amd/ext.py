@@ -1,0 +1,379 @@
+"""Tensor-level operator surface of the gfx950 kernels.
+
+Mirrors the reference extension module ``rac_cuda_ext``
+(rac_torch/rac_torch_bind.cpp:223-258): ``matmul_forward``,
+``matmul_backward``, ``linear_forward``, ``linear_backward``,
+``set/get_cordic_iters``, ``set/get_cordic_mode`` and ``MODE_*`` keep their
+names, keyword arguments, defaults (iters=24, mode=FAST,
+rac_torch_bind.cpp:54-55) and argument checks.  Added ops (new names, so the
+reference's ``hasattr`` probing keeps working): ``rope_cache``,
+``rope_apply_``, ``softmax``, ``rmsnorm``, ``layernorm``, ``silu``, ``gelu``,
+``sigmoid``, ``tanh``, ``exp``, ``relu``, ``rsqrt``, ``sincos``.
+
+Every op launches on torch's current HIP stream of the tensor's device and
+returns without synchronising.  Only ROCm device tensors are accepted: there
+is no CPU path.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import RACError, check
+
+MODE_FAST = 0
+MODE_CORDIC = 1
+MODE_SHIFTADD = 2
+
+_g_cordic_iters = 24          # rac_torch_bind.cpp:54
+_g_cordic_mode = MODE_FAST    # rac_torch_bind.cpp:55
+
+
+def set_cordic_iters(iters: int) -> None:
+    """Process-wide iteration count; <= 0 restores 24, clamp to [1, 24]
+    (rac_torch_bind.cpp:205-210)."""
+    global _g_cordic_iters
+    iters = int(iters)
+    if iters <= 0:
+        _g_cordic_iters = 24
+        return
+    _g_cordic_iters = max(1, min(24, iters))
+
+
+def get_cordic_iters() -> int:
+    return _g_cordic_iters
+
+
+def set_cordic_mode(mode: int) -> None:
+    """0=FAST, 1=CORDIC, 2=SHIFTADD; anything else selects FAST
+    (rac_torch_bind.cpp:216-219)."""
+    global _g_cordic_mode
+    mode = int(mode)
+    _g_cordic_mode = mode if 0 <= mode <= 2 else MODE_FAST
+
+
+def get_cordic_mode() -> int:
+    return _g_cordic_mode
+
+
+def _resolve(iters: int, mode: int) -> Tuple[int, int]:
+    if iters <= 0:
+        iters = _g_cordic_iters
+    if mode < 0:
+        mode = _g_cordic_mode
+    return max(1, min(24, int(iters))), int(mode)
+
+
+def _resolve_iters(iters: int) -> int:
+    return _resolve(iters, 0)[0]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return _lib.stream_handle(t.device)
+
+
+def _require_gpu(t: torch.Tensor, what: str = "input") -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"RAC: {what} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"RAC: {what} must be a GPU tensor (the gfx950 kernels have no CPU path)")
+
+
+def _require_f32(t: torch.Tensor, what: str = "input") -> None:
+    _require_gpu(t, what)
+    if t.dtype != torch.float32:
+        raise RuntimeError("RAC: float32 only")
+
+
+def _gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, M: int, N: int, K: int,
+          ta: int, tb: int, iters: int, mode: int, alpha: float = 1.0, beta: float = 0.0) -> None:
+    lib = _lib.load()
+    rc = lib.rac_gemm_dev(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, ta, tb,
+                          alpha, beta, iters, mode, _stream(C))
+    check(rc, "rac_gemm_dev")
+
+
+# ── reference surface (rac_torch_bind.cpp:68-199) ─────────────────────────
+
+def matmul_forward(A: torch.Tensor, B: torch.Tensor, iters: int = 0, mode: int = -1) -> torch.Tensor:
+    """C = A @ B (rac_torch_bind.cpp:68-88): GPU fp32 2-D tensors."""
+    _require_gpu(A, "A")
+    _require_gpu(B, "B")
+    if A.dtype != torch.float32:
+        raise RuntimeError("RAC: float32 only")
+    if A.dim() != 2 or B.dim() != 2:
+        raise RuntimeError("RAC: 2D tensors required")
+    if A.size(1) != B.size(0):
+        raise RuntimeError("RAC: dimension mismatch")
+    A = A.contiguous()
+    B = B.contiguous().to(torch.float32)
+    M, K = A.shape
+    N = B.size(1)
+    C = torch.empty((M, N), device=A.device, dtype=torch.float32)
+    iters, mode = _resolve(iters, mode)
+    _gemm(A, B, C, M, N, K, 0, 0, iters, mode)
+    return C
+
+
+def matmul_backward(grad_C: torch.Tensor, A: torch.Tensor, B: torch.Tensor,
+                    need_grad_A: bool = True, need_grad_B: bool = True,
+                    iters: int = 0, mode: int = -1) -> List[Optional[torch.Tensor]]:
+    """grad_A = grad_C @ B^T (NT), grad_B = A^T @ grad_C (TN)
+    (rac_torch_bind.cpp:130-163)."""
+    grad_C = grad_C.contiguous()
+    A = A.contiguous()
+    B = B.contiguous()
+    for t, n in ((grad_C, "grad_C"), (A, "A"), (B, "B")):
+        _require_f32(t, n)
+    M, K = A.shape
+    N = B.size(1)
+    iters, mode = _resolve(iters, mode)
+    grad_A = grad_B = None
+    if need_grad_A:
+        grad_A = torch.empty((M, K), device=A.device, dtype=A.dtype)
+        _gemm(grad_C, B, grad_A, M, K, N, 0, 1, iters, mode)
+    if need_grad_B:
+        grad_B = torch.empty((K, N), device=B.device, dtype=B.dtype)
+        _gemm(A, grad_C, grad_B, K, N, M, 1, 0, iters, mode)
+    return [grad_A, grad_B]
+
+
+def linear_forward(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                   iters: int = 0, mode: int = -1) -> torch.Tensor:
+    """output = input @ weight^T + bias with the NT kernel
+    (rac_torch_bind.cpp:90-128): fp16/bf16 promoted to fp32 and cast back;
+    an empty bias tensor means no bias."""
+    _require_gpu(input, "input")
+    orig_dtype = input.dtype
+    if orig_dtype != torch.float32:
+        input = input.to(torch.float32)
+        weight = weight.to(torch.float32)
+        if bias is not None and bias.numel() > 0:
+            bias = bias.to(torch.float32)
+    in_shape = list(input.shape)
+    out_features, in_features = weight.shape
+    if in_shape[-1] != in_features:
+        raise RuntimeError("RAC: dimension mismatch")
+    x2 = input.reshape(-1, in_features).contiguous()
+    w = weight.contiguous()
+    _require_f32(w, "weight")
+    M = x2.size(0)
+    out = torch.empty((M, out_features), device=x2.device, dtype=torch.float32)
+    iters, mode = _resolve(iters, mode)
+    if M > 0:
+        _gemm(x2, w, out, M, out_features, in_features, 0, 1, iters, mode)
+    if bias is not None and bias.numel() > 0:
+        out.add_(bias)
+    in_shape[-1] = out_features
+    res = out.reshape(in_shape)
+    if orig_dtype != torch.float32:
+        res = res.to(orig_dtype)
+    return res
+
+
+def linear_backward(grad_output: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
+                    need_bias_grad: bool, iters: int = 0, mode: int = -1) -> List[Optional[torch.Tensor]]:
+    """grad_input = go @ W (NN), grad_weight = go^T @ inp (TN), grad_bias =
+    go.sum(0) (rac_torch_bind.cpp:165-199)."""
+    out_features, in_features = weight.shape
+    iters, mode = _resolve(iters, mode)
+    go = grad_output.reshape(-1, out_features).contiguous().to(torch.float32)
+    inp = input.reshape(-1, in_features).contiguous().to(torch.float32)
+    w = weight.contiguous().to(torch.float32)
+    for t, n in ((go, "grad_output"), (inp, "input"), (w, "weight")):
+        _require_f32(t, n)
+    M = inp.size(0)
+    grad_input = torch.empty((M, in_features), device=inp.device, dtype=torch.float32)
+    grad_weight = torch.empty((out_features, in_features), device=w.device, dtype=torch.float32)
+    if M > 0:
+        _gemm(go, w, grad_input, M, in_features, out_features, 0, 0, iters, mode)
+        _gemm(go, inp, grad_weight, out_features, in_features, M, 1, 0, iters, mode)
+    else:
+        grad_weight.zero_()
+    grad_bias = go.sum(0) if need_bias_grad else None
+    shape = list(input.shape)
+    shape[-1] = in_features
+    return [grad_input.reshape(shape), grad_weight, grad_bias]
+
+
+# ── transformer primitives on the gfx950 kernels ──────────────────────────
+
+def _rows(x: torch.Tensor, what: str) -> Tuple[torch.Tensor, int, int]:
+    _require_f32(x, what)
+    x = x.contiguous()
+    n = x.size(-1) if x.dim() > 0 else 1
+    rows = x.numel() // n if n > 0 else 0
+    return x, rows, n
+
+
+def softmax(x: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    """Row softmax over the last dim with the n-step hyperbolic-CORDIC exp
+    (rac_cpu.c:258-271 structure)."""
+    x, rows, n = _rows(x, "x")
+    y = torch.empty_like(x)
+    if rows > 0 and n > 0:
+        check(_lib.load().rac_softmax_dev(x.data_ptr(), y.data_ptr(), rows, n,
+                                          _resolve_iters(iters), _stream(x)), "rac_softmax_dev")
+    return y
+
+
+def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """y = (x * rsqrt(mean(x^2) + eps)) * weight over the last dim
+    (rac_cpu.c:548-574), rsqrt by hyperbolic vectoring."""
+    x, rows, d = _rows(x, "x")
+    if weight is not None:
+        _require_f32(weight, "weight")
+        weight = weight.contiguous()
+        if weight.numel() != d:
+            raise RuntimeError("RAC: weight must have the size of the last dim")
+    y = torch.empty_like(x)
+    if rows > 0:
+        check(_lib.load().rac_rmsnorm_dev(x.data_ptr(), y.data_ptr(),
+                                          weight.data_ptr() if weight is not None else None,
+                                          float(eps), rows, d, _stream(x)), "rac_rmsnorm_dev")
+    return y
+
+
+def layernorm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+              eps: float) -> torch.Tensor:
+    """y = weight * (x - mean) * rsqrt(var + eps) + bias (rac_cpu.c:507-546)."""
+    x, rows, d = _rows(x, "x")
+    ptrs = []
+    for t, n in ((weight, "weight"), (bias, "bias")):
+        if t is not None:
+            _require_f32(t, n)
+            if t.numel() != d:
+                raise RuntimeError(f"RAC: {n} must have the size of the last dim")
+            t = t.contiguous()
+        ptrs.append(t)
+    y = torch.empty_like(x)
+    if rows > 0:
+        check(_lib.load().rac_layernorm_dev(
+            x.data_ptr(), y.data_ptr(),
+            ptrs[0].data_ptr() if ptrs[0] is not None else None,
+            ptrs[1].data_ptr() if ptrs[1] is not None else None,
+            float(eps), rows, d, _stream(x)), "rac_layernorm_dev")
+    return y
+
+
+def _elementwise(name: str, x: torch.Tensor, iters: Optional[int]) -> torch.Tensor:
+    _require_f32(x, "x")
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    n = x.numel()
+    if n:
+        fn = getattr(_lib.load(), name)
+        if iters is None:
+            rc = fn(x.data_ptr(), y.data_ptr(), n, _stream(x))
+        else:
+            rc = fn(x.data_ptr(), y.data_ptr(), n, _resolve_iters(iters), _stream(x))
+        check(rc, name)
+    return y
+
+
+def exp(x: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    return _elementwise("rac_exp_dev", x, iters)
+
+
+def silu(x: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    """x / (1 + e^-x), e^-x by the n-step CORDIC (rac_cpu.c:453-457)."""
+    return _elementwise("rac_silu_dev", x, iters)
+
+
+def sigmoid(x: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    return _elementwise("rac_sigmoid_dev", x, iters)
+
+
+def tanh(x: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    return _elementwise("rac_tanh_dev", x, iters)
+
+
+def gelu(x: torch.Tensor) -> torch.Tensor:
+    """x * 0.5 * (1 + erf(x / sqrt 2)) (rac_cpu.c:447-451)."""
+    return _elementwise("rac_gelu_dev", x, None)
+
+
+def relu(x: torch.Tensor) -> torch.Tensor:
+    return _elementwise("rac_relu_dev", x, None)
+
+
+def rsqrt(x: torch.Tensor) -> torch.Tensor:
+    return _elementwise("rac_rsqrt_dev", x, None)
+
+
+def sincos(theta: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(sin, cos) by one 16-step circular CORDIC rotation of (K_INV, 0)
+    (rac_cpu.c:322-328)."""
+    _require_f32(theta, "theta")
+    theta = theta.contiguous()
+    s = torch.empty_like(theta)
+    c = torch.empty_like(theta)
+    if theta.numel():
+        check(_lib.load().rac_sincos_dev(theta.data_ptr(), s.data_ptr(), c.data_ptr(),
+                                         theta.numel(), _stream(theta)), "rac_sincos_dev")
+    return s, c
+
+
+def rope_inv_freq(head_dim: int, base: float = 10000.0) -> torch.Tensor:
+    """inv_freq[i] = 1/powf(base, 2i/head_dim), computed on the host by the
+    library exactly as rac_cpu.c:588-589 (a CPU tensor of head_dim/2)."""
+    if head_dim <= 0 or head_dim % 2:
+        raise RuntimeError("RAC: head_dim must be even and > 0")
+    out = torch.empty(head_dim // 2, dtype=torch.float32)
+    check(_lib.load().rac_rope_inv_freq(out.data_ptr(), head_dim, float(base)), "rac_rope_inv_freq")
+    return out
+
+
+def rope_cache(max_seq: int, head_dim: int, base: float = 10000.0,
+               device: Optional[torch.device] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables [max_seq, head_dim/2] by circular CORDIC
+    (rac_cpu.c:576-598), bit-exact with the reference table."""
+    device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    if device.type != "cuda":
+        raise RuntimeError("RAC: rope_cache builds its tables on a GPU device")
+    if max_seq <= 0 or head_dim <= 0 or head_dim % 2:
+        raise RuntimeError("RAC: max_seq > 0 and even head_dim > 0 required")
+    half = head_dim // 2
+    inv = rope_inv_freq(head_dim, base).to(device)
+    cos = torch.empty((max_seq, half), device=device, dtype=torch.float32)
+    sin = torch.empty((max_seq, half), device=device, dtype=torch.float32)
+    check(_lib.load().rac_rope_cache_dev(cos.data_ptr(), sin.data_ptr(), max_seq, head_dim,
+                                         float(base), inv.data_ptr(), _stream(cos)),
+          "rac_rope_cache_dev")
+    return cos, sin
+
+
+def rope_apply_(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """In-place Givens rotation of x[b, h, t, 2i:2i+2] by (cos[t,i], sin[t,i])
+    (rac_cpu.c:600-635).  x is a [B, H, T, D] tensor whose last dim is
+    contiguous; the other dims may be strided (e.g. the transposed
+    [B, T, H, D] projection view).  cos/sin: [>= T, D/2] contiguous."""
+    _require_f32(x, "x")
+    if x.dim() != 4:
+        raise RuntimeError("RAC: rope_apply_ expects [batch, heads, seq, head_dim]")
+    if x.stride(-1) != 1:
+        raise RuntimeError("RAC: rope_apply_ needs a contiguous last dim")
+    B, H, T, D = x.shape
+    if D % 2:
+        raise RuntimeError("RAC: head_dim must be even")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _require_f32(t, n)
+        if not t.is_contiguous() or t.dim() != 2 or t.size(1) != D // 2 or t.size(0) < T:
+            raise RuntimeError(f"RAC: {n} must be a contiguous [>= seq, head_dim/2] table")
+    if x.numel() == 0:
+        return x
+    check(_lib.load().rac_rope_apply_dev(x.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, H, T, D,
+                                         x.stride(0), x.stride(1), x.stride(2), _stream(x)),
+          "rac_rope_apply_dev")
+    return x
+
+
+__all__ = [
+    "MODE_FAST", "MODE_CORDIC", "MODE_SHIFTADD", "RACError",
+    "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
+    "matmul_forward", "matmul_backward", "linear_forward", "linear_backward",
+    "softmax", "rmsnorm", "layernorm", "exp", "silu", "sigmoid", "tanh", "gelu", "relu",
+    "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_",
+]

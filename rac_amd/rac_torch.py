@@ -1,0 +1,843 @@
+"""rac_torch operator surface on the gfx950 kernels.
+
+Same public names, constructor signatures, defaults and knobs as the
+reference ``rac_torch`` (rac_torch/rac_torch.py:163-1409): ``RACLinear``,
+``FusedRACLinear``, ``RACFusedQKV``, ``RACFusedFFN``, ``RACAttention``,
+``RACTransformerBlock``, ``RACRoPE``, ``RACRMSNorm``, ``RACLayerNorm``,
+``RACRoPEAttention``, ``RACLlamaBlock``, ``rac_matmul``, ``rac_linear``,
+``rac_matmul_adaptive``, ``patch_model``, ``unpatch_model``,
+``benchmark_model``, ``rac_info``, ``rac_set_precision``,
+``rac_get_precision``, ``rac_set_mode``, ``rac_get_mode``, ``ACT_*``,
+``MODE_*``; environment ``RAC_CORDIC_ITERS`` (default 24),
+``RAC_CORDIC_MODE`` (default fast), ``RAC_MIN_ELEMENTS``.
+
+Differences by design:
+  * every op runs on the gfx950 kernels of librac_amd.so, including RoPE,
+    RMSNorm, LayerNorm, softmax and SiLU, which the reference leaves to
+    plain torch (rac_torch.py:1132-1343);
+  * there is no pure-torch fallback: CPU tensors or a missing library raise;
+  * RACRoPE's table is the CORDIC-16 table of rac_rope_cache
+    (rac_cpu.c:576-598), not torch cos/sin;
+  * backward passes of RoPE, the norms, softmax and the activations are
+    written with torch tensor ops on the device (the forward kernels are the
+    product; the reference's own backward for these modules is torch
+    autograd).
+"""
+from __future__ import annotations
+
+import os
+import warnings
+from typing import Optional
+
+import torch
+import torch.nn as nn
+from torch.autograd import Function
+
+from . import ext as _rac
+from .ext import MODE_CORDIC, MODE_FAST, MODE_SHIFTADD
+
+_FLOAT_TYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _rac_available() -> bool:
+    """True when the kernel library loads and a ROCm device is present."""
+    try:
+        _rac._lib.load()
+    except Exception:
+        return False
+    return torch.cuda.is_available()
+
+
+def _rac_has(op: str) -> bool:
+    return _rac_available() and hasattr(_rac, op)
+
+
+def _need_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"RAC: {what} must be on the ROCm device; the gfx950 kernels have no CPU path")
+
+
+# ── knobs (rac_torch.py:1017-1118) ─────────────────────────────────────────
+
+_MODE_NAMES = {'fast': MODE_FAST, 'cordic': MODE_CORDIC, 'shiftadd': MODE_SHIFTADD,
+               0: MODE_FAST, 1: MODE_CORDIC, 2: MODE_SHIFTADD}
+
+
+def _resolve_mode(m) -> int:
+    if isinstance(m, int):
+        return m if m in (0, 1, 2) else MODE_FAST
+    if isinstance(m, str) and m.lower() in _MODE_NAMES:
+        return _MODE_NAMES[m.lower()]
+    raise ValueError(f"Unknown RAC mode: {m}. Use 'fast', 'cordic', or 'shiftadd'.")
+
+
+_RAC_CORDIC_ITERS = int(os.environ.get('RAC_CORDIC_ITERS', '24'))
+_RAC_CORDIC_MODE = _resolve_mode(os.environ.get('RAC_CORDIC_MODE', 'fast'))
+_RAC_MIN_ELEMENTS = int(os.environ.get('RAC_MIN_ELEMENTS', '4096'))
+
+
+def rac_set_precision(iters: int) -> None:
+    """Global CORDIC iteration count, clamped to [4, 24]
+    (rac_torch.py:1075-1114).  Used by matmul/linear in CORDIC and SHIFTADD
+    modes and by the hyperbolic-CORDIC exp inside softmax, SiLU, sigmoid."""
+    global _RAC_CORDIC_ITERS
+    iters = max(4, min(24, int(iters)))
+    _RAC_CORDIC_ITERS = iters
+    _rac.set_cordic_iters(iters)
+
+
+def rac_get_precision() -> int:
+    return _RAC_CORDIC_ITERS
+
+
+def rac_set_mode(mode) -> None:
+    """'fast' (sign-XOR FMA), 'cordic' (n micro-rotations per MAC) or
+    'shiftadd' (integer shift-add product) for matmul/linear."""
+    global _RAC_CORDIC_MODE
+    _RAC_CORDIC_MODE = _resolve_mode(mode)
+    _rac.set_cordic_mode(_RAC_CORDIC_MODE)
+
+
+def rac_get_mode() -> int:
+    return _RAC_CORDIC_MODE
+
+
+def _kw():
+    return dict(iters=_RAC_CORDIC_ITERS, mode=_RAC_CORDIC_MODE)
+
+
+# ── autograd: matmul / linear (rac_torch.py:163-258) ──────────────────────
+
+class RACMatmulFunction(Function):
+    """C = A @ B forward; dA = dC @ B^T (NT), dB = A^T @ dC (TN)."""
+
+    @staticmethod
+    def forward(ctx, A, B):
+        _need_gpu(A, "A")
+        ctx.save_for_backward(A, B)
+        dtype = A.dtype
+        C = _rac.matmul_forward(A.float(), B.float(), **_kw())
+        return C if dtype == torch.float32 else C.to(dtype)
+
+    @staticmethod
+    def backward(ctx, grad_C):
+        A, B = ctx.saved_tensors
+        gA, gB = _rac.matmul_backward(grad_C.float().contiguous(), A.float(), B.float(),
+                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1], **_kw())
+        if gA is not None:
+            gA = gA.to(A.dtype)
+        if gB is not None:
+            gB = gB.to(B.dtype)
+        return gA, gB
+
+
+class RACLinearFunction(Function):
+    """output = input @ weight^T + bias; backward through the NN/TN kernels."""
+
+    @staticmethod
+    def forward(ctx, input, weight, bias):
+        _need_gpu(input, "input")
+        ctx.save_for_backward(input, weight, bias)
+        ctx.has_bias = bias is not None
+        b = bias if bias is not None else torch.empty(0, device=input.device)
+        return _rac.linear_forward(input, weight, b, **_kw())
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight, bias = ctx.saved_tensors
+        gi, gw, gb = _rac.linear_backward(grad_output.contiguous(), input, weight, ctx.has_bias, **_kw())
+        grad_input = gi.to(input.dtype) if ctx.needs_input_grad[0] else None
+        grad_weight = gw.to(weight.dtype) if ctx.needs_input_grad[1] else None
+        grad_bias = gb.to(bias.dtype) if ctx.has_bias else None
+        return grad_input, grad_weight, grad_bias
+
+
+def rac_matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """Drop-in for torch.matmul / torch.mm on 2-D tensors."""
+    return RACMatmulFunction.apply(A, B)
+
+
+def rac_linear(input: torch.Tensor, weight: torch.Tensor,
+               bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Drop-in for F.linear."""
+    return RACLinearFunction.apply(input, weight, bias)
+
+
+class RACLinear(nn.Module):
+    """Drop-in nn.Linear (rac_torch.py:288-376): same parameters and init."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 device=None, dtype=None):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        factory_kwargs = {'device': device, 'dtype': dtype}
+        self.weight = nn.Parameter(torch.empty((out_features, in_features), **factory_kwargs))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, **factory_kwargs))
+        else:
+            self.register_parameter('bias', None)
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        nn.init.kaiming_uniform_(self.weight, a=5 ** 0.5)
+        if self.bias is not None:
+            fan_in, _ = nn.init._calculate_fan_in_and_fan_out(self.weight)
+            bound = 1.0 / (fan_in ** 0.5) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def forward(self, input: torch.Tensor) -> torch.Tensor:
+        return RACLinearFunction.apply(input, self.weight, self.bias)
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear) -> 'RACLinear':
+        rac = cls(linear.in_features, linear.out_features, bias=linear.bias is not None,
+                  device=linear.weight.device, dtype=linear.weight.dtype)
+        with torch.no_grad():
+            rac.weight.copy_(linear.weight)
+            if linear.bias is not None:
+                rac.bias.copy_(linear.bias)
+        return rac
+
+    def extra_repr(self) -> str:
+        return (f'in_features={self.in_features}, out_features={self.out_features}, '
+                f'bias={self.bias is not None}, backend=RAC')
+
+
+# ── activations (rac_torch.py:381-401) ─────────────────────────────────────
+
+ACT_NONE = 0
+ACT_RELU = 1
+ACT_GELU = 2
+ACT_SILU = 3
+
+_ACT_MAP = {'none': ACT_NONE, None: ACT_NONE, 'relu': ACT_RELU, 'gelu': ACT_GELU,
+            'silu': ACT_SILU, 'swish': ACT_SILU}
+
+
+def _resolve_act(act) -> int:
+    if isinstance(act, int):
+        return act
+    if isinstance(act, str):
+        act = act.lower()
+    if act in _ACT_MAP:
+        return _ACT_MAP[act]
+    raise ValueError(f"Unknown activation: {act}. Use 'relu', 'gelu', 'silu', or None.")
+
+
+def _act_forward(x32: torch.Tensor, act_id: int) -> torch.Tensor:
+    if act_id == ACT_RELU:
+        return _rac.relu(x32)
+    if act_id == ACT_GELU:
+        return _rac.gelu(x32)
+    if act_id == ACT_SILU:
+        return _rac.silu(x32, iters=_RAC_CORDIC_ITERS)
+    return x32
+
+
+def _act_backward(go: torch.Tensor, pa: torch.Tensor, act_id: int) -> torch.Tensor:
+    # derivative formulas of rac_torch.py:466-477
+    if act_id == ACT_RELU:
+        return go * (pa > 0).float()
+    if act_id == ACT_GELU:
+        cdf = 0.5 * (1.0 + torch.erf(pa * 0.7071067811865))
+        pdf = 0.3989422804 * torch.exp(-0.5 * pa * pa)
+        return go * (cdf + pa * pdf)
+    if act_id == ACT_SILU:
+        sig = _rac.sigmoid(pa.contiguous(), iters=_RAC_CORDIC_ITERS)
+        return go * (sig * (1.0 + pa * (1.0 - sig)))
+    return go
+
+
+class RACActivationFunction(Function):
+    """Elementwise activation on the gfx950 kernels (SiLU by CORDIC exp)."""
+
+    @staticmethod
+    def forward(ctx, x, act_id):
+        _need_gpu(x, "input")
+        ctx.act_id = act_id
+        ctx.save_for_backward(x)
+        return _act_forward(x.float().contiguous(), act_id).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, go):
+        (x,) = ctx.saved_tensors
+        return _act_backward(go.float(), x.float(), ctx.act_id).to(x.dtype), None
+
+
+class RACFusedLinearFunction(Function):
+    """output = act(input @ weight^T + bias) (rac_torch.py:405-496): the NT
+    kernel followed by the activation kernel; backward keeps the
+    pre-activation."""
+
+    @staticmethod
+    def forward(ctx, input, weight, bias, act_id):
+        _need_gpu(input, "input")
+        ctx.act_id = act_id
+        ctx.has_bias = bias is not None
+        b = bias if bias is not None else torch.empty(0, device=input.device)
+        pre = _rac.linear_forward(input, weight, b, **_kw())
+        out = _act_forward(pre.float().contiguous(), act_id).to(input.dtype)
+        ctx.save_for_backward(input, weight, bias, pre)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight, bias, pre = ctx.saved_tensors
+        d_act = _act_backward(grad_output.float(), pre.float(), ctx.act_id)
+        gi, gw, gb = _rac.linear_backward(d_act.contiguous(), input, weight, ctx.has_bias, **_kw())
+        grad_input = gi.to(input.dtype) if ctx.needs_input_grad[0] else None
+        grad_weight = gw.to(weight.dtype) if ctx.needs_input_grad[1] else None
+        grad_bias = gb.to(bias.dtype) if ctx.has_bias else None
+        return grad_input, grad_weight, grad_bias, None
+
+
+class FusedRACLinear(nn.Module):
+    """Linear + activation (rac_torch.py:506-563)."""
+
+    def __init__(self, in_features, out_features, bias=True, activation='relu',
+                 device=None, dtype=None):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.act_id = _resolve_act(activation)
+        self.activation = activation
+        factory_kwargs = {'device': device, 'dtype': dtype}
+        self.weight = nn.Parameter(torch.empty((out_features, in_features), **factory_kwargs))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, **factory_kwargs))
+        else:
+            self.register_parameter('bias', None)
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        nn.init.kaiming_uniform_(self.weight, a=5 ** 0.5)
+        if self.bias is not None:
+            fan_in, _ = nn.init._calculate_fan_in_and_fan_out(self.weight)
+            bound = 1.0 / (fan_in ** 0.5) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def forward(self, input):
+        return RACFusedLinearFunction.apply(input, self.weight, self.bias, self.act_id)
+
+    @classmethod
+    def from_linear_and_act(cls, linear, activation='relu'):
+        fused = cls(linear.in_features, linear.out_features, bias=linear.bias is not None,
+                    activation=activation, device=linear.weight.device, dtype=linear.weight.dtype)
+        with torch.no_grad():
+            fused.weight.copy_(linear.weight)
+            if linear.bias is not None:
+                fused.bias.copy_(linear.bias)
+        return fused
+
+    def extra_repr(self):
+        return (f'in_features={self.in_features}, out_features={self.out_features}, '
+                f'bias={self.bias is not None}, activation={self.activation}, backend=RAC-fused')
+
+
+def rac_matmul_adaptive(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """RAC for M*N >= RAC_MIN_ELEMENTS, torch.matmul below (rac_torch.py:570-583)."""
+    M, K = A.shape
+    N = B.shape[1]
+    if M * N >= _RAC_MIN_ELEMENTS and A.is_cuda:
+        return RACMatmulFunction.apply(A, B)
+    return torch.matmul(A, B)
+
+
+class RACFusedQKV(nn.Module):
+    """One [3*d_model, d_model] projection, split into Q, K, V (rac_torch.py:588-626)."""
+
+    def __init__(self, d_model, bias=True, device=None, dtype=None):
+        super().__init__()
+        self.d_model = d_model
+        self.qkv = RACLinear(d_model, 3 * d_model, bias=bias, device=device, dtype=dtype)
+
+    def forward(self, x):
+        return self.qkv(x).chunk(3, dim=-1)
+
+    @classmethod
+    def from_qkv_linears(cls, q_linear, k_linear, v_linear):
+        d_model = q_linear.in_features
+        has_bias = q_linear.bias is not None
+        fused = cls(d_model, bias=has_bias, device=q_linear.weight.device, dtype=q_linear.weight.dtype)
+        with torch.no_grad():
+            fused.qkv.weight.copy_(torch.cat([q_linear.weight, k_linear.weight, v_linear.weight], dim=0))
+            if has_bias:
+                fused.qkv.bias.copy_(torch.cat([q_linear.bias, k_linear.bias, v_linear.bias], dim=0))
+        return fused
+
+    def extra_repr(self):
+        return f'd_model={self.d_model}, backend=RAC-fused-QKV'
+
+
+class RACFusedFFN(nn.Module):
+    """fc2(act(fc1(x))) (rac_torch.py:631-655); not a gated SwiGLU."""
+
+    def __init__(self, d_model, ff_dim, activation='gelu', bias=True, device=None, dtype=None):
+        super().__init__()
+        self.fc1 = FusedRACLinear(d_model, ff_dim, bias=bias, activation=activation,
+                                  device=device, dtype=dtype)
+        self.fc2 = RACLinear(ff_dim, d_model, bias=bias, device=device, dtype=dtype)
+
+    def forward(self, x):
+        return self.fc2(self.fc1(x))
+
+    def extra_repr(self):
+        return f'd_model={self.fc2.out_features}, ff_dim={self.fc1.out_features}'
+
+
+# ── softmax / norms / RoPE on the kernels ──────────────────────────────────
+
+class RACSoftmaxFunction(Function):
+    """Last-dim softmax with the hyperbolic-CORDIC exp."""
+
+    @staticmethod
+    def forward(ctx, x, iters):
+        _need_gpu(x, "scores")
+        y = _rac.softmax(x.float().contiguous(), iters=iters)
+        ctx.save_for_backward(y)
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        (y,) = ctx.saved_tensors
+        g = g.float()
+        return (y * (g - (g * y).sum(-1, keepdim=True))), None
+
+
+def rac_softmax(x: torch.Tensor, iters: Optional[int] = None) -> torch.Tensor:
+    return RACSoftmaxFunction.apply(x, _RAC_CORDIC_ITERS if iters is None else iters)
+
+
+def rac_silu(x: torch.Tensor) -> torch.Tensor:
+    return RACActivationFunction.apply(x, ACT_SILU)
+
+
+class RACRMSNormFunction(Function):
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        _need_gpu(x, "input")
+        x32 = x.float().contiguous()
+        w32 = weight.float().contiguous() if weight is not None else None
+        y = _rac.rmsnorm(x32, w32, eps)
+        ctx.save_for_backward(x32, w32)
+        ctx.eps = eps
+        ctx.has_w = weight is not None
+        ctx.wdtype = weight.dtype if weight is not None else None
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        g = g.float()
+        d = x.size(-1)
+        inv = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + ctx.eps)
+        xhat = x * inv
+        gw = g * w if w is not None else g
+        gx = inv * (gw - xhat * (gw * xhat).sum(-1, keepdim=True) / d)
+        gwt = (g * xhat).reshape(-1, d).sum(0).to(ctx.wdtype) if ctx.has_w else None
+        return gx, gwt, None
+
+
+class RACRoPE(nn.Module):
+    """Rotary embeddings by circular CORDIC (rac_torch.py:1132-1196).
+
+    The cos/sin cache is rac_rope_cache's CORDIC-16 table (bit-exact with
+    rac_cpu.c:576-598), built on the device; ``forward`` applies the Givens
+    rotation with the rope kernel.  Shapes: Q, K [batch, n_heads, seq,
+    head_dim] (any strides with a contiguous last dim), head_dim even."""
+
+    def __init__(self, head_dim: int, max_seq_len: int = 2048, base: float = 10000.0,
+                 device=None, dtype=torch.float32):
+        super().__init__()
+        assert head_dim % 2 == 0, f"head_dim must be even, got {head_dim}"
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.base = base
+        self._dtype = dtype
+        self._tables = {}
+        if device is not None and torch.device(device).type == 'cuda':
+            self._get_tables(torch.device(device))
+
+    def _get_tables(self, device: torch.device):
+        key = (device.type, device.index)
+        if key not in self._tables:
+            cos, sin = _rac.rope_cache(self.max_seq_len, self.head_dim, self.base, device=device)
+            self._tables[key] = (cos, sin, -sin)
+        return self._tables[key]
+
+    @property
+    def cos_cache(self):
+        return self._get_tables(torch.device('cuda', torch.cuda.current_device()))[0]
+
+    @property
+    def sin_cache(self):
+        return self._get_tables(torch.device('cuda', torch.cuda.current_device()))[1]
+
+    def _apply(self, fn, *args, **kwargs):
+        self._tables = {}
+        return super()._apply(fn, *args, **kwargs)
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, positions: Optional[torch.Tensor] = None):
+        _need_gpu(q, "q")
+        seq = q.shape[-2]
+        if seq > self.max_seq_len:
+            raise RuntimeError(f"RAC: seq {seq} exceeds max_seq_len {self.max_seq_len}")
+        cos, sin, nsin = self._get_tables(q.device)
+        if positions is not None:
+            positions = positions.to(q.device)
+            cos, sin, nsin = cos[positions].contiguous(), sin[positions].contiguous(), nsin[positions].contiguous()
+        return _RoPEFunction.apply(q, cos, sin, nsin), _RoPEFunction.apply(k, cos, sin, nsin)
+
+    def extra_repr(self):
+        return (f'head_dim={self.head_dim}, max_seq_len={self.max_seq_len}, '
+                f'base={self.base}, backend=RAC-CORDIC')
+
+
+class _RoPEFunction(Function):
+    @staticmethod
+    def forward(ctx, x, cos, sin, nsin):
+        ctx.save_for_backward(cos, nsin)
+        out = x.float().clone() if x.dtype != torch.float32 else x.clone()
+        _rac.rope_apply_(out, cos, sin)
+        return out.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        cos, nsin = ctx.saved_tensors
+        gx = g.float().contiguous().clone()
+        _rac.rope_apply_(gx, cos, nsin)      # transpose of a rotation: angle -> -angle
+        return gx.to(g.dtype), None, None, None
+
+
+class RACRMSNorm(nn.Module):
+    """y = weight * x / sqrt(mean(x^2) + eps) with CORDIC-vectoring rsqrt
+    (rac_torch.py:1205-1234)."""
+
+    def __init__(self, d_model: int, eps: float = 1e-6, device=None, dtype=None):
+        super().__init__()
+        self.d_model = d_model
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d_model, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return RACRMSNormFunction.apply(x, self.weight, self.eps)
+
+    def extra_repr(self):
+        return f'd_model={self.d_model}, eps={self.eps}, backend=RAC-rsqrt'
+
+
+class RACLayerNormFunction(Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        _need_gpu(x, "input")
+        x32 = x.float().contiguous()
+        w32 = weight.float().contiguous() if weight is not None else None
+        b32 = bias.float().contiguous() if bias is not None else None
+        y = _rac.layernorm(x32, w32, b32, eps)
+        ctx.save_for_backward(x32, w32)
+        ctx.eps = eps
+        ctx.has_b = bias is not None
+        ctx.wdtype = weight.dtype if weight is not None else None
+        ctx.bdtype = bias.dtype if bias is not None else None
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        g = g.float()
+        d = x.size(-1)
+        mean = x.mean(-1, keepdim=True)
+        inv = torch.rsqrt((x - mean).pow(2).mean(-1, keepdim=True) + ctx.eps)
+        xhat = (x - mean) * inv
+        gxh = g * w if w is not None else g
+        gx = inv * (gxh - gxh.mean(-1, keepdim=True) - xhat * (gxh * xhat).mean(-1, keepdim=True))
+        gw = (g * xhat).reshape(-1, d).sum(0).to(ctx.wdtype) if w is not None else None
+        gb = g.reshape(-1, d).sum(0).to(ctx.bdtype) if ctx.has_b else None
+        return gx, gw, gb, None
+
+
+class RACLayerNorm(nn.Module):
+    """y = weight * (x - mean) / sqrt(var + eps) + bias (rac_torch.py:1239-1274)."""
+
+    def __init__(self, d_model: int, eps: float = 1e-5, bias: bool = True, device=None, dtype=None):
+        super().__init__()
+        self.d_model = d_model
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d_model, device=device, dtype=dtype))
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(d_model, device=device, dtype=dtype))
+        else:
+            self.register_parameter('bias', None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return RACLayerNormFunction.apply(x, self.weight, self.bias, self.eps)
+
+    def extra_repr(self):
+        return f'd_model={self.d_model}, eps={self.eps}, backend=RAC-rsqrt'
+
+
+# ── attention and blocks ───────────────────────────────────────────────────
+
+def _causal_scores(scores: torch.Tensor, T: int) -> torch.Tensor:
+    causal = torch.triu(torch.full((T, T), float('-inf'), device=scores.device,
+                                   dtype=scores.dtype), diagonal=1)
+    return scores + causal
+
+
+class RACAttention(nn.Module):
+    """Multi-head attention with RAC projections and per-head RAC matmuls
+    (rac_torch.py:660-818); softmax on the CORDIC-exp kernel."""
+
+    def __init__(self, d_model, n_heads, bias=True, dropout=0.0, device=None, dtype=None):
+        super().__init__()
+        assert d_model % n_heads == 0, f"d_model ({d_model}) must be divisible by n_heads ({n_heads})"
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.d_head = d_model // n_heads
+        self.scale = self.d_head ** -0.5
+        self.qkv = RACLinear(d_model, 3 * d_model, bias=bias, device=device, dtype=dtype)
+        self.out_proj = RACLinear(d_model, d_model, bias=bias, device=device, dtype=dtype)
+        self.dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
+
+    def forward(self, x, mask=None, is_causal=False):
+        B, T, D = x.shape
+        Q, K, V = self.qkv(x).chunk(3, dim=-1)
+        Q = Q.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        K = K.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        V = V.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        scores = self._rac_bmm(Q, K.transpose(-2, -1)) * self.scale
+        if is_causal:
+            scores = _causal_scores(scores, T)
+        if mask is not None:
+            scores = scores + mask
+        attn = self.dropout(rac_softmax(scores))
+        out = self._rac_bmm(attn, V)
+        out = out.transpose(1, 2).contiguous().view(B, T, D)
+        return self.out_proj(out)
+
+    def _rac_bmm(self, A, B):
+        Bd, H, M, K = A.shape
+        N = B.shape[-1]
+        A_flat = A.reshape(-1, M, K)
+        B_flat = B.reshape(-1, K, N)
+        outs = [RACMatmulFunction.apply(A_flat[i].contiguous(), B_flat[i].contiguous())
+                for i in range(A_flat.shape[0])]
+        return torch.stack(outs, 0).view(Bd, H, M, N)
+
+    @classmethod
+    def from_attention_layers(cls, q_linear, k_linear, v_linear, out_linear, n_heads, dropout=0.0):
+        d_model = q_linear.in_features
+        has_bias = q_linear.bias is not None
+        attn = cls(d_model, n_heads, bias=has_bias, dropout=dropout,
+                   device=q_linear.weight.device, dtype=q_linear.weight.dtype)
+        with torch.no_grad():
+            attn.qkv.weight.copy_(torch.cat([q_linear.weight, k_linear.weight, v_linear.weight], dim=0))
+            if has_bias:
+                attn.qkv.bias.copy_(torch.cat([q_linear.bias, k_linear.bias, v_linear.bias], dim=0))
+            attn.out_proj.weight.copy_(out_linear.weight)
+            if has_bias:
+                attn.out_proj.bias.copy_(out_linear.bias)
+        return attn
+
+    def extra_repr(self):
+        return (f'd_model={self.d_model}, n_heads={self.n_heads}, '
+                f'd_head={self.d_head}, backend=RAC')
+
+
+class RACTransformerBlock(nn.Module):
+    """Post-norm block: norm1(x + attn(x)), norm2(x + ffn(x)) (rac_torch.py:823-860)."""
+
+    def __init__(self, d_model, n_heads, ff_dim=None, activation='gelu', dropout=0.0,
+                 bias=True, device=None, dtype=None):
+        super().__init__()
+        if ff_dim is None:
+            ff_dim = 4 * d_model
+        self.attn = RACAttention(d_model, n_heads, bias=bias, dropout=dropout, device=device, dtype=dtype)
+        self.ffn = RACFusedFFN(d_model, ff_dim, activation=activation, bias=bias, device=device, dtype=dtype)
+        self.norm1 = RACLayerNorm(d_model, device=device, dtype=dtype)
+        self.norm2 = RACLayerNorm(d_model, device=device, dtype=dtype)
+
+    def forward(self, x, mask=None, is_causal=False):
+        x = self.norm1(x + self.attn(x, mask=mask, is_causal=is_causal))
+        x = self.norm2(x + self.ffn(x))
+        return x
+
+    def extra_repr(self):
+        return (f'd_model={self.attn.d_model}, n_heads={self.attn.n_heads}, '
+                f'ff_dim={self.ffn.fc1.out_features}')
+
+
+class RACRoPEAttention(nn.Module):
+    """Llama-style attention (rac_torch.py:1279-1343): RAC QKV and output
+    projections, RoPE kernel on the strided Q/K views, QK^T and AV as fp32
+    torch matmuls (as in the reference), softmax on the CORDIC-exp kernel."""
+
+    def __init__(self, d_model: int, n_heads: int, max_seq_len: int = 4096, bias: bool = False,
+                 dropout: float = 0.0, rope_base: float = 10000.0, device=None, dtype=None):
+        super().__init__()
+        assert d_model % n_heads == 0
+        self.d_model = d_model
+        self.n_heads = n_heads
+        self.d_head = d_model // n_heads
+        self.scale = self.d_head ** -0.5
+        self.qkv = RACLinear(d_model, 3 * d_model, bias=bias, device=device, dtype=dtype)
+        self.out_proj = RACLinear(d_model, d_model, bias=bias, device=device, dtype=dtype)
+        self.rope = RACRoPE(self.d_head, max_seq_len=max_seq_len, base=rope_base,
+                            device=device, dtype=dtype or torch.float32)
+        self.dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, is_causal: bool = False,
+                positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, T, D = x.shape
+        qkv = self.qkv(x)
+        Q, K, V = qkv.chunk(3, dim=-1)
+        Q = Q.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        K = K.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        V = V.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
+        Q, K = self.rope(Q, K, positions=positions)
+        scores = torch.matmul(Q.float().contiguous(), K.float().transpose(-2, -1).contiguous()) * self.scale
+        if is_causal:
+            scores = _causal_scores(scores, T)
+        if mask is not None:
+            scores = scores + mask
+        attn = self.dropout(rac_softmax(scores))
+        out = torch.matmul(attn, V.float().contiguous()).to(x.dtype)
+        out = out.transpose(1, 2).contiguous().view(B, T, D)
+        return self.out_proj(out)
+
+    def extra_repr(self):
+        return (f'd_model={self.d_model}, n_heads={self.n_heads}, '
+                f'd_head={self.d_head}, backend=RAC-RoPE')
+
+
+class RACLlamaBlock(nn.Module):
+    """x = x + attn(RMSNorm(x)); x = x + ffn(RMSNorm(x)) (rac_torch.py:1348-1383)."""
+
+    def __init__(self, d_model: int, n_heads: int, ff_dim: int = None, max_seq_len: int = 4096,
+                 activation: str = 'silu', dropout: float = 0.0, bias: bool = False,
+                 rms_eps: float = 1e-6, rope_base: float = 10000.0, device=None, dtype=None):
+        super().__init__()
+        if ff_dim is None:
+            ff_dim = 4 * d_model
+        self.norm1 = RACRMSNorm(d_model, eps=rms_eps, device=device, dtype=dtype)
+        self.attn = RACRoPEAttention(d_model, n_heads, max_seq_len=max_seq_len, bias=bias,
+                                     dropout=dropout, rope_base=rope_base, device=device, dtype=dtype)
+        self.norm2 = RACRMSNorm(d_model, eps=rms_eps, device=device, dtype=dtype)
+        self.ffn = RACFusedFFN(d_model, ff_dim, activation=activation, bias=bias,
+                               device=device, dtype=dtype)
+
+    def forward(self, x, mask=None, is_causal=False, positions=None):
+        x = x + self.attn(self.norm1(x), mask=mask, is_causal=is_causal, positions=positions)
+        x = x + self.ffn(self.norm2(x))
+        return x
+
+    def extra_repr(self):
+        return (f'd_model={self.norm1.d_model}, n_heads={self.attn.n_heads}, '
+                f'ff_dim={self.ffn.fc1.out_features}')
+
+
+# ── model patching (rac_torch.py:865-940) ──────────────────────────────────
+
+def patch_model(model: nn.Module, verbose: bool = True, min_features: int = 64) -> nn.Module:
+    """Replace every nn.Linear (both dims >= min_features) with RACLinear."""
+    replaced = []
+
+    def _replace(module: nn.Module, prefix: str = ''):
+        for name, child in module.named_children():
+            full = f'{prefix}.{name}' if prefix else name
+            if isinstance(child, nn.Linear) and not isinstance(child, RACLinear):
+                if child.in_features >= min_features and child.out_features >= min_features:
+                    setattr(module, name, RACLinear.from_linear(child))
+                    replaced.append((full, child.in_features, child.out_features))
+                elif verbose:
+                    print(f'  skip  {full}: {child.in_features}->{child.out_features} (below min_features)')
+            else:
+                _replace(child, full)
+
+    _replace(model)
+    if verbose:
+        print(f'patch_model: replaced {len(replaced)} Linear layers with RACLinear')
+        for name, inf, outf in replaced:
+            print(f'  +  {name}: {inf}->{outf}')
+    return model
+
+
+def unpatch_model(model: nn.Module, verbose: bool = True) -> nn.Module:
+    """Reverse patch_model."""
+    restored = []
+
+    def _restore(module: nn.Module, prefix: str = ''):
+        for name, child in module.named_children():
+            full = f'{prefix}.{name}' if prefix else name
+            if isinstance(child, RACLinear):
+                lin = nn.Linear(child.in_features, child.out_features, bias=child.bias is not None,
+                                device=child.weight.device, dtype=child.weight.dtype)
+                with torch.no_grad():
+                    lin.weight.copy_(child.weight)
+                    if child.bias is not None:
+                        lin.bias.copy_(child.bias)
+                setattr(module, name, lin)
+                restored.append(full)
+            else:
+                _restore(child, full)
+
+    _restore(model)
+    if verbose:
+        print(f'unpatch_model: restored {len(restored)} RACLinear -> Linear')
+    return model
+
+
+def benchmark_model(model: nn.Module, input_shape: tuple, n_warmup: int = 10, n_iters: int = 100,
+                    device: str = 'cuda') -> dict:
+    """Time a model before and after patch_model (rac_torch.py:945-985)."""
+    import time
+
+    model = model.to(device).eval()
+    x = torch.randn(*input_shape, device=device)
+
+    def _time(m):
+        with torch.no_grad():
+            for _ in range(n_warmup):
+                m(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            for _ in range(n_iters):
+                m(x)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_iters * 1000
+
+    base = _time(model)
+    patched = patch_model(model, verbose=False)
+    rac_ms = _time(patched)
+    unpatch_model(patched, verbose=False)
+    return {'baseline_ms': base, 'rac_ms': rac_ms,
+            'speedup': base / rac_ms if rac_ms > 0 else float('inf'), 'n_iters': n_iters}
+
+
+def rac_info():
+    """Print the extension status (rac_torch.py:1388-1409)."""
+    print("RAC on MI355X (gfx950) — rotation-accumulate kernels")
+    print(f"  ROCm device available: {torch.cuda.is_available()}")
+    try:
+        lib = _rac._lib.load()
+        print(f"  kernel library:        {_rac._lib.LIB_PATH} (v{lib.rac_version()})")
+    except Exception as e:  # noqa: BLE001
+        print(f"  kernel library:        NOT LOADED ({e})")
+    if torch.cuda.is_available():
+        print(f"  device:                {torch.cuda.get_device_properties(0).name}")
+    mode_name = {0: 'fast', 1: 'cordic', 2: 'shiftadd'}.get(_RAC_CORDIC_MODE, '?')
+    print(f"  CORDIC iters:          {_RAC_CORDIC_ITERS} (rac_set_precision)")
+    print(f"  compute mode:          {mode_name} (rac_set_mode)")
+    print("  kernels:               matmul/linear (FAST/CORDIC/SHIFTADD), softmax + SiLU + sigmoid "
+          "(hyperbolic CORDIC exp), RMSNorm/LayerNorm (CORDIC rsqrt), RoPE (circular CORDIC)")
+    print(f"  adaptive threshold:    {_RAC_MIN_ELEMENTS} elements (RAC_MIN_ELEMENTS)")
+
+
+try:
+    if hasattr(torch, '_dynamo') and hasattr(torch._dynamo, 'allow_in_graph'):
+        for _fn in (RACMatmulFunction, RACLinearFunction, RACFusedLinearFunction):
+            torch._dynamo.allow_in_graph(_fn)
+except Exception:  # noqa: BLE001
+    warnings.warn("torch.compile registration of RAC functions failed; eager mode only", RuntimeWarning)

@@ -1,0 +1,222 @@
+"""Test helpers: ctypes bindings of the CPU checker (oracle/liboracle.so), of
+the compiled reference (oracle/_ref/librac_ref.so, when built), and a
+deterministic input generator.
+
+Only tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
+module; the product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "librac_ref.so")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+_vp, _i, _l, _f = C.c_void_p, C.c_int, C.c_long, C.c_float
+_fp = C.POINTER(C.c_float)
+
+_ORACLE_SIGS = {
+    "orc_tables": (None, [_vp, _vp, _vp]),
+    "orc_cordic_rotate": (None, [_f, _f, _f, _i, _fp, _fp]),
+    "orc_cordic_dirs": (None, [_i, _vp]),
+    "orc_cordic_kinv": (_f, [_i]),
+    "orc_fma_cordic": (_f, [_f, _f, _f, _i]),
+    "orc_cordic_project": (_f, [_f, _i]),
+    "orc_cordic_chain_fast": (_f, [_f, _i]),
+    "orc_shiftadd_mul": (_f, [_f, _f, _i]),
+    "orc_fma_iters": (_f, [_f, _f, _f, _i, _i]),
+    "orc_matmul": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _f, _f, _i, _i, _i]),
+    "orc_matmul_entries": (_i, [_i, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
+    "orc_rope_inv_freq": (None, [_vp, _i, _f]),
+    "orc_sincos": (None, [_f, _fp, _fp]),
+    "orc_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
+    "orc_rope_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "orc_rope_apply_strided": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l]),
+    "orc_hyp_schedule": (_i, [_i, _vp]),
+    "orc_hyp_kinv": (_f, [_i]),
+    "orc_exp_xy": (_f, [_f, _i, _f]),
+    "orc_exp_n": (_f, [_f, _i]),
+    "orc_exp_batch": (None, [_vp, _vp, _l, _i]),
+    "orc_softmax_rows": (None, [_vp, _vp, _i, _i, _i]),
+    "orc_rsqrt": (_f, [_f]),
+    "orc_rmsnorm": (_i, [_vp, _vp, _vp, _f, _i, _i, _i]),
+    "orc_layernorm": (_i, [_vp, _vp, _vp, _vp, _f, _i, _i, _i]),
+    "orc_silu": (None, [_vp, _vp, _l, _i]),
+    "orc_sigmoid": (None, [_vp, _vp, _l, _i]),
+    "orc_gelu": (None, [_vp, _vp, _l]),
+    "orc_tanh": (None, [_vp, _vp, _l, _i]),
+    "orc_check_chain_all_mantissas": (_l, [_i, _i]),
+    "orc_check_projection_identity": (_l, [_i, _l, C.c_uint64]),
+}
+
+_REF_SIGS = {
+    "ref_tables": (None, [_vp, _vp, _vp, _vp]),
+    "ref_cordic_rotate": (None, [_f, _f, _f, _i, _fp, _fp]),
+    "rac_matmul": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rac_sgemm": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]),
+    "rac_hal_matmul": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "rac_softmax_batch": (None, [_vp, _vp, _i, _i]),
+    "rac_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
+    "rac_rope_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rac_rmsnorm": (_i, [_vp, _vp, _vp, _f, _i, _i, _vp]),
+    "rac_layernorm": (_i, [_vp, _vp, _vp, _vp, _f, _i, _i, _vp]),
+    "rac_silu": (None, [_vp, _vp, _i]),
+    "rac_gelu": (None, [_vp, _vp, _i]),
+    "rac_hal_silu": (None, [_vp, _vp, _i]),
+    "rac_rsqrt": (_f, [_f]),
+    "rac_sigmoid": (_f, [_f]),
+    "rac_sincos": (None, [_f, _fp, _fp]),
+    "rac_alu_exp": (_f, [_f]),
+}
+
+_cache = {}
+
+
+def _load(path, sigs):
+    if path in _cache:
+        return _cache[path]
+    lib = C.CDLL(path, mode=C.RTLD_LOCAL)
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _cache[path] = lib
+    return lib
+
+
+def oracle():
+    return _load(ORACLE_SO, _ORACLE_SIGS)
+
+
+def have_ref() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    return _load(REF_SO, _REF_SIGS)
+
+
+def p(a: np.ndarray) -> int:
+    """Data pointer of a C-contiguous numpy array."""
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ── deterministic inputs ────────────────────────────────────────────────────
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _splitmix(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        x = x + np.uint64(0x9E3779B97F4A7C15)
+        x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return x ^ (x >> np.uint64(31))
+
+
+def gen_u01(count: int, seed: int) -> np.ndarray:
+    """u = (splitmix64(seed*C + i) >> 40) * 2^-24, exactly representable."""
+    with np.errstate(over="ignore"):
+        base = np.uint64(seed) * np.uint64(0xD1B54A32D192ED03)
+        idx = np.arange(count, dtype=np.uint64) + base
+    z = _splitmix(idx)
+    return (z >> np.uint64(40)).astype(np.float64) * (1.0 / 16777216.0)
+
+
+def gen_uniform(shape, seed: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+    n = int(np.prod(shape))
+    return (lo + (hi - lo) * gen_u01(n, seed)).astype(np.float32).reshape(shape)
+
+
+def gen_normal(shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    """Box-Muller in float64 from two uniform streams, cast to float32."""
+    n = int(np.prod(shape))
+    u = gen_u01(2 * n, seed)
+    u1, u2 = u[0::2], u[1::2]
+    r = np.sqrt(-2.0 * np.log(1.0 - u1))
+    return (mean + std * r * np.cos(2.0 * np.pi * u2)).astype(np.float32).reshape(shape)
+
+
+def sha256(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ── oracle wrappers on numpy arrays ─────────────────────────────────────────
+
+def orc_matmul(A, B, M, N, K, iters, mode, ta=0, tb=0, alpha=1.0, beta=0.0, C0=None, literal=0):
+    Cm = np.zeros((M, N), np.float32) if C0 is None else np.array(C0, np.float32, copy=True)
+    rc = oracle().orc_matmul(ta, tb, p(A), p(B), p(Cm), M, N, K, alpha, beta, iters, mode, literal)
+    assert rc == 0
+    return Cm
+
+
+def orc_matmul_entries(A, B, M, N, K, iters, mode, rows, cols, ta=0, tb=0):
+    rows = np.ascontiguousarray(rows, np.int32)
+    cols = np.ascontiguousarray(cols, np.int32)
+    out = np.empty(len(rows), np.float32)
+    oracle().orc_matmul_entries(ta, tb, p(A), p(B), M, N, K, iters, mode, p(rows), p(cols),
+                                len(rows), p(out))
+    return out
+
+
+def orc_unary(name, x, iters=None):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    fn = getattr(oracle(), name)
+    if iters is None:
+        fn(p(x), p(y), x.size)
+    else:
+        fn(p(x), p(y), x.size, iters)
+    return y
+
+
+def orc_softmax(x, iters):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    oracle().orc_softmax_rows(p(x), p(y), x.shape[0], x.shape[1], iters)
+    return y
+
+
+def orc_rmsnorm(x, g, eps, use_cordic=1):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    assert oracle().orc_rmsnorm(p(x), p(y), p(g) if g is not None else None, eps,
+                                x.shape[0], x.shape[1], use_cordic) == 0
+    return y
+
+
+def orc_layernorm(x, g, b, eps, use_cordic=1):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    assert oracle().orc_layernorm(p(x), p(y), p(g) if g is not None else None,
+                                  p(b) if b is not None else None, eps,
+                                  x.shape[0], x.shape[1], use_cordic) == 0
+    return y
+
+
+def orc_rope_cache(max_seq, head_dim, base=10000.0):
+    half = head_dim // 2
+    c = np.empty((max_seq, half), np.float32)
+    s = np.empty((max_seq, half), np.float32)
+    assert oracle().orc_rope_cache(p(c), p(s), max_seq, head_dim, base) == 0
+    return c, s
+
+
+def orc_rope_apply(x, c, s):
+    x = np.array(x, np.float32, copy=True, order="C")
+    B, H, T, D = x.shape
+    assert oracle().orc_rope_apply(p(x), p(c), p(s), B, H, T, D) == 0
+    return x
+
+
+def max_rel(a, b, floor=1e-30):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), floor))) if a.size else 0.0

@@ -1,0 +1,173 @@
+"""C ABI of librac_amd.so and the Python surface — CPU only (no kernel launch).
+
+Checks that the library loads, exports every function include/*.h declares,
+that the headers compile as plain C against it, that the host-side constants
+equal the CPU checker's, and that argument errors are reported before any
+device call.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import raclib as rl
+
+ROOT = rl.ROOT
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h")]
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b([a-z_][a-z0-9_]*)\s*\(", text):
+            name = m.group(1)
+            if name.startswith("rac_") and not name.startswith("rac_context"):
+                names.add(name)
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch  # noqa: F401  (share torch's HIP runtime, as the product does)
+    import rac_amd
+    return rac_amd.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", os.path.join(ROOT, "rac_amd", "librac_amd.so")],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+    assert len(declared_functions()) > 40
+
+
+def test_python_binding_covers_headers():
+    from rac_amd import _lib
+    assert set(declared_functions()) <= set(_lib.symbols())
+
+
+def test_headers_compile_and_link_as_c(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "rac.h"\n#include "rac_ext.h"\n'
+                   "int main(void){ rac_set_cordic_iters(8); return rac_get_cordic_iters() == 8 ? 0 : 1; }\n")
+    exe = tmp_path / "t"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe), "-L", os.path.join(ROOT, "rac_amd"), "-lrac_amd",
+                    "-Wl,-rpath," + os.path.join(ROOT, "rac_amd")], check=True)
+
+
+def test_constants_match_checker(lib):
+    o = rl.oracle()
+    d = (ctypes.c_int * 24)()
+    dd = np.zeros(24, np.int32)
+    for n in (1, 8, 16, 24):
+        assert lib.rac_cordic_direction_bits(n, d) == n
+        o.orc_cordic_dirs(n, rl.p(dd))
+        assert list(d)[:n] == list(dd[:n])
+    for n in range(1, 25):
+        assert np.float32(lib.rac_exp_gain_inverse(n)) == np.float32(o.orc_hyp_kinv(n))
+    assert np.float32(lib.rac_rsqrt_gain_inverse()) == np.float32(o.orc_hyp_kinv(16))
+    inv = np.zeros(64, np.float32)
+    ref = np.zeros(64, np.float32)
+    assert lib.rac_rope_inv_freq(rl.p(inv), 128, 10000.0) == 0
+    o.orc_rope_inv_freq(rl.p(ref), 128, 10000.0)
+    assert np.array_equal(inv, ref)
+
+
+def test_knob_semantics(lib):
+    lib.rac_set_cordic_iters(99)
+    assert lib.rac_get_cordic_iters() == 24
+    lib.rac_set_cordic_iters(0)
+    assert lib.rac_get_cordic_iters() == 16
+    lib.rac_set_cordic_iters(8)
+    assert lib.rac_get_cordic_iters() == 8
+    lib.rac_set_cordic_mode(7)
+    assert lib.rac_get_cordic_mode() == 0
+    lib.rac_set_cordic_mode(1)
+    assert lib.rac_get_cordic_mode() == 1
+    lib.rac_set_cordic_iters(16)
+
+
+def test_argument_errors_before_device(lib):
+    assert lib.rac_gemm_dev(None, None, None, 4, 4, 4, 0, 0, 1.0, 0.0, 16, 1, None) == -1
+    assert b"null" in lib.rac_last_error()
+    buf = (ctypes.c_float * 16)()
+    a = ctypes.addressof(buf)
+    assert lib.rac_gemm_dev(a, a, a, 0, 4, 4, 0, 0, 1.0, 0.0, 16, 1, None) == -2
+    assert lib.rac_gemm_dev(a, a, a, 4, 4, 4, 0, 0, 1.0, 0.0, 16, 5, None) == -2
+    assert lib.rac_softmax_dev(a, a, 0, 4, 16, None) == -2
+    assert lib.rac_rmsnorm_dev(None, a, None, 1e-6, 1, 4, None) == -1
+    assert lib.rac_rope_apply_dev(a, a, a, 1, 1, 4, 3, 12, 12, 3, None) == -2   # odd head_dim
+    assert lib.rac_rope_cache_dev(a, a, 4, 6, 1e4, None, None) == -1
+    assert lib.rac_rope_inv_freq(a, 5, 1e4) == -2
+    # reference-style void entry points report through rac_last_error
+    lib.rac_clear_error()
+    lib.rac_matmul(None, a, a, 2, 2, 2)
+    assert b"null" in lib.rac_last_error()
+    lib.rac_rmsnorm(a, a, None, 1e-6, 0, 4)
+    assert b"must be > 0" in lib.rac_last_error()
+    # context stub semantics of rac_hip.cpp:416-435
+    ctx = lib.rac_create_context(1)
+    assert ctx
+    assert lib.rac_query_capability(ctx, 0xFF) == 0 and lib.rac_query_capability(ctx, 16) == 1
+    assert lib.rac_execute(ctx, 16, None) == 0
+    lib.rac_destroy_context(ctx)
+
+
+def test_python_knobs_and_cpu_tensors_raise():
+    import torch
+    from rac_amd import ext, rac_torch as rt
+
+    ext.set_cordic_iters(0)
+    assert ext.get_cordic_iters() == 24
+    ext.set_cordic_iters(30)
+    assert ext.get_cordic_iters() == 24
+    ext.set_cordic_iters(5)
+    assert ext.get_cordic_iters() == 5
+    ext.set_cordic_mode(9)
+    assert ext.get_cordic_mode() == ext.MODE_FAST
+    rt.rac_set_precision(2)
+    assert rt.rac_get_precision() == 4          # rac_torch.py:1100 clamp
+    rt.rac_set_precision(99)
+    assert rt.rac_get_precision() == 24
+    rt.rac_set_mode('cordic')
+    assert rt.rac_get_mode() == rt.MODE_CORDIC
+    with pytest.raises(ValueError):
+        rt.rac_set_mode('bogus')
+    rt.rac_set_mode('fast')
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.matmul_forward(torch.ones(2, 2), torch.ones(2, 2))
+    with pytest.raises(RuntimeError):
+        rt.RACLinear(4, 4)(torch.ones(2, 4))
+    with pytest.raises(RuntimeError):
+        ext.softmax(torch.ones(2, 4))
+
+
+def test_module_shapes_and_parameters():
+    import torch.nn as nn
+    from rac_amd import rac_torch as rt
+
+    lin = rt.RACLinear(16, 8)
+    assert lin.weight.shape == (8, 16) and lin.bias.shape == (8,)
+    ref = nn.Linear(16, 8)
+    r2 = rt.RACLinear.from_linear(ref)
+    assert (r2.weight == ref.weight).all()
+    blk = rt.RACLlamaBlock(64, 4, ff_dim=176, max_seq_len=32)
+    names = {n for n, _ in blk.named_parameters()}
+    assert {"norm1.weight", "attn.qkv.weight", "attn.out_proj.weight", "norm2.weight",
+            "ffn.fc1.weight", "ffn.fc2.weight"} <= names
+    assert blk.attn.qkv.bias is None                        # bias=False default
+    model = nn.Sequential(nn.Linear(128, 128), nn.ReLU(), nn.Linear(128, 32))
+    rt.patch_model(model, verbose=False, min_features=64)
+    assert isinstance(model[0], rt.RACLinear) and not isinstance(model[2], rt.RACLinear)
+    rt.unpatch_model(model, verbose=False)
+    assert type(model[0]) is nn.Linear
+    assert rt._resolve_act('swish') == rt.ACT_SILU
+    with pytest.raises(ValueError):
+        rt._resolve_act('tanhh')

@@ -1,0 +1,437 @@
+"""GPU parity: the gfx950 kernels (through librac_amd.so) vs the CPU checker.
+
+Bars: bit-exact wherever the kernel and the checker evaluate the same
+roundings (CORDIC/FAST/SHIFTADD matmul, exp, SiLU, sigmoid, tanh, rsqrt,
+sin/cos, RoPE table and apply); elementwise relative error <= 1e-5 where a
+row sum is reduced in a different order (softmax, RMSNorm, LayerNorm); matmul
+vs the reference lib/c within 1e-4*|a_i|*|b_j| per element.  Full BASELINE
+sizes are covered through sampled entries and digests.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+import raclib as rl
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    import rac_amd
+    rac_amd.load()
+    yield
+    torch.cuda.synchronize()
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def H(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def ext():
+    from rac_amd import ext as e
+    return e
+
+
+def lib():
+    import rac_amd
+    return rac_amd.load()
+
+
+def gemm(A, B, M, N, K, ta, tb, iters, mode, alpha=1.0, beta=0.0, C0=None):
+    Ad, Bd = T(A), T(B)
+    Cd = T(C0) if C0 is not None else torch.zeros((M, N), device=DEV)
+    rc = lib().rac_gemm_dev(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, ta, tb, alpha,
+                            beta, iters, mode, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    return H(Cd)
+
+
+# ── matmul ─────────────────────────────────────────────────────────────────
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 16), (67, 45, 83), (128, 130, 129), (200, 96, 300)]
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24, 5, 1])
+@pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_cordic_matmul_bit_exact(iters, layout):
+    ta, tb = layout
+    for (M, N, K) in SHAPES:
+        print(f"cordic iters={iters} layout={layout} shape={(M, N, K)}", flush=True)
+        A = rl.gen_uniform((M, K), seed=M * 7 + K)
+        B = rl.gen_uniform((K, N), seed=N * 3 + K)
+        As = np.ascontiguousarray(A.T) if ta else A
+        Bs = np.ascontiguousarray(B.T) if tb else B
+        got = gemm(As, Bs, M, N, K, ta, tb, iters, 1)
+        ref = rl.orc_matmul(As, Bs, M, N, K, iters, 1, ta=ta, tb=tb)
+        assert np.array_equal(got, ref), (M, N, K, float(np.max(np.abs(got - ref))))
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_fast_and_shiftadd_bit_exact(mode):
+    for (M, N, K) in [(3, 5, 7), (67, 45, 83), (130, 129, 40)]:
+        for ta, tb in [(0, 0), (0, 1), (1, 0)]:
+            print(f"mode={mode} shape={(M, N, K)} layout={(ta, tb)}", flush=True)
+            A = rl.gen_normal((M, K), seed=1)
+            B = rl.gen_normal((K, N), seed=2)
+            As = np.ascontiguousarray(A.T) if ta else A
+            Bs = np.ascontiguousarray(B.T) if tb else B
+            for iters in ((24,) if mode == 0 else (4, 8, 16, 24)):
+                got = gemm(As, Bs, M, N, K, ta, tb, iters, mode)
+                ref = rl.orc_matmul(As, Bs, M, N, K, iters, mode, ta=ta, tb=tb, literal=1)
+                assert np.array_equal(got, ref), (mode, iters, (M, N, K))
+
+
+def test_alpha_beta_epilogue():
+    M, N, K = 70, 33, 20
+    A = rl.gen_normal((M, K), 3)
+    B = rl.gen_normal((K, N), 4)
+    C0 = rl.gen_normal((M, N), 5)
+    for mode in (0, 1):
+        got = gemm(A, B, M, N, K, 0, 0, 16, mode, alpha=0.5, beta=-2.0, C0=C0)
+        ref = rl.orc_matmul(A, B, M, N, K, 16, mode, alpha=0.5, beta=-2.0, C0=C0)
+        assert np.array_equal(got, ref)
+    # reference DVT known answer: I*B with alpha=1, beta=2 over C0
+    got = gemm(np.eye(2, dtype=np.float32), np.float32([[5, 6], [7, 8]]), 2, 2, 2, 0, 0, 24, 0,
+               alpha=1.0, beta=2.0, C0=np.float32([[1, 2], [3, 4]]))
+    assert got[0, 0] == 7 and got[1, 1] == 16
+
+
+def test_rac_h_matmul_1024_config1_host_pointers():
+    """rac_matmul 1024^3, U[-1,1] seeds 0/1, n=16, through
+    the synchronous rac.h entry point with host buffers."""
+    M = N = K = 1024
+    A = rl.gen_uniform((M, K), seed=0)
+    B = rl.gen_uniform((K, N), seed=1)
+    C = np.zeros((M, N), np.float32)
+    L = lib()
+    L.rac_set_cordic_iters(16)
+    L.rac_set_cordic_mode(1)
+    L.rac_clear_error()
+    L.rac_matmul(rl.p(A), rl.p(B), rl.p(C), M, N, K)
+    assert L.rac_last_error() == b"", L.rac_last_error()
+    d = np.load(os.path.join(rl.GOLDEN, "matmul.npz"))
+    idx = d["idx"]
+    rows, cols = idx // N, idx % N
+    na = np.linalg.norm(A.astype(np.float64), axis=1)[rows]
+    nb = np.linalg.norm(B.astype(np.float64), axis=0)[cols]
+    err = np.abs(C.ravel()[idx].astype(np.float64) - d["C_samples"])
+    assert np.all(err <= 1e-4 * na * nb), float((err / (na * nb)).max())
+    ref = rl.orc_matmul_entries(A, B, M, N, K, 16, 1, rows, cols)
+    assert np.array_equal(C.ravel()[idx], ref)
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24])
+def test_cordic_matmul_4096_sampled(iters):
+    """The metric shape, 4096^3: sampled entries bit-exact vs the checker."""
+    M = N = K = 4096
+    A = rl.gen_uniform((M, K), seed=0)
+    B = rl.gen_uniform((K, N), seed=1)
+    got = gemm(A, B, M, N, K, 0, 0, iters, 1)
+    rng = np.random.default_rng(iters)
+    rows = rng.integers(0, M, 600)
+    cols = rng.integers(0, N, 600)
+    rows[:4] = [0, 0, M - 1, M - 1]
+    cols[:4] = [0, N - 1, 0, N - 1]
+    ref = rl.orc_matmul_entries(A, B, M, N, K, iters, 1, rows, cols)
+    assert np.array_equal(got[rows, cols], ref)
+
+
+def test_reference_launcher_abi():
+    M, N, K = 48, 40, 56
+    A = rl.gen_normal((M, K), 8)
+    Bt = rl.gen_normal((N, K), 9)
+    Ad, Bd = T(A), T(Bt)
+    Cd = torch.zeros((M, N), device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    lib().rac_launch_nt_iters(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, 1.0, 0.0, 16, 1, s)
+    assert np.array_equal(H(Cd), rl.orc_matmul(A, Bt, M, N, K, 16, 1, tb=1))
+    lib().rac_launch_nt(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, 1.0, 0.0, s)
+    assert np.array_equal(H(Cd), rl.orc_matmul(A, Bt, M, N, K, 24, 0, tb=1))
+
+
+# ── exp / activations ──────────────────────────────────────────────────────
+
+SPECIAL = np.float32([0.0, -0.0, 1.0, -1.0, 0.5, 88.0, 88.8, 89.0, -87.0, -88.0, -103.0, -104.0,
+                      200.0, -200.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 0.34657359, -0.34657359])
+
+
+@pytest.mark.parametrize("iters", [1, 5, 8, 16, 24])
+def test_exp_and_activations_bit_exact(iters):
+    x = np.concatenate([rl.gen_normal((100003,), 11, std=4.0), SPECIAL]).astype(np.float32)
+    e = ext()
+    xd = T(x)
+    for name, oname in (("exp", "orc_exp_batch"), ("silu", "orc_silu"),
+                        ("sigmoid", "orc_sigmoid"), ("tanh", "orc_tanh")):
+        print(f"{name} iters={iters}", flush=True)
+        got = H(getattr(e, name)(xd, iters=iters))
+        ref = rl.orc_unary(oname, x, iters)
+        assert np.array_equal(got, ref, equal_nan=True), (name, iters)
+
+
+def test_elementwise_odd_length_and_offsets():
+    e = ext()
+    x = rl.gen_normal((1031,), 12, std=3.0)
+    full = T(x)
+    sub = full[1:]                                   # misaligned, odd length -> scalar path
+    got = H(e.silu(sub, iters=16))
+    assert np.array_equal(got, rl.orc_unary("orc_silu", x[1:], 16))
+
+
+def test_gelu_relu_vs_reference():
+    d = np.load(os.path.join(rl.GOLDEN, "activations.npz"))
+    e = ext()
+    g = H(e.gelu(T(d["x"])))
+    assert np.max(np.abs(g - d["gelu"]) / np.maximum(np.abs(d["gelu"]), 1e-3)) < 2e-6
+    r = H(e.relu(T(d["x"])))
+    assert np.array_equal(r, np.maximum(d["x"], 0))
+
+
+def test_rsqrt_sincos_bit_exact():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([np.exp(rng.uniform(-87, 88, 50000)).astype(np.float32),
+                        np.float32([4.0, 1.0, 0.0, -1.0, np.inf, np.nan, 1e-40, 3e38])])
+    got = H(ext().rsqrt(T(x)))
+    ref = np.array([rl.oracle().orc_rsqrt(float(v)) for v in x], np.float32)
+    assert np.array_equal(got, ref, equal_nan=True)
+    th = np.concatenate([rng.uniform(-7000, 7000, 20000), [0.0, math.pi / 2, 1e9, np.inf, np.nan]]).astype(np.float32)
+    s, c = ext().sincos(T(th))
+    s, c = H(s), H(c)
+    for i in range(0, len(th), 97):
+        so, co = ctypes.c_float(), ctypes.c_float()
+        rl.oracle().orc_sincos(float(th[i]), ctypes.byref(so), ctypes.byref(co))
+        assert (np.float32(so.value) == s[i] or (np.isnan(s[i]) and math.isnan(so.value)))
+        assert (np.float32(co.value) == c[i] or (np.isnan(c[i]) and math.isnan(co.value)))
+    assert np.isnan(s[-3]) and np.isnan(s[-2])   # wrap-loop guard
+
+
+def test_scalar_rac_h_entry_points():
+    L = lib()
+    L.rac_set_cordic_iters(16)
+    assert abs(L.rac_rsqrt(4.0) - 0.5) < 1e-6                       # BVT-12
+    assert L.rac_rsqrt(0.0) == 0.0 and L.rac_rsqrt(-1.0) == 0.0
+    assert abs(L.rac_sigmoid(0.0) - 0.5) < 1e-5
+    assert L.rac_sigmoid(10.0) > 0.999 and L.rac_sigmoid(-10.0) < 0.001
+    assert np.float32(L.rac_exp(0.75)) == np.float32(rl.oracle().orc_exp_n(0.75, 16))
+    s, c = ctypes.c_float(), ctypes.c_float()
+    L.rac_sincos(np.float32(math.pi / 2), ctypes.byref(s), ctypes.byref(c))
+    assert abs(s.value - 1) < 0.01 and abs(c.value) < 0.01          # BVT-12
+    x = rl.gen_normal((300,), 4, std=2.0)
+    y = np.zeros_like(x)
+    L.rac_softmax(rl.p(x), rl.p(y), 300)
+    assert abs(float(y.sum()) - 1) < 1e-5
+    assert rl.max_rel(y, rl.orc_softmax(x[None], 16)[0]) < 1e-5
+    kat = np.float32([3, 4, 0, 0])
+    ko = np.zeros(4, np.float32)
+    L.rac_rmsnorm(rl.p(kat), rl.p(ko), None, 1e-6, 1, 4)                # BVT-13
+    assert np.allclose(ko, [1.2, 1.6, 0, 0], atol=1e-6)
+    xs = rl.gen_normal((257,), 5)
+    so = np.zeros_like(xs)
+    L.rac_silu(rl.p(xs), rl.p(so), 257)
+    assert np.array_equal(so, rl.orc_unary("orc_silu", xs, 16))
+
+
+# ── softmax / norms ────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("iters", [8, 16, 24])
+def test_softmax_config2(iters):
+    """4096 x 4096, N(0, std 2)."""
+    x = rl.gen_normal((4096, 4096), 0, std=2.0)
+    got = H(ext().softmax(T(x), iters=iters))
+    ref = rl.orc_softmax(x, iters)
+    assert rl.max_rel(got, ref, 1e-37) <= 1e-5
+    assert np.allclose(got.sum(1), 1.0, atol=2e-5)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (3, 3), (5, 257), (2, 1024), (7, 16384), (3, 20000), (2, 4099)])
+def test_softmax_shapes(shape):
+    x = rl.gen_normal(shape, 6, std=2.0)
+    if shape[1] > 1:
+        x[0, 0] = -np.inf        # masked entry (causal attention): e^-inf = 0
+    got = H(ext().softmax(T(x), iters=16))
+    ref = rl.orc_softmax(x, 16)
+    assert rl.max_rel(got, ref, 1e-37) <= 1e-5
+
+
+def test_softmax_vs_libm_reference_reported():
+    d = np.load(os.path.join(rl.GOLDEN, "softmax.npz"))
+    for iters, bound in ((8, 2 * 2.0 ** -7), (16, 2 * 2.0 ** -14), (24, 3e-6)):
+        got = H(ext().softmax(T(d["x"]), iters=iters))
+        assert rl.max_rel(got, d["y"]) < bound + 1e-6
+
+
+@pytest.mark.parametrize("shape", [(16384, 4096), (5, 64), (3, 4099), (4, 1), (2, 40000)])
+def test_rmsnorm_layernorm(shape):
+    """BASELINE config 4 (16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6) and edge shapes."""
+    x = rl.gen_normal(shape, 1)
+    g = rl.gen_normal((shape[1],), 2, mean=1.0, std=0.02)
+    b = rl.gen_normal((shape[1],), 3, std=0.1)
+    e = ext()
+    y = H(e.rmsnorm(T(x), T(g), 1e-6))
+    assert rl.max_rel(y, rl.orc_rmsnorm(x, g, 1e-6), 1e-30) <= 1e-5
+    y0 = H(e.rmsnorm(T(x), None, 1e-6))
+    assert rl.max_rel(y0, rl.orc_rmsnorm(x, None, 1e-6), 1e-30) <= 1e-5
+    if shape[0] <= 16:
+        z = H(e.layernorm(T(x), T(g), T(b), 1e-5))
+        zr = rl.orc_layernorm(x, g, b, 1e-5)
+        assert np.max(np.abs(z - zr) / np.maximum(np.abs(zr), 1e-2)) <= 1e-5
+
+
+def test_norms_vs_reference_golden():
+    d = np.load(os.path.join(rl.GOLDEN, "norms.npz"))
+    e = ext()
+    assert rl.max_rel(H(e.rmsnorm(T(d["x"]), T(d["gamma"]), 1e-6)), d["rms"], 1e-30) <= 1e-5
+    assert rl.max_rel(H(e.rmsnorm(T(d["xw"]), T(d["gw"]), 1e-6)), d["rmsw"], 1e-30) <= 1e-5
+    ln = H(e.layernorm(T(d["x"]), T(d["gamma"]), T(d["beta"]), 1e-5))
+    assert np.max(np.abs(ln - d["ln"]) / np.maximum(np.abs(d["ln"]), 1e-2)) <= 1e-5
+
+
+# ── RoPE ───────────────────────────────────────────────────────────────────
+
+def test_rope_cache_bit_exact_vs_reference_digest():
+    d = np.load(os.path.join(rl.GOLDEN, "rope.npz"))
+    c, s = ext().rope_cache(4096, 128, 10000.0, device=DEV)
+    c, s = H(c), H(s)
+    assert rl.sha256(c) == str(d["big_cos_sha"]) and rl.sha256(s) == str(d["big_sin_sha"])
+    c2 = np.zeros((64, 16), np.float32)
+    s2 = np.zeros((64, 16), np.float32)
+    lib().rac_rope_cache(rl.p(c2), rl.p(s2), 64, 32, 10000.0)
+    assert np.array_equal(c2, d["small_cos"]) and np.array_equal(s2, d["small_sin"])
+
+
+@pytest.mark.parametrize("shape", [(2, 2, 16, 64), (1, 3, 37, 6), (2, 1, 9, 2), (1, 2, 40, 1024), (3, 5, 33, 128)])
+def test_rope_apply_bit_exact(shape):
+    B, Hh, Tt, D = shape
+    x = rl.gen_normal(shape, 17)
+    c, s = rl.orc_rope_cache(Tt, D)
+    ref = rl.orc_rope_apply(x, c, s)
+    xd = T(x)
+    ext().rope_apply_(xd, T(c), T(s))
+    assert np.array_equal(H(xd), ref)
+    # the [B, T, H, D] storage used by attention projections
+    xt = T(np.ascontiguousarray(x.transpose(0, 2, 1, 3)))
+    view = xt.transpose(1, 2)
+    ext().rope_apply_(view, T(c), T(s))
+    assert np.array_equal(H(view), ref)
+
+
+def test_rope_apply_golden_and_rac_h():
+    d = np.load(os.path.join(rl.GOLDEN, "rope.npz"))
+    x = np.array(d["apply_x"], copy=True)
+    lib().rac_rope_apply(rl.p(x), rl.p(d["apply_cos"]), rl.p(d["apply_sin"]), 2, 2, 16, 64)
+    assert np.array_equal(x, d["apply_out"])
+
+
+def test_rope_config3_full_size():
+    """Q and K [8, 32, 4096, 128] (B,H,T,D), tables from
+    rac_rope_cache(4096, 128, 10000): bit-exact over the full tensors."""
+    shape = (8, 32, 4096, 128)
+    c, s = ext().rope_cache(4096, 128, device=DEV)
+    ch, sh = H(c), H(s)
+    gen = torch.Generator(device=DEV)
+    for seed in (0, 1):
+        gen.manual_seed(seed)
+        xd = torch.randn(shape, device=DEV, generator=gen)
+        x = H(xd)
+        ref = rl.orc_rope_apply(x, ch, sh)
+        ext().rope_apply_(xd, c, s)
+        got = H(xd)
+        assert np.array_equal(got, ref)
+        del xd, got, ref, x
+
+
+# ── torch surface ──────────────────────────────────────────────────────────
+
+def test_rac_linear_forward_backward():
+    from rac_amd import rac_torch as rt
+    rt.rac_set_mode('cordic')
+    rt.rac_set_precision(16)
+    try:
+        torch.manual_seed(0)
+        lin = rt.RACLinear(96, 80).to(DEV)
+        x = torch.randn(3, 7, 96, device=DEV, requires_grad=True)
+        y = lin(x)
+        W = H(lin.weight)
+        xin = H(x).reshape(-1, 96)
+        ref = rl.orc_matmul(xin, W, 21, 80, 96, 16, 1, tb=1) + H(lin.bias)[None]
+        assert np.array_equal(H(y).reshape(21, 80), ref.astype(np.float32))
+        g = torch.randn_like(y)
+        y.backward(g)
+        go = H(g).reshape(21, 80)
+        gi_ref = rl.orc_matmul(go, W, 21, 96, 80, 16, 1)
+        gw_ref = rl.orc_matmul(go, xin, 80, 96, 21, 16, 1, ta=1)
+        assert np.array_equal(H(x.grad).reshape(21, 96), gi_ref)
+        assert np.array_equal(H(lin.weight.grad), gw_ref)
+        assert np.allclose(H(lin.bias.grad), go.sum(0), rtol=1e-5, atol=1e-5)
+    finally:
+        rt.rac_set_mode('fast')
+        rt.rac_set_precision(24)
+
+
+def test_rac_matmul_fast_mode_matches_torch():
+    from rac_amd import rac_torch as rt
+    A = torch.randn(70, 50, device=DEV)
+    B = torch.randn(50, 30, device=DEV)
+    C = rt.rac_matmul(A, B)
+    assert torch.allclose(C, A.double().matmul(B.double()).float(), rtol=1e-4, atol=1e-4)
+
+
+def test_reference_dvt_properties():
+    from rac_amd import rac_torch as rt
+    torch.manual_seed(42)
+    rope = rt.RACRoPE(head_dim=16, max_seq_len=32)
+    q = torch.randn(2, 4, 8, 16, device=DEV)
+    k = torch.randn_like(q)
+    q2, k2 = rope(q, k)
+    m0 = q.view(2, 4, 8, 8, 2).pow(2).sum(-1).sqrt()
+    m1 = q2.view(2, 4, 8, 8, 2).pow(2).sum(-1).sqrt()
+    assert torch.allclose(m0, m1, atol=1e-4)                          # DVT-27
+    assert torch.allclose(q[:, :, 0], q2[:, :, 0], atol=1e-4)
+    q3, _ = rope(q, k, positions=torch.arange(8))
+    assert torch.allclose(q3, q2, atol=1e-4)
+    ql = torch.randn(1, 1, 4, 16, device=DEV, requires_grad=True)
+    kl = torch.randn(1, 1, 4, 16, device=DEV, requires_grad=True)
+    qo, ko = rope(ql, kl)
+    (qo.sum() + ko.sum()).backward()
+    assert ql.grad is not None and kl.grad is not None
+    # RMSNorm vs formula (DVT-28, atol 1e-5)
+    rms = rt.RACRMSNorm(64, eps=1e-6).to(DEV)
+    x = torch.randn(8, 64, device=DEV)
+    yref = (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)) * rms.weight
+    assert torch.allclose(rms(x), yref, atol=1e-5)
+    # LayerNorm vs nn.LayerNorm (DVT-29, atol 1e-5)
+    ln = rt.RACLayerNorm(48, eps=1e-5).to(DEV)
+    tn = torch.nn.LayerNorm(48, eps=1e-5).to(DEV)
+    x = torch.randn(4, 7, 48, device=DEV)
+    assert torch.allclose(ln(x), tn(x), atol=1e-5)
+
+
+def test_llama_block_small_forward_backward_and_causality():
+    from rac_amd import rac_torch as rt
+    torch.manual_seed(0)
+    blk = rt.RACLlamaBlock(64, 4, ff_dim=176, max_seq_len=32).to(DEV)
+    x = torch.randn(2, 16, 64, device=DEV, requires_grad=True)
+    y = blk(x, is_causal=True)
+    assert y.shape == x.shape and torch.isfinite(y).all()
+    y.sum().backward()
+    assert x.grad is not None and all(p.grad is not None for p in blk.parameters())
+    blk.eval()
+    xa = torch.randn(1, 8, 64, device=DEV)
+    xb = xa.clone()
+    xb[:, -1] = torch.randn(64, device=DEV)
+    with torch.no_grad():
+        ya, yb = blk(xa, is_causal=True), blk(xb, is_causal=True)
+    assert torch.allclose(ya[:, :-1], yb[:, :-1], atol=1e-4)         # DVT-30

@@ -1,0 +1,329 @@
+"""Pins of the CPU checker (oracle/rac_oracle.c) — CPU only.
+
+Each oracle function is checked against something it was not derived from:
+golden vectors written by the compiled reference (tests/golden/), the
+compiled reference itself where it is built here (oracle/_ref), closed forms,
+exhaustive enumeration, or libm within an analytic bound.  Map:
+
+  tables                  golden tables.json (reference rac_cpu.c:20-52)
+  orc_cordic_rotate       golden rotate.npz; compiled _cordic_rotate
+  orc_cordic_chain_fast   exhaustive over all mantissas vs the literal chain
+  orc_fma_cordic /
+  orc_cordic_project      odd-symmetry + projection identity (exhaustive /
+                          random); closed form |P(a)/a - 1| = bias of K-hat
+  orc_shiftadd_mul        integer closed form ma * (mb with low bits cleared)
+  orc_matmul (FAST)       2x2 known answer; golden 1024^3 samples (tolerance,
+                          the reference groups k in 64-tiles)
+  orc_matmul (CORDIC)     per-element bound 1e-4*|a_i|*|b_j| vs golden C
+  orc_rope_cache/apply    golden rope.npz, bit-exact (incl. 4096x64 digest)
+  orc_exp_xy              golden alu_exp.npz (rac_alu_exp), bit-exact
+  orc_exp_n               libm within the CORDIC bound; vs orc_exp_xy
+  orc_softmax_rows        iters=0: golden softmax.npz bit-exact; CORDIC: bound
+  orc_rsqrt               libm 1/sqrt within 1e-6; guard cases; golden KATs
+  orc_rmsnorm/layernorm   libm variant bit-exact vs golden; CORDIC within 1e-6
+  orc_silu/gelu/sigmoid   libm variant vs golden; CORDIC within bound
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import raclib as rl
+
+G = rl.GOLDEN
+
+
+def npz(name):
+    return np.load(os.path.join(G, name))
+
+
+@pytest.fixture(scope="module")
+def o():
+    return rl.oracle()
+
+
+def tables(o):
+    a24 = np.zeros(24, np.float32)
+    h24 = np.zeros(24, np.float32)
+    k25 = np.zeros(25, np.float32)
+    o.orc_tables(rl.p(a24), rl.p(h24), rl.p(k25))
+    return a24, h24, k25
+
+
+def test_tables_match_reference(o):
+    a24, h24, k25 = tables(o)
+    t = json.load(open(os.path.join(G, "tables.json")))
+    assert np.array_equal(a24[:16], np.float32(t["atan16"]))
+    assert np.array_equal(a24[16:], np.float32(t["atan_ext8"]))
+    assert np.array_equal(h24[:16], np.float32(t["atanh16"]))
+    assert np.array_equal(k25, np.float32(t["khat25"]))
+    # extension entries s = 17..24 are exactly 2^-s
+    assert np.array_equal(h24[16:], np.float32([2.0 ** -s for s in range(17, 25)]))
+    # K-hat departs from the textbook gain (documented property of the data)
+    true16 = np.prod([math.sqrt(1 + 4.0 ** -i) for i in range(16)])
+    assert abs(k25[16] / true16 - 1 + 5.9e-6) < 2e-7
+
+
+def test_rotate_matches_reference_golden(o):
+    d = npz("rotate.npz")
+    import ctypes as C
+    bad = 0
+    for vx, vy, th, it, x, y in zip(d["vx"], d["vy"], d["theta"], d["iters"], d["x"], d["y"]):
+        ox, oy = C.c_float(), C.c_float()
+        o.orc_cordic_rotate(float(vx), float(vy), float(th), int(it), C.byref(ox), C.byref(oy))
+        bad += (np.float32(ox.value) != x) or (np.float32(oy.value) != y)
+    assert bad == 0
+
+
+@pytest.mark.skipif(not rl.have_ref(), reason="oracle/_ref not built")
+def test_rotate_matches_compiled_reference(o):
+    import ctypes as C
+    r = rl.ref()
+    rng = np.random.default_rng(5)
+    for _ in range(5000):
+        vx, vy = rng.uniform(-3, 3, 2)
+        th = rng.uniform(-10000, 10000)
+        it = int(rng.integers(4, 25))
+        a, b, c, d = C.c_float(), C.c_float(), C.c_float(), C.c_float()
+        o.orc_cordic_rotate(vx, vy, th, it, C.byref(a), C.byref(b))
+        r.ref_cordic_rotate(vx, vy, th, it, C.byref(c), C.byref(d))
+        assert (a.value, b.value) == (c.value, d.value)
+
+
+def test_direction_sequence(o):
+    d = (np.zeros(24, np.int32))
+    o.orc_cordic_dirs(24, rl.p(d))
+    assert "".join("+" if v > 0 else "-" for v in d) == "+---+-++----++--++--+--+"
+
+
+@pytest.mark.parametrize("iters", [1, 2, 3, 4, 8, 12, 16, 20, 24])
+def test_fast_chain_exhaustive(o, iters):
+    # all 2^23 mantissas at exponent 0; scaling by 2^e is exact, so spot
+    # exponents -60 and +60 as well
+    for e in (0, -60, 60):
+        assert o.orc_check_chain_all_mantissas(iters, e) == 0
+
+
+@pytest.mark.parametrize("iters", [1, 5, 8, 16, 24])
+def test_projection_identity(o, iters):
+    assert o.orc_check_projection_identity(iters, 300000, 0xC0FFEE + iters) == 0
+
+
+def test_projection_gain_bias(o):
+    # P_n(a)/a - 1 is the reference's K-hat bias: -1.9e-5 at n=8,
+    # +5.8e-6 at n=16 and n=24 (independent of a up to rounding)
+    exp = {8: -1.9e-5, 16: 5.8e-6, 24: 5.8e-6}
+    for n, b in exp.items():
+        r = o.orc_cordic_project(1.0, n) - 1.0
+        assert abs(r - b) < 0.1e-5 * (1 if n == 8 else 0.2) + 1e-7, (n, r)
+
+
+def _shiftadd_closed_form(a, b, iters):
+    a, b = np.float32(a), np.float32(b)
+    if a == 0 or b == 0:
+        return np.float32(0)
+    ai = int(a.view(np.uint32))
+    bi = int(b.view(np.uint32))
+    ma = 0x800000 | (ai & 0x7FFFFF)
+    mb = 0x800000 | (bi & 0x7FFFFF)
+    lim = max(1, min(24, iters))
+    mb_t = mb & ~((1 << (24 - lim)) - 1)
+    prod = ma * mb_t
+    top = prod.bit_length() - 1
+    mant = (prod >> (top - 23)) & 0x7FFFFF if top >= 23 else (prod << (23 - top)) & 0x7FFFFF
+    rexp = ((ai >> 23) & 0xFF) - 127 + ((bi >> 23) & 0xFF) - 127 + (top - 46) + 127
+    if rexp <= 0 or rexp >= 255:
+        return np.float32(0)
+    sign = (ai ^ bi) & 0x80000000
+    return np.uint32(sign | (rexp << 23) | mant).view(np.float32)
+
+
+def test_shiftadd_closed_form(o):
+    rng = np.random.default_rng(9)
+    xs = np.concatenate([rng.standard_normal(3000), rng.uniform(-1e30, 1e30, 200),
+                         rng.uniform(-1e-30, 1e-30, 200), [0.0, -0.0, 1.0, -1.0]]).astype(np.float32)
+    for i in range(0, len(xs) - 1):
+        a, b = xs[i], xs[(i * 7919 + 13) % len(xs)]
+        for it in (1, 4, 8, 16, 24):
+            assert np.float32(o.orc_shiftadd_mul(float(a), float(b), it)) == _shiftadd_closed_form(a, b, it)
+    # at 24 bits the product is the exact product truncated toward zero
+    a, b = np.float32(1.1), np.float32(3.3)
+    exact = float(a) * float(b)
+    got = o.orc_shiftadd_mul(float(a), float(b), 24)
+    assert got <= exact and exact - got < 2 * np.spacing(np.float32(got))
+
+
+def test_matmul_known_answers(o):
+    A = np.array([[1, 2], [3, 4]], np.float32)
+    B = np.array([[5, 6], [7, 8]], np.float32)
+    d = npz("matmul.npz")
+    C = rl.orc_matmul(A, B, 2, 2, 2, 24, 0)
+    assert np.array_equal(C, d["kat_C"])
+    assert np.array_equal(C, np.float32([[19, 22], [43, 50]]))
+    # alpha/beta known answer of the reference DVT (C[0]=7, C[3]=28)
+    I2 = np.eye(2, dtype=np.float32)
+    C0 = np.array([[1, 2], [3, 4]], np.float32)
+    Cb = rl.orc_matmul(I2, np.float32([[5, 6], [7, 8]]), 2, 2, 2, 24, 0, alpha=1.0, beta=2.0, C0=C0)
+    assert Cb[0, 0] == 7 and Cb[1, 1] == 16
+    for mode in (1, 2):
+        Cm = rl.orc_matmul(A, B, 2, 2, 2, 16, mode)
+        assert np.allclose(Cm, [[19, 22], [43, 50]], rtol=1e-4)
+
+
+def test_matmul_1024_vs_reference_golden(o):
+    d = npz("matmul.npz")
+    M = N = K = 1024
+    A = rl.gen_uniform((M, K), seed=0)
+    B = rl.gen_uniform((K, N), seed=1)
+    assert rl.sha256(A) == str(d["A_sha"]) and rl.sha256(B) == str(d["B_sha"])
+    idx = d["idx"][::4]
+    rows, cols = (idx // N).astype(np.int32), (idx % N).astype(np.int32)
+    ref = d["C_samples"][::4]
+    na = np.linalg.norm(A.astype(np.float64), axis=1)[rows]
+    nb = np.linalg.norm(B.astype(np.float64), axis=0)[cols]
+    for mode, iters in ((0, 24), (1, 8), (1, 16), (1, 24)):
+        got = rl.orc_matmul_entries(A, B, M, N, K, iters, mode, rows, cols)
+        err = np.abs(got.astype(np.float64) - ref)
+        assert np.all(err <= 1e-4 * na * nb), (mode, iters, float((err / (na * nb)).max()))
+    # the FAST-mode oracle differs from lib/c only by k-grouping
+    got = rl.orc_matmul_entries(A, B, M, N, K, 24, 0, rows, cols)
+    assert np.max(np.abs(got - ref)) < 1e-4
+
+
+def test_matmul_literal_equals_projection_form(o):
+    rng = np.random.default_rng(3)
+    M, N, K = 9, 7, 13
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    for ta, tb in ((0, 0), (0, 1), (1, 0)):
+        Aa = np.ascontiguousarray(A.T) if ta else A
+        Bb = np.ascontiguousarray(B.T) if tb else B
+        for it in (1, 8, 16, 24):
+            c1 = rl.orc_matmul(Aa, Bb, M, N, K, it, 1, ta=ta, tb=tb, literal=1)
+            c2 = rl.orc_matmul(Aa, Bb, M, N, K, it, 1, ta=ta, tb=tb, literal=0)
+            assert np.array_equal(c1, c2)
+        c3 = rl.orc_matmul(Aa, Bb, M, N, K, 24, 0, ta=ta, tb=tb)
+        assert np.allclose(c3, A.astype(np.float64) @ B, rtol=1e-5, atol=1e-5)
+
+
+def test_rope_cache_bit_exact_vs_golden(o):
+    d = npz("rope.npz")
+    c, s = rl.orc_rope_cache(4096, 128)
+    assert rl.sha256(c) == str(d["big_cos_sha"]) and rl.sha256(s) == str(d["big_sin_sha"])
+    c2, s2 = rl.orc_rope_cache(64, 32)
+    assert np.array_equal(c2, d["small_cos"]) and np.array_equal(s2, d["small_sin"])
+    # invariants (reference BVT-14 tolerance 0.001): p=0 gives (1, 0) up to
+    # the 16-step residual angle; |(c,s)| ~ 1
+    assert np.all(np.abs(c[0] - 1) < 1e-3) and np.all(np.abs(s[0]) < 1e-3)
+    assert np.all(np.abs(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2 - 1) < 1e-2)
+
+
+def test_rope_apply_bit_exact_vs_golden(o):
+    d = npz("rope.npz")
+    out = rl.orc_rope_apply(d["apply_x"], d["apply_cos"], d["apply_sin"])
+    assert np.array_equal(out, d["apply_out"])
+
+
+def test_rope_apply_strided_matches_contiguous(o):
+    x = rl.gen_normal((2, 3, 5, 8), seed=4)
+    c, s = rl.orc_rope_cache(5, 8)
+    ref = rl.orc_rope_apply(x, c, s)
+    xt = np.ascontiguousarray(x.transpose(0, 2, 1, 3))  # [B, T, H, D] storage
+    B, T, H, D = xt.shape
+    assert o.orc_rope_apply_strided(rl.p(xt), rl.p(c), rl.p(s), 2, 3, 5, 8, T * H * D, D, H * D) == 0
+    assert np.array_equal(xt.transpose(0, 2, 1, 3), ref)
+
+
+def test_exp_xy_bit_exact_vs_rac_alu_exp(o):
+    d = npz("alu_exp.npz")
+    got = np.array([o.orc_exp_xy(float(v), 16, 1.2074970) for v in d["x"]], np.float32)
+    assert np.array_equal(got, d["y"])
+
+
+def _hyp_last_shift(n):
+    sh = np.zeros(64, np.int32)
+    rl.oracle().orc_hyp_schedule(n, rl.p(sh))
+    return int(sh[n - 1]), sh[:n]
+
+
+def test_hyperbolic_schedule():
+    _, s16 = _hyp_last_shift(16)
+    assert list(s16) == [1, 2, 3, 4, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 13, 14]
+    _, s24 = _hyp_last_shift(24)
+    assert list(s24) == [1, 2, 3, 4, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22]
+    assert abs(rl.oracle().orc_hyp_kinv(16) - 1.2074970) < 2e-7
+
+
+@pytest.mark.parametrize("n", [8, 16, 24])
+def test_exp_cordic_error_bound(o, n):
+    x = np.concatenate([np.linspace(-87, 88, 20001), rl.gen_normal((5000,), 3, std=2.0)]).astype(np.float32)
+    y = rl.orc_unary("orc_exp_batch", x, n)
+    true = np.exp(x.astype(np.float64))
+    rel = np.abs(y - true) / true
+    last, _ = _hyp_last_shift(n)
+    # residual angle <= atanh(2^-s) ~ 2^-s, plus ~n roundings
+    assert rel.max() <= 1.05 * 2.0 ** -last + n * 6e-8, rel.max()
+    xy = np.array([o.orc_exp_xy(float(v), n, o.orc_hyp_kinv(n)) for v in x[::7]], np.float32)
+    assert rl.max_rel(y[::7], xy) < 1e-6
+
+
+def test_exp_special_values(o):
+    assert o.orc_exp_n(0.0, 16) == pytest.approx(1.0, rel=7e-5)
+    assert o.orc_exp_n(-200.0, 16) == 0.0
+    assert math.isinf(o.orc_exp_n(200.0, 16))
+    assert math.isnan(o.orc_exp_n(float("nan"), 16))
+    assert o.orc_exp_n(float("-inf"), 16) == 0.0
+
+
+def test_softmax_libm_bit_exact_and_cordic_bound(o):
+    d = npz("softmax.npz")
+    assert np.array_equal(rl.orc_softmax(d["x"], 0), d["y"])
+    for n in (8, 16, 24):
+        last, _ = _hyp_last_shift(n)
+        y = rl.orc_softmax(d["x"], n)
+        assert np.allclose(y.sum(1), 1.0, atol=1e-5)
+        assert rl.max_rel(y, d["y"]) <= 2.2 * 2.0 ** -last + 1e-6
+
+
+def test_rsqrt_against_libm_and_guards(o):
+    x = np.exp(np.random.default_rng(1).uniform(-85, 85, 50000)).astype(np.float32)
+    got = np.array([o.orc_rsqrt(float(v)) for v in x])
+    assert rl.max_rel(got, 1 / np.sqrt(x.astype(np.float64))) < 1e-6
+    assert abs(o.orc_rsqrt(4.0) - 0.5) < 1e-6
+    assert o.orc_rsqrt(0.0) == 0.0 and o.orc_rsqrt(-1.0) == 0.0 and o.orc_rsqrt(float("inf")) == 0.0
+    assert math.isnan(o.orc_rsqrt(float("nan")))
+    d = npz("activations.npz")
+    got = np.array([o.orc_rsqrt(float(v)) for v in d["xq"]], np.float32)
+    assert rl.max_rel(got, d["rsqrt"], floor=1e-30) < 1e-6
+    # subnormal input
+    assert rl.max_rel([o.orc_rsqrt(1e-40)], [1 / math.sqrt(np.float32(1e-40))]) < 1e-6
+
+
+def test_norms(o):
+    d = npz("norms.npz")
+    assert np.array_equal(rl.orc_rmsnorm(d["x"], d["gamma"], 1e-6, 0), d["rms"])
+    assert np.array_equal(rl.orc_layernorm(d["x"], d["gamma"], d["beta"], 1e-5, 0), d["ln"])
+    assert np.array_equal(rl.orc_rmsnorm(d["xw"], d["gw"], 1e-6, 0), d["rmsw"])
+    assert rl.max_rel(rl.orc_rmsnorm(d["x"], d["gamma"], 1e-6, 1), d["rms"], 1e-6) < 1e-6
+    assert rl.max_rel(rl.orc_layernorm(d["x"], d["gamma"], d["beta"], 1e-5, 1), d["ln"], 1e-3) < 1e-5
+    kat = rl.orc_rmsnorm(d["kat"], None, 1e-6, 1)
+    assert np.allclose(kat, [[1.2, 1.6, 0, 0]], atol=1e-6)
+
+
+def test_activations(o):
+    d = npz("activations.npz")
+    x = d["x"]
+    assert np.array_equal(rl.orc_unary("orc_silu", x, 0), d["silu"])
+    assert np.array_equal(rl.orc_unary("orc_gelu", x), d["gelu"])
+    sig0 = rl.orc_unary("orc_sigmoid", x, 0)
+    # reference form 0.5(1+tanh(x/2)) cancels to 0 for x << 0, so an absolute
+    # floor: both are the same function to ~1 ulp of 0.5
+    assert np.max(np.abs(sig0 - d["sigmoid"]) / np.maximum(np.abs(d["sigmoid"]), 0.1)) < 1e-6
+    for n in (8, 16, 24):
+        last, _ = _hyp_last_shift(n)
+        s = rl.orc_unary("orc_silu", x, n)
+        assert np.max(np.abs(s - d["silu"]) / np.maximum(np.abs(d["silu"]), 1e-3)) < 1.1 * 2.0 ** -last + 1e-6
+        t = rl.orc_unary("orc_tanh", x, n)
+        assert np.max(np.abs(t - np.tanh(x.astype(np.float64)))) < 2 * 2.0 ** -last + 1e-6
