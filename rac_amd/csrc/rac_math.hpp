@@ -32,6 +32,23 @@ __device__ __forceinline__ void st4_stream(float4* p, float4 v) {
 // y is carried doubled (yh = x0); each later micro-rotation is two FMAs with
 // power-of-two constants; the final y update is never needed.  Bit-identical
 // to the literal chain for all finite x0 whose products stay normal.
+// Micro-rotation i >= 2 of the chain, constants forced to compile time.
+template <int N, int I>
+struct ChainStep {
+    __device__ __forceinline__ static void run(float& x, float& yh) {
+        constexpr float cx = chain_cx(I);
+        constexpr float cy = chain_cy(I);
+        const float xn = __builtin_fmaf(cx, yh, x);
+        if constexpr (I + 1 < N) {
+            yh = __builtin_fmaf(cy, x, yh);
+            x = xn;
+            ChainStep<N, I + 1>::run(x, yh);
+        } else {
+            x = xn;
+        }
+    }
+};
+
 template <int N>
 __device__ __forceinline__ float cordic_rot_x(float x0) {
     static_assert(N >= 1 && N <= kMaxIters, "iteration count");
@@ -40,12 +57,7 @@ __device__ __forceinline__ float cordic_rot_x(float x0) {
     } else {
         float x = x0 * 1.5f;
         float yh = x0;
-#pragma unroll
-        for (int i = 2; i < N; i++) {
-            const float xn = __builtin_fmaf(chain_cx(i), yh, x);
-            if (i + 1 < N) yh = __builtin_fmaf(chain_cy(i), x, yh);
-            x = xn;
-        }
+        if constexpr (N > 2) ChainStep<N, 2>::run(x, yh);
         return x;
     }
 }
@@ -147,18 +159,29 @@ __device__ __forceinline__ float exp_scale(float er, int k) {
     return (bias_k < 0) ? 0.0f : res;
 }
 
+// Step J of the product-register exp, constants forced to compile time.
+template <int N, int J>
+struct HypStep {
+    __device__ __forceinline__ static void run(float& p, float& z) {
+        constexpr float S = hyp_S(J);
+        constexpr float C = hyp_C(J);
+        const float ds = __builtin_copysignf(S, z);
+        p = __builtin_fmaf(ds, p, p);
+        if constexpr (J + 1 < N) {
+            z = __builtin_fmaf(-ds, C, z);
+            HypStep<N, J + 1>::run(p, z);
+        }
+    }
+};
+
 template <int N>
 __device__ __forceinline__ float exp_cordic(float x, float khinv) {
+    static_assert(N >= 1 && N <= kMaxIters, "iteration count");
     int k;
     float r;
     exp_reduce(x, k, r);
     float p = 1.0f, z = r;
-#pragma unroll
-    for (int j = 0; j < N; j++) {
-        const float ds = __builtin_copysignf(hyp_S(j), z);
-        p = __builtin_fmaf(ds, p, p);
-        if (j + 1 < N) z = __builtin_fmaf(-ds, hyp_C(j), z);
-    }
+    HypStep<N, 0>::run(p, z);
     const float res = exp_scale(p * khinv, k);
     return (x != x) ? x : res;
 }
@@ -178,6 +201,20 @@ __device__ __forceinline__ float exp_cordic_rt(float x, int n, float khinv) {
 }
 
 // ── rsqrt by hyperbolic vectoring ────────────────────────────────────────
+
+// Vectoring step J (d = -sign(Y)), constants forced to compile time.
+template <int N, int J>
+struct VecStep {
+    __device__ __forceinline__ static void run(float& X, float& Y) {
+        constexpr float S = hyp_S(J);
+        const float ds = __builtin_copysignf(S, Y);
+        const float Xn = __builtin_fmaf(-ds, Y, X);
+        const float Yn = __builtin_fmaf(-ds, X, Y);
+        X = Xn;
+        Y = Yn;
+        if constexpr (J + 1 < N) VecStep<N, J + 1>::run(X, Y);
+    }
+};
 //
 // rac_rsqrt's contract (rac_cpu.c:330-335): v <= 0 -> 0, NaN -> NaN,
 // +inf -> 0.  v = m 4^e, m in [0.5, 2); vectoring (m + 1/4, m - 1/4) to
@@ -193,20 +230,30 @@ __device__ __forceinline__ float rsqrt_cordic(float v, float khinv16) {
     if (ex & 1) { m = mant * 2.0f; e = (ex - 1) / 2; }
     else { m = mant; e = ex / 2; }
     float X = m + 0.25f, Y = m - 0.25f;
-#pragma unroll
-    for (int j = 0; j < kRsqrtSteps; j++) {
-        const float ds = __builtin_copysignf(hyp_S(j), Y);
-        const float Xn = __builtin_fmaf(-ds, Y, X);
-        const float Yn = __builtin_fmaf(-ds, X, Y);
-        X = Xn;
-        Y = Yn;
-    }
+    VecStep<kRsqrtSteps, 0>::run(X, Y);
     const float root = X * khinv16;
     const float r = 1.0f / root;
     return __builtin_ldexpf(r, -e);
 }
 
 // ── Circular CORDIC sin/cos (rac_cpu.c:90-118, 322-328) ──────────────────
+
+// Rotation step I: d from the residual angle (angle >= 0 -> +1), x/y moved by
+// d*y*2^-I exactly as written in the reference (the products are exact).
+template <int N, int I>
+struct CircStep {
+    __device__ __forceinline__ static void run(float& x, float& y, float& angle) {
+        constexpr float scale = pow2(-I);
+        constexpr float at = kAtan[I];
+        const float d = (angle >= 0.0f) ? 1.0f : -1.0f;
+        const float xn = x - d * y * scale;
+        const float yn = y + d * x * scale;
+        angle -= d * at;
+        x = xn;
+        y = yn;
+        if constexpr (I + 1 < N) CircStep<N, I + 1>::run(x, y, angle);
+    }
+};
 // One 16-step rotation of (K_INV, 0) by theta, with the reference's
 // sequential float wrap of theta into (-pi, pi] (a loop, not a remainder:
 // its rounding drift at large angles is part of the table's values).
@@ -225,17 +272,8 @@ __device__ __forceinline__ void sincos_cordic(float theta, float& s, float& c) {
     float x = kKInv, y = 0.0f;
     if (theta > kPi * 0.5f) { x = -x; y = -y; theta -= kPi; }
     else if (theta < -kPi * 0.5f) { x = -x; y = -y; theta += kPi; }
-    float angle = theta, scale = 1.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float d = (angle >= 0.0f) ? 1.0f : -1.0f;
-        const float xn = x - d * y * scale;
-        const float yn = y + d * x * scale;
-        angle -= d * kAtan[i];
-        x = xn;
-        y = yn;
-        scale *= 0.5f;
-    }
+    float angle = theta;
+    CircStep<16, 0>::run(x, y, angle);
     c = x;
     s = y;
 }

