@@ -115,12 +115,22 @@ def bench_gpu(args):
 
     w = 2 * n + 1
     achieved = M * N * K * 2 * w / launch_s / 1e12
+    traffic = None
+    try:   # HBM bytes per launch from the committed rocprofv3 --pmc runs
+        with open(os.path.join(ROOT, "profiles", "pmc_traffic.json")) as f:
+            pm = json.load(f)
+        k = pm["kernels"][f"gemm_cordic_4096_n{n}"]
+        traffic = int(k["fetch_kib"] * 1024 * pm["fetch_scale"] + k["write_kib"] * 1024 * pm["write_scale"])
+    except (OSError, KeyError, ValueError):
+        pass
     return {
         "value": round(2 * M * N * K / (ms_per_step / 1e3) / 1e9, 1),
         "ms_per_step": round(ms_per_step, 3),
         "roofline": {"bound": "valu", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
+                     "traffic_note": "HBM bytes/launch (FETCH_SIZE x2 + WRITE_SIZE, copy-calibrated; "
+                                     "profiles/gemm_cordic16_4096_pmc.md); algorithmic A+B+C = 2.01e8",
                      "kernel": f"gemm_kernel<CORDIC,{n},NN> 64x64 tile, 4x4 per lane",
                      "avg_launch_ms": round(launch_s * 1e3, 3),
                      "work_per_mac": f"{w} FMA lane-ops (2n+1)"},
@@ -286,11 +296,23 @@ def main():
     ap.add_argument("--iters", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--matmul-only", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device-to-device tensor copy 3 times (scales the "
+                         "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc runs)")
     ap.add_argument("--cpu-baseline-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.cpu_baseline_child:
         cpu_baseline_child()
+        return
+    if args.copy_calibration:
+        import torch
+        x = torch.ones(64 * 1024 * 1024, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_dispatch": x.numel() * 4}))
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

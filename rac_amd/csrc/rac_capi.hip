@@ -223,7 +223,6 @@ static int check_rope(const void* x, const void* c, const void* s, long b, long 
     if (!x || !c || !s) return fail(RAC_ERR_NULL_PTR, "rac_rope_apply: null buffer");
     if (b <= 0 || h <= 0 || t <= 0 || d <= 0 || (d & 1))
         return fail(RAC_ERR_INVALID_DIM, "rac_rope_apply: dims must be > 0 and head_dim even");
-    if ((b * h + 15) / 16 > 65535L) return fail(RAC_ERR_INVALID_DIM, "rac_rope_apply: batch*heads too large");
     return RAC_OK;
 }
 

@@ -5,10 +5,11 @@
 //
 // RoPE apply (rac_cpu.c:600-635) is pure HBM streaming: each (b, h, t) row of
 // head_dim floats is rotated pairwise by the table row t.  A workgroup owns a
-// fixed block of positions t and walks a slice of the (b, h) rows, so its
+// fixed block of positions t and a slice of kRopeRslice (b, h) rows, so its
 // cos/sin values are loaded once into registers and reused; each lane moves
-// 16 bytes per row with one load and one store (1 read + 1 write per element,
-// the HBM minimum), and consecutive lanes touch consecutive addresses.
+// 16 bytes per row with one non-temporal load and store (1 read + 1 write per
+// element, the HBM minimum), and consecutive lanes touch consecutive
+// addresses.
 #include <hip/hip_runtime.h>
 #include "rac_math.hpp"
 #include "rac_internal.hpp"
@@ -174,7 +175,10 @@ hipError_t rope_cache_launch(float* cos_out, float* sin_out, const float* inv_fr
 // owns one float4 (two pairs) of a row.  A block covers RPB positions and
 // RSLICE consecutive (b, h) rows.
 
-constexpr int kRopeRslice = 16;
+// (b, h) rows per lane: 2 measured best on MI355X (335 us for Q+K
+// [8,32,4096,128], ~the 1:1 streaming-copy rate); more rows per lane cut
+// the number of workgroups in flight and lost bandwidth (16 rows: 394 us).
+constexpr int kRopeRslice = 2;
 
 template <int LPR>   // lanes per row = head_dim / 4, a power of two <= 256
 __global__ __launch_bounds__(256) void rope_apply_vec_kernel(
@@ -246,9 +250,10 @@ hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_ta
                          (sh % 4 == 0) && (st % 4 == 0) &&
                          ((reinterpret_cast<uintptr_t>(cos_tab) & 7) == 0) &&
                          ((reinterpret_cast<uintptr_t>(sin_tab) & 7) == 0);
-    if (pow2_lpr && aligned) {
+    const long grid_y = (bh_total + kRopeRslice - 1) / kRopeRslice;
+    if (pow2_lpr && aligned && grid_y <= 65535) {
         const int rpb = 256 / lpr;
-        dim3 grid((unsigned)((seq + rpb - 1) / rpb), (unsigned)((bh_total + kRopeRslice - 1) / kRopeRslice));
+        dim3 grid((unsigned)((seq + rpb - 1) / rpb), (unsigned)grid_y);
 #define RAC_ROPE_CASE(L)                                                                          \
     case L:                                                                                       \
         hipLaunchKernelGGL((rope_apply_vec_kernel<L>), grid, dim3(256), 0, s, x, cos_tab, sin_tab, \

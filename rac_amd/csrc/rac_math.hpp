@@ -145,18 +145,23 @@ __device__ __forceinline__ float shiftadd_mul(float a, float b, int iters) {
 // p <- p (1 + d 2^-s) as one FMA, z <- z - d atanh(2^-s) as one FMA with
 // the constant atanh(2^-s) 2^s, d = copysign(1, z) (rac_alu.c:246).  Output
 // (p / K_h(n)) 2^k through the exponent field (rac_alu.c:572-581).
+// t = fma(x, 1/ln2, +-0.5) truncated; (x >= 0 ? 0.5 : -0.5) is written as
+// copysign(0.5, x): they differ only at x = -0, where both truncate to 0.
+// t is clamped to +-2^30 (one v_med3) so the conversion is always defined.
 __device__ __forceinline__ void exp_reduce(float x, int& k, float& r) {
-    float t = __builtin_fmaf(x, kInvLn2, (x >= 0.0f) ? 0.5f : -0.5f);
-    t = fminf(fmaxf(t, -1073741824.0f), 1073741824.0f);
+    float t = __builtin_fmaf(x, kInvLn2, __builtin_copysignf(0.5f, x));
+    t = __builtin_amdgcn_fmed3f(t, -1073741824.0f, 1073741824.0f);
     k = (int)t;
     r = __builtin_fmaf(-(float)k, kLn2, x);
 }
 
+// er * 2^k with the reference's exponent-field semantics (k + 127 <= 0 ->
+// 0; k + 127 > 254 -> er * inf; otherwise the product er * 2^k, rounded
+// once).  v_ldexp_f32 computes er * 2^k with one rounding for every k, so
+// only the flush of k <= -127 needs a select.
 __device__ __forceinline__ float exp_scale(float er, int k) {
-    const int bias_k = k + 127;
-    const float scaled = er * as_f((uint32_t)(bias_k & 0xFF) << 23);
-    float res = (bias_k > 254) ? er * __builtin_inff() : scaled;
-    return (bias_k < 0) ? 0.0f : res;
+    const float res = __builtin_ldexpf(er, k);
+    return (k <= -127) ? 0.0f : res;
 }
 
 // Step J of the product-register exp, constants forced to compile time.
