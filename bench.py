@@ -202,6 +202,33 @@ def bench_hbm_ops(torch, ext, dev, g):
     record("rmsnorm_16384x4096", 2 * 4 * R * D + 4 * D, _events_time(rms, reps, torch))
     del xr, yr
 
+    # RACLlamaBlock forward, d=4096, H=32, ff=11008, batch 1,
+    # seq 2048, causal, weights ~ N(0, 0.02), x ~ N(0, 1), CORDIC mode
+    from rac_amd import rac_torch as rt
+    torch.manual_seed(0)
+    blk = rt.RACLlamaBlock(4096, 32, ff_dim=11008, max_seq_len=2048).to(dev)
+    with torch.no_grad():
+        for prm in blk.parameters():
+            if prm.dim() == 2:
+                prm.normal_(0.0, 0.02, generator=g)
+    xb = torch.randn((1, 2048, 4096), device=dev, generator=g)
+    prev_mode, prev_iters = rt.rac_get_mode(), rt.rac_get_precision()
+    rt.rac_set_mode("cordic")
+    try:
+        for n in (8, 16, 24):
+            rt.rac_set_precision(n)
+            with torch.no_grad():
+                blk(xb, is_causal=True)
+                torch.cuda.synchronize()
+                t = _events_time(lambda: blk(xb, is_causal=True), 2, torch)
+            out[f"llama_block_T2048_n{n}"] = {"ms": round(t * 1e3, 2),
+                                              "linear_equiv_TFLOPs": round(644.2e9 / t / 1e12, 3)}
+            print(f"# llama block n={n}: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    finally:
+        rt.rac_set_mode(prev_mode)
+        rt.rac_set_precision(prev_iters)
+    del blk, xb
+
     # SiLU 16384 x 11008 (n = 16)
     xsilu = torch.randn((16384, 11008), device=dev, generator=g)
     ysilu = torch.empty_like(xsilu)

@@ -22,6 +22,17 @@
 extern "C" {
 #endif
 
+/* The reference's pair type (rac.h:25-33): HIP's float2 in HIP code, the
+ * same two-float struct for C and C++ hosts. */
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#else
+typedef struct {
+    float x;
+    float y;
+} float2;
+#endif
+
 #define RAC_K_INV 0.60725f /* rac.h:39 */
 #define RAC_K 1.64676f     /* rac.h:40 */
 #define RAC_ITERS 16       /* rac.h:41 */
@@ -54,6 +65,25 @@ void rac_destroy_context(rac_context ctx);
 int rac_query_capability(rac_context ctx, rac_op_type op);
 int rac_execute(rac_context ctx, rac_op_type op, void *desc);
 
+/* ── core rotation, polar, similarity, complex (rac.h:101-189) ─────────────
+ * Semantics of the reference CPU library (rac_cpu.c:136-228): angles are
+ * reduced to (-pi, pi] and vectors with x < 0 are pre-rotated by pi, so
+ * every call holds over the whole plane; 16 CORDIC steps; projections use
+ * cosf/sinf of the angle.  Angles with |theta| >= 2^27 or +-inf give NaN
+ * (the reference's reduction loop does not end there). */
+float2 rac_rotate(float2 v, float theta);          /* (v * K_INV) rotated by theta */
+float2 rac_rotate_raw(float2 v, float theta);      /* no gain compensation */
+float2 rac_compensate(float2 v, int chain_length); /* v * K_INV^chain_length */
+float rac_project(float2 v, float theta);          /* v.x cos(theta) + v.y sin(theta) */
+void rac_polar(float2 v, float *mag, float *angle);
+float rac_norm(float2 v);
+float2 rac_normalize(float2 v);
+float rac_dot(float2 a, float2 b);
+float rac_coherence(float2 a, float2 b);
+float2 rac_complex_mul(float2 a, float2 b);
+/* DCT-II: X[k] = sum_i x[i] cos(pi (2i+1) k / 2n).  rac.h:189. */
+void rac_dct(float *x, float *X, int n);
+
 /* ── hyperbolic / activations (rac.h:198-214) ────────────────────────────── */
 
 /* e^x by hyperbolic CORDIC (RAC_CORDIC_ITERS Walther steps, ln2 range
@@ -64,6 +94,14 @@ float rac_tanh(float x);
 /* Row softmax of n floats (max, CORDIC exp, sum, multiply by 1/sum).
  * Replaces rac.h:214 / rac_hip.cpp:315-329. */
 void rac_softmax(float *x, float *out, int n);
+
+/* ── batch vector operations (rac.h:223-240) ─────────────────────────────── */
+
+void rac_rotate_batch(float2 *v, float *theta, float2 *out, int n);
+/* sum_i rac_project(a[i], angle(b[i])) * |b[i]| */
+float rac_inner(float2 *a, float2 *b, int n);
+/* C[i*n + j] = rac_project(a[i], angle(b[j])) * |b[j]| */
+void rac_outer(float2 *a, float2 *b, float *C, int m, int n);
 
 /* ── matmul (rac.h:249) ──────────────────────────────────────────────────── */
 
@@ -93,6 +131,21 @@ void rac_rope_cache(float *cos_out, float *sin_out, int max_seq, int head_dim, f
  * (semantics of rac_cpu.c:600-635). */
 void rac_rope_apply(float *x, const float *cos_tab, const float *sin_tab, int batch,
                     int n_heads, int seq, int head_dim);
+
+/* Scaled dot-product attention on [batch, n_heads, seq, head_dim] tensors,
+ * composed of RAC stages (rac.h:323-335): scores = Q K^T / sqrt(head_dim)
+ * by rac_matmul, is_causal -> -inf above the diagonal, plus the optional
+ * additive [seq, seq] mask, row softmax with the CORDIC exp, out = P V by
+ * rac_matmul.  Mode and iteration count from the process knobs. */
+void rac_attention(const float *q, const float *k, const float *v, const float *mask,
+                   int is_causal, float *out, int batch, int n_heads, int seq, int head_dim);
+
+/* ── tunable precision (rac.h:345-346; semantics of rac_cpu.c:275-288) ────── */
+
+/* rac_rotate with iters (clamped to [4, 24]) steps and gain 1/K(iters). */
+float2 rac_rotate_precision(float2 v, float theta, int iters);
+/* v . (cos, sin)(theta), the pair from one iters-step CORDIC rotation. */
+float rac_project_precision(float2 v, float theta, int iters);
 
 /* ── batch activations with the rac_cpu.h signatures (rac_cpu.h:169-172) ── */
 

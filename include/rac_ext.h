@@ -56,6 +56,17 @@ float rac_rsqrt_gain_inverse(void);
 int rac_gemm_dev(const float *A, const float *B, float *C, int M, int N, int K,
                  int trans_a, int trans_b, float alpha, float beta, int iters, int mode,
                  void *stream);
+/* `batch` independent products (batch <= 65535): C_z = alpha op(A_z) op(B_z)
+ * (+ beta C_z) with A_z = A + z*stride_a etc. (element strides). */
+int rac_gemm_batched_dev(const float *A, const float *B, float *C, int M, int N, int K,
+                         int trans_a, int trans_b, float alpha, float beta, int iters, int mode,
+                         int batch, long stride_a, long stride_b, long stride_c, void *stream);
+/* Attention softmax of rows that form [.., seq, seq] score blocks: row r is
+ * query position t = r % seq; is_causal sets -inf for columns > t, then the
+ * optional additive mask[t*seq + col] is added; 1/sum is 0 for a sum that is
+ * not > 0 (rac_cpu.c:664-687).  x == y is allowed. */
+int rac_softmax_masked_dev(const float *x, float *y, long rows, long seq, const float *mask,
+                           int is_causal, int iters, void *stream);
 /* Softmax of each of `rows` rows of n floats (rac_cpu.c:258-271 with the
  * n-step CORDIC exp). */
 int rac_softmax_dev(const float *x, float *y, long rows, long n, int iters, void *stream);
@@ -89,6 +100,52 @@ int rac_rope_cache_dev(float *cos_out, float *sin_out, int max_seq, int head_dim
 int rac_rope_apply_dev(float *x, const float *cos_tab, const float *sin_tab, int batch,
                        int n_heads, int seq, int head_dim, long stride_b, long stride_h,
                        long stride_t, void *stream);
+
+/* Vector primitives over n items of interleaved (x, y) pairs.  `op` selects
+ * the rac.h primitive evaluated per item i (rac.h:101-250, 345-346, with the
+ * semantics of rac_cpu.c:136-288):
+ *   RAC_V2_ROTATE      out2[i] = rac_rotate(a[i], theta[i])
+ *   RAC_V2_ROTATE_RAW  out2[i] = rac_rotate_raw(a[i], theta[i])
+ *   RAC_V2_COMPENSATE  out2[i] = rac_compensate(a[i], iarg)
+ *   RAC_V2_PROJECT     out1[i] = rac_project(a[i], theta[i])
+ *   RAC_V2_POLAR       out2[i] = (mag, angle) of rac_polar(a[i])
+ *   RAC_V2_NORMALIZE   out2[i] = rac_normalize(a[i])
+ *   RAC_V2_DOT         out1[i] = rac_dot(a[i], b[i])
+ *   RAC_V2_COHERENCE   out1[i] = rac_coherence(a[i], b[i])
+ *   RAC_V2_COMPLEX_MUL out2[i] = rac_complex_mul(a[i], b[i])
+ *   RAC_V2_ROTATE_N    out2[i] = rac_rotate_precision(a[i], theta[i], iarg)
+ *   RAC_V2_PROJECT_N   out1[i] = rac_project_precision(a[i], theta[i], iarg)
+ *   RAC_V2_INNER_TERM  out1[i] = rac_project(a[i], angle(b[i])) * |b[i]|
+ * Operands an op does not use may be NULL. */
+#define RAC_V2_ROTATE 0
+#define RAC_V2_ROTATE_RAW 1
+#define RAC_V2_COMPENSATE 2
+#define RAC_V2_PROJECT 3
+#define RAC_V2_POLAR 4
+#define RAC_V2_NORMALIZE 5
+#define RAC_V2_DOT 6
+#define RAC_V2_COHERENCE 7
+#define RAC_V2_COMPLEX_MUL 8
+#define RAC_V2_ROTATE_N 9
+#define RAC_V2_PROJECT_N 10
+#define RAC_V2_INNER_TERM 11
+int rac_vec2_dev(int op, long n, const float *a, const float *b, const float *theta, int iarg,
+                 float *out2, float *out1, void *stream);
+/* *out = rac_inner(a, b, n) (rac.h:233), one workgroup, fixed-order tree sum. */
+int rac_inner_dev(const float *a, const float *b, long n, float *out, void *stream);
+/* C[m,n] = rac_outer(a, b) (rac.h:240). */
+int rac_outer_dev(const float *a, const float *b, float *C, int m, int n, void *stream);
+/* X = rac_dct(x) (rac.h:189), one lane per output k. */
+int rac_dct_dev(const float *x, float *X, int n, void *stream);
+/* rac_attention (rac.h:330) on device buffers [batch, n_heads, seq, head_dim]:
+ * scores = Q K^T / sqrt(head_dim) by the RAC matmul (mode, iters), causal
+ * and additive [seq, seq] mask, CORDIC softmax in place, out = P V by the RAC
+ * matmul.  workspace: rac_attention_workspace_bytes(batch, n_heads, seq)
+ * bytes of device memory owned by the caller (the scores). */
+long rac_attention_workspace_bytes(int batch, int n_heads, int seq);
+int rac_attention_dev(const float *q, const float *k, const float *v, const float *mask,
+                      int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
+                      float *workspace, int iters, int mode, void *stream);
 
 /* ── reference launcher ABI (rac_kernels.hip:822-909; bound by
  *    rac_torch_bind.cpp:16-45 with the stream as void*) ──────────────────── */

@@ -763,3 +763,198 @@ ORC_API long orc_check_projection_identity(int iters, long count, uint64_t seed)
     }
     return bad;
 }
+
+/* ── Vector primitives of rac.h (rac.h:101-250, 345-346) ─────────────────
+ * Restated from the CPU library's definitions (rac_cpu.c:136-228, 275-288,
+ * 351-371), which reduce the angle to (-pi, pi] and pre-rotate left-half-
+ * plane vectors, so they hold over the whole plane.  cosf/sinf/powf are
+ * glibc's here and the device's own on the GPU (a few ulp apart); every
+ * CORDIC step is exact in either. */
+
+/* rac_polar, rac_cpu.c:158-180 (16 vectoring steps). */
+ORC_API void orc_polar(float vx, float vy, float *mag, float *angle)
+{
+    orc_init();
+    float pre = 0.0f;
+    if (vx < 0.0f) {
+        pre = (vy >= 0.0f) ? ORC_PI : -ORC_PI;
+        vx = -vx;
+        vy = -vy;
+    }
+    float x = vx, y = vy, z = 0.0f, scale = 1.0f;
+    for (int i = 0; i < 16; i++) {
+        float d = (y < 0.0f) ? 1.0f : -1.0f;
+        float xn = x - d * y * scale;
+        float yn = y + d * x * scale;
+        z += d * orc_atan[i];
+        x = xn;
+        y = yn;
+        scale *= 0.5f;
+    }
+    *mag = x * ORC_K_INV;
+    *angle = pre - z;
+}
+
+/* rac_project, rac_cpu.c:150-154. */
+ORC_API float orc_project(float vx, float vy, float theta)
+{
+    return fmaf(vx, cosf(theta), vy * sinf(theta));
+}
+
+static int clamp_prec(int iters)                 /* _clamp_iters, rac_cpu.c:54-58 */
+{
+    return iters < 4 ? 4 : (iters > 24 ? 24 : iters);
+}
+
+/* Elementwise primitive `op` over n items (the device library's op codes):
+ *  0 rac_rotate        (rac_cpu.c:136-139)   a, th -> o2
+ *  1 rac_rotate_raw    (:141-143)            a, th -> o2
+ *  2 rac_compensate    (:145-148)            a, iarg -> o2
+ *  3 rac_project       (:150-154)            a, th -> o1
+ *  4 rac_polar         (:158-180)            a -> o2 = (mag, angle)
+ *  5 rac_normalize     (:188-192)            a -> o2
+ *  6 rac_dot           (:196-201)            a, b -> o1
+ *  7 rac_coherence     (:203-208)            a, b -> o1
+ *  8 rac_complex_mul   (:212-217)            a, b -> o2
+ *  9 rac_rotate_n      (:275-280)            a, th, iarg -> o2
+ * 10 rac_project_n     (:282-288)            a, th, iarg -> o1
+ * 11 rac_inner's term  (:355-357)            a, b -> o1
+ * a, b, o2 are interleaved (x, y) pairs. */
+ORC_API void orc_prim(int op, long n, const float *a, const float *b, const float *th,
+                      int iarg, float *o2, float *o1)
+{
+    orc_init();
+    for (long i = 0; i < n; i++) {
+        const float ax = a[2 * i], ay = a[2 * i + 1];
+        float x = 0, y = 0, m, ang, mb, ab;
+        switch (op) {
+        case 0:
+            orc_cordic_rotate(ax * ORC_K_INV, ay * ORC_K_INV, th[i], 16, &x, &y);
+            o2[2 * i] = x; o2[2 * i + 1] = y;
+            break;
+        case 1:
+            orc_cordic_rotate(ax, ay, th[i], 16, &x, &y);
+            o2[2 * i] = x; o2[2 * i + 1] = y;
+            break;
+        case 2: {
+            const float c = powf(ORC_K_INV, (float)iarg);
+            o2[2 * i] = ax * c; o2[2 * i + 1] = ay * c;
+            break;
+        }
+        case 3:
+            o1[i] = orc_project(ax, ay, th[i]);
+            break;
+        case 4:
+            orc_polar(ax, ay, &m, &ang);
+            o2[2 * i] = m; o2[2 * i + 1] = ang;
+            break;
+        case 5:
+            orc_polar(ax, ay, &m, &ang);
+            o2[2 * i] = cosf(ang); o2[2 * i + 1] = sinf(ang);
+            break;
+        case 6:
+            orc_polar(ax, ay, &m, &ang);
+            orc_polar(b[2 * i], b[2 * i + 1], &mb, &ab);
+            o1[i] = m * mb * cosf(ang - ab);
+            break;
+        case 7:
+            orc_polar(ax, ay, &m, &ang);
+            orc_polar(b[2 * i], b[2 * i + 1], &mb, &ab);
+            o1[i] = cosf(ang - ab);
+            break;
+        case 8:
+            orc_polar(b[2 * i], b[2 * i + 1], &mb, &ab);
+            orc_cordic_rotate(ax * ORC_K_INV, ay * ORC_K_INV, ab, 16, &x, &y);
+            o2[2 * i] = x * mb; o2[2 * i + 1] = y * mb;
+            break;
+        case 9: {
+            const int it = clamp_prec(iarg);
+            const float kinv = 1.0f / ORC_KHAT[it];
+            orc_cordic_rotate(ax * kinv, ay * kinv, th[i], it, &x, &y);
+            o2[2 * i] = x; o2[2 * i + 1] = y;
+            break;
+        }
+        case 10: {
+            const int it = clamp_prec(iarg);
+            orc_cordic_rotate(1.0f / ORC_KHAT[it], 0.0f, th[i], it, &x, &y);
+            o1[i] = fmaf(ax, x, ay * y);
+            break;
+        }
+        case 11:
+            orc_polar(b[2 * i], b[2 * i + 1], &mb, &ab);
+            o1[i] = orc_project(ax, ay, ab) * mb;
+            break;
+        default:
+            break;
+        }
+    }
+}
+
+/* rac_outer, rac_cpu.c:362-371. */
+ORC_API void orc_outer(const float *a, const float *b, float *C, int m, int n)
+{
+    for (int i = 0; i < m; i++)
+        for (int j = 0; j < n; j++) {
+            float mb, ab;
+            orc_polar(b[2 * j], b[2 * j + 1], &mb, &ab);
+            C[(size_t)i * n + j] = orc_project(a[2 * i], a[2 * i + 1], ab) * mb;
+        }
+}
+
+/* rac_dct, rac_cpu.c:219-228 (sum in order i = 0..n-1). */
+ORC_API void orc_dct(const float *x, float *X, int n)
+{
+    for (int k = 0; k < n; k++) {
+        float sum = 0.0f;
+        for (int i = 0; i < n; i++) {
+            float theta = ORC_PI * (float)(2 * i + 1) * (float)k / (float)(2 * n);
+            sum += orc_project(x[i], 0.0f, theta);
+        }
+        X[k] = sum;
+    }
+}
+
+/* ── Scaled dot-product attention (rac.h:323-335) ──────────────────────────
+ * The reference CPU definition (rac_cpu.c:637-703) per (batch, head):
+ * scores[t,s] = (sum_d fmaf q.k) * (1/sqrtf(D)); causal -> -inf for s > t;
+ * then += mask[t*T+s]; row softmax with inv = sum > 0 ? 1/sum : 0; then
+ * out[t,d] = sum_s fmaf(p, v).  rac.h asks for every stage through the RAC
+ * primitives: the two products are rac_matmul (orc_matmul with `mode`,
+ * `iters`) and exp is the CORDIC exp of `iters` steps; iters <= 0 selects
+ * expf, which with mode 0 (FAST == fmaf) reproduces rac_cpu.c exactly. */
+ORC_API int orc_attention(const float *q, const float *k, const float *v, const float *mask,
+                          int is_causal, float *out, int batch, int heads, int seq, int dim,
+                          int iters, int mode)
+{
+    if (!q || !k || !v || !out) return -1;
+    if (batch <= 0 || heads <= 0 || seq <= 0 || dim <= 0) return -2;
+    const float scale = 1.0f / sqrtf((float)dim);
+    const size_t tt = (size_t)seq * seq, td = (size_t)seq * dim;
+    float *sc = (float *)malloc(tt * sizeof(float));
+    if (!sc) return -3;
+    const int mm_iters = iters > 0 ? iters : 24;
+    for (int bh = 0; bh < batch * heads; bh++) {
+        orc_matmul(0, 1, q + bh * td, k + bh * td, sc, seq, seq, dim, scale, 0.0f,
+                   mm_iters, mode, 0);
+        for (int t = 0; t < seq; t++) {
+            float *row = sc + (size_t)t * seq;
+            for (int s = 0; s < seq; s++) {
+                if (is_causal && s > t) row[s] = -INFINITY;
+                if (mask) row[s] += mask[(size_t)t * seq + s];
+            }
+            float m = row[0];
+            for (int s = 1; s < seq; s++) if (row[s] > m) m = row[s];
+            float sum = 0.0f;
+            for (int s = 0; s < seq; s++) {
+                row[s] = (iters > 0) ? orc_exp_n(row[s] - m, iters) : expf(row[s] - m);
+                sum += row[s];
+            }
+            float inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+            for (int s = 0; s < seq; s++) row[s] *= inv;
+        }
+        orc_matmul(0, 0, sc, v + bh * td, out + bh * td, seq, dim, seq, 1.0f, 0.0f,
+                   mm_iters, mode, 0);
+    }
+    free(sc);
+    return 0;
+}

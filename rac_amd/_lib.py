@@ -25,10 +25,22 @@ _i = ctypes.c_int
 _l = ctypes.c_long
 _f = ctypes.c_float
 
+
+
+class Vec2(ctypes.Structure):
+    """The rac.h pair type: struct { float x, y; } (rac.h:31), by value."""
+
+    _fields_ = [("x", ctypes.c_float), ("y", ctypes.c_float)]
+
+
+_v2 = Vec2
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     # rac_ext.h — device pointers, explicit stream
     "rac_gemm_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
+    "rac_gemm_batched_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _l, _l, _l, _vp]),
+    "rac_softmax_masked_dev": (_i, [_vp, _vp, _l, _l, _vp, _i, _i, _vp]),
     "rac_softmax_dev": (_i, [_vp, _vp, _l, _l, _i, _vp]),
     "rac_exp_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_silu_dev": (_i, [_vp, _vp, _l, _i, _vp]),
@@ -43,6 +55,12 @@ _SIGNATURES = {
     "rac_rope_cache_dev": (_i, [_vp, _vp, _i, _i, _f, _vp, _vp]),
     "rac_rope_inv_freq": (_i, [_vp, _i, _f]),
     "rac_rope_apply_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l, _vp]),
+    "rac_vec2_dev": (_i, [_i, _l, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    "rac_inner_dev": (_i, [_vp, _vp, _l, _vp, _vp]),
+    "rac_outer_dev": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "rac_dct_dev": (_i, [_vp, _vp, _i, _vp]),
+    "rac_attention_workspace_bytes": (_l, [_i, _i, _i]),
+    "rac_attention_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "rac_last_error": (ctypes.c_char_p, []),
     "rac_clear_error": (None, []),
     "rac_set_cordic_iters": (None, [_i]),
@@ -71,6 +89,23 @@ _SIGNATURES = {
     "rac_relu": (None, [_vp, _vp, _i]),
     "rac_gelu": (None, [_vp, _vp, _i]),
     "rac_silu": (None, [_vp, _vp, _i]),
+    "rac_rotate": (_v2, [_v2, _f]),
+    "rac_rotate_raw": (_v2, [_v2, _f]),
+    "rac_compensate": (_v2, [_v2, _i]),
+    "rac_project": (_f, [_v2, _f]),
+    "rac_polar": (None, [_v2, c_float_p, c_float_p]),
+    "rac_norm": (_f, [_v2]),
+    "rac_normalize": (_v2, [_v2]),
+    "rac_dot": (_f, [_v2, _v2]),
+    "rac_coherence": (_f, [_v2, _v2]),
+    "rac_complex_mul": (_v2, [_v2, _v2]),
+    "rac_dct": (None, [_vp, _vp, _i]),
+    "rac_rotate_batch": (None, [_vp, _vp, _vp, _i]),
+    "rac_inner": (_f, [_vp, _vp, _i]),
+    "rac_outer": (None, [_vp, _vp, _vp, _i, _i]),
+    "rac_attention": (None, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i]),
+    "rac_rotate_precision": (_v2, [_v2, _f, _i]),
+    "rac_project_precision": (_f, [_v2, _f, _i]),
     "rac_create_context": (_vp, [_i]),
     "rac_destroy_context": (None, [_vp]),
     "rac_query_capability": (_i, [_vp, _i]),

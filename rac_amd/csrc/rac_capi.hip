@@ -239,6 +239,39 @@ RAC_EXPORT int rac_gemm_dev(const float* A, const float* B, float* C, int M, int
                      "rac_gemm_dev launch");
 }
 
+RAC_EXPORT int rac_gemm_batched_dev(const float* A, const float* B, float* C, int M, int N, int K,
+                                    int trans_a, int trans_b, float alpha, float beta, int iters,
+                                    int mode, int batch, long stride_a, long stride_b, long stride_c,
+                                    void* stream) {
+    int rc = check_gemm(A, B, C, M, N, K);
+    if (rc) return rc;
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_gemm_batched_dev: mode must be 0, 1 or 2");
+    if (batch <= 0 || batch > 65535) return fail(RAC_ERR_INVALID_DIM, "rac_gemm_batched_dev: batch must be in [1, 65535]");
+    if (stride_a < 0 || stride_b < 0 || stride_c < 0)
+        return fail(RAC_ERR_INVALID_DIM, "rac_gemm_batched_dev: negative stride");
+    return check_hip(gemm_launch(trans_a != 0, trans_b != 0, A, B, C, M, N, K, alpha, beta,
+                                 clamp_iters(iters), mode, (hipStream_t)stream, batch, stride_a, stride_b,
+                                 stride_c),
+                     "rac_gemm_batched_dev launch");
+}
+
+// Row softmax with attention masking of rows laid out as [.., seq, seq]:
+// causal and/or an additive [seq, seq] mask (either may be off); in place
+// when x == y.
+RAC_EXPORT int rac_softmax_masked_dev(const float* x, float* y, long rows, long seq, const float* mask,
+                                      int is_causal, int iters, void* stream) {
+    int rc = check_rows("rac_softmax_masked_dev", x, y, rows, seq);
+    if (rc) return rc;
+    if (rows % seq) return fail(RAC_ERR_INVALID_DIM, "rac_softmax_masked_dev: rows must be a multiple of seq");
+    SoftmaxMask mk;
+    mk.mask = mask;
+    mk.causal = is_causal != 0;
+    mk.seq = seq;
+    mk.zero_guard = 1;
+    return check_hip(softmax_launch(x, y, rows, seq, iters, (hipStream_t)stream, mk),
+                     "rac_softmax_masked_dev launch");
+}
+
 RAC_EXPORT int rac_softmax_dev(const float* x, float* y, long rows, long n, int iters, void* stream) {
     int rc = check_rows("rac_softmax_dev", x, y, rows, n);
     if (rc) return rc;
@@ -339,6 +372,117 @@ RAC_EXPORT int rac_rope_apply_dev(float* x, const float* cos_tab, const float* s
     return check_hip(rope_apply_launch(x, cos_tab, sin_tab, batch, n_heads, seq, head_dim, stride_b,
                                        stride_h, stride_t, (hipStream_t)stream),
                      "rac_rope_apply_dev launch");
+}
+
+// ── vector primitives on device buffers ──────────────────────────────────
+
+// Which operands each primitive op reads / writes (see PrimOp).
+static bool prim_needs_b(int op) {
+    return op == kPrimDot || op == kPrimCoherence || op == kPrimComplexMul || op == kPrimInnerTerm;
+}
+static bool prim_needs_theta(int op) {
+    return op == kPrimRotate || op == kPrimRotateRaw || op == kPrimProject || op == kPrimRotateN ||
+           op == kPrimProjectN;
+}
+static bool prim_writes_pair(int op) {
+    return op == kPrimRotate || op == kPrimRotateRaw || op == kPrimCompensate || op == kPrimPolar ||
+           op == kPrimNormalize || op == kPrimComplexMul || op == kPrimRotateN;
+}
+
+static int check_prim(int op, long n, const void* a, const void* b, const void* th, const void* o2,
+                      const void* o1) {
+    if (op < kPrimRotate || op > kPrimInnerTerm) return fail(RAC_ERR_INVALID_DIM, "rac_vec2_dev: unknown op %d", op);
+    if (n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_vec2_dev: negative count");
+    if (n > 2147483647L * 128L) return fail(RAC_ERR_INVALID_DIM, "rac_vec2_dev: count too large for one launch");
+    if (!a || (prim_needs_b(op) && !b) || (prim_needs_theta(op) && !th) ||
+        (prim_writes_pair(op) ? !o2 : !o1))
+        return fail(RAC_ERR_NULL_PTR, "rac_vec2_dev: null operand for op %d", op);
+    return RAC_OK;
+}
+
+RAC_EXPORT int rac_vec2_dev(int op, long n, const float* a, const float* b, const float* theta,
+                            int iarg, float* out2, float* out1, void* stream) {
+    int rc = check_prim(op, n, a, b, theta, out2, out1);
+    if (rc || n == 0) return rc;
+    return check_hip(prim_launch(op, n, reinterpret_cast<const float2*>(a), reinterpret_cast<const float2*>(b),
+                                 theta, iarg, reinterpret_cast<float2*>(out2), out1, (hipStream_t)stream),
+                     "rac_vec2_dev launch");
+}
+
+RAC_EXPORT int rac_inner_dev(const float* a, const float* b, long n, float* out, void* stream) {
+    if (!a || !b || !out) return fail(RAC_ERR_NULL_PTR, "rac_inner_dev: null buffer");
+    if (n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_inner_dev: negative count");
+    return check_hip(inner_launch(reinterpret_cast<const float2*>(a), reinterpret_cast<const float2*>(b), n, out,
+                                  (hipStream_t)stream),
+                     "rac_inner_dev launch");
+}
+
+RAC_EXPORT int rac_outer_dev(const float* a, const float* b, float* C, int m, int n, void* stream) {
+    if (!a || !b || !C) return fail(RAC_ERR_NULL_PTR, "rac_outer_dev: null buffer");
+    if (m < 0 || n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_outer_dev: negative dimension");
+    if ((long)m * n > 2147483647L * 128L) return fail(RAC_ERR_INVALID_DIM, "rac_outer_dev: too large for one launch");
+    if ((long)m * n == 0) return RAC_OK;
+    return check_hip(outer_launch(reinterpret_cast<const float2*>(a), reinterpret_cast<const float2*>(b), C, m, n,
+                                  (hipStream_t)stream),
+                     "rac_outer_dev launch");
+}
+
+RAC_EXPORT int rac_dct_dev(const float* x, float* X, int n, void* stream) {
+    if (!x || !X) return fail(RAC_ERR_NULL_PTR, "rac_dct_dev: null buffer");
+    if (n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_dct_dev: negative length");
+    if (n == 0) return RAC_OK;
+    return check_hip(dct_launch(x, X, n, (hipStream_t)stream), "rac_dct_dev launch");
+}
+
+// ── scaled dot-product attention (rac.h:323-335) ────────────────────────
+
+static int check_attention(const void* q, const void* k, const void* v, const void* out, long b,
+                           long h, long t, long d) {
+    if (!q || !k || !v || !out) return fail(RAC_ERR_NULL_PTR, "rac_attention: null buffer");
+    if (b <= 0 || h <= 0 || t <= 0 || d <= 0) return fail(RAC_ERR_INVALID_DIM, "rac_attention: dims must be > 0");
+    if (b * h > 65535L) return fail(RAC_ERR_INVALID_DIM, "rac_attention: batch*n_heads must be <= 65535");
+    if (b * h * t > 2147483647L || t > 2147483647L / 16)
+        return fail(RAC_ERR_INVALID_DIM, "rac_attention: batch*n_heads*seq too large");
+    return RAC_OK;
+}
+
+// Bytes of the score workspace rac_attention_dev needs: batch*n_heads*seq*seq floats.
+RAC_EXPORT long rac_attention_workspace_bytes(int batch, int n_heads, int seq) {
+    if (batch <= 0 || n_heads <= 0 || seq <= 0) return 0;
+    return (long)sizeof(float) * batch * n_heads * (long)seq * seq;
+}
+
+// scores = (Q K^T) / sqrt(D) by the RAC matmul (batched over b*h), masked
+// row softmax with CORDIC exp in place, out = P V by the RAC matmul.
+static int attention_launch(const float* q, const float* k, const float* v, const float* mask, int causal,
+                            float* out, int b, int h, int t, int d, float* ws, int iters, int mode,
+                            hipStream_t s) {
+    const int bh = b * h;
+    const long td = (long)t * d, tt = (long)t * t;
+    const float scale = 1.0f / sqrtf((float)d);
+    int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt),
+                       "rac_attention scores launch");
+    if (rc) return rc;
+    SoftmaxMask mk;
+    mk.mask = mask;
+    mk.causal = causal != 0;
+    mk.seq = t;
+    mk.zero_guard = 1;
+    rc = check_hip(softmax_launch(ws, ws, (long)bh * t, t, iters, s, mk), "rac_attention softmax launch");
+    if (rc) return rc;
+    return check_hip(gemm_launch(0, 0, ws, v, out, t, d, t, 1.0f, 0.0f, iters, mode, s, bh, tt, td, td),
+                     "rac_attention output launch");
+}
+
+RAC_EXPORT int rac_attention_dev(const float* q, const float* k, const float* v, const float* mask,
+                                 int is_causal, float* out, int batch, int n_heads, int seq,
+                                 int head_dim, float* workspace, int iters, int mode, void* stream) {
+    int rc = check_attention(q, k, v, out, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (!workspace) return fail(RAC_ERR_NULL_PTR, "rac_attention_dev: null workspace");
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_dev: mode must be 0, 1 or 2");
+    return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, workspace,
+                            clamp_iters(iters), mode, (hipStream_t)stream);
 }
 
 // ═════════════════ reference launcher ABI (rac_kernels.hip) ═══════════════
@@ -521,6 +665,144 @@ RAC_EXPORT void rac_rope_apply(float* x, const float* cos_tab, const float* sin_
     if (!rc) rc = check_hip(rope_apply_launch(a.f(), c.f(), sn.f(), batch, n_heads, seq, head_dim, sb, sh, st, s),
                             "rac_rope_apply launch");
     if (!rc) rc = a.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+// ── vector primitives (rac.h:101-250, 345-346) ───────────────────────────
+// A pair {float x, y} passed and returned by value: the C layout of the
+// reference's float2 (rac.h:31), classified the same way by the host ABI.
+struct RacVec2 {
+    float x, y;
+};
+
+// Runs one primitive op over n items in caller memory (host or device).
+static int prim_sync(int op, long n, const void* a, const void* b, const float* th, int iarg, void* o2,
+                     float* o1) {
+    if (n <= 0) return RAC_OK;
+    hipStream_t s = g_stream.load();
+    Staged sa, sb, st, so2, so1;
+    const size_t n2 = sizeof(float) * 2 * (size_t)n, n1 = sizeof(float) * (size_t)n;
+    int rc = sa.bind(a, n2, true, s);
+    if (!rc && prim_needs_b(op)) rc = sb.bind(b, n2, true, s);
+    if (!rc && prim_needs_theta(op)) rc = st.bind(th, n1, true, s);
+    if (!rc && prim_writes_pair(op)) rc = so2.bind(o2, n2, false, s);
+    if (!rc && !prim_writes_pair(op)) rc = so1.bind(o1, n1, false, s);
+    if (!rc) rc = rac_vec2_dev(op, n, sa.f(), sb.f(), st.f(), iarg, so2.f(), so1.f(), s);
+    if (!rc) rc = so2.copy_out(s);
+    if (!rc) rc = so1.copy_out(s);
+    return finish_sync(s, rc);
+}
+
+static RacVec2 prim_pair(int op, RacVec2 a, RacVec2 b, float theta, int iarg) {
+    RacVec2 r = {0.0f, 0.0f};
+    RacVec2 out = {0.0f, 0.0f};
+    if (prim_sync(op, 1, &a, &b, &theta, iarg, &out, nullptr) == RAC_OK) r = out;
+    return r;
+}
+static float prim_scalar(int op, RacVec2 a, RacVec2 b, float theta, int iarg) {
+    float out = 0.0f;
+    if (prim_sync(op, 1, &a, &b, &theta, iarg, nullptr, &out) != RAC_OK) return 0.0f;
+    return out;
+}
+
+RAC_EXPORT RacVec2 rac_rotate(RacVec2 v, float theta) { return prim_pair(kPrimRotate, v, v, theta, 0); }
+RAC_EXPORT RacVec2 rac_rotate_raw(RacVec2 v, float theta) { return prim_pair(kPrimRotateRaw, v, v, theta, 0); }
+RAC_EXPORT RacVec2 rac_compensate(RacVec2 v, int chain_length) {
+    return prim_pair(kPrimCompensate, v, v, 0.0f, chain_length);
+}
+RAC_EXPORT float rac_project(RacVec2 v, float theta) { return prim_scalar(kPrimProject, v, v, theta, 0); }
+RAC_EXPORT void rac_polar(RacVec2 v, float* mag, float* angle) {
+    if (!mag || !angle) { fail(RAC_ERR_NULL_PTR, "rac_polar: null output"); return; }
+    RacVec2 out = {0.0f, 0.0f};
+    if (prim_sync(kPrimPolar, 1, &v, nullptr, nullptr, 0, &out, nullptr) == RAC_OK) {
+        *mag = out.x;
+        *angle = out.y;
+    }
+}
+RAC_EXPORT float rac_norm(RacVec2 v) {
+    float m = 0.0f, a = 0.0f;
+    rac_polar(v, &m, &a);
+    return m;
+}
+RAC_EXPORT RacVec2 rac_normalize(RacVec2 v) { return prim_pair(kPrimNormalize, v, v, 0.0f, 0); }
+RAC_EXPORT float rac_dot(RacVec2 a, RacVec2 b) { return prim_scalar(kPrimDot, a, b, 0.0f, 0); }
+RAC_EXPORT float rac_coherence(RacVec2 a, RacVec2 b) { return prim_scalar(kPrimCoherence, a, b, 0.0f, 0); }
+RAC_EXPORT RacVec2 rac_complex_mul(RacVec2 a, RacVec2 b) { return prim_pair(kPrimComplexMul, a, b, 0.0f, 0); }
+RAC_EXPORT RacVec2 rac_rotate_precision(RacVec2 v, float theta, int iters) {
+    return prim_pair(kPrimRotateN, v, v, theta, iters);
+}
+RAC_EXPORT float rac_project_precision(RacVec2 v, float theta, int iters) {
+    return prim_scalar(kPrimProjectN, v, v, theta, iters);
+}
+
+RAC_EXPORT void rac_rotate_batch(RacVec2* v, float* theta, RacVec2* out, int n) {
+    if (!v || !theta || !out) { fail(RAC_ERR_NULL_PTR, "rac_rotate_batch: null buffer"); return; }
+    (void)prim_sync(kPrimRotate, n, v, nullptr, theta, 0, out, nullptr);
+}
+
+RAC_EXPORT float rac_inner(RacVec2* a, RacVec2* b, int n) {
+    if (!a || !b) { fail(RAC_ERR_NULL_PTR, "rac_inner: null buffer"); return 0.0f; }
+    if (n <= 0) return 0.0f;
+    hipStream_t s = g_stream.load();
+    float result = 0.0f;
+    Staged sa, sb, so;
+    int rc = sa.bind(a, sizeof(float) * 2 * (size_t)n, true, s);
+    if (!rc) rc = sb.bind(b, sizeof(float) * 2 * (size_t)n, true, s);
+    if (!rc) rc = so.bind(&result, sizeof(float), false, s);
+    if (!rc) rc = rac_inner_dev(sa.f(), sb.f(), n, so.f(), s);
+    if (!rc) rc = so.copy_out(s);
+    return finish_sync(s, rc) == RAC_OK ? result : 0.0f;
+}
+
+RAC_EXPORT void rac_outer(RacVec2* a, RacVec2* b, float* C, int m, int n) {
+    if (!a || !b || !C) { fail(RAC_ERR_NULL_PTR, "rac_outer: null buffer"); return; }
+    if (m <= 0 || n <= 0) return;
+    hipStream_t s = g_stream.load();
+    Staged sa, sb, sc;
+    int rc = sa.bind(a, sizeof(float) * 2 * (size_t)m, true, s);
+    if (!rc) rc = sb.bind(b, sizeof(float) * 2 * (size_t)n, true, s);
+    if (!rc) rc = sc.bind(C, sizeof(float) * (size_t)m * n, false, s);
+    if (!rc) rc = rac_outer_dev(sa.f(), sb.f(), sc.f(), m, n, s);
+    if (!rc) rc = sc.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_dct(float* x, float* X, int n) {
+    if (!x || !X) { fail(RAC_ERR_NULL_PTR, "rac_dct: null buffer"); return; }
+    if (n <= 0) return;
+    hipStream_t s = g_stream.load();
+    Staged sx, sX;
+    int rc = sx.bind(x, sizeof(float) * (size_t)n, true, s);
+    if (!rc) rc = sX.bind(X, sizeof(float) * (size_t)n, false, s);
+    if (!rc) rc = rac_dct_dev(sx.f(), sX.f(), n, s);
+    if (!rc) rc = sX.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_attention(const float* q, const float* k, const float* v, const float* mask,
+                              int is_causal, float* out, int batch, int n_heads, int seq, int head_dim) {
+    if (check_attention(q, k, v, out, batch, n_heads, seq, head_dim)) return;
+    hipStream_t s = g_stream.load();
+    const size_t xb = sizeof(float) * (size_t)batch * n_heads * seq * head_dim;
+    Staged sq, sk, sv, sm, so, ws;
+    int rc = sq.bind(q, xb, true, s);
+    if (!rc) rc = sk.bind(k, xb, true, s);
+    if (!rc) rc = sv.bind(v, xb, true, s);
+    if (!rc) rc = sm.bind(mask, sizeof(float) * (size_t)seq * seq, true, s);
+    if (!rc) rc = so.bind(out, xb, false, s);
+    if (!rc) {
+        const size_t wb = (size_t)rac_attention_workspace_bytes(batch, n_heads, seq);
+        if (hipMalloc(&ws.dev, wb) != hipSuccess) {
+            (void)hipGetLastError();
+            ws.dev = nullptr;
+            rc = fail(RAC_ERR_ALLOC, "rac_attention: score workspace of %zu bytes failed", wb);
+        } else {
+            ws.owned = true;
+        }
+    }
+    if (!rc) rc = attention_launch(sq.f(), sk.f(), sv.f(), sm.f(), is_causal, so.f(), batch, n_heads, seq,
+                                   head_dim, ws.f(), rac_get_cordic_iters(), rac_get_cordic_mode(), s);
+    if (!rc) rc = so.copy_out(s);
     (void)finish_sync(s, rc);
 }
 

@@ -58,9 +58,12 @@ __device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc
 template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
-    int M, int N, int K, float alpha, float beta, int iters, float kinv)
+    int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
+    A += (long)blockIdx.z * sa;
+    B += (long)blockIdx.z * sb;
+    C += (long)blockIdx.z * sc;
     constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
     __shared__ __attribute__((aligned(16))) float sA[BK][BM + PAD];
     __shared__ __attribute__((aligned(16))) float sB[BK][BN + PAD];
@@ -169,39 +172,49 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     }
 }
 
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    float alpha, beta;
+    int iters;
+    int batch;
+    long sa, sb, sc;
+};
+
 template <int MODE, int NITER, bool TA, bool TB>
-static hipError_t launch_cfg(const float* A, const float* B, float* C, int M, int N, int K,
-                             float alpha, float beta, int iters, hipStream_t stream) {
+static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     constexpr int TM = (MODE == kModeFast) ? 8 : 4;
     constexpr int TN = TM;
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
-    const float kinv = cordic_kinv(iters);
-    dim3 grid((unsigned)((N + Cfg::kBN - 1) / Cfg::kBN), (unsigned)((M + Cfg::kBM - 1) / Cfg::kBM));
+    const float kinv = cordic_kinv(g.iters);
+    dim3 grid((unsigned)((g.N + Cfg::kBN - 1) / Cfg::kBN), (unsigned)((g.M + Cfg::kBM - 1) / Cfg::kBM),
+              (unsigned)g.batch);
     hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN>), grid, dim3(256), 0, stream,
-                       A, B, C, M, N, K, alpha, beta, iters, kinv);
+                       g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc);
     return hipGetLastError();
 }
 
 template <int MODE, int NITER>
-static hipError_t launch_layout(int ta, int tb, const float* A, const float* B, float* C,
-                                int M, int N, int K, float alpha, float beta, int iters,
-                                hipStream_t s) {
-    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false>(A, B, C, M, N, K, alpha, beta, iters, s);
-    if (!ta && tb) return launch_cfg<MODE, NITER, false, true>(A, B, C, M, N, K, alpha, beta, iters, s);
-    if (ta && !tb) return launch_cfg<MODE, NITER, true, false>(A, B, C, M, N, K, alpha, beta, iters, s);
-    return launch_cfg<MODE, NITER, true, true>(A, B, C, M, N, K, alpha, beta, iters, s);
+static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s) {
+    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false>(g, s);
+    if (!ta && tb) return launch_cfg<MODE, NITER, false, true>(g, s);
+    if (ta && !tb) return launch_cfg<MODE, NITER, true, false>(g, s);
+    return launch_cfg<MODE, NITER, true, true>(g, s);
 }
 
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
-                       hipStream_t s) {
-    if (mode == kModeFast) return launch_layout<kModeFast, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
-    if (mode == kModeShiftAdd) return launch_layout<kModeShiftAdd, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
-    switch (iters) {
-        case 8: return launch_layout<kModeCordic, 8>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
-        case 16: return launch_layout<kModeCordic, 16>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
-        case 24: return launch_layout<kModeCordic, 24>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
-        default: return launch_layout<kModeCordic, 0>(ta, tb, A, B, C, M, N, K, alpha, beta, iters, s);
+                       hipStream_t s, int batch, long sa, long sb, long sc) {
+    const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc};
+    if (mode == kModeFast) return launch_layout<kModeFast, 0>(ta, tb, g, s);
+    if (mode == kModeShiftAdd) return launch_layout<kModeShiftAdd, 0>(ta, tb, g, s);
+    switch (g.iters) {
+        case 8: return launch_layout<kModeCordic, 8>(ta, tb, g, s);
+        case 16: return launch_layout<kModeCordic, 16>(ta, tb, g, s);
+        case 24: return launch_layout<kModeCordic, 24>(ta, tb, g, s);
+        default: return launch_layout<kModeCordic, 0>(ta, tb, g, s);
     }
 }
 

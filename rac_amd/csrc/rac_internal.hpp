@@ -21,12 +21,24 @@ struct HostConsts {
 };
 const HostConsts& host_consts();
 
+// batch > 1: C_z = alpha op(A_z) op(B_z) + beta C_z for z < batch, with
+// A_z = A + z*sa, B_z = B + z*sb, C_z = C + z*sc (element strides).
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
-                       hipStream_t s);
+                       hipStream_t s, int batch = 1, long sa = 0, long sb = 0, long sc = 0);
 
+// Optional attention masking of each row r (position t = r % seq, column j):
+// causal -> x = -inf for j > t; then x += mask[t*seq + j] when mask != null.
+// zero_guard: 1/sum replaced by 0 when sum is not > 0 (rac_cpu.c:687).
+// x and y may be the same buffer (in-place softmax).
+struct SoftmaxMask {
+    const float* mask = nullptr;
+    int causal = 0;
+    long seq = 0;
+    int zero_guard = 0;
+};
 hipError_t softmax_launch(const float* x, float* y, long rows, long n, int iters,
-                          hipStream_t s);
+                          hipStream_t s, const SoftmaxMask& mk = SoftmaxMask());
 hipError_t rmsnorm_launch(const float* x, float* y, const float* gamma, float eps,
                           long rows, long d, hipStream_t s);
 hipError_t layernorm_launch(const float* x, float* y, const float* gamma, const float* beta,
@@ -42,6 +54,17 @@ hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_ta
                              int batch, int heads, int seq, int head_dim,
                              long sb, long sh, long st, hipStream_t s);
 hipError_t rsqrt_launch(const float* x, float* y, long count, hipStream_t s);
+
+enum PrimOp {
+    kPrimRotate = 0, kPrimRotateRaw = 1, kPrimCompensate = 2, kPrimProject = 3, kPrimPolar = 4,
+    kPrimNormalize = 5, kPrimDot = 6, kPrimCoherence = 7, kPrimComplexMul = 8, kPrimRotateN = 9,
+    kPrimProjectN = 10, kPrimInnerTerm = 11
+};
+hipError_t prim_launch(int op, long n, const float2* a, const float2* b, const float* th, int iarg,
+                       float2* o2, float* o1, hipStream_t s);
+hipError_t outer_launch(const float2* a, const float2* b, float* C, int m, int n, hipStream_t s);
+hipError_t dct_launch(const float* x, float* X, int n, hipStream_t s);
+hipError_t inner_launch(const float2* a, const float2* b, long n, float* out, hipStream_t s);
 hipError_t sincos_launch(const float* theta, float* s_out, float* c_out, long count,
                          hipStream_t s);
 

@@ -66,9 +66,24 @@ __device__ __forceinline__ float exp_n(float x, int iters, float khinv) {
 
 // ── softmax ──────────────────────────────────────────────────────────────
 
-template <int VPT, int NITER>
+// Attention masking of score x at (query position t, key column j), in the
+// order of rac_cpu.c:668-670: causal sets -inf above the diagonal, then the
+// additive mask is added.
+__device__ __forceinline__ float mask_score(float x, long t, long j, const SoftmaxMask& mk) {
+    if (mk.causal && j > t) x = -__builtin_inff();
+    if (mk.mask) x += mk.mask[t * mk.seq + j];
+    return x;
+}
+
+// 1/sum, or 0 for a non-positive sum when the guard of rac_cpu.c:687 is on.
+__device__ __forceinline__ float inv_sum(float s, int zero_guard) {
+    return (zero_guard && !(s > 0.0f)) ? 0.0f : 1.0f / s;
+}
+
+template <int VPT, int NITER, bool MASKED>
 __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
-    const float* __restrict__ x, float* __restrict__ y, long n, int iters, float khinv)
+    const float* x, float* y, long n, int iters, float khinv,
+    SoftmaxMask mk)
 {
     __shared__ float red[kRowWaves];
     const long row = blockIdx.x;
@@ -82,6 +97,19 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
         const long idx = threadIdx.x + (long)i * kRowThreads;
         if (idx < n4) v[i] = ld4_stream(&xr[idx]);
         else v[i] = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+    }
+    if constexpr (MASKED) {
+        const long t = row % mk.seq;
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const long idx = threadIdx.x + (long)i * kRowThreads;
+            if (idx < n4) {
+                v[i].x = mask_score(v[i].x, t, 4 * idx + 0, mk);
+                v[i].y = mask_score(v[i].y, t, 4 * idx + 1, mk);
+                v[i].z = mask_score(v[i].z, t, 4 * idx + 2, mk);
+                v[i].w = mask_score(v[i].w, t, 4 * idx + 3, mk);
+            }
+        }
     }
 #pragma unroll
     for (int i = 0; i < VPT; i++) m = fmaxf(fmaxf(fmaxf(m, v[i].x), fmaxf(v[i].y, v[i].z)), v[i].w);
@@ -102,7 +130,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
         }
     }
     s = block_sum(s, red);
-    const float inv = 1.0f / s;
+    const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const long idx = threadIdx.x + (long)i * kRowThreads;
@@ -114,58 +142,78 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     }
 }
 
-template <int NITER>
+template <int NITER, bool MASKED>
 __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
-    const float* __restrict__ x, float* __restrict__ y, long n, int iters, float khinv)
+    const float* x, float* y, long n, int iters, float khinv,
+    SoftmaxMask mk)
 {
     __shared__ float red[kRowWaves];
     const long row = blockIdx.x;
+    const long t = MASKED ? row % mk.seq : 0;
     const float* xr = x + row * n;
     float* yr = y + row * n;
     float m = -__builtin_inff();
-    for (long i = threadIdx.x; i < n; i += kRowThreads) m = fmaxf(m, xr[i]);
+    for (long i = threadIdx.x; i < n; i += kRowThreads) {
+        float v = xr[i];
+        if constexpr (MASKED) v = mask_score(v, t, i, mk);
+        m = fmaxf(m, v);
+    }
     m = block_max(m, red);
     float s = 0.0f;
     for (long i = threadIdx.x; i < n; i += kRowThreads) {
-        const float e = exp_n<NITER>(xr[i] - m, iters, khinv);
+        float v = xr[i];
+        if constexpr (MASKED) v = mask_score(v, t, i, mk);
+        const float e = exp_n<NITER>(v - m, iters, khinv);
         yr[i] = e;
         s += e;
     }
     s = block_sum(s, red);
-    const float inv = 1.0f / s;
+    const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
     for (long i = threadIdx.x; i < n; i += kRowThreads) yr[i] = yr[i] * inv;
 }
 
-template <int NITER>
+template <int NITER, bool MASKED>
 static hipError_t softmax_dispatch(const float* x, float* y, long rows, long n, int iters,
-                                   float khinv, hipStream_t s) {
+                                   float khinv, hipStream_t s, const SoftmaxMask& mk) {
     const bool vec_ok = (n % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
                         ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
     const long n4 = n / 4;
     dim3 grid((unsigned)rows), block(kRowThreads);
     if (vec_ok && n4 <= 1 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<1, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_reg_kernel<1, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 2 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<2, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_reg_kernel<2, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 4 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<4, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_reg_kernel<4, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 8 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<8, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_reg_kernel<8, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 16 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<16, NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_reg_kernel<16, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     else
-        hipLaunchKernelGGL((softmax_loop_kernel<NITER>), grid, block, 0, s, x, y, n, iters, khinv);
+        hipLaunchKernelGGL((softmax_loop_kernel<NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     return hipGetLastError();
 }
 
-hipError_t softmax_launch(const float* x, float* y, long rows, long n, int iters, hipStream_t s) {
+template <int NITER>
+static hipError_t softmax_mask_dispatch(const float* x, float* y, long rows, long n, int iters,
+                                        float khinv, hipStream_t s, const SoftmaxMask& mk) {
+    if (mk.mask || mk.causal || mk.zero_guard) {
+        SoftmaxMask m2 = mk;
+        if (m2.seq <= 0) m2.seq = n;   // square scores: row length = sequence length
+        return softmax_dispatch<NITER, true>(x, y, rows, n, iters, khinv, s, m2);
+    }
+    return softmax_dispatch<NITER, false>(x, y, rows, n, iters, khinv, s, mk);
+}
+
+hipError_t softmax_launch(const float* x, float* y, long rows, long n, int iters, hipStream_t s,
+                          const SoftmaxMask& mk) {
     iters = clamp_iters(iters);
     const float khinv = host_consts().exp_khinv[iters];
     switch (iters) {
-        case 8: return softmax_dispatch<8>(x, y, rows, n, iters, khinv, s);
-        case 16: return softmax_dispatch<16>(x, y, rows, n, iters, khinv, s);
-        case 24: return softmax_dispatch<24>(x, y, rows, n, iters, khinv, s);
-        default: return softmax_dispatch<0>(x, y, rows, n, iters, khinv, s);
+        case 8: return softmax_mask_dispatch<8>(x, y, rows, n, iters, khinv, s, mk);
+        case 16: return softmax_mask_dispatch<16>(x, y, rows, n, iters, khinv, s, mk);
+        case 24: return softmax_mask_dispatch<24>(x, y, rows, n, iters, khinv, s, mk);
+        default: return softmax_mask_dispatch<0>(x, y, rows, n, iters, khinv, s, mk);
     }
 }
 

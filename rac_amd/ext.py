@@ -8,7 +8,9 @@ names, keyword arguments, defaults (iters=24, mode=FAST,
 rac_torch_bind.cpp:54-55) and argument checks.  Added ops (new names, so the
 reference's ``hasattr`` probing keeps working): ``rope_cache``,
 ``rope_apply_``, ``softmax``, ``rmsnorm``, ``layernorm``, ``silu``, ``gelu``,
-``sigmoid``, ``tanh``, ``exp``, ``relu``, ``rsqrt``, ``sincos``.
+``sigmoid``, ``tanh``, ``exp``, ``relu``, ``rsqrt``, ``sincos``, ``bmm``,
+``softmax_masked_``, ``attention``, and the rac.h vector primitives
+``vec2``, ``inner``, ``outer``, ``dct``.
 
 Every op launches on torch's current HIP stream of the tensor's device and
 returns without synchronising.  Only ROCm device tensors are accepted: there
@@ -18,6 +20,7 @@ from __future__ import annotations
 
 from typing import List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -370,10 +373,178 @@ def rope_apply_(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.
     return x
 
 
+# ── batched products and attention ───────────────────────────────────────
+
+def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool = False,
+        alpha: float = 1.0, iters: int = 0, mode: int = -1) -> torch.Tensor:
+    """C[z] = alpha * op(A[z]) @ op(B[z]) for 3-D contiguous fp32 tensors, one
+    launch over the batch (grid z).  op(A[z]) = A[z] [M, K], or A[z]^T with
+    A stored [Z, K, M] when trans_a; op(B[z]) = B[z] [K, N], or B[z]^T with B
+    stored [Z, N, K] when trans_b."""
+    _require_f32(A, "A")
+    _require_f32(B, "B")
+    if A.dim() != 3 or B.dim() != 3 or A.size(0) != B.size(0):
+        raise RuntimeError("RAC: bmm expects [Z, ., .] tensors with the same Z")
+    A = A.contiguous()
+    B = B.contiguous()
+    Z = A.size(0)
+    M, K = (A.size(2), A.size(1)) if trans_a else (A.size(1), A.size(2))
+    Kb, N = (B.size(2), B.size(1)) if trans_b else (B.size(1), B.size(2))
+    if K != Kb:
+        raise RuntimeError("RAC: dimension mismatch")
+    C = torch.empty((Z, M, N), device=A.device, dtype=torch.float32)
+    if C.numel() == 0:
+        return C
+    if K == 0:
+        return C.zero_()
+    iters, mode = _resolve(iters, mode)
+    lib = _lib.load()
+    for z0 in range(0, Z, 65535):
+        zb = min(65535, Z - z0)
+        check(lib.rac_gemm_batched_dev(A[z0].data_ptr(), B[z0].data_ptr(), C[z0].data_ptr(), M, N, K,
+                                       int(trans_a), int(trans_b), float(alpha), 0.0, iters, mode, zb,
+                                       A.stride(0), B.stride(0), C.stride(0), _stream(C)),
+              "rac_gemm_batched_dev")
+    return C
+
+
+def softmax_masked_(scores: torch.Tensor, mask: Optional[torch.Tensor] = None, is_causal: bool = False,
+                    iters: int = 0) -> torch.Tensor:
+    """In-place attention softmax of contiguous scores [..., T, T]:
+    causal -inf above the diagonal, then + mask[T, T], then the CORDIC
+    softmax of each row (rac_cpu.c:664-687)."""
+    _require_f32(scores, "scores")
+    if not scores.is_contiguous() or scores.dim() < 2 or scores.size(-1) != scores.size(-2):
+        raise RuntimeError("RAC: scores must be a contiguous [..., T, T] tensor")
+    T = scores.size(-1)
+    mptr = None
+    if mask is not None:
+        _require_f32(mask, "mask")
+        if mask.shape != (T, T) or not mask.is_contiguous():
+            raise RuntimeError("RAC: mask must be a contiguous [T, T] float32 tensor")
+        mptr = mask.data_ptr()
+    if scores.numel():
+        check(_lib.load().rac_softmax_masked_dev(scores.data_ptr(), scores.data_ptr(), scores.numel() // T, T,
+                                                 mptr, int(bool(is_causal)), _resolve_iters(iters),
+                                                 _stream(scores)),
+              "rac_softmax_masked_dev")
+    return scores
+
+
+def attention_scale(head_dim: int) -> float:
+    """1.0f / sqrtf((float)head_dim) in float32 arithmetic (rac_cpu.c:652)."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
+              is_causal: bool = False, iters: int = 0, mode: int = -1,
+              return_probs: bool = False):
+    """rac_attention (rac.h:323-335) on [B, H, T, D] tensors: scores =
+    Q K^T / sqrt(D) by the RAC matmul, causal/additive mask, CORDIC softmax,
+    out = P V by the RAC matmul.  With return_probs, also returns P
+    [B, H, T, T] (what the backward pass needs)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require_f32(t, n)
+        if t.dim() != 4:
+            raise RuntimeError("RAC: attention expects [batch, heads, seq, head_dim]")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise RuntimeError("RAC: q, k, v must have the same shape")
+    B, H, T, D = q.shape
+    q3 = q.contiguous().view(B * H, T, D)
+    k3 = k.contiguous().view(B * H, T, D)
+    v3 = v.contiguous().view(B * H, T, D)
+    iters, mode = _resolve(iters, mode)
+    P = bmm(q3, k3, trans_b=True, alpha=attention_scale(D), iters=iters, mode=mode)
+    softmax_masked_(P, mask, is_causal, iters)
+    out = bmm(P, v3, iters=iters, mode=mode).view(B, H, T, D)
+    if return_probs:
+        return out, P.view(B, H, T, T)
+    return out
+
+
+# ── vector primitives (rac.h:101-250) ───────────────────────────────────────
+
+VEC2_OPS = {
+    "rotate": 0, "rotate_raw": 1, "compensate": 2, "project": 3, "polar": 4, "normalize": 5,
+    "dot": 6, "coherence": 7, "complex_mul": 8, "rotate_precision": 9, "project_precision": 10,
+    "inner_term": 11,
+}
+_PAIR_OUT = {"rotate", "rotate_raw", "compensate", "polar", "normalize", "complex_mul", "rotate_precision"}
+
+
+def vec2(op: str, a: torch.Tensor, b: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None,
+         iarg: int = 0) -> torch.Tensor:
+    """Elementwise rac.h primitive over pairs a [n, 2] (b [n, 2], theta [n]);
+    returns [n, 2] for pair-valued ops, [n] otherwise."""
+    code = VEC2_OPS[op]
+    _require_f32(a, "a")
+    a = a.contiguous()
+    if a.dim() != 2 or a.size(1) != 2:
+        raise RuntimeError("RAC: pairs must be [n, 2]")
+    n = a.size(0)
+    ptrs = []
+    for t, name in ((b, "b"), (theta, "theta")):
+        if t is None:
+            ptrs.append(None)
+            continue
+        _require_f32(t, name)
+        t = t.contiguous()
+        if t.numel() != (2 * n if name == "b" else n):
+            raise RuntimeError(f"RAC: {name} has the wrong length")
+        ptrs.append(t)
+    out = torch.empty((n, 2) if op in _PAIR_OUT else (n,), device=a.device, dtype=torch.float32)
+    o2 = out.data_ptr() if op in _PAIR_OUT else None
+    o1 = None if op in _PAIR_OUT else out.data_ptr()
+    check(_lib.load().rac_vec2_dev(code, n, a.data_ptr(), ptrs[0].data_ptr() if ptrs[0] is not None else None,
+                                   ptrs[1].data_ptr() if ptrs[1] is not None else None, int(iarg), o2, o1,
+                                   _stream(out)), "rac_vec2_dev")
+    return out
+
+
+def inner(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """rac_inner (rac.h:233): sum_i project(a[i], angle b[i]) |b[i]|, a 0-d tensor."""
+    _require_f32(a, "a")
+    _require_f32(b, "b")
+    a = a.contiguous()
+    b = b.contiguous()
+    if a.shape != b.shape or a.dim() != 2 or a.size(1) != 2:
+        raise RuntimeError("RAC: inner expects two [n, 2] tensors")
+    out = torch.empty((), device=a.device, dtype=torch.float32)
+    check(_lib.load().rac_inner_dev(a.data_ptr(), b.data_ptr(), a.size(0), out.data_ptr(), _stream(out)),
+          "rac_inner_dev")
+    return out
+
+
+def outer(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """rac_outer (rac.h:240): C[i, j] = project(a[i], angle b[j]) |b[j]|."""
+    _require_f32(a, "a")
+    _require_f32(b, "b")
+    a = a.contiguous()
+    b = b.contiguous()
+    if a.dim() != 2 or b.dim() != 2 or a.size(1) != 2 or b.size(1) != 2:
+        raise RuntimeError("RAC: outer expects [m, 2] and [n, 2] tensors")
+    C = torch.empty((a.size(0), b.size(0)), device=a.device, dtype=torch.float32)
+    check(_lib.load().rac_outer_dev(a.data_ptr(), b.data_ptr(), C.data_ptr(), a.size(0), b.size(0),
+                                    _stream(C)), "rac_outer_dev")
+    return C
+
+
+def dct(x: torch.Tensor) -> torch.Tensor:
+    """rac_dct (rac.h:189): DCT-II of a 1-D tensor."""
+    _require_f32(x, "x")
+    x = x.contiguous()
+    if x.dim() != 1:
+        raise RuntimeError("RAC: dct expects a 1-D tensor")
+    X = torch.empty_like(x)
+    check(_lib.load().rac_dct_dev(x.data_ptr(), X.data_ptr(), x.numel(), _stream(X)), "rac_dct_dev")
+    return X
+
+
 __all__ = [
     "MODE_FAST", "MODE_CORDIC", "MODE_SHIFTADD", "RACError",
     "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
     "matmul_forward", "matmul_backward", "linear_forward", "linear_backward",
     "softmax", "rmsnorm", "layernorm", "exp", "silu", "sigmoid", "tanh", "gelu", "relu",
     "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_",
+    "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
 ]

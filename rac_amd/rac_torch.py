@@ -585,6 +585,85 @@ def _causal_scores(scores: torch.Tensor, T: int) -> torch.Tensor:
     return scores + causal
 
 
+class RACBmmFunction(Function):
+    """Batched C[z] = A[z] @ B[z] in one RAC-matmul launch; backward
+    dA = dC B^T (NT) and dB = A^T dC (TN), batched the same way."""
+
+    @staticmethod
+    def forward(ctx, A, B):
+        _need_gpu(A, "A")
+        A32 = A.float().contiguous()
+        B32 = B.float().contiguous()
+        ctx.save_for_backward(A32, B32)
+        return _rac.bmm(A32, B32, **_kw()).to(A.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        A, B = ctx.saved_tensors
+        g = g.float().contiguous()
+        dA = _rac.bmm(g, B, trans_b=True, **_kw()) if ctx.needs_input_grad[0] else None
+        dB = _rac.bmm(A, g, trans_a=True, **_kw()) if ctx.needs_input_grad[1] else None
+        return dA, dB
+
+
+def rac_bmm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """A [..., M, K] @ B [..., K, N] with leading dims flattened into one
+    batched RAC-matmul launch."""
+    lead = A.shape[:-2]
+    out = RACBmmFunction.apply(A.reshape(-1, A.shape[-2], A.shape[-1]),
+                               B.reshape(-1, B.shape[-2], B.shape[-1]))
+    return out.view(*lead, A.shape[-2], B.shape[-1])
+
+
+class RACAttentionFunction(Function):
+    """Scaled dot-product attention through RAC (rac.h:323-335): Q K^T and
+    P V on the CORDIC matmul, causal / [T, T] additive mask and softmax on
+    the CORDIC-exp kernel.  Backward (standard softmax-attention gradients,
+    every product on the RAC matmul): dV = P^T dO, dP = dO V^T,
+    dS = P (dP - rowsum(dP P)), dQ = s dS K, dK = s dS^T Q."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, is_causal):
+        _need_gpu(q, "q")
+        q32, k32, v32 = (t.float().contiguous() for t in (q, k, v))
+        m32 = mask.float().contiguous() if mask is not None else None
+        out, P = _rac.attention(q32, k32, v32, m32, bool(is_causal), return_probs=True, **_kw())
+        ctx.save_for_backward(q32, k32, v32, P)
+        return out.to(q.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, v, P = ctx.saved_tensors
+        B, H, T, D = q.shape
+        Z = B * H
+        scale = _rac.attention_scale(D)
+        g3 = g.float().contiguous().view(Z, T, D)
+        q3, k3, v3, P3 = q.view(Z, T, D), k.view(Z, T, D), v.view(Z, T, D), P.view(Z, T, T)
+        dV = _rac.bmm(P3, g3, trans_a=True, **_kw())
+        dP = _rac.bmm(g3, v3, trans_b=True, **_kw())
+        dS = P3 * (dP - (dP * P3).sum(-1, keepdim=True))
+        dQ = _rac.bmm(dS, k3, alpha=scale, **_kw()) if ctx.needs_input_grad[0] else None
+        dK = _rac.bmm(dS, q3, trans_a=True, alpha=scale, **_kw()) if ctx.needs_input_grad[1] else None
+        shape = (B, H, T, D)
+        return (dQ.view(shape) if dQ is not None else None, dK.view(shape) if dK is not None else None,
+                dV.view(shape), None, None)
+
+
+def rac_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
+                  is_causal: bool = False) -> torch.Tensor:
+    """Attention core of [B, H, T, D] tensors through RAC; mask: optional
+    additive [T, T]."""
+    return RACAttentionFunction.apply(q, k, v, mask, is_causal)
+
+
+def _rac_core_ok(mask: Optional[torch.Tensor], T: int, dropout: nn.Module) -> bool:
+    """The fused RAC attention core takes a [T, T] additive mask and no
+    dropout between softmax and P V; other cases compose the stages."""
+    if isinstance(dropout, nn.Dropout) and dropout.training and dropout.p > 0:
+        return False
+    return mask is None or (mask.dim() == 2 and tuple(mask.shape) == (T, T) and mask.is_floating_point())
+
+
 class RACAttention(nn.Module):
     """Multi-head attention with RAC projections and per-head RAC matmuls
     (rac_torch.py:660-818); softmax on the CORDIC-exp kernel."""
@@ -606,24 +685,23 @@ class RACAttention(nn.Module):
         Q = Q.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
         K = K.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
         V = V.reshape(B, T, self.n_heads, self.d_head).transpose(1, 2)
-        scores = self._rac_bmm(Q, K.transpose(-2, -1)) * self.scale
-        if is_causal:
-            scores = _causal_scores(scores, T)
-        if mask is not None:
-            scores = scores + mask
-        attn = self.dropout(rac_softmax(scores))
-        out = self._rac_bmm(attn, V)
+        if _rac_core_ok(mask, T, self.dropout):
+            out = rac_attention(Q, K, V, mask, is_causal)
+        else:
+            scores = self._rac_bmm(Q, K.transpose(-2, -1)) * self.scale
+            if is_causal:
+                scores = _causal_scores(scores, T)
+            if mask is not None:
+                scores = scores + mask
+            attn = self.dropout(rac_softmax(scores))
+            out = self._rac_bmm(attn, V)
         out = out.transpose(1, 2).contiguous().view(B, T, D)
         return self.out_proj(out)
 
     def _rac_bmm(self, A, B):
-        Bd, H, M, K = A.shape
-        N = B.shape[-1]
-        A_flat = A.reshape(-1, M, K)
-        B_flat = B.reshape(-1, K, N)
-        outs = [RACMatmulFunction.apply(A_flat[i].contiguous(), B_flat[i].contiguous())
-                for i in range(A_flat.shape[0])]
-        return torch.stack(outs, 0).view(Bd, H, M, N)
+        # the reference loops RACMatmulFunction over heads
+        # (rac_torch.py:781-795); one batched launch does the same products
+        return rac_bmm(A, B)
 
     @classmethod
     def from_attention_layers(cls, q_linear, k_linear, v_linear, out_linear, n_heads, dropout=0.0):
@@ -670,8 +748,11 @@ class RACTransformerBlock(nn.Module):
 
 class RACRoPEAttention(nn.Module):
     """Llama-style attention (rac_torch.py:1279-1343): RAC QKV and output
-    projections, RoPE kernel on the strided Q/K views, QK^T and AV as fp32
-    torch matmuls (as in the reference), softmax on the CORDIC-exp kernel."""
+    projections, RoPE kernel on the strided Q/K views, and the attention core
+    through RAC (Q K^T and P V on the CORDIC matmul, causal / [T, T] mask and
+    CORDIC softmax).  With dropout active or another mask shape, the
+    reference's composition is kept: fp32 torch matmuls around the
+    CORDIC-exp softmax."""
 
     def __init__(self, d_model: int, n_heads: int, max_seq_len: int = 4096, bias: bool = False,
                  dropout: float = 0.0, rope_base: float = 10000.0, device=None, dtype=None):
@@ -696,13 +777,16 @@ class RACRoPEAttention(nn.Module):
         K = K.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         V = V.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         Q, K = self.rope(Q, K, positions=positions)
-        scores = torch.matmul(Q.float().contiguous(), K.float().transpose(-2, -1).contiguous()) * self.scale
-        if is_causal:
-            scores = _causal_scores(scores, T)
-        if mask is not None:
-            scores = scores + mask
-        attn = self.dropout(rac_softmax(scores))
-        out = torch.matmul(attn, V.float().contiguous()).to(x.dtype)
+        if _rac_core_ok(mask, T, self.dropout):
+            out = rac_attention(Q, K, V, mask, is_causal).to(x.dtype)
+        else:
+            scores = torch.matmul(Q.float().contiguous(), K.float().transpose(-2, -1).contiguous()) * self.scale
+            if is_causal:
+                scores = _causal_scores(scores, T)
+            if mask is not None:
+                scores = scores + mask
+            attn = self.dropout(rac_softmax(scores))
+            out = torch.matmul(attn, V.float().contiguous()).to(x.dtype)
         out = out.transpose(1, 2).contiguous().view(B, T, D)
         return self.out_proj(out)
 

@@ -7,7 +7,7 @@ oracle/ref_probe.c.  Every value below is produced by reference code; the
 inputs come from tests/raclib.py's seeded generator and are stored too, so
 the fixtures are self-contained data (nothing of the reference's source).
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [core] [prims] [attention]
 
 Outputs (tests/golden/):
   tables.json            reference CORDIC tables (rac_cpu.c:20-52)
@@ -20,6 +20,12 @@ Outputs (tests/golden/):
   alu_exp.npz            rac_alu_exp (16-step hyperbolic CORDIC exp) samples
   matmul.npz             rac_matmul 1024^3, U[-1,1] seeds 0/1: digest + samples;
                          the 2x2 known answer
+  prims.npz              rac_rotate/_raw/_n, rac_compensate, rac_project/_n,
+                         rac_polar, rac_norm, rac_normalize, rac_dot,
+                         rac_coherence, rac_complex_mul on 512 pairs;
+                         rac_inner, rac_outer, rac_dct
+  attention.npz          rac_scaled_dot_attention on [2,3,16,8], with and
+                         without causal / additive mask
 """
 from __future__ import annotations
 
@@ -35,10 +41,20 @@ sys.path.insert(0, os.path.dirname(HERE))
 import raclib as rl  # noqa: E402
 
 
-def main() -> None:
+def main(sections) -> None:
     if not rl.have_ref():
         raise SystemExit("oracle/_ref/librac_ref.so is not built (make -C oracle ref)")
     r = rl.ref()
+    if "core" in sections:
+        write_core(r)
+    if "prims" in sections:
+        write_prims(r)
+    if "attention" in sections:
+        write_attention(r)
+    print("golden fixtures written to", HERE)
+
+
+def write_core(r) -> None:
     rng = np.random.default_rng(20261201)
 
     # tables
@@ -140,8 +156,77 @@ def main() -> None:
     assert r.rac_matmul(rl.p(A2), rl.p(B2), rl.p(C2), 2, 2, 2, None) == 0
     np.savez_compressed(os.path.join(HERE, "matmul.npz"), A_sha=rl.sha256(A), B_sha=rl.sha256(B),
                         C_sha=rl.sha256(Cm), idx=idx, C_samples=Cm.ravel()[idx], kat_C=C2)
-    print("golden fixtures written to", HERE)
+
+
+def _v(x, y):
+    return rl.Vec2(float(x), float(y))
+
+
+def write_prims(r) -> None:
+    """rac.h vector primitives from the reference CPU library (rac_cpu.c:136-371)."""
+    rng = np.random.default_rng(20261202)
+    n = 512
+    # pairs over all four quadrants, the axes, zero, and a wide magnitude range
+    a = rng.uniform(-3, 3, (n, 2)).astype(np.float32)
+    b = rng.uniform(-3, 3, (n, 2)).astype(np.float32)
+    a[:8] = [[0, 0], [1, 0], [-1, 0], [0, 1], [0, -1], [-2, 1e-3], [-2, -1e-3], [1e-20, -1e-20]]
+    a[8:16] *= np.float32(1e4)
+    b[:4] = [[0, 0], [-1, 0], [0, -2], [-3, 3]]
+    th = rng.uniform(-4, 4, n).astype(np.float32)
+    th[:8] = [0.0, np.pi / 2, -np.pi / 2, np.pi, -np.pi, 3.0, -3.0, 1e-7]
+    th[16:32] = rng.uniform(-5000, 5000, 16).astype(np.float32)
+    it = rng.integers(1, 30, n).astype(np.int32)   # includes out-of-range counts (clamped to [4, 24])
+    chain = rng.integers(0, 40, n).astype(np.int32)
+    out = {k: np.zeros((n, 2), np.float32) for k in ("rotate", "rotate_raw", "compensate", "polar",
+                                                     "normalize", "complex_mul", "rotate_n")}
+    out.update({k: np.zeros(n, np.float32) for k in ("project", "norm", "dot", "coherence", "project_n")})
+    m, ang = C.c_float(), C.c_float()
+    for i in range(n):
+        va, vb = _v(*a[i]), _v(*b[i])
+        for key, res in (("rotate", r.rac_rotate(va, th[i])), ("rotate_raw", r.rac_rotate_raw(va, th[i])),
+                         ("compensate", r.rac_compensate(va, int(chain[i]))),
+                         ("normalize", r.rac_normalize(va)), ("complex_mul", r.rac_complex_mul(va, vb)),
+                         ("rotate_n", r.rac_rotate_n(va, th[i], int(it[i])))):
+            out[key][i] = (res.x, res.y)
+        r.rac_polar(va, C.byref(m), C.byref(ang))
+        out["polar"][i] = (m.value, ang.value)
+        out["project"][i] = r.rac_project(va, th[i])
+        out["norm"][i] = r.rac_norm(va)
+        out["dot"][i] = r.rac_dot(va, vb)
+        out["coherence"][i] = r.rac_coherence(va, vb)
+        out["project_n"][i] = r.rac_project_n(va, th[i], int(it[i]))
+    # batch forms
+    rb = np.zeros((n, 2), np.float32)
+    r.rac_rotate_batch(rl.p(a), rl.p(th), rl.p(rb), n)
+    assert np.array_equal(rb, out["rotate"])
+    inner = np.float32(r.rac_inner(rl.p(a[:64]), rl.p(b[:64]), 64))
+    outer = np.zeros((24, 40), np.float32)
+    r.rac_outer(rl.p(a[:24]), rl.p(b[:40]), rl.p(outer), 24, 40)
+    dct_x = rng.normal(0, 1, 64).astype(np.float32)
+    dct = np.zeros(64, np.float32)
+    r.rac_dct(rl.p(dct_x), rl.p(dct), 64)
+    np.savez_compressed(os.path.join(HERE, "prims.npz"), a=a, b=b, theta=th, iters=it, chain=chain,
+                        inner=inner, outer=outer, dct_x=dct_x, dct=dct, **out)
+
+
+def write_attention(r) -> None:
+    """rac_scaled_dot_attention (rac_cpu.c:637-703) on [2, 3, 16, 8]: plain,
+    causal, additive mask, and causal + mask."""
+    B, H, T, D = 2, 3, 16, 8
+    q = rl.gen_normal((B, H, T, D), seed=11)
+    k = rl.gen_normal((B, H, T, D), seed=12)
+    v = rl.gen_normal((B, H, T, D), seed=13)
+    mask = (rl.gen_normal((T, T), seed=14) * np.float32(0.5)).astype(np.float32)
+    mask[3, 5] = -np.inf
+    res = {}
+    for name, mk, causal in (("out_plain", None, 0), ("out_causal", None, 1), ("out_mask", mask, 0),
+                             ("out_causal_mask", mask, 1)):
+        o = np.zeros_like(q)
+        assert r.rac_scaled_dot_attention(rl.p(q), rl.p(k), rl.p(v), rl.p(mk) if mk is not None else None,
+                                          causal, rl.p(o), B, H, T, D, None) == 0
+        res[name] = o
+    np.savez_compressed(os.path.join(HERE, "attention.npz"), q=q, k=k, v=v, mask=mask, **res)
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or ["core", "prims", "attention"])

@@ -21,6 +21,14 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 _vp, _i, _l, _f = C.c_void_p, C.c_int, C.c_long, C.c_float
 _fp = C.POINTER(C.c_float)
 
+
+
+class Vec2(C.Structure):
+    """struct { float x, y; }: rac_vec2 (rac_cpu.h:35) / float2 (rac.h:31)."""
+
+    _fields_ = [("x", C.c_float), ("y", C.c_float)]
+
+
 _ORACLE_SIGS = {
     "orc_tables": (None, [_vp, _vp, _vp]),
     "orc_cordic_rotate": (None, [_f, _f, _f, _i, _fp, _fp]),
@@ -51,6 +59,12 @@ _ORACLE_SIGS = {
     "orc_sigmoid": (None, [_vp, _vp, _l, _i]),
     "orc_gelu": (None, [_vp, _vp, _l]),
     "orc_tanh": (None, [_vp, _vp, _l, _i]),
+    "orc_polar": (None, [_f, _f, _fp, _fp]),
+    "orc_project": (_f, [_f, _f, _f]),
+    "orc_prim": (None, [_i, _l, _vp, _vp, _vp, _i, _vp, _vp]),
+    "orc_outer": (None, [_vp, _vp, _vp, _i, _i]),
+    "orc_dct": (None, [_vp, _vp, _i]),
+    "orc_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
     "orc_check_chain_all_mantissas": (_l, [_i, _i]),
     "orc_check_projection_identity": (_l, [_i, _l, C.c_uint64]),
 }
@@ -73,6 +87,40 @@ _REF_SIGS = {
     "rac_sigmoid": (_f, [_f]),
     "rac_sincos": (None, [_f, _fp, _fp]),
     "rac_alu_exp": (_f, [_f]),
+    "rac_rotate": (Vec2, [Vec2, _f]),
+    "rac_rotate_raw": (Vec2, [Vec2, _f]),
+    "rac_compensate": (Vec2, [Vec2, _i]),
+    "rac_project": (_f, [Vec2, _f]),
+    "rac_polar": (None, [Vec2, _fp, _fp]),
+    "rac_norm": (_f, [Vec2]),
+    "rac_normalize": (Vec2, [Vec2]),
+    "rac_dot": (_f, [Vec2, Vec2]),
+    "rac_coherence": (_f, [Vec2, Vec2]),
+    "rac_complex_mul": (Vec2, [Vec2, Vec2]),
+    "rac_rotate_n": (Vec2, [Vec2, _f, _i]),
+    "rac_project_n": (_f, [Vec2, _f, _i]),
+    "rac_dct": (None, [_vp, _vp, _i]),
+    "rac_rotate_batch": (None, [_vp, _vp, _vp, _i]),
+    "rac_inner": (_f, [_vp, _vp, _i]),
+    "rac_outer": (None, [_vp, _vp, _vp, _i, _i]),
+    "rac_scaled_dot_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+}
+
+# Vector-primitive op codes shared by orc_prim and rac_vec2_dev:
+# name -> (code, writes a pair, reads b, reads theta)
+PRIM_OPS = {
+    "rotate": (0, True, False, True),
+    "rotate_raw": (1, True, False, True),
+    "compensate": (2, True, False, False),
+    "project": (3, False, False, True),
+    "polar": (4, True, False, False),
+    "normalize": (5, True, False, False),
+    "dot": (6, False, True, False),
+    "coherence": (7, False, True, False),
+    "complex_mul": (8, True, True, False),
+    "rotate_n": (9, True, False, True),
+    "project_n": (10, False, False, True),
+    "inner_term": (11, False, True, False),
 }
 
 _cache = {}
@@ -220,3 +268,27 @@ def max_rel(a, b, floor=1e-30):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), floor))) if a.size else 0.0
+
+
+def orc_prim(name, a, b=None, th=None, iarg=0):
+    """Oracle primitive `name` over pairs a [n, 2] (and b [n, 2], th [n])."""
+    code, pair, _, _ = PRIM_OPS[name]
+    a = np.ascontiguousarray(a, np.float32).reshape(-1, 2)
+    n = a.shape[0]
+    b = None if b is None else np.ascontiguousarray(b, np.float32).reshape(-1, 2)
+    th = None if th is None else np.ascontiguousarray(th, np.float32)
+    out = np.zeros((n, 2) if pair else (n,), np.float32)
+    oracle().orc_prim(code, n, p(a), p(b) if b is not None else None,
+                      p(th) if th is not None else None, iarg,
+                      p(out) if pair else None, None if pair else p(out))
+    return out
+
+
+def orc_attention(q, k, v, mask, causal, iters, mode):
+    q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+    B, H, T, D = q.shape
+    out = np.empty_like(q)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    assert oracle().orc_attention(p(q), p(k), p(v), p(m) if m is not None else None, int(causal),
+                                  p(out), B, H, T, D, iters, mode) == 0
+    return out

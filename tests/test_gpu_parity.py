@@ -442,3 +442,55 @@ def test_llama_block_small_forward_backward_and_causality():
     with torch.no_grad():
         ya, yb = blk(xa, is_causal=True), blk(xb, is_causal=True)
     assert torch.allclose(ya[:, :-1], yb[:, :-1], atol=1e-4)         # DVT-30
+
+
+def test_llama_block_matches_oracle_composition():
+    """RACLlamaBlock (CORDIC mode, n=16) vs the same block composed on the CPU
+    from the checker's ops (CORDIC matmul, RoPE table/apply, RMSNorm with
+    CORDIC rsqrt, CORDIC softmax and SiLU); QK^T and AV, which the reference
+    leaves to torch.matmul, are float64 on the CPU side."""
+    from rac_amd import rac_torch as rt
+    d, nh, ff, T = 128, 4, 352, 48
+    hd = d // nh
+    torch.manual_seed(3)
+    blk = rt.RACLlamaBlock(d, nh, ff_dim=ff, max_seq_len=64).to(DEV)
+    with torch.no_grad():
+        for prm in blk.parameters():
+            if prm.dim() == 2:
+                prm.normal_(0.0, 0.05)
+        blk.norm1.weight.normal_(1.0, 0.02)
+        blk.norm2.weight.normal_(1.0, 0.02)
+    x = torch.randn(1, T, d, device=DEV)
+    rt.rac_set_mode('cordic')
+    rt.rac_set_precision(16)
+    try:
+        with torch.no_grad():
+            y = H(blk(x, is_causal=True))
+    finally:
+        rt.rac_set_mode('fast')
+        rt.rac_set_precision(24)
+    P = {k: H(v) for k, v in blk.state_dict().items()}
+    xn = H(x)[0]
+
+    def lin(a, w):
+        return rl.orc_matmul(np.ascontiguousarray(a, np.float32), np.ascontiguousarray(w), a.shape[0],
+                             w.shape[0], a.shape[1], 16, 1, tb=1)
+
+    h = rl.orc_rmsnorm(xn, P["norm1.weight"], 1e-6)
+    qkv = lin(h, P["attn.qkv.weight"])
+    q, k, v = qkv[:, :d], qkv[:, d:2 * d], qkv[:, 2 * d:]
+    c, s = rl.orc_rope_cache(64, hd)
+    q = rl.orc_rope_apply(q.reshape(1, T, nh, hd).transpose(0, 2, 1, 3), c, s)
+    k = rl.orc_rope_apply(k.reshape(1, T, nh, hd).transpose(0, 2, 1, 3), c, s)
+    v = v.reshape(1, T, nh, hd).transpose(0, 2, 1, 3)
+    sc = (q.astype(np.float64) @ k.astype(np.float64).transpose(0, 1, 3, 2)) * hd ** -0.5
+    sc = sc + np.triu(np.full((T, T), -np.inf), 1)
+    att = rl.orc_softmax(sc.astype(np.float32).reshape(-1, T), 16).reshape(1, nh, T, T)
+    o = (att.astype(np.float64) @ v.astype(np.float64)).transpose(0, 2, 1, 3).reshape(T, d)
+    x1 = xn + lin(o.astype(np.float32), P["attn.out_proj.weight"])
+    h2 = rl.orc_rmsnorm(x1, P["norm2.weight"], 1e-6)
+    f1 = rl.orc_unary("orc_silu", lin(h2, P["ffn.fc1.weight"]), 16)
+    ref = x1 + lin(f1, P["ffn.fc2.weight"])
+    err = np.abs(y[0] - ref) / np.maximum(np.abs(ref), 1.0)
+    assert err.max() < 1e-4, err.max()
+

@@ -22,6 +22,14 @@ exhaustive enumeration, or libm within an analytic bound.  Map:
   orc_rsqrt               libm 1/sqrt within 1e-6; guard cases; golden KATs
   orc_rmsnorm/layernorm   libm variant bit-exact vs golden; CORDIC within 1e-6
   orc_silu/gelu/sigmoid   libm variant vs golden; CORDIC within bound
+  orc_prim/outer/dct      golden prims.npz (compiled rac_cpu.c primitives),
+                          bit-exact; rac_inner within its summation-order
+                          bound; closed forms (hypot/atan2, exact rotation,
+                          complex product, float64 DCT-II)
+  orc_attention           golden attention.npz (compiled
+                          rac_scaled_dot_attention) bit-exact with expf and
+                          FAST products; float64 softmax attention within the
+                          CORDIC bound
 """
 import json
 import math
@@ -327,3 +335,130 @@ def test_activations(o):
         assert np.max(np.abs(s - d["silu"]) / np.maximum(np.abs(d["silu"]), 1e-3)) < 1.1 * 2.0 ** -last + 1e-6
         t = rl.orc_unary("orc_tanh", x, n)
         assert np.max(np.abs(t - np.tanh(x.astype(np.float64)))) < 2 * 2.0 ** -last + 1e-6
+
+
+# ── vector primitives (rac.h:101-250, 345-346) ─────────────────────────────
+
+_PAIR_ARG = {"compensate": "chain", "rotate_n": "iters", "project_n": "iters"}
+
+
+def _prim_from_golden(d, name):
+    code, pair, nb, nt = rl.PRIM_OPS[name]
+    a, b, th = d["a"], d["b"], d["theta"]
+    if name in _PAIR_ARG:
+        arg = d[_PAIR_ARG[name]]
+        return np.stack([rl.orc_prim(name, a[i:i + 1], None, th[i:i + 1], int(arg[i]))[0]
+                         for i in range(len(a))])
+    return rl.orc_prim(name, a, b if nb else None, th if nt else None)
+
+
+@pytest.mark.parametrize("name", ["rotate", "rotate_raw", "compensate", "project", "polar", "normalize",
+                                  "dot", "coherence", "complex_mul", "rotate_n", "project_n"])
+def test_prims_bit_exact_vs_reference_golden(o, name):
+    d = npz("prims.npz")
+    assert np.array_equal(_prim_from_golden(d, name), d[name], equal_nan=True)
+
+
+def test_prims_batch_forms_vs_reference_golden(o):
+    d = npz("prims.npz")
+    a, b = d["a"], d["b"]
+    pol = rl.orc_prim("polar", a)
+    assert np.array_equal(pol[:, 0], d["norm"])
+    outer = np.zeros((24, 40), np.float32)
+    o.orc_outer(rl.p(np.ascontiguousarray(a[:24])), rl.p(np.ascontiguousarray(b[:40])), rl.p(outer), 24, 40)
+    assert np.array_equal(outer, d["outer"])
+    X = np.zeros(64, np.float32)
+    o.orc_dct(rl.p(d["dct_x"]), rl.p(X), 64)
+    assert np.array_equal(X, d["dct"])
+    # rac_inner sums with an OpenMP reduction (order not fixed): bound by
+    # n * 2^-24 * sum |term|
+    terms = rl.orc_prim("inner_term", a[:64], b[:64]).astype(np.float64)
+    assert abs(terms.sum() - float(d["inner"])) <= 64 * 2.0 ** -24 * np.abs(terms).sum()
+
+
+def test_prims_closed_forms(o):
+    rng = np.random.default_rng(7)
+    n = 2000
+    a = rng.uniform(-5, 5, (n, 2)).astype(np.float32)
+    b = rng.uniform(-5, 5, (n, 2)).astype(np.float32)
+    th = rng.uniform(-20, 20, n).astype(np.float32)
+    a64, b64, th64 = a.astype(np.float64), b.astype(np.float64), th.astype(np.float64)
+    r = np.hypot(a64[:, 0], a64[:, 1])
+    # polar: 16 vectoring steps leave an angle residual <= atan(2^-15) and
+    # the magnitude carries K_INV = 0.60725 against K_16 (|bias| < 2e-5)
+    pol = rl.orc_prim("polar", a).astype(np.float64)
+    ang_err = np.angle(np.exp(1j * (pol[:, 1] - np.arctan2(a64[:, 1], a64[:, 0]))))
+    assert np.max(np.abs(ang_err)) < 4e-5
+    assert np.max(np.abs(pol[:, 0] / r - 1)) < 5e-5
+    # rotate: exact rotation to the 16-step residual (plus the sequential
+    # float reduction of theta, whose drift grows with |theta|)
+    rot = rl.orc_prim("rotate", a, None, th).astype(np.float64)
+    c, s_ = np.cos(th64), np.sin(th64)
+    ex = np.stack([a64[:, 0] * c - a64[:, 1] * s_, a64[:, 0] * s_ + a64[:, 1] * c], 1)
+    assert np.max(np.hypot(*(rot - ex).T) / r) < 1e-4
+    # complex_mul: the complex product a*b
+    cm = rl.orc_prim("complex_mul", a, b).astype(np.float64)
+    prod = (a64[:, 0] + 1j * a64[:, 1]) * (b64[:, 0] + 1j * b64[:, 1])
+    assert np.max(np.abs(cm[:, 0] + 1j * cm[:, 1] - prod) / np.abs(prod)) < 2e-4
+    # dot / coherence: the Euclidean dot product and cosine similarity
+    dot = rl.orc_prim("dot", a, b).astype(np.float64)
+    rb = np.hypot(b64[:, 0], b64[:, 1])
+    assert np.max(np.abs(dot - (a64 * b64).sum(1)) / (r * rb)) < 2e-4
+    coh = rl.orc_prim("coherence", a, b).astype(np.float64)
+    assert np.max(np.abs(coh - (a64 * b64).sum(1) / (r * rb))) < 1e-4
+    # rotate_n at 24 steps: residual angle ~2^-23, but the gain 1/K-hat(24)
+    # of the reference table is 5.93e-6 above 1/K_24, so |error| / |v| is
+    # that bias plus rounding
+    rn = rl.orc_prim("rotate_n", a[:200], None, th[:200] * np.float32(0.1), 24).astype(np.float64)
+    th2 = (th[:200] * np.float32(0.1)).astype(np.float64)
+    ex2 = np.stack([a64[:200, 0] * np.cos(th2) - a64[:200, 1] * np.sin(th2),
+                    a64[:200, 0] * np.sin(th2) + a64[:200, 1] * np.cos(th2)], 1)
+    assert np.max(np.hypot(*(rn - ex2).T) / r[:200]) < 5.93e-6 + 1e-6
+    # DCT-II of a constant and of a cosine basis vector
+    X = np.zeros(32, np.float32)
+    one = np.ones(32, np.float32)
+    o.orc_dct(rl.p(one), rl.p(X), 32)
+    assert abs(X[0] - 32) < 1e-4 and np.max(np.abs(X[1:])) < 1e-4
+    x5 = np.cos(np.pi * (2 * np.arange(32) + 1) * 5 / 64).astype(np.float32)
+    o.orc_dct(rl.p(x5), rl.p(X), 32)
+    expect = np.zeros(32)
+    expect[5] = 16.0
+    assert np.max(np.abs(X - expect)) < 1e-4
+
+
+# ── attention (rac.h:323-335) ───────────────────────────────────────────────
+
+@pytest.mark.parametrize("case", ["plain", "causal", "mask", "causal_mask"])
+def test_attention_bit_exact_vs_reference_golden(o, case):
+    d = npz("attention.npz")
+    mask = d["mask"] if "mask" in case else None
+    causal = "causal" in case
+    out = rl.orc_attention(d["q"], d["k"], d["v"], mask, causal, 0, 0)
+    assert np.array_equal(out, d["out_" + case])
+
+
+def _attention64(q, k, v, mask, causal):
+    q, k, v = (t.astype(np.float64) for t in (q, k, v))
+    T, D = q.shape[2], q.shape[3]
+    s = q @ np.swapaxes(k, 2, 3) / math.sqrt(D)
+    if causal:
+        s = np.where(np.triu(np.ones((T, T), bool), 1), -np.inf, s)
+    if mask is not None:
+        s = s + mask.astype(np.float64)
+    s = s - s.max(-1, keepdims=True)
+    p_ = np.exp(s)
+    p_ /= p_.sum(-1, keepdims=True)
+    return p_ @ v
+
+
+@pytest.mark.parametrize("iters,mode", [(16, 1), (24, 1), (16, 0), (8, 1)])
+def test_attention_cordic_bound(o, iters, mode):
+    d = npz("attention.npz")
+    for mask, causal in ((None, 0), (d["mask"], 1)):
+        ref = _attention64(d["q"], d["k"], d["v"], mask, causal)
+        out = rl.orc_attention(d["q"], d["k"], d["v"], mask, causal, iters, mode)
+        last, _ = _hyp_last_shift(iters)
+        # CORDIC exp relative error ~2^-last moves each probability by that
+        # fraction; the CORDIC products add ~2e-5 (n >= 16) relative
+        bound = 4 * (2.0 ** -last + (2e-5 if iters >= 16 else 2e-4)) * np.abs(d["v"]).max()
+        assert np.max(np.abs(out - ref)) < bound
