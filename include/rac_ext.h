@@ -61,6 +61,15 @@ int rac_gemm_dev(const float *A, const float *B, float *C, int M, int N, int K,
 int rac_gemm_batched_dev(const float *A, const float *B, float *C, int M, int N, int K,
                          int trans_a, int trans_b, float alpha, float beta, int iters, int mode,
                          int batch, long stride_a, long stride_b, long stride_c, void *stream);
+/* Fused linear layer (rac_torch.cu:705-780): out[M,N] = act(input[M,K]
+ * weight[N,K]^T + bias[N]) with the RAC MAC of `mode`; act 0 none, 1 ReLU,
+ * 2 GELU (erf), 3 SiLU (CORDIC exp of `iters` steps); bias and pre may be
+ * NULL; pre receives the pre-activation values when given. */
+int rac_fused_linear_dev(const float *input, const float *weight, const float *bias, float *out,
+                         float *pre, int M, int N, int K, int act, int iters, int mode, void *stream);
+/* d[i] = g[i] * act'(pre[i]) (rac_torch.cu:680-694), same activation ids. */
+int rac_act_grad_dev(const float *g, const float *pre, float *d, long count, int act, int iters,
+                     void *stream);
 /* Attention softmax of rows that form [.., seq, seq] score blocks: row r is
  * query position t = r % seq; is_causal sets -inf for columns > t, then the
  * optional additive mask[t*seq + col] is added; 1/sum is 0 for a sum that is

@@ -41,6 +41,8 @@ _SIGNATURES = {
     "rac_gemm_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f, _i, _i, _vp]),
     "rac_gemm_batched_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _l, _l, _l, _vp]),
     "rac_softmax_masked_dev": (_i, [_vp, _vp, _l, _l, _vp, _i, _i, _vp]),
+    "rac_fused_linear_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "rac_act_grad_dev": (_i, [_vp, _vp, _vp, _l, _i, _i, _vp]),
     "rac_softmax_dev": (_i, [_vp, _vp, _l, _l, _i, _vp]),
     "rac_exp_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_silu_dev": (_i, [_vp, _vp, _l, _i, _vp]),

@@ -1,0 +1,67 @@
+// rac_act.hpp — the activation functions shared by the elementwise kernels
+// and the fused GEMM epilogue, so both produce the same bits.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include "rac_internal.hpp"
+#include "rac_math.hpp"
+
+namespace rac {
+
+template <int OP, int NITER>
+__device__ __forceinline__ float elt(float x, int iters, float khinv) {
+    if constexpr (OP == kEltRelu) {
+        return (x > 0.0f) ? x : 0.0f;                           // rac_cpu.c:441-445
+    } else if constexpr (OP == kEltGelu) {
+        return x * 0.5f * (1.0f + erff(x * 0.7071067811865f));  // rac_cpu.c:447-451
+    } else {
+        auto ex = [&](float v) {
+            if constexpr (NITER > 0) return exp_cordic<NITER>(v, khinv);
+            else return exp_cordic_rt(v, iters, khinv);
+        };
+        if constexpr (OP == kEltExp) {
+            return ex(x);
+        } else if constexpr (OP == kEltSilu) {
+            return x / (1.0f + ex(-x));                         // rac_cpu.c:453-457
+        } else if constexpr (OP == kEltSigmoid) {
+            return 1.0f / (1.0f + ex(-x));
+        } else {                                                // tanh
+            const float e = ex(-2.0f * __builtin_fabsf(x));
+            return __builtin_copysignf((1.0f - e) / (1.0f + e), x);
+        }
+    }
+}
+
+// Activation ids of the fused linear path (rac_torch.cu:669-675):
+// 0 identity, 1 ReLU, 2 GELU (exact erf), 3 SiLU (CORDIC exp).
+constexpr int kActNone = 0, kActRelu = 1, kActGelu = 2, kActSilu = 3;
+
+__device__ __forceinline__ float act_rt(float x, int act, int iters, float khinv) {
+    switch (act) {
+    case kActRelu: return elt<kEltRelu, 0>(x, iters, khinv);
+    case kActGelu: return elt<kEltGelu, 0>(x, iters, khinv);
+    case kActSilu: return elt<kEltSilu, 0>(x, iters, khinv);
+    default: return x;
+    }
+}
+
+// d act / dx at the pre-activation x, times the incoming gradient g
+// (derivative formulas of rac_torch.cu:680-694; the SiLU sigmoid uses the
+// same CORDIC exp as the forward pass).
+__device__ __forceinline__ float act_grad(float g, float x, int act, int iters, float khinv) {
+    switch (act) {
+    case kActRelu: return g * ((x > 0.0f) ? 1.0f : 0.0f);
+    case kActGelu: {
+        const float cdf = 0.5f * (1.0f + erff(x * 0.7071067811865f));
+        const float pdf = 0.3989422804f * expf(-0.5f * x * x);
+        return g * (cdf + x * pdf);
+    }
+    case kActSilu: {
+        const float sig = elt<kEltSigmoid, 0>(x, iters, khinv);
+        return g * (sig * (1.0f + x * (1.0f - sig)));
+    }
+    default: return g;
+    }
+}
+
+}  // namespace rac

@@ -255,6 +255,36 @@ RAC_EXPORT int rac_gemm_batched_dev(const float* A, const float* B, float* C, in
                      "rac_gemm_batched_dev launch");
 }
 
+// output[M,N] = act(input[M,K] weight[N,K]^T + bias) in one launch
+// (rac_torch.cu:705-780 with the RAC MAC of `mode`); pre, when not null,
+// receives the pre-activation (what the backward pass needs).
+RAC_EXPORT int rac_fused_linear_dev(const float* input, const float* weight, const float* bias, float* out,
+                                    float* pre, int M, int N, int K, int act, int iters, int mode,
+                                    void* stream) {
+    int rc = check_gemm(input, weight, out, M, N, K);
+    if (rc) return rc;
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_fused_linear_dev: mode must be 0, 1 or 2");
+    if (act < 0 || act > 3) return fail(RAC_ERR_INVALID_DIM, "rac_fused_linear_dev: act must be 0..3");
+    GemmEpilogue ep;
+    ep.bias = bias;
+    ep.pre = pre;
+    ep.act = act;
+    ep.khinv = host_consts().exp_khinv[clamp_iters(iters)];
+    return check_hip(gemm_fused_launch(input, weight, out, M, N, K, ep, iters, mode, (hipStream_t)stream),
+                     "rac_fused_linear_dev launch");
+}
+
+// d[i] = g[i] * act'(pre[i]) for the activation ids of rac_fused_linear_dev.
+RAC_EXPORT int rac_act_grad_dev(const float* g, const float* pre, float* d, long count, int act, int iters,
+                                void* stream) {
+    if (!g || !pre || !d) return fail(RAC_ERR_NULL_PTR, "rac_act_grad_dev: null buffer");
+    if (count < 0) return fail(RAC_ERR_INVALID_DIM, "rac_act_grad_dev: negative count");
+    if (act < 0 || act > 3) return fail(RAC_ERR_INVALID_DIM, "rac_act_grad_dev: act must be 0..3");
+    if (count == 0) return RAC_OK;
+    return check_hip(act_grad_launch(g, pre, d, count, act, iters, (hipStream_t)stream),
+                     "rac_act_grad_dev launch");
+}
+
 // Row softmax with attention masking of rows laid out as [.., seq, seq]:
 // causal and/or an additive [seq, seq] mask (either may be off); in place
 // when x == y.

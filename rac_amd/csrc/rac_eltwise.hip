@@ -11,36 +11,11 @@
 // element, the HBM minimum), and consecutive lanes touch consecutive
 // addresses.
 #include <hip/hip_runtime.h>
-#include "rac_math.hpp"
-#include "rac_internal.hpp"
+#include "rac_act.hpp"
 
 namespace rac {
 
 // ── elementwise ──────────────────────────────────────────────────────────
-
-template <int OP, int NITER>
-__device__ __forceinline__ float elt(float x, int iters, float khinv) {
-    if constexpr (OP == kEltRelu) {
-        return (x > 0.0f) ? x : 0.0f;                           // rac_cpu.c:441-445
-    } else if constexpr (OP == kEltGelu) {
-        return x * 0.5f * (1.0f + erff(x * 0.7071067811865f));  // rac_cpu.c:447-451
-    } else {
-        auto ex = [&](float v) {
-            if constexpr (NITER > 0) return exp_cordic<NITER>(v, khinv);
-            else return exp_cordic_rt(v, iters, khinv);
-        };
-        if constexpr (OP == kEltExp) {
-            return ex(x);
-        } else if constexpr (OP == kEltSilu) {
-            return x / (1.0f + ex(-x));                         // rac_cpu.c:453-457
-        } else if constexpr (OP == kEltSigmoid) {
-            return 1.0f / (1.0f + ex(-x));
-        } else {                                                // tanh
-            const float e = ex(-2.0f * __builtin_fabsf(x));
-            return __builtin_copysignf((1.0f - e) / (1.0f + e), x);
-        }
-    }
-}
 
 template <int OP, int NITER>
 __global__ __launch_bounds__(256) void eltwise_vec_kernel(
@@ -73,6 +48,23 @@ static unsigned stream_grid(long items) {
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     return (unsigned)blocks;
+}
+
+__global__ __launch_bounds__(256) void act_grad_kernel(const float* __restrict__ g,
+                                                       const float* __restrict__ pre,
+                                                       float* __restrict__ d, long n, int act,
+                                                       int iters, float khinv) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        d[i] = act_grad(g[i], pre[i], act, iters, khinv);
+}
+
+hipError_t act_grad_launch(const float* g, const float* pre, float* d, long count, int act, int iters,
+                           hipStream_t s) {
+    iters = clamp_iters(iters);
+    hipLaunchKernelGGL(act_grad_kernel, dim3(stream_grid(count)), dim3(256), 0, s, g, pre, d, count, act,
+                       iters, host_consts().exp_khinv[iters]);
+    return hipGetLastError();
 }
 
 template <int OP, int NITER>

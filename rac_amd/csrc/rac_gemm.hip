@@ -21,8 +21,7 @@
 // rate.  The next K-tile is prefetched into registers while the current one
 // is computed.
 #include <hip/hip_runtime.h>
-#include "rac_math.hpp"
-#include "rac_internal.hpp"
+#include "rac_act.hpp"
 
 namespace rac {
 
@@ -55,10 +54,11 @@ __device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc
     }
 }
 
-template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
+template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
-    int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc)
+    int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc,
+    GemmEpilogue ep)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     A += (long)blockIdx.z * sa;
@@ -166,8 +166,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             if (gn >= N) continue;
             float* cp = C + gm * N + gn;
             // rac_kernels.hip:267-272
-            *cp = (beta != 0.0f) ? __builtin_fmaf(alpha, acc[i][j], beta * *cp)
-                                 : alpha * acc[i][j];
+            float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc[i][j], beta * *cp)
+                                     : alpha * acc[i][j];
+            if constexpr (FUSED) {
+                // rac_torch.cu:770-775: + bias, then the activation in
+                // registers (the pre-activation is kept when asked for)
+                if (ep.bias) v = v + ep.bias[gn];
+                if (ep.pre) ep.pre[gm * N + gn] = v;
+                v = act_rt(v, ep.act, iters, ep.khinv);
+            }
+            *cp = v;
         }
     }
 }
@@ -181,9 +189,11 @@ struct GemmArgs {
     int iters;
     int batch;
     long sa, sb, sc;
+    GemmEpilogue ep;
+    bool fused;
 };
 
-template <int MODE, int NITER, bool TA, bool TB>
+template <int MODE, int NITER, bool TA, bool TB, bool FUSED>
 static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     constexpr int TM = (MODE == kModeFast) ? 8 : 4;
     constexpr int TN = TM;
@@ -191,23 +201,24 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     const float kinv = cordic_kinv(g.iters);
     dim3 grid((unsigned)((g.N + Cfg::kBN - 1) / Cfg::kBN), (unsigned)((g.M + Cfg::kBM - 1) / Cfg::kBM),
               (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN>), grid, dim3(256), 0, stream,
-                       g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc);
+    hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED>), grid, dim3(256), 0, stream,
+                       g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
+                       g.ep);
     return hipGetLastError();
 }
 
+// The fused epilogue exists for the NT layout only (input @ weight^T, the
+// linear layer); gemm_fused_launch never asks for another.
 template <int MODE, int NITER>
 static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s) {
-    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false>(g, s);
-    if (!ta && tb) return launch_cfg<MODE, NITER, false, true>(g, s);
-    if (ta && !tb) return launch_cfg<MODE, NITER, true, false>(g, s);
-    return launch_cfg<MODE, NITER, true, true>(g, s);
+    if (g.fused) return launch_cfg<MODE, NITER, false, true, true>(g, s);
+    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false, false>(g, s);
+    if (!ta && tb) return launch_cfg<MODE, NITER, false, true, false>(g, s);
+    if (ta && !tb) return launch_cfg<MODE, NITER, true, false, false>(g, s);
+    return launch_cfg<MODE, NITER, true, true, false>(g, s);
 }
 
-hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
-                       int M, int N, int K, float alpha, float beta, int iters, int mode,
-                       hipStream_t s, int batch, long sa, long sb, long sc) {
-    const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc};
+static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStream_t s) {
     if (mode == kModeFast) return launch_layout<kModeFast, 0>(ta, tb, g, s);
     if (mode == kModeShiftAdd) return launch_layout<kModeShiftAdd, 0>(ta, tb, g, s);
     switch (g.iters) {
@@ -216,6 +227,20 @@ hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
         case 24: return launch_layout<kModeCordic, 24>(ta, tb, g, s);
         default: return launch_layout<kModeCordic, 0>(ta, tb, g, s);
     }
+}
+
+hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
+                       int M, int N, int K, float alpha, float beta, int iters, int mode,
+                       hipStream_t s, int batch, long sa, long sb, long sc) {
+    const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc,
+                     GemmEpilogue(), false};
+    return dispatch(ta, tb, mode, g, s);
+}
+
+hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
+                             const GemmEpilogue& ep, int iters, int mode, hipStream_t s) {
+    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true};
+    return dispatch(0, 1, mode, g, s);
 }
 
 }  // namespace rac

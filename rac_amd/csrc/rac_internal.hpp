@@ -21,6 +21,22 @@ struct HostConsts {
 };
 const HostConsts& host_consts();
 
+// Fused epilogue of the linear layer: v = acc (+ bias[n]); pre[m, n] = v when
+// pre != null; C = act(v) with the activation ids of rac_act.hpp; khinv is
+// 1/K_h of the SiLU's CORDIC exp at the launch's iteration count.
+struct GemmEpilogue {
+    const float* bias = nullptr;
+    float* pre = nullptr;
+    int act = 0;
+    float khinv = 0.0f;
+};
+// C[M,N] = act(A[M,K] W[N,K]^T + bias) in one launch.
+hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
+                             const GemmEpilogue& ep, int iters, int mode, hipStream_t s);
+// d[i] = g[i] * act'(pre[i]) (rac_torch.cu:680-694).
+hipError_t act_grad_launch(const float* g, const float* pre, float* d, long count, int act, int iters,
+                           hipStream_t s);
+
 // batch > 1: C_z = alpha op(A_z) op(B_z) + beta C_z for z < batch, with
 // A_z = A + z*sa, B_z = B + z*sb, C_z = C + z*sc (element strides).
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,

@@ -98,6 +98,22 @@ def _gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, M: int, N: int, K: 
     check(rc, "rac_gemm_dev")
 
 
+def _bias_f32(bias: torch.Tensor, n: int) -> torch.Tensor:
+    _require_f32(bias, "bias")
+    if bias.numel() != n:
+        raise RuntimeError("RAC: bias must have out_features elements")
+    return bias.contiguous()
+
+
+def _fused(x2: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor,
+           pre: Optional[torch.Tensor], M: int, N: int, K: int, act: int, iters: int, mode: int) -> None:
+    check(_lib.load().rac_fused_linear_dev(x2.data_ptr(), w.data_ptr(),
+                                           bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                                           pre.data_ptr() if pre is not None else None, M, N, K, act,
+                                           iters, mode, _stream(out)),
+          "rac_fused_linear_dev")
+
+
 # ── reference surface (rac_torch_bind.cpp:68-199) ─────────────────────────
 
 def matmul_forward(A: torch.Tensor, B: torch.Tensor, iters: int = 0, mode: int = -1) -> torch.Tensor:
@@ -165,10 +181,16 @@ def linear_forward(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
     M = x2.size(0)
     out = torch.empty((M, out_features), device=x2.device, dtype=torch.float32)
     iters, mode = _resolve(iters, mode)
-    if M > 0:
+    has_bias = bias is not None and bias.numel() > 0
+    if M > 0 and in_features == 0:
+        out.zero_()
+        if has_bias:
+            out.add_(bias)
+    elif M > 0 and has_bias:
+        # bias added in the GEMM epilogue (same rounding as a separate add)
+        _fused(x2, w, _bias_f32(bias, out_features), out, None, M, out_features, in_features, 0, iters, mode)
+    elif M > 0:
         _gemm(x2, w, out, M, out_features, in_features, 0, 1, iters, mode)
-    if bias is not None and bias.numel() > 0:
-        out.add_(bias)
     in_shape[-1] = out_features
     res = out.reshape(in_shape)
     if orig_dtype != torch.float32:
@@ -199,6 +221,98 @@ def linear_backward(grad_output: torch.Tensor, input: torch.Tensor, weight: torc
     shape = list(input.shape)
     shape[-1] = in_features
     return [grad_input.reshape(shape), grad_weight, grad_bias]
+
+
+def fused_linear_forward(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, act: int = 0,
+                         iters: int = 0, mode: int = -1, return_pre: bool = False):
+    """output = act(input @ weight^T + bias) in one kernel (rac_torch.cu:1037-1083):
+    act 0 none, 1 ReLU, 2 GELU, 3 SiLU (CORDIC exp).  fp16/bf16 promoted to
+    fp32 and cast back; an empty bias tensor means no bias.  With
+    return_pre, also returns the fp32 pre-activation written by the same
+    kernel (the reference recomputes it with a second matmul)."""
+    _require_gpu(input, "input")
+    if not 0 <= int(act) <= 3:
+        raise RuntimeError("RAC: act must be 0(none), 1(relu), 2(gelu), 3(silu)")
+    orig_dtype = input.dtype
+    if orig_dtype != torch.float32:
+        input = input.to(torch.float32)
+        weight = weight.to(torch.float32)
+        if bias is not None and bias.numel() > 0:
+            bias = bias.to(torch.float32)
+    in_shape = list(input.shape)
+    out_features, in_features = weight.shape
+    if in_shape[-1] != in_features:
+        raise RuntimeError("RAC: dimension mismatch")
+    x2 = input.reshape(-1, in_features).contiguous()
+    w = weight.contiguous()
+    _require_f32(w, "weight")
+    M = x2.size(0)
+    b = _bias_f32(bias, out_features) if bias is not None and bias.numel() > 0 else None
+    out = torch.empty((M, out_features), device=x2.device, dtype=torch.float32)
+    pre = torch.empty_like(out) if return_pre else None
+    iters, mode = _resolve(iters, mode)
+    if M > 0:
+        if in_features == 0:
+            # no products: pre = bias (or 0), out = act(pre)
+            p0 = torch.zeros_like(out) if b is None else b.expand(M, out_features).contiguous()
+            if pre is not None:
+                pre.copy_(p0)
+            act = int(act)
+            out.copy_(relu(p0) if act == 1 else gelu(p0) if act == 2 else silu(p0, iters) if act == 3 else p0)
+        else:
+            _fused(x2, w, b, out, pre, M, out_features, in_features, int(act), iters, mode)
+    in_shape[-1] = out_features
+    res = out.reshape(in_shape)
+    if orig_dtype != torch.float32:
+        res = res.to(orig_dtype)
+    if return_pre:
+        return res, pre.reshape(in_shape)
+    return res
+
+
+def fused_linear_backward(grad_output: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
+                          bias: torch.Tensor, pre_act: torch.Tensor, act: int, need_bias_grad: bool,
+                          iters: int = 0, mode: int = -1) -> List[Optional[torch.Tensor]]:
+    """(rac_torch.cu:1085-1185) d = grad * act'(pre_act) in one elementwise
+    kernel, then grad_input = d @ W (NN), grad_weight = d^T @ input (TN),
+    grad_bias = d.sum(0)."""
+    _require_gpu(grad_output, "grad_output")
+    if not 0 <= int(act) <= 3:
+        raise RuntimeError("RAC: act must be 0(none), 1(relu), 2(gelu), 3(silu)")
+    orig_dtype = grad_output.dtype
+    go = grad_output.to(torch.float32).reshape(-1, weight.size(0)).contiguous()
+    pre = pre_act.to(torch.float32).reshape(-1, weight.size(0)).contiguous()
+    iters, mode = _resolve(iters, mode)
+    if int(act) > 0:
+        d = torch.empty_like(go)
+        if go.numel():
+            check(_lib.load().rac_act_grad_dev(go.data_ptr(), pre.data_ptr(), d.data_ptr(), go.numel(),
+                                               int(act), iters, _stream(d)), "rac_act_grad_dev")
+    else:
+        d = go
+    gi, gw, gb = linear_backward(d.reshape(*grad_output.shape[:-1], weight.size(0)), input.to(torch.float32),
+                                 weight.to(torch.float32), need_bias_grad, iters, mode)
+    if orig_dtype != torch.float32:
+        gi = gi.to(orig_dtype)
+        gw = gw.to(orig_dtype)
+        if gb is not None:
+            gb = gb.to(orig_dtype)
+    return [gi, gw, gb]
+
+
+def act_grad(grad: torch.Tensor, pre: torch.Tensor, act: int, iters: int = 0) -> torch.Tensor:
+    """grad * act'(pre) elementwise (rac_torch.cu:680-694)."""
+    _require_f32(grad, "grad")
+    _require_f32(pre, "pre")
+    g = grad.contiguous()
+    p = pre.contiguous()
+    if g.shape != p.shape:
+        raise RuntimeError("RAC: grad and pre must have the same shape")
+    d = torch.empty_like(g)
+    if g.numel():
+        check(_lib.load().rac_act_grad_dev(g.data_ptr(), p.data_ptr(), d.data_ptr(), g.numel(), int(act),
+                                           _resolve_iters(iters), _stream(d)), "rac_act_grad_dev")
+    return d
 
 
 # ── transformer primitives on the gfx950 kernels ──────────────────────────
@@ -547,4 +661,5 @@ __all__ = [
     "softmax", "rmsnorm", "layernorm", "exp", "silu", "sigmoid", "tanh", "gelu", "relu",
     "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_",
     "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
+    "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
 ]

@@ -266,9 +266,10 @@ class RACActivationFunction(Function):
 
 
 class RACFusedLinearFunction(Function):
-    """output = act(input @ weight^T + bias) (rac_torch.py:405-496): the NT
-    kernel followed by the activation kernel; backward keeps the
-    pre-activation."""
+    """output = act(input @ weight^T + bias) (rac_torch.py:405-496) in one
+    kernel: bias and activation in the RAC GEMM's epilogue, which also
+    writes the pre-activation for backward when gradients are needed.
+    Backward: act' in one elementwise kernel, then the NN/TN RAC GEMMs."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, act_id):
@@ -276,16 +277,21 @@ class RACFusedLinearFunction(Function):
         ctx.act_id = act_id
         ctx.has_bias = bias is not None
         b = bias if bias is not None else torch.empty(0, device=input.device)
-        pre = _rac.linear_forward(input, weight, b, **_kw())
-        out = _act_forward(pre.float().contiguous(), act_id).to(input.dtype)
+        need_pre = act_id != ACT_NONE and any(ctx.needs_input_grad[:3])
+        if need_pre:
+            out, pre = _rac.fused_linear_forward(input, weight, b, act_id, return_pre=True, **_kw())
+        else:
+            out = _rac.fused_linear_forward(input, weight, b, act_id, **_kw())
+            pre = out
         ctx.save_for_backward(input, weight, bias, pre)
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
         input, weight, bias, pre = ctx.saved_tensors
-        d_act = _act_backward(grad_output.float(), pre.float(), ctx.act_id)
-        gi, gw, gb = _rac.linear_backward(d_act.contiguous(), input, weight, ctx.has_bias, **_kw())
+        b = bias if bias is not None else torch.empty(0, device=input.device)
+        gi, gw, gb = _rac.fused_linear_backward(grad_output.contiguous(), input, weight, b, pre, ctx.act_id,
+                                                ctx.has_bias, **_kw())
         grad_input = gi.to(input.dtype) if ctx.needs_input_grad[0] else None
         grad_weight = gw.to(weight.dtype) if ctx.needs_input_grad[1] else None
         grad_bias = gb.to(bias.dtype) if ctx.has_bias else None
