@@ -32,6 +32,33 @@ __device__ __forceinline__ float elt(float x, int iters, float khinv) {
     }
 }
 
+// elt<OP, NITER> on E values at once: for the exp-based ops with a
+// compile-time step count the E exps run step-major (exp_cordic_vec);
+// bit-identical to E calls of elt<OP, NITER>.
+template <int OP, int NITER, int E>
+__device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
+    if constexpr (NITER > 0 && (OP == kEltExp || OP == kEltSilu || OP == kEltSigmoid || OP == kEltTanh)) {
+        float a[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            if constexpr (OP == kEltExp) a[e] = v[e];
+            else if constexpr (OP == kEltTanh) a[e] = -2.0f * __builtin_fabsf(v[e]);
+            else a[e] = -v[e];
+        }
+        exp_cordic_vec<NITER, E>(a, khinv);
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            if constexpr (OP == kEltExp) v[e] = a[e];
+            else if constexpr (OP == kEltSilu) v[e] = v[e] / (1.0f + a[e]);
+            else if constexpr (OP == kEltSigmoid) v[e] = 1.0f / (1.0f + a[e]);
+            else v[e] = __builtin_copysignf((1.0f - a[e]) / (1.0f + a[e]), v[e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; e++) v[e] = elt<OP, NITER>(v[e], iters, khinv);
+    }
+}
+
 // Activation ids of the fused linear path (rac_torch.cu:669-675):
 // 0 identity, 1 ReLU, 2 GELU (exact erf), 3 SiLU (CORDIC exp).
 constexpr int kActNone = 0, kActRelu = 1, kActGelu = 2, kActSilu = 3;

@@ -17,18 +17,22 @@ namespace rac {
 
 // ── elementwise ──────────────────────────────────────────────────────────
 
+// Two float4 per lane per trip (i and i + stride, both coalesced across
+// the grid), so eight CORDIC chains interleave; the second slot past the
+// end computes on zeros and is not stored.
 template <int OP, int NITER>
 __global__ __launch_bounds__(256) void eltwise_vec_kernel(
     const float4* __restrict__ x, float4* __restrict__ y, long n4, int iters, float khinv)
 {
     const long stride = (long)gridDim.x * blockDim.x;
-    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 v = ld4_stream(&x[i]);
-        v.x = elt<OP, NITER>(v.x, iters, khinv);
-        v.y = elt<OP, NITER>(v.y, iters, khinv);
-        v.z = elt<OP, NITER>(v.z, iters, khinv);
-        v.w = elt<OP, NITER>(v.w, iters, khinv);
-        st4_stream(&y[i], v);
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += 2 * stride) {
+        const long j = i + stride;
+        const float4 a = ld4_stream(&x[i]);
+        const float4 b = (j < n4) ? ld4_stream(&x[j]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        elt_vec<OP, NITER, 8>(v, iters, khinv);
+        st4_stream(&y[i], make_float4(v[0], v[1], v[2], v[3]));
+        if (j < n4) st4_stream(&y[j], make_float4(v[4], v[5], v[6], v[7]));
     }
 }
 

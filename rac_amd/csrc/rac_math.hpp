@@ -191,6 +191,43 @@ __device__ __forceinline__ float exp_cordic(float x, float khinv) {
     return (x != x) ? x : res;
 }
 
+// The same exp on E independent arguments, step-major: step J is applied to
+// all E registers before step J+1, so the E dependency chains interleave
+// and each step's constants are materialised once.  Bit-identical to E
+// calls of exp_cordic<N>.
+template <int N, int J, int E>
+struct HypStepV {
+    __device__ __forceinline__ static void run(float* p, float* z) {
+        constexpr float S = hyp_S(J);
+        constexpr float C = hyp_C(J);
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const float ds = __builtin_copysignf(S, z[e]);
+            p[e] = __builtin_fmaf(ds, p[e], p[e]);
+            if constexpr (J + 1 < N) z[e] = __builtin_fmaf(-ds, C, z[e]);
+        }
+        if constexpr (J + 1 < N) HypStepV<N, J + 1, E>::run(p, z);
+    }
+};
+
+template <int N, int E>
+__device__ __forceinline__ void exp_cordic_vec(float* x, float khinv) {
+    static_assert(N >= 1 && N <= kMaxIters, "iteration count");
+    int k[E];
+    float p[E], z[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        exp_reduce(x[e], k[e], z[e]);
+        p[e] = 1.0f;
+    }
+    HypStepV<N, 0, E>::run(p, z);
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const float res = exp_scale(p[e] * khinv, k[e]);
+        x[e] = (x[e] != x[e]) ? x[e] : res;
+    }
+}
+
 __device__ __forceinline__ float exp_cordic_rt(float x, int n, float khinv) {
     int k;
     float r;

@@ -80,7 +80,28 @@ __device__ __forceinline__ float inv_sum(float s, int zero_guard) {
     return (zero_guard && !(s > 0.0f)) ? 0.0f : 1.0f / s;
 }
 
-template <int VPT, int NITER, bool MASKED>
+// Exps of the E = 4*VPT row elements a lane holds.  Compile-time step
+// counts use the step-major form (all elements advance one step at a time:
+// independent chains interleave and constants are shared); bit-identical
+// to one exp_cordic call per element.
+template <int NITER, int E>
+__device__ __forceinline__ void exp_lane(float* v, int iters, float khinv) {
+    if constexpr (NITER > 0) {
+        constexpr int G = E < 16 ? E : 16;
+#pragma unroll
+        for (int b = 0; b < E; b += G) exp_cordic_vec<NITER, G>(v + b, khinv);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; e++) v[e] = exp_cordic_rt(v[e], iters, khinv);
+    }
+}
+
+// The row is read once into registers (16-byte loads), reduced, exponentiated
+// and written once.  Lanes past the row end hold -inf, whose exp is +0, so
+// the max, the lane sums (s + 0 == s) and the output are those of the
+// elements that exist.
+// FULL: n == 1024 * VPT exactly, so no lane needs a bounds check.
+template <int VPT, int NITER, bool MASKED, bool FULL>
 __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     const float* x, float* y, long n, int iters, float khinv,
     SoftmaxMask mk)
@@ -90,53 +111,45 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     const float4* xr = reinterpret_cast<const float4*>(x + row * n);
     float4* yr = reinterpret_cast<float4*>(y + row * n);
     const long n4 = n / 4;
-    float4 v[VPT];
-    float m = -__builtin_inff();
+    constexpr int E = 4 * VPT;
+    float v[E];
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const long idx = threadIdx.x + (long)i * kRowThreads;
-        if (idx < n4) v[i] = ld4_stream(&xr[idx]);
-        else v[i] = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+        float4 t = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+        if (FULL || idx < n4) t = ld4_stream(&xr[idx]);
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
     if constexpr (MASKED) {
         const long t = row % mk.seq;
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const long idx = threadIdx.x + (long)i * kRowThreads;
-            if (idx < n4) {
-                v[i].x = mask_score(v[i].x, t, 4 * idx + 0, mk);
-                v[i].y = mask_score(v[i].y, t, 4 * idx + 1, mk);
-                v[i].z = mask_score(v[i].z, t, 4 * idx + 2, mk);
-                v[i].w = mask_score(v[i].w, t, 4 * idx + 3, mk);
+            if (FULL || idx < n4) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[4 * i + c] = mask_score(v[4 * i + c], t, 4 * idx + c, mk);
             }
         }
     }
+    float m = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < VPT; i++) m = fmaxf(fmaxf(fmaxf(m, v[i].x), fmaxf(v[i].y, v[i].z)), v[i].w);
+    for (int i = 0; i < VPT; i++)
+        m = fmaxf(fmaxf(fmaxf(m, v[4 * i]), fmaxf(v[4 * i + 1], v[4 * i + 2])), v[4 * i + 3]);
     m = block_max(m, red);
+#pragma unroll
+    for (int e = 0; e < E; e++) v[e] = v[e] - m;
+    exp_lane<NITER, E>(v, iters, khinv);
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-        const long idx = threadIdx.x + (long)i * kRowThreads;
-        if (idx < n4) {
-            v[i].x = exp_n<NITER>(v[i].x - m, iters, khinv);
-            v[i].y = exp_n<NITER>(v[i].y - m, iters, khinv);
-            v[i].z = exp_n<NITER>(v[i].z - m, iters, khinv);
-            v[i].w = exp_n<NITER>(v[i].w - m, iters, khinv);
-            s += v[i].x;
-            s += v[i].y;
-            s += v[i].z;
-            s += v[i].w;
-        }
-    }
+    for (int e = 0; e < E; e++) s += v[e];
     s = block_sum(s, red);
     const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const long idx = threadIdx.x + (long)i * kRowThreads;
-        if (idx < n4) {
+        if (FULL || idx < n4) {
             float4 o;
-            o.x = v[i].x * inv; o.y = v[i].y * inv; o.z = v[i].z * inv; o.w = v[i].w * inv;
+            o.x = v[4 * i] * inv; o.y = v[4 * i + 1] * inv; o.z = v[4 * i + 2] * inv; o.w = v[4 * i + 3] * inv;
             st4_stream(&yr[idx], o);
         }
     }
@@ -172,6 +185,17 @@ __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
     for (long i = threadIdx.x; i < n; i += kRowThreads) yr[i] = yr[i] * inv;
 }
 
+template <int VPT, int NITER, bool MASKED>
+static void softmax_reg_launch(dim3 grid, hipStream_t s, const float* x, float* y, long n, int iters,
+                               float khinv, const SoftmaxMask& mk) {
+    if (n == 4L * VPT * kRowThreads)
+        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, true>), grid, dim3(kRowThreads), 0, s, x, y,
+                           n, iters, khinv, mk);
+    else
+        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, false>), grid, dim3(kRowThreads), 0, s, x,
+                           y, n, iters, khinv, mk);
+}
+
 template <int NITER, bool MASKED>
 static hipError_t softmax_dispatch(const float* x, float* y, long rows, long n, int iters,
                                    float khinv, hipStream_t s, const SoftmaxMask& mk) {
@@ -180,15 +204,15 @@ static hipError_t softmax_dispatch(const float* x, float* y, long rows, long n, 
     const long n4 = n / 4;
     dim3 grid((unsigned)rows), block(kRowThreads);
     if (vec_ok && n4 <= 1 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<1, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
+        softmax_reg_launch<1, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 2 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<2, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
+        softmax_reg_launch<2, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 4 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<4, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
+        softmax_reg_launch<4, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 8 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<8, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
+        softmax_reg_launch<8, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 16 * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<16, NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
+        softmax_reg_launch<16, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else
         hipLaunchKernelGGL((softmax_loop_kernel<NITER, MASKED>), grid, block, 0, s, x, y, n, iters, khinv, mk);
     return hipGetLastError();
