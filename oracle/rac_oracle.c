@@ -958,3 +958,146 @@ ORC_API int orc_attention(const float *q, const float *k, const float *v, const 
     free(sc);
     return 0;
 }
+
+/* ── Q8_0 weights and the decode GEMV (lib/c/rac_q8_0.h:35-100) ──────────
+ * Block: uint16 fp16 scale d, then 32 int8 q (34 bytes, packed, little
+ * endian); value = fp16_to_fp32(d) * q. */
+
+#define ORC_Q8_BLOCK 32
+#define ORC_Q8_BYTES 34
+
+/* rac_fp16_to_fp32, rac_q8_0.c:21-45 (exact; subnormal halves normalised). */
+ORC_API float orc_fp16_to_fp32(uint16_t h)
+{
+    uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1fu, mant = h & 0x3ffu, bits;
+    if (ex == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            int e = -14;
+            while ((mant & 0x400u) == 0) { mant <<= 1; e--; }
+            mant &= 0x3ffu;
+            bits = (sign << 31) | ((uint32_t)(e + 127) << 23) | (mant << 13);
+        }
+    } else if (ex == 31) {
+        bits = (sign << 31) | (0xffu << 23) | (mant << 13);
+    } else {
+        bits = (sign << 31) | ((ex - 15 + 127) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* rac_fp32_to_fp16, rac_q8_0.c:47-64: mantissa TRUNCATED (no rounding),
+ * exponents below the half range flush to signed zero, above to inf. */
+ORC_API uint16_t orc_fp32_to_fp16(float f)
+{
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    uint32_t sign = (b >> 16) & 0x8000u;
+    int32_t ex = (int32_t)((b >> 23) & 0xffu) - 127 + 15;
+    uint32_t mant = b & 0x7fffffu;
+    if (ex <= 0) {
+        if (ex < -10) return (uint16_t)sign;
+        mant = (mant | 0x800000u) >> (1 - ex);
+        return (uint16_t)(sign | (mant >> 13));
+    }
+    if (ex >= 31) return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0u));
+    return (uint16_t)(sign | ((uint32_t)ex << 10) | (mant >> 13));
+}
+
+/* rac_q8_0_quantize_row / _matrix, rac_q8_0.c:68-100: per block amax,
+ * d = amax / 127, id = 1/d (0 when d == 0), q = lrintf(x * id) clamped to
+ * [-127, 127]; d stored through orc_fp32_to_fp16. */
+ORC_API void orc_q8_0_quantize(const float *src, uint8_t *dst, long rows, int K)
+{
+    const int nb = K / ORC_Q8_BLOCK;
+    for (long r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const float *blk = src + (size_t)r * K + (size_t)b * ORC_Q8_BLOCK;
+            uint8_t *o = dst + ((size_t)r * nb + b) * ORC_Q8_BYTES;
+            float amax = 0.0f;
+            for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+                float a = fabsf(blk[i]);
+                if (a > amax) amax = a;
+            }
+            float d = amax / 127.0f;
+            float id = (d > 0.0f) ? 1.0f / d : 0.0f;
+            uint16_t h = orc_fp32_to_fp16(d);
+            o[0] = (uint8_t)(h & 0xff);
+            o[1] = (uint8_t)(h >> 8);
+            for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+                int q = (int)lrintf(blk[i] * id);
+                if (q < -127) q = -127;
+                if (q > 127) q = 127;
+                o[2 + i] = (uint8_t)(int8_t)q;
+            }
+        }
+}
+
+/* rac_q8_0_dequantize_row, rac_q8_0.c:102-111. */
+ORC_API void orc_q8_0_dequantize(const uint8_t *src, float *dst, long rows, int K)
+{
+    const long nblk = rows * (long)(K / ORC_Q8_BLOCK);
+    for (long b = 0; b < nblk; b++) {
+        const uint8_t *blk = src + (size_t)b * ORC_Q8_BYTES;
+        float d = orc_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int i = 0; i < ORC_Q8_BLOCK; i++)
+            dst[(size_t)b * ORC_Q8_BLOCK + i] = d * (float)(int8_t)blk[2 + i];
+    }
+}
+
+/* One block's dot product in the order of the AVX2 kernel
+ * (rac_q8_0.c:128-165): lane l of 8 accumulates q[l] x[l] (a product),
+ * then fma with q[8+l] x[8+l], q[16+l] x[16+l], q[24+l] x[24+l]; the 8 lane
+ * sums combine as ((a0+a4) + (a1+a5)) + ((a2+a6) + (a3+a7)). */
+ORC_API float orc_q8_0_block_dot(const uint8_t *blk, const float *x)
+{
+    const int8_t *q = (const int8_t *)(blk + 2);
+    float a[8];
+    for (int l = 0; l < 8; l++) {
+        float s = (float)q[l] * x[l];
+        s = fmaf((float)q[8 + l], x[8 + l], s);
+        s = fmaf((float)q[16 + l], x[16 + l], s);
+        s = fmaf((float)q[24 + l], x[24 + l], s);
+        a[l] = s;
+    }
+    float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* rac_q8_0_gemv, rac_q8_0.c:178-211, for M input rows: out[m][j] =
+ * act(sum_b d_b dot_b + bias[j]) with the block terms accumulated in block
+ * order as acc = fmaf(d_b, dot_b, acc) (the reference build contracts
+ * `acc += d * dot`; contract = 0 gives the unfused form).  act: 0 none,
+ * 1 ReLU, 2 GELU (erff), 3 SiLU (expf), as rac_q8_0.c:167-174. */
+ORC_API int orc_q8_0_gemv(const float *x, const uint8_t *w, const float *bias, float *out,
+                          int M, int N, int K, int act, int contract)
+{
+    if (!x || !w || !out) return -1;
+    if (M <= 0 || N <= 0 || K <= 0 || K % ORC_Q8_BLOCK) return -2;
+    const int nb = K / ORC_Q8_BLOCK;
+    #pragma omp parallel for schedule(static)
+    for (long t = 0; t < (long)M * N; t++) {
+        const int m = (int)(t / N), j = (int)(t % N);
+        const uint8_t *row = w + (size_t)j * nb * ORC_Q8_BYTES;
+        float acc = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *blk = row + (size_t)b * ORC_Q8_BYTES;
+            float dot = orc_q8_0_block_dot(blk, x + (size_t)m * K + (size_t)b * ORC_Q8_BLOCK);
+            float d = orc_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+            acc = contract ? fmaf(d, dot, acc) : acc + d * dot;
+        }
+        if (bias) acc += bias[j];
+        float s = acc;
+        switch (act) {
+        case 1: s = s > 0.0f ? s : 0.0f; break;
+        case 2: s = 0.5f * s * (1.0f + erff(s * 0.7071067811865f)); break;
+        case 3: s = s / (1.0f + expf(-s)); break;
+        default: break;
+        }
+        out[t] = s;
+    }
+    return 0;
+}

@@ -63,6 +63,15 @@ _SIGNATURES = {
     "rac_dct_dev": (_i, [_vp, _vp, _i, _vp]),
     "rac_attention_workspace_bytes": (_l, [_i, _i, _i]),
     "rac_attention_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
+    "rac_q8_0_gemv_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rac_q8_0_quantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_q8_0_dequantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_q8_0_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "rac_q8_0_quantize_row": (None, [_vp, _vp, _i]),
+    "rac_q8_0_quantize_matrix": (None, [_vp, _vp, _i, _i]),
+    "rac_q8_0_dequantize_row": (None, [_vp, _vp, _i]),
+    "rac_fp16_to_fp32": (_f, [ctypes.c_uint16]),
+    "rac_fp32_to_fp16": (ctypes.c_uint16, [_f]),
     "rac_last_error": (ctypes.c_char_p, []),
     "rac_clear_error": (None, []),
     "rac_set_cordic_iters": (None, [_i]),

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -515,6 +516,43 @@ RAC_EXPORT int rac_attention_dev(const float* q, const float* k, const float* v,
                             clamp_iters(iters), mode, (hipStream_t)stream);
 }
 
+// ── Q8_0 weights and decode GEMV (lib/c/rac_q8_0.h) ─────────────────────
+
+static int check_q8(const char* who, const void* a, const void* b, long rows, long K) {
+    if (!a || !b) return fail(RAC_ERR_NULL_PTR, "%s: null buffer", who);
+    if (rows <= 0 || K <= 0 || K % 32) return fail(RAC_ERR_INVALID_DIM, "%s: rows > 0 and K a positive multiple of 32 required", who);
+    if (rows * (K / 32) > 2147483647L * 128L) return fail(RAC_ERR_INVALID_DIM, "%s: too many blocks", who);
+    return RAC_OK;
+}
+
+RAC_EXPORT int rac_q8_0_gemv_dev(const float* x, const void* weight, const float* bias, float* out, int M, int N,
+                                 int K, int act, void* stream) {
+    int rc = check_q8("rac_q8_0_gemv_dev", x, weight, N, K);
+    if (rc) return rc;
+    if (!out) return fail(RAC_ERR_NULL_PTR, "rac_q8_0_gemv_dev: null output");
+    if (M <= 0) return fail(RAC_ERR_INVALID_DIM, "rac_q8_0_gemv_dev: M must be > 0");
+    if (act < 0 || act > 3) return fail(RAC_ERR_INVALID_DIM, "rac_q8_0_gemv_dev: act must be 0..3");
+    if ((long)M * N > 2147483647L * 2L) return fail(RAC_ERR_INVALID_DIM, "rac_q8_0_gemv_dev: M*N too large");
+    return check_hip(q8_gemv_launch(x, static_cast<const uint8_t*>(weight), bias, out, M, N, K, act,
+                                    (hipStream_t)stream),
+                     "rac_q8_0_gemv_dev launch");
+}
+
+RAC_EXPORT int rac_q8_0_quantize_dev(const float* src, void* dst, long rows, int K, void* stream) {
+    int rc = check_q8("rac_q8_0_quantize_dev", src, dst, rows, K);
+    if (rc) return rc;
+    return check_hip(q8_quantize_launch(src, static_cast<uint8_t*>(dst), rows * (K / 32), (hipStream_t)stream),
+                     "rac_q8_0_quantize_dev launch");
+}
+
+RAC_EXPORT int rac_q8_0_dequantize_dev(const void* src, float* dst, long rows, int K, void* stream) {
+    int rc = check_q8("rac_q8_0_dequantize_dev", src, dst, rows, K);
+    if (rc) return rc;
+    return check_hip(q8_dequantize_launch(static_cast<const uint8_t*>(src), dst, rows * (K / 32),
+                                          (hipStream_t)stream),
+                     "rac_q8_0_dequantize_dev launch");
+}
+
 // ═════════════════ reference launcher ABI (rac_kernels.hip) ═══════════════
 
 RAC_EXPORT void rac_launch_nn_iters(const float* A, const float* B, float* C, int M, int N, int K,
@@ -834,6 +872,95 @@ RAC_EXPORT void rac_attention(const float* q, const float* k, const float* v, co
                                    head_dim, ws.f(), rac_get_cordic_iters(), rac_get_cordic_mode(), s);
     if (!rc) rc = so.copy_out(s);
     (void)finish_sync(s, rc);
+}
+
+// ── Q8_0 with the rac_q8_0.h signatures (host or device buffers) ────────
+
+// rac_fp16_to_fp32 / rac_fp32_to_fp16 (rac_q8_0.h:47-48): scalar format
+// helpers of the block layout, evaluated on the host.
+RAC_EXPORT float rac_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1fu;
+    uint32_t mant = h & 0x3ffu, bits;
+    if (ex == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            int e = -14;
+            while ((mant & 0x400u) == 0) { mant <<= 1; e--; }
+            mant &= 0x3ffu;
+            bits = (sign << 31) | ((uint32_t)(e + 127) << 23) | (mant << 13);
+        }
+    } else if (ex == 31) {
+        bits = (sign << 31) | (0xffu << 23) | (mant << 13);
+    } else {
+        bits = (sign << 31) | ((ex - 15 + 127) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+RAC_EXPORT uint16_t rac_fp32_to_fp16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const int ex = (int)((b >> 23) & 0xffu) - 127 + 15;
+    uint32_t mant = b & 0x7fffffu;
+    if (ex <= 0) {
+        if (ex < -10) return (uint16_t)sign;
+        mant = (mant | 0x800000u) >> (1 - ex);
+        return (uint16_t)(sign | (mant >> 13));
+    }
+    if (ex >= 31) return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0u));
+    return (uint16_t)(sign | ((uint32_t)ex << 10) | (mant >> 13));
+}
+
+static void q8_quantize_sync(const char* who, const float* src, void* dst, long rows, int K) {
+    if (check_q8(who, src, dst, rows, K)) return;
+    hipStream_t s = g_stream.load();
+    const long nblk = rows * (K / 32);
+    Staged a, b;
+    int rc = a.bind(src, sizeof(float) * (size_t)rows * K, true, s);
+    if (!rc) rc = b.bind(dst, 34 * (size_t)nblk, false, s);
+    if (!rc) rc = check_hip(q8_quantize_launch(a.f(), static_cast<uint8_t*>(b.dev), nblk, s), who);
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+RAC_EXPORT void rac_q8_0_quantize_row(const float* src, void* dst, int N) {
+    q8_quantize_sync("rac_q8_0_quantize_row", src, dst, 1, N);
+}
+RAC_EXPORT void rac_q8_0_quantize_matrix(const float* src, void* dst, int rows, int K) {
+    q8_quantize_sync("rac_q8_0_quantize_matrix", src, dst, rows, K);
+}
+
+RAC_EXPORT void rac_q8_0_dequantize_row(const void* src, float* dst, int N) {
+    if (check_q8("rac_q8_0_dequantize_row", src, dst, 1, N)) return;
+    hipStream_t s = g_stream.load();
+    Staged a, b;
+    int rc = a.bind(src, 34 * (size_t)(N / 32), true, s);
+    if (!rc) rc = b.bind(dst, sizeof(float) * (size_t)N, false, s);
+    if (!rc) rc = check_hip(q8_dequantize_launch(static_cast<const uint8_t*>(a.dev), b.f(), N / 32, s),
+                            "rac_q8_0_dequantize_row launch");
+    if (!rc) rc = b.copy_out(s);
+    (void)finish_sync(s, rc);
+}
+
+// rac_q8_0_gemv (rac_q8_0.h:94-100): returns the rac_status code.
+RAC_EXPORT int rac_q8_0_gemv(const float* input, const void* weight, const float* bias, float* output, int N,
+                             int K, int act) {
+    int rc = check_q8("rac_q8_0_gemv", input, weight, N, K);
+    if (rc) return rc;
+    if (!output) return fail(RAC_ERR_NULL_PTR, "rac_q8_0_gemv: null output");
+    hipStream_t s = g_stream.load();
+    Staged a, w, bb, o;
+    rc = a.bind(input, sizeof(float) * (size_t)K, true, s);
+    if (!rc) rc = w.bind(weight, 34 * (size_t)N * (K / 32), true, s);
+    if (!rc) rc = bb.bind(bias, sizeof(float) * (size_t)N, true, s);
+    if (!rc) rc = o.bind(output, sizeof(float) * (size_t)N, false, s);
+    if (!rc) rc = rac_q8_0_gemv_dev(a.f(), w.dev, bb.f(), o.f(), 1, N, K, act, s);
+    if (!rc) rc = o.copy_out(s);
+    return finish_sync(s, rc);
 }
 
 // ── context (rac.h:85-88; the reference's HIP backend is a stub,

@@ -81,6 +81,12 @@ hipError_t prim_launch(int op, long n, const float2* a, const float2* b, const f
 hipError_t outer_launch(const float2* a, const float2* b, float* C, int m, int n, hipStream_t s);
 hipError_t dct_launch(const float* x, float* X, int n, hipStream_t s);
 hipError_t inner_launch(const float2* a, const float2* b, long n, float* out, hipStream_t s);
+// Q8_0 (34-byte blocks of 32 int8 + fp16 scale): out[M,N] = act(x[M,K] W^T
+// + bias), W [N, K/32] blocks; quantize / dequantize nblocks blocks.
+hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, float* out, int M, int N,
+                          int K, int act, hipStream_t s);
+hipError_t q8_quantize_launch(const float* src, uint8_t* dst, long nblocks, hipStream_t s);
+hipError_t q8_dequantize_launch(const uint8_t* src, float* dst, long nblocks, hipStream_t s);
 hipError_t sincos_launch(const float* theta, float* s_out, float* c_out, long count,
                          hipStream_t s);
 

@@ -654,6 +654,68 @@ def dct(x: torch.Tensor) -> torch.Tensor:
     return X
 
 
+# ── Q8_0 weights and decode GEMV (lib/c/rac_q8_0.h) ─────────────────────────
+
+Q8_BLOCK_BYTES = 34
+
+
+def q8_quantize(w: torch.Tensor) -> torch.Tensor:
+    """fp32 [rows, K] -> Q8_0 blocks as a uint8 tensor [rows, K/32, 34]
+    (rac_q8_0.c:68-100: per-block amax/127 scale in fp16, int8 lrintf)."""
+    _require_f32(w, "w")
+    if w.dim() != 2 or w.size(1) % 32:
+        raise RuntimeError("RAC: q8_quantize expects [rows, K] with K % 32 == 0")
+    w = w.contiguous()
+    rows, K = w.shape
+    out = torch.empty((rows, K // 32, Q8_BLOCK_BYTES), device=w.device, dtype=torch.uint8)
+    if rows:
+        check(_lib.load().rac_q8_0_quantize_dev(w.data_ptr(), out.data_ptr(), rows, K, _stream(out)),
+              "rac_q8_0_quantize_dev")
+    return out
+
+
+def q8_dequantize(wq: torch.Tensor) -> torch.Tensor:
+    """Q8_0 blocks [rows, K/32, 34] -> fp32 [rows, K]."""
+    _require_gpu(wq, "wq")
+    if wq.dtype != torch.uint8 or wq.dim() != 3 or wq.size(2) != Q8_BLOCK_BYTES:
+        raise RuntimeError("RAC: Q8_0 weights must be a uint8 [rows, K/32, 34] tensor")
+    wq = wq.contiguous()
+    rows, nb = wq.shape[0], wq.shape[1]
+    out = torch.empty((rows, nb * 32), device=wq.device, dtype=torch.float32)
+    if rows and nb:
+        check(_lib.load().rac_q8_0_dequantize_dev(wq.data_ptr(), out.data_ptr(), rows, nb * 32, _stream(out)),
+              "rac_q8_0_dequantize_dev")
+    return out
+
+
+def q8_gemv(x: torch.Tensor, wq: torch.Tensor, bias: Optional[torch.Tensor] = None, act: int = 0) -> torch.Tensor:
+    """out[..., N] = act(x[..., K] @ W^T + bias) with W as Q8_0 blocks
+    [N, K/32, 34] (rac_q8_0.c:178-211, bit-identical to its AVX2 build for
+    act 0/1).  Leading dims of x are decode rows (the weights stream once
+    per 16 rows)."""
+    _require_f32(x, "x")
+    _require_gpu(wq, "wq")
+    if wq.dtype != torch.uint8 or wq.dim() != 3 or wq.size(2) != Q8_BLOCK_BYTES:
+        raise RuntimeError("RAC: Q8_0 weights must be a uint8 [N, K/32, 34] tensor")
+    N, K = wq.size(0), wq.size(1) * 32
+    if x.size(-1) != K:
+        raise RuntimeError("RAC: dimension mismatch")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K).contiguous()
+    wq = wq.contiguous()
+    b = None
+    if bias is not None:
+        b = _bias_f32(bias, N)
+    out = torch.empty((x2.size(0), N), device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    for m0 in range(0, x2.size(0), 16):
+        mm = min(16, x2.size(0) - m0)
+        check(lib.rac_q8_0_gemv_dev(x2[m0].data_ptr(), wq.data_ptr(), b.data_ptr() if b is not None else None,
+                                    out[m0].data_ptr(), mm, N, K, int(act), _stream(out)),
+              "rac_q8_0_gemv_dev")
+    return out.reshape(*lead, N)
+
+
 __all__ = [
     "MODE_FAST", "MODE_CORDIC", "MODE_SHIFTADD", "RACError",
     "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
@@ -662,4 +724,5 @@ __all__ = [
     "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_",
     "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
     "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
+    "q8_quantize", "q8_dequantize", "q8_gemv", "Q8_BLOCK_BYTES",
 ]

@@ -7,7 +7,7 @@ oracle/ref_probe.c.  Every value below is produced by reference code; the
 inputs come from tests/raclib.py's seeded generator and are stored too, so
 the fixtures are self-contained data (nothing of the reference's source).
 
-    python tests/golden/make_golden.py [core] [prims] [attention]
+    python tests/golden/make_golden.py [core] [prims] [attention] [q8]
 
 Outputs (tests/golden/):
   tables.json            reference CORDIC tables (rac_cpu.c:20-52)
@@ -26,6 +26,9 @@ Outputs (tests/golden/):
                          rac_inner, rac_outer, rac_dct
   attention.npz          rac_scaled_dot_attention on [2,3,16,8], with and
                          without causal / additive mask
+  q8.npz                 rac_fp16_to_fp32 / rac_fp32_to_fp16 samples,
+                         rac_q8_0_quantize_matrix of a 40x512 matrix, and
+                         rac_q8_0_gemv with each activation, +- bias
 """
 from __future__ import annotations
 
@@ -51,6 +54,8 @@ def main(sections) -> None:
         write_prims(r)
     if "attention" in sections:
         write_attention(r)
+    if "q8" in sections:
+        write_q8(r)
     print("golden fixtures written to", HERE)
 
 
@@ -228,5 +233,35 @@ def write_attention(r) -> None:
     np.savez_compressed(os.path.join(HERE, "attention.npz"), q=q, k=k, v=v, mask=mask, **res)
 
 
+def write_q8(r) -> None:
+    """Q8_0 format and decode GEMV (rac_q8_0.c): fp16 conversions, quantize,
+    and rac_q8_0_gemv with each activation, bias and no bias."""
+    rng = np.random.default_rng(20261203)
+    halves = np.concatenate([np.arange(0, 65536, 7), [0x0000, 0x8000, 0x0001, 0x03ff, 0x0400, 0x7bff, 0x7c00,
+                                                       0xfc00, 0x7e00, 0x7c01]]).astype(np.uint16)
+    h2f = np.array([r.rac_fp16_to_fp32(int(h)) for h in halves], np.float32)
+    fl = np.concatenate([rng.normal(0, 1, 4000), rng.normal(0, 1e-5, 2000), rng.normal(0, 3e4, 2000),
+                         [0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e-8, 6e-8, 5.96e-8, np.inf, -np.inf,
+                          np.nan]]).astype(np.float32)
+    f2h = np.array([r.rac_fp32_to_fp16(float(v)) for v in fl], np.uint16)
+    N, K = 40, 512
+    W = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+    W[2, :32] = 0.0              # all-zero block (d = 0)
+    W[7, 100] = 40.0             # outlier
+    W[9, 64:96] = 1e-30          # underflowing scale
+    wq = np.zeros((N, K // 32, 34), np.uint8)
+    r.rac_q8_0_quantize_matrix(rl.p(W), rl.p(wq), N, K)
+    x = rng.normal(0, 1, K).astype(np.float32)
+    bias = rng.normal(0, 1, N).astype(np.float32)
+    outs = {}
+    for act in range(4):
+        for with_bias in (0, 1):
+            o = np.zeros(N, np.float32)
+            assert r.rac_q8_0_gemv(rl.p(x), rl.p(wq), rl.p(bias) if with_bias else None, rl.p(o), N, K, act) == 0
+            outs[f"out_a{act}_b{with_bias}"] = o
+    np.savez_compressed(os.path.join(HERE, "q8.npz"), halves=halves, h2f=h2f, floats=fl, f2h=f2h, W=W, wq=wq,
+                        x=x, bias=bias, **outs)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1:] or ["core", "prims", "attention"])
+    main(sys.argv[1:] or ["core", "prims", "attention", "q8"])

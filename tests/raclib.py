@@ -65,6 +65,12 @@ _ORACLE_SIGS = {
     "orc_outer": (None, [_vp, _vp, _vp, _i, _i]),
     "orc_dct": (None, [_vp, _vp, _i]),
     "orc_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i]),
+    "orc_fp16_to_fp32": (_f, [C.c_uint16]),
+    "orc_fp32_to_fp16": (C.c_uint16, [_f]),
+    "orc_q8_0_quantize": (None, [_vp, _vp, _l, _i]),
+    "orc_q8_0_dequantize": (None, [_vp, _vp, _l, _i]),
+    "orc_q8_0_block_dot": (_f, [_vp, _vp]),
+    "orc_q8_0_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "orc_check_chain_all_mantissas": (_l, [_i, _i]),
     "orc_check_projection_identity": (_l, [_i, _l, C.c_uint64]),
 }
@@ -104,6 +110,11 @@ _REF_SIGS = {
     "rac_inner": (_f, [_vp, _vp, _i]),
     "rac_outer": (None, [_vp, _vp, _vp, _i, _i]),
     "rac_scaled_dot_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "rac_fp16_to_fp32": (_f, [C.c_uint16]),
+    "rac_fp32_to_fp16": (C.c_uint16, [_f]),
+    "rac_q8_0_quantize_matrix": (None, [_vp, _vp, _i, _i]),
+    "rac_q8_0_dequantize_row": (None, [_vp, _vp, _i]),
+    "rac_q8_0_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
 }
 
 # Vector-primitive op codes shared by orc_prim and rac_vec2_dev:
@@ -291,4 +302,27 @@ def orc_attention(q, k, v, mask, causal, iters, mode):
     m = None if mask is None else np.ascontiguousarray(mask, np.float32)
     assert oracle().orc_attention(p(q), p(k), p(v), p(m) if m is not None else None, int(causal),
                                   p(out), B, H, T, D, iters, mode) == 0
+    return out
+
+
+Q8_BYTES = 34
+
+
+def orc_q8_quantize(w):
+    """[rows, K] float32 -> [rows, K/32, 34] uint8 Q8_0 blocks (oracle)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, K = w.shape
+    out = np.zeros((rows, K // 32, Q8_BYTES), np.uint8)
+    oracle().orc_q8_0_quantize(p(w), p(out), rows, K)
+    return out
+
+
+def orc_q8_gemv(x, wq, bias, act, contract=1):
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    M, K = x.shape
+    N = wq.shape[0]
+    out = np.zeros((M, N), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    assert oracle().orc_q8_0_gemv(p(x), p(np.ascontiguousarray(wq)), p(b) if b is not None else None, p(out),
+                                  M, N, K, act, contract) == 0
     return out

@@ -16,7 +16,7 @@ import pytest
 import raclib as rl
 
 ROOT = rl.ROOT
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h")]
 
 
 def declared_functions():
@@ -54,7 +54,7 @@ def test_python_binding_covers_headers():
 
 def test_headers_compile_and_link_as_c(tmp_path):
     src = tmp_path / "t.c"
-    src.write_text('#include "rac.h"\n#include "rac_ext.h"\n'
+    src.write_text('#include "rac.h"\n#include "rac_ext.h"\n#include "rac_q8_0.h"\n'
                    "int main(void){ rac_set_cordic_iters(8); return rac_get_cordic_iters() == 8 ? 0 : 1; }\n")
     exe = tmp_path / "t"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
@@ -171,3 +171,20 @@ def test_module_shapes_and_parameters():
     assert rt._resolve_act('swish') == rt.ACT_SILU
     with pytest.raises(ValueError):
         rt._resolve_act('tanhh')
+
+
+def test_fp16_helpers_match_reference_golden(lib):
+    d = np.load(os.path.join(rl.GOLDEN, "q8.npz"))
+    h2f = np.array([lib.rac_fp16_to_fp32(int(h)) for h in d["halves"]], np.float32)
+    assert np.array_equal(h2f.view(np.uint32), d["h2f"].view(np.uint32))
+    f2h = np.array([lib.rac_fp32_to_fp16(float(v)) for v in d["floats"]], np.uint16)
+    assert np.array_equal(f2h, d["f2h"])
+
+
+def test_q8_argument_errors_before_device(lib):
+    buf = (ctypes.c_float * 64)()
+    a = ctypes.addressof(buf)
+    assert lib.rac_q8_0_gemv(a, a, None, a, 4, 48, 0) == -2       # K not a multiple of 32
+    assert lib.rac_q8_0_gemv(None, a, None, a, 4, 64, 0) == -1
+    assert lib.rac_q8_0_gemv_dev(a, a, None, a, 1, 4, 64, 9, None) == -2   # act
+    assert lib.rac_q8_0_quantize_dev(a, a, 0, 64, None) == -2

@@ -26,6 +26,12 @@ exhaustive enumeration, or libm within an analytic bound.  Map:
                           bit-exact; rac_inner within its summation-order
                           bound; closed forms (hypot/atan2, exact rotation,
                           complex product, float64 DCT-II)
+  orc_fp16/fp32 convert   golden q8.npz (compiled rac_q8_0.c) bit-exact;
+                          every half round-trips; IEEE closed forms
+  orc_q8_0_quantize/gemv  golden q8.npz bit-exact (quantized blocks, GEMV
+                          outputs for each activation); dequantize error
+                          <= d/2 per weight; GEMV = float64 dot of the
+                          dequantized weights within the summation bound
   orc_attention           golden attention.npz (compiled
                           rac_scaled_dot_attention) bit-exact with expf and
                           FAST products; float64 softmax attention within the
@@ -368,7 +374,8 @@ def test_prims_batch_forms_vs_reference_golden(o):
     o.orc_outer(rl.p(np.ascontiguousarray(a[:24])), rl.p(np.ascontiguousarray(b[:40])), rl.p(outer), 24, 40)
     assert np.array_equal(outer, d["outer"])
     X = np.zeros(64, np.float32)
-    o.orc_dct(rl.p(d["dct_x"]), rl.p(X), 64)
+    dct_x = d["dct_x"]
+    o.orc_dct(rl.p(dct_x), rl.p(X), 64)
     assert np.array_equal(X, d["dct"])
     # rac_inner sums with an OpenMP reduction (order not fixed): bound by
     # n * 2^-24 * sum |term|
@@ -462,3 +469,56 @@ def test_attention_cordic_bound(o, iters, mode):
         # fraction; the CORDIC products add ~2e-5 (n >= 16) relative
         bound = 4 * (2.0 ** -last + (2e-5 if iters >= 16 else 2e-4)) * np.abs(d["v"]).max()
         assert np.max(np.abs(out - ref)) < bound
+
+
+# ── Q8_0 (lib/c/rac_q8_0.h) ─────────────────────────────────────────────────
+
+def test_fp16_conversions_vs_reference_golden(o):
+    d = npz("q8.npz")
+    h2f = np.array([o.orc_fp16_to_fp32(int(h)) for h in d["halves"]], np.float32)
+    assert np.array_equal(h2f.view(np.uint32), d["h2f"].view(np.uint32))
+    f2h = np.array([o.orc_fp32_to_fp16(float(v)) for v in d["floats"]], np.uint16)
+    assert np.array_equal(f2h, d["f2h"])
+    # closed forms: every finite half is exactly representable, so fp16 ->
+    # fp32 -> fp16 is the identity; fp16 -> fp32 equals numpy's conversion
+    hs = np.arange(65536, dtype=np.uint16)
+    fin = (hs & 0x7c00) != 0x7c00
+    f = np.array([o.orc_fp16_to_fp32(int(h)) for h in hs[fin]], np.float32)
+    assert np.array_equal(f, hs[fin].view(np.float16).astype(np.float32))
+    back = np.array([o.orc_fp32_to_fp16(float(v)) for v in f], np.uint16)
+    assert np.array_equal(back, hs[fin])
+
+
+def test_q8_quantize_and_gemv_vs_reference_golden(o):
+    d = npz("q8.npz")
+    wq = rl.orc_q8_quantize(d["W"])
+    assert np.array_equal(wq, d["wq"])
+    for act in range(4):
+        for with_bias in (0, 1):
+            out = rl.orc_q8_gemv(d["x"], wq, d["bias"] if with_bias else None, act)[0]
+            assert np.array_equal(out, d[f"out_a{act}_b{with_bias}"]), (act, with_bias)
+
+
+def test_q8_closed_forms(o):
+    rng = np.random.default_rng(5)
+    N, K = 37, 320
+    W = rng.normal(0, 1, (N, K)).astype(np.float32)
+    wq = rl.orc_q8_quantize(W)
+    deq = np.zeros((N, K), np.float32)
+    o.orc_q8_0_dequantize(rl.p(wq), rl.p(deq), N, K)
+    scale = np.array([[o.orc_fp16_to_fp32(int(b[0]) | int(b[1]) << 8) for b in row] for row in wq], np.float32)
+    # |x - d q| <= d/2 (+ the scale's truncation to fp16, < 2^-10 relative)
+    err = np.abs(W - deq).reshape(N, K // 32, 32)
+    amax = np.abs(W).reshape(N, K // 32, 32).max(-1)
+    assert np.all(err <= (0.5 * amax / 127 + amax * 2.0 ** -10)[..., None] * 1.0001)
+    assert np.array_equal(np.abs(wq[..., 2:].view(np.int8)).max(-1), np.full((N, K // 32), 127))
+    # GEMV = float64 dot of the dequantized weights, within the summation bound
+    x = rng.normal(0, 1, (3, K)).astype(np.float32)
+    out = rl.orc_q8_gemv(x, wq, None, 0)
+    ref = x.astype(np.float64) @ deq.astype(np.float64).T
+    bound = (K + 8) * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(deq).astype(np.float64).T)
+    assert np.all(np.abs(out - ref) <= bound)
+    # a zero block quantizes to d = 0, q = 0
+    Z = np.zeros((1, 64), np.float32)
+    zq = rl.orc_q8_quantize(Z)
+    assert not zq.any()
