@@ -51,7 +51,7 @@ int rac_q8_0_gemv(const float *input, const rac_q8_0_block *weight, const float 
 
 /* Device-buffer, stream-ordered forms (same conventions as rac_ext.h).
  * gemv_dev takes M input rows x[M, K] (batched decode; the weights stream
- * from HBM once for up to 16 rows) and writes out[M, N]. */
+ * from HBM once per 8 rows) and writes out[M, N]. */
 int rac_q8_0_gemv_dev(const float *x, const void *weight, const float *bias, float *out, int M,
                       int N, int K, int act, void *stream);
 int rac_q8_0_quantize_dev(const float *src, void *dst, long rows, int K, void *stream);

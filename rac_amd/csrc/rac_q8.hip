@@ -5,19 +5,11 @@
 // weights, 3.8x less than fp32).  Results are bit-identical to the
 // reference's AVX2 build (rac_q8_0.c:128-211): each block's 32 products
 // combine in the order of its 8-lane vector tree, and the block terms of a
-// row accumulate in block order as acc = fma(d_b, dot_b, acc).  That serial
-// order is kept without serialising the memory stream:
-//
-//   * a workgroup owns 64 consecutive weight rows and walks K in chunks of
-//     8 blocks (272 bytes per row, 16-byte aligned when K % 256 == 0);
-//   * each chunk is fetched with 16-byte loads (64 x 272 contiguous-row
-//     segments) into registers one chunk ahead, then written to LDS;
-//   * all 256 lanes compute the 64 x 8 block dots (per input row) from LDS;
-//   * one lane per (input row, weight row) then folds the chunk's 8 terms
-//     into its accumulator in block order.
-//
-// Shapes the fast kernel does not cover (K % 256 != 0, unaligned buffers)
-// take a generic kernel with the same arithmetic.
+// row accumulate in block order as acc = fma(d_b, dot_b, acc).  The fast
+// kernel keeps that serial order while the loads of a whole chunk (16 rows
+// x up to 128 blocks) are in flight at once; shapes it does not cover
+// (K % 256 != 0, unaligned weights) take a generic kernel with the same
+// arithmetic.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -27,11 +19,6 @@ namespace rac {
 
 constexpr int kQ8Block = 32;
 constexpr int kQ8Bytes = 34;
-constexpr int kQ8Rows = 64;                    // weight rows per workgroup
-constexpr int kQ8Chunk = 8;                    // blocks per chunk
-constexpr int kQ8Seg = kQ8Chunk * kQ8Bytes;    // 272 bytes of one row per chunk
-constexpr int kQ8Vec = kQ8Seg / 16;            // 17 16-byte vectors per segment
-constexpr int kQ8Loads = (kQ8Rows * kQ8Vec + 255) / 256;   // per lane per chunk
 
 // rac_fp16_to_fp32 (rac_q8_0.c:21-45) as bit operations.
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
@@ -99,128 +86,169 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
     }
 }
 
-// Fast path: K % 256 == 0, weights and inputs 16-byte aligned.  MG groups of
-// 4 input rows (M <= 4 * MG); lane t accumulates outputs (m, j0 + t % 64)
-// for m = t / 64 + 4 g.
-template <int MG>
+// Fast path (K % 256 == 0, 16-byte aligned buffers).  A workgroup owns
+// kQ8R = 16 consecutive weight rows and walks K in chunks of up to CB
+// blocks (64 for one input row: 16 x 2176 bytes, all requested at once, so
+// the whole chunk is in flight before any of it is used; LDS leaves room
+// for 3 workgroups per CU):
+//   1. 16-byte loads of the chunk (contiguous per row) -> registers -> LDS;
+//   2. every lane computes block dots, lane-fast along a row (consecutive
+//      lanes read consecutive blocks, the x slice is padded to 33 floats
+//      per block, so LDS reads do not collide), and stores (d, dot);
+//   3. lane (m, r) folds its row's terms in block order.
+// Up to 4 input rows (batched decode) share one pass over the weights.
+constexpr int kQ8R = 16;
+constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
+
+template <int MX, int CB>
 __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ x,
                                                       const uint8_t* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ out, int M, int N, int K,
                                                       int act) {
-    __shared__ __attribute__((aligned(16))) uint8_t sw[kQ8Rows * kQ8Seg];
-    __shared__ __attribute__((aligned(16))) float sx[4 * MG][kQ8Chunk * kQ8Block];
-    __shared__ float sdot[4 * MG][kQ8Rows][kQ8Chunk + 1];
+    static_assert(256 % CB == 0 && CB % 8 == 0, "chunk shape");
+    constexpr int kRowLds = CB * kQ8Bytes + 16;                       // row stride in LDS (16-byte multiple)
+    constexpr int kVPT = (kQ8R * CB * kQ8Bytes / 16 + 255) / 256;     // weight vectors per lane
+    constexpr int kXPT = MX * CB * kQ8Block / 4 / 256;                // x float4 per lane
+    constexpr int kRPT = kQ8R * CB / 256;                             // rows per lane in the dot phase
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) uint8_t sw[kQ8R * kRowLds];
+    __shared__ float sx[MX][CB * kQ8XPad];
+    __shared__ float sdot[MX][kQ8R][CB + 1];
+    __shared__ float sd[kQ8R][CB + 1];
 
     const int tid = threadIdx.x;
-    const long j0 = (long)blockIdx.x * kQ8Rows;
-    const int nrows = (int)min((long)kQ8Rows, (long)N - j0);
+    const long j0 = (long)blockIdx.x * kQ8R;
+    const int nrows = (int)min((long)kQ8R, (long)N - j0);
     const int nb = K / kQ8Block;
     const long rowB = (long)nb * kQ8Bytes;
-    const int nchunks = nb / kQ8Chunk;
 
-    uint4 rw[kQ8Loads];
-    float4 rx[MG];
-    auto fetch = [&](int c) {
+    // Chunk staging in registers: every load is unconditional (lanes past
+    // the chunk or past the last row re-read valid bytes and never store
+    // them), so a chunk's loads are all in flight together.
+    u4 rw[kVPT];
+    float4 rx[kXPT];
+    // Per-lane vector placement for a full chunk (the common case), computed
+    // once: global byte offset relative to the chunk start, LDS offset (-1:
+    // nothing to store).  Only a short last chunk re-derives them.
+    constexpr int kVrow = CB * kQ8Bytes / 16;
+    long gfull[kVPT];
+    int sfull[kVPT];
 #pragma unroll
-        for (int i = 0; i < kQ8Loads; i++) {
-            const int v = tid + i * 256;
-            if (v < nrows * kQ8Vec) {
-                const int r = v / kQ8Vec, o = v % kQ8Vec;
-                rw[i] = *reinterpret_cast<const uint4*>(w + (j0 + r) * rowB + (long)c * kQ8Seg + o * 16);
-            }
+    for (int i = 0; i < kVPT; i++) {
+        const int v = tid + i * 256;
+        const bool live = v < kQ8R * kVrow;
+        const int r = live ? v / kVrow : 0, o = live ? v % kVrow : 0;
+        gfull[i] = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
+        sfull[i] = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
+    }
+    auto place = [&](int i, int cb, long& goff, int& soff) {
+        if (cb == CB) {
+            goff = gfull[i];
+            soff = sfull[i];
+            return;
         }
-        // inputs: 64 float4 per input row per chunk
+        const int vrow = cb * kQ8Bytes / 16;
+        const int v = tid + i * 256;
+        const bool live = v < kQ8R * vrow;
+        const int r = live ? v / vrow : 0, o = live ? v % vrow : 0;
+        goff = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
+        soff = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
+    };
+    auto fetch = [&](int b0, int cb) {
 #pragma unroll
-        for (int g = 0; g < MG; g++) {
-            const int m = tid / 64 + 4 * g;
-            if (m < M)
-                rx[g] = *reinterpret_cast<const float4*>(x + (long)m * K + (long)c * (kQ8Chunk * kQ8Block) +
-                                                         (tid % 64) * 4);
+        for (int i = 0; i < kVPT; i++) {
+            long goff;
+            int soff;
+            place(i, cb, goff, soff);
+            rw[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u4*>(w + j0 * rowB + (long)b0 * kQ8Bytes + goff));
+        }
+#pragma unroll
+        for (int i = 0; i < kXPT; i++) {
+            const int e = (tid + i * 256) * 4;                        // float index in [MX][CB*32]
+            const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
+            const int qq = q < cb * kQ8Block ? q : 0;
+            rx[i] = *reinterpret_cast<const float4*>(x + (long)min(m, M - 1) * K + (long)b0 * kQ8Block + qq);
         }
     };
-    auto stash = [&]() {
+
+    float acc = 0.0f;          // lane tid < MX * 16 owns output (tid / 16, j0 + tid % 16)
+    fetch(0, min(CB, nb));
+    for (int b0 = 0; b0 < nb; b0 += CB) {
+        const int cb = min(CB, nb - b0);             // multiple of 8
+        __syncthreads();                             // previous chunk's LDS consumed
 #pragma unroll
-        for (int i = 0; i < kQ8Loads; i++) {
-            const int v = tid + i * 256;
-            if (v < nrows * kQ8Vec) {
-                const int r = v / kQ8Vec, o = v % kQ8Vec;
-                *reinterpret_cast<uint4*>(&sw[r * kQ8Seg + o * 16]) = rw[i];
+        for (int i = 0; i < kVPT; i++) {
+            long goff;
+            int soff;
+            place(i, cb, goff, soff);
+            if (soff >= 0) *reinterpret_cast<u4*>(&sw[soff]) = rw[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kXPT; i++) {
+            const int e = (tid + i * 256) * 4;
+            const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
+            if (q < cb * kQ8Block) {
+                float* dst = &sx[m][(q / kQ8Block) * kQ8XPad + q % kQ8Block];
+                dst[0] = rx[i].x; dst[1] = rx[i].y; dst[2] = rx[i].z; dst[3] = rx[i].w;
             }
         }
-#pragma unroll
-        for (int g = 0; g < MG; g++) {
-            const int m = tid / 64 + 4 * g;
-            if (m < M) *reinterpret_cast<float4*>(&sx[m][(tid % 64) * 4]) = rx[g];
-        }
-    };
-
-    float acc[MG];
-#pragma unroll
-    for (int g = 0; g < MG; g++) acc[g] = 0.0f;
-
-    fetch(0);
-    for (int c = 0; c < nchunks; c++) {
-        __syncthreads();          // previous chunk's LDS fully consumed
-        stash();
         __syncthreads();
-        if (c + 1 < nchunks) fetch(c + 1);   // next chunk in flight during the math
-        // block dots: lane t covers row r = t % 64, blocks t / 64 and t / 64 + 4
-        const int r = tid % 64;
-        if (r < nrows) {
+        if (b0 + CB < nb) fetch(b0 + CB, min(CB, nb - b0 - CB));   // in flight during the math
+        // block dots: lane owns block k = tid % CB of rows tid / CB + (256 / CB) i
+        const int k = tid % CB;
+        if (k < cb) {
+            float xr[kQ8Block];
+            if constexpr (MX == 1) {
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int k = tid / 64 + 4 * h;      // uniform across the wave
-                // the block's 32 q bytes start at byte A = r*272 + k*34 + 2,
-                // 4-aligned for odd k and 2 past a dword for even k: read
-                // dwords and realign with one alignbit each
-                const int A = r * kQ8Seg + k * kQ8Bytes + 2;
+                for (int i = 0; i < kQ8Block; i++) xr[i] = sx[0][k * kQ8XPad + i];
+            }
+#pragma unroll
+            for (int i = 0; i < kRPT; i++) {
+                const int r = tid / CB + (256 / CB) * i;
+                const int A = r * kRowLds + k * kQ8Bytes;     // block start (2-byte aligned)
                 const uint32_t* dw = reinterpret_cast<const uint32_t*>(&sw[A & ~3]);
-                uint32_t word[8];
-                if (k & 1) {
+                uint32_t d0[10];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) word[i] = dw[i];
-                } else {
-                    uint32_t d[9];
+                for (int t = 0; t < 10; t++) d0[t] = dw[t];
+                uint32_t wd[9];
 #pragma unroll
-                    for (int i = 0; i < 9; i++) d[i] = dw[i];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) word[i] = __builtin_amdgcn_alignbit(d[i + 1], d[i], 16);
-                }
+                for (int t = 0; t < 9; t++) wd[t] = (A & 2) ? __builtin_amdgcn_alignbit(d0[t + 1], d0[t], 16) : d0[t];
                 float qf[kQ8Block];
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int t = 0; t < kQ8Block; t++) qf[t] = (float)(int8_t)(wd[(2 + t) / 4] >> (8 * ((2 + t) % 4)));
+                sd[r][k] = half_bits_to_float(wd[0] & 0xffffu);
+                if constexpr (MX == 1) {
+                    sdot[0][r][k] = q8_block_dot(qf, xr);
+                } else {
 #pragma unroll
-                    for (int b = 0; b < 4; b++) qf[4 * i + b] = (float)(int8_t)(word[i] >> (8 * b));
-#pragma unroll
-                for (int m = 0; m < 4 * MG; m++)
-                    if (m < M) sdot[m][r][k] = q8_block_dot(qf, &sx[m][k * kQ8Block]);
+                    for (int m = 0; m < MX; m++)
+                        if (m < M) sdot[m][r][k] = q8_block_dot(qf, &sx[m][k * kQ8XPad]);
+                }
             }
         }
         __syncthreads();
-        // ordered fold of the chunk's 8 terms
-        if (r < nrows) {
+        // ordered fold of this chunk's terms
+        if (tid < MX * kQ8R) {
+            const int m = tid / kQ8R, r = tid % kQ8R;
+            if (m < M && r < nrows) {
+                for (int kk = 0; kk < cb; kk += 8) {
+                    float dv[8], tv[8];
 #pragma unroll
-            for (int g = 0; g < MG; g++) {
-                const int m = tid / 64 + 4 * g;
-                if (m < M) {
-#pragma unroll
-                    for (int k = 0; k < kQ8Chunk; k++) {
-                        const uint8_t* blk = &sw[r * kQ8Seg + k * kQ8Bytes];
-                        const float d = half_bits_to_float((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-                        acc[g] = __builtin_fmaf(d, sdot[m][r][k], acc[g]);
+                    for (int u = 0; u < 8; u++) {
+                        dv[u] = sd[r][kk + u];
+                        tv[u] = sdot[m][r][kk + u];
                     }
+#pragma unroll
+                    for (int u = 0; u < 8; u++) acc = __builtin_fmaf(dv[u], tv[u], acc);
                 }
             }
         }
     }
-    const int r = tid % 64;
-    if (r < nrows) {
-#pragma unroll
-        for (int g = 0; g < MG; g++) {
-            const int m = tid / 64 + 4 * g;
-            if (m < M) out[(long)m * N + j0 + r] = q8_finish(acc[g], bias, j0 + r, act);
-        }
+    if (tid < MX * kQ8R) {
+        const int m = tid / kQ8R, r = tid % kQ8R;
+        if (m < M && r < nrows) out[(long)m * N + j0 + r] = q8_finish(acc, bias, j0 + r, act);
     }
 }
 
@@ -257,16 +285,17 @@ __global__ __launch_bounds__(256) void q8_gemv_generic_kernel(const float* __res
 
 hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, float* out, int M, int N,
                           int K, int act, hipStream_t s) {
-    const bool fast = (K % (kQ8Chunk * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && M <= 16;
+    const bool fast = (K % (8 * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
     if (fast) {
-        const dim3 grid((unsigned)((N + kQ8Rows - 1) / kQ8Rows));
-        const int mg = (M + 3) / 4;
-        switch (mg) {
-        case 1: hipLaunchKernelGGL((q8_gemv_kernel<1>), grid, dim3(256), 0, s, x, w, bias, out, M, N, K, act); break;
-        case 2: hipLaunchKernelGGL((q8_gemv_kernel<2>), grid, dim3(256), 0, s, x, w, bias, out, M, N, K, act); break;
-        case 3: hipLaunchKernelGGL((q8_gemv_kernel<3>), grid, dim3(256), 0, s, x, w, bias, out, M, N, K, act); break;
-        default: hipLaunchKernelGGL((q8_gemv_kernel<4>), grid, dim3(256), 0, s, x, w, bias, out, M, N, K, act); break;
+        const dim3 grid((unsigned)((N + kQ8R - 1) / kQ8R));
+        for (int m0 = 0; m0 < M; m0 += 4) {
+            const int mm = min(4, M - m0);
+            const float* xg = x + (long)m0 * K;
+            float* og = out + (long)m0 * N;
+            if (mm == 1)
+                hipLaunchKernelGGL((q8_gemv_kernel<1, 64>), grid, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+            else
+                hipLaunchKernelGGL((q8_gemv_kernel<4, 32>), grid, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
         }
     } else {
         const long outs = (long)M * N;

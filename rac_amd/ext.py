@@ -692,7 +692,7 @@ def q8_gemv(x: torch.Tensor, wq: torch.Tensor, bias: Optional[torch.Tensor] = No
     """out[..., N] = act(x[..., K] @ W^T + bias) with W as Q8_0 blocks
     [N, K/32, 34] (rac_q8_0.c:178-211, bit-identical to its AVX2 build for
     act 0/1).  Leading dims of x are decode rows (the weights stream once
-    per 16 rows)."""
+    per 8 rows)."""
     _require_f32(x, "x")
     _require_gpu(wq, "wq")
     if wq.dtype != torch.uint8 or wq.dim() != 3 or wq.size(2) != Q8_BLOCK_BYTES:
@@ -708,8 +708,8 @@ def q8_gemv(x: torch.Tensor, wq: torch.Tensor, bias: Optional[torch.Tensor] = No
         b = _bias_f32(bias, N)
     out = torch.empty((x2.size(0), N), device=x.device, dtype=torch.float32)
     lib = _lib.load()
-    for m0 in range(0, x2.size(0), 16):
-        mm = min(16, x2.size(0) - m0)
+    for m0 in range(0, x2.size(0), 4096):
+        mm = min(4096, x2.size(0) - m0)
         check(lib.rac_q8_0_gemv_dev(x2[m0].data_ptr(), wq.data_ptr(), b.data_ptr() if b is not None else None,
                                     out[m0].data_ptr(), mm, N, K, int(act), _stream(out)),
               "rac_q8_0_gemv_dev")
