@@ -8,6 +8,8 @@ over synthetic U[-1,1] operands resident in HBM.  value = 2*4096^3 / t.
 
 Also measured in the same run (fields "ops" and "cpu_baseline"):
   * the matmul at n = 8 and 24;
+  * the config-5 attention core through RAC ([1,32,2048,128], causal, n=16)
+    and the Q8_0 decode GEMV (11008x4096, 32000x4096, 65536x8192; HBM GB/s);
   * softmax 4096x4096 N(0, std 2) at n = 8/16/24, RoPE on Q and K
     [8,32,4096,128], RMSNorm 16384x4096, SiLU 16384x11008 (n=16): HBM GB/s
     of 1 read + 1 write per element, buffers rotated past the 256 MB MALL;
@@ -229,6 +231,52 @@ def bench_hbm_ops(torch, ext, dev, g):
         rt.rac_set_precision(prev_iters)
     del blk, xb
 
+    # attention core of config 5 through RAC (rac_attention_dev): [1, 32, 2048,
+    # 128], causal, CORDIC mode n = 16; Q K^T and P V are 2 x 34.4 GFLOP
+    Ba, Ha, Ta, Da = 1, 32, 2048, 128
+    qa, ka, va = (torch.randn((Ba, Ha, Ta, Da), device=dev, generator=g) for _ in range(3))
+    oa = torch.empty_like(qa)
+    wsa = torch.empty(lib.rac_attention_workspace_bytes(Ba, Ha, Ta) // 4, device=dev)
+
+    def attn():
+        chk(lib.rac_attention_dev(qa.data_ptr(), ka.data_ptr(), va.data_ptr(), None, 1, oa.data_ptr(), Ba, Ha,
+                                  Ta, Da, wsa.data_ptr(), 16, ext.MODE_CORDIC, stream))
+
+    attn()
+    torch.cuda.synchronize()
+    t = _events_time(attn, 3, torch)
+    macs = 2 * Ba * Ha * Ta * Ta * Da
+    out["attention_core_1x32x2048x128_n16"] = {
+        "ms": round(t * 1e3, 3), "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
+        "valu_frac_of_fp32_peak": round(macs * 2 * 33 / t / 1e12 / PEAK_FP32_TFLOPS, 4)}
+    print(f"# attention core n=16: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    del qa, ka, va, oa, wsa
+
+    # Q8_0 decode GEMV (M = 1): weight bytes N*K/32*34 streamed once; buffer
+    # sets rotate past the MALL
+    for (Nq, Kq) in ((11008, 4096), (32000, 4096), (65536, 8192)):
+        wbytes = Nq * (Kq // 32) * 34
+        nsets = max(2, -(-600_000_000 // wbytes))
+        wsets = []
+        for _ in range(nsets):
+            wq = torch.randint(0, 256, (Nq, Kq // 32, 34), device=dev, dtype=torch.uint8, generator=g)
+            wq[:, :, 0] = 0x00
+            wq[:, :, 1] = 0x20          # block scale 2^-7 (fp16 0x2000)
+            wsets.append(wq)
+        xq = torch.randn((1, Kq), device=dev, generator=g)
+        yq = torch.empty((1, Nq), device=dev)
+        stq = {"i": 0}
+
+        def q8():
+            i = stq["i"] = (stq["i"] + 1) % nsets
+            chk(lib.rac_q8_0_gemv_dev(xq.data_ptr(), wsets[i].data_ptr(), None, yq.data_ptr(), 1, Nq, Kq, 0,
+                                      stream))
+
+        q8()
+        torch.cuda.synchronize()
+        record(f"q8_0_gemv_{Nq}x{Kq}", wbytes + 4 * (Kq + Nq), _events_time(q8, reps, torch))
+        del wsets
+
     # SiLU 16384 x 11008 (n = 16)
     xsilu = torch.randn((16384, 11008), device=dev, generator=g)
     ysilu = torch.empty_like(xsilu)
@@ -299,6 +347,16 @@ def cpu_baseline_child():
     gam = np.ones(4096, np.float32)
     t = timeit(lambda: r.rac_rmsnorm(rl.p(x), rl.p(y), rl.p(gam), 1e-6, 16384, 4096, None), 2)
     res["rmsnorm"] = {"seconds": t, "GBps": 2 * x.nbytes / t / 1e9}
+    del x, y
+    # Q8_0 decode GEMV 11008 x 4096 (reference AVX2 path)
+    Wf = np.random.default_rng(2).standard_normal((11008, 4096), dtype=np.float32) * np.float32(0.02)
+    wq = np.zeros((11008, 128, 34), np.uint8)
+    r.rac_q8_0_quantize_matrix(rl.p(Wf), rl.p(wq), 11008, 4096)
+    del Wf
+    xv = np.random.default_rng(3).standard_normal(4096, dtype=np.float32)
+    yv = np.zeros(11008, np.float32)
+    t = timeit(lambda: r.rac_q8_0_gemv(rl.p(xv), rl.p(wq), None, rl.p(yv), 11008, 4096, 0), 20)
+    res["q8_0_gemv_11008x4096"] = {"seconds": t, "GBps": wq.nbytes / t / 1e9}
     print(json.dumps(res))
 
 

@@ -491,7 +491,10 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
     const int bh = b * h;
     const long td = (long)t * d, tt = (long)t * t;
     const float scale = 1.0f / sqrtf((float)d);
-    int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt),
+    // causal: score tiles wholly above the diagonal are masked by the
+    // softmax regardless of their contents, so the scores GEMM skips them
+    int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt,
+                                   causal != 0),
                        "rac_attention scores launch");
     if (rc) return rc;
     SoftmaxMask mk;

@@ -58,13 +58,17 @@ template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc,
-    GemmEpilogue ep)
+    GemmEpilogue ep, int skip_upper)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
+    constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
+    // Causal attention scores: a tile whose every column lies above the
+    // diagonal (n0 >= m0 + BM) is masked to -inf by the softmax whatever it
+    // holds, so it is not computed (the whole workgroup leaves together).
+    if (skip_upper && (long)blockIdx.x * BN >= (long)blockIdx.y * BM + BM) return;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
-    constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
     __shared__ __attribute__((aligned(16))) float sA[BK][BM + PAD];
     __shared__ __attribute__((aligned(16))) float sB[BK][BN + PAD];
 
@@ -191,6 +195,7 @@ struct GemmArgs {
     long sa, sb, sc;
     GemmEpilogue ep;
     bool fused;
+    int skip_upper;
 };
 
 template <int MODE, int NITER, bool TA, bool TB, bool FUSED>
@@ -203,7 +208,7 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
               (unsigned)g.batch);
     hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED>), grid, dim3(256), 0, stream,
                        g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
-                       g.ep);
+                       g.ep, g.skip_upper);
     return hipGetLastError();
 }
 
@@ -231,15 +236,15 @@ static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStrea
 
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
-                       hipStream_t s, int batch, long sa, long sb, long sc) {
+                       hipStream_t s, int batch, long sa, long sb, long sc, int skip_upper) {
     const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc,
-                     GemmEpilogue(), false};
+                     GemmEpilogue(), false, skip_upper};
     return dispatch(ta, tb, mode, g, s);
 }
 
 hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
                              const GemmEpilogue& ep, int iters, int mode, hipStream_t s) {
-    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true};
+    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0};
     return dispatch(0, 1, mode, g, s);
 }
 
