@@ -150,7 +150,7 @@ int rac_dct_dev(const float *x, float *X, int n, void *stream);
  * scores = Q K^T / sqrt(head_dim) by the RAC matmul (mode, iters), causal
  * and additive [seq, seq] mask, CORDIC softmax in place, out = P V by the RAC
  * matmul.  workspace: rac_attention_workspace_bytes(batch, n_heads, seq)
- * bytes of device memory owned by the caller (the scores). */
+ * bytes of device memory owned by the caller (the scores, and a flag). */
 long rac_attention_workspace_bytes(int batch, int n_heads, int seq);
 int rac_attention_dev(const float *q, const float *k, const float *v, const float *mask,
                       int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,

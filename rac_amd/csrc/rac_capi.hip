@@ -477,10 +477,14 @@ static int check_attention(const void* q, const void* k, const void* v, const vo
     return RAC_OK;
 }
 
-// Bytes of the score workspace rac_attention_dev needs: batch*n_heads*seq*seq floats.
+// Bytes of the workspace rac_attention_dev needs: the batch*n_heads*seq*seq
+// float scores plus 256 bytes for a device flag.
+static long attention_scores_bytes(long batch, long n_heads, long seq) {
+    return (long)sizeof(float) * batch * n_heads * seq * seq;
+}
 RAC_EXPORT long rac_attention_workspace_bytes(int batch, int n_heads, int seq) {
     if (batch <= 0 || n_heads <= 0 || seq <= 0) return 0;
-    return (long)sizeof(float) * batch * n_heads * (long)seq * seq;
+    return attention_scores_bytes(batch, n_heads, seq) + 256;
 }
 
 // scores = (Q K^T) / sqrt(D) by the RAC matmul (batched over b*h), masked
@@ -492,9 +496,10 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
     const long td = (long)t * d, tt = (long)t * t;
     const float scale = 1.0f / sqrtf((float)d);
     // causal: score tiles wholly above the diagonal are masked by the
-    // softmax regardless of their contents, so the scores GEMM skips them
+    // softmax regardless of their contents, so the scores GEMM schedules only
+    // the tiles on or below it
     int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt,
-                                   causal != 0),
+                                   causal ? 1 : 0),
                        "rac_attention scores launch");
     if (rc) return rc;
     SoftmaxMask mk;
@@ -504,7 +509,17 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
     mk.zero_guard = 1;
     rc = check_hip(softmax_launch(ws, ws, (long)bh * t, t, iters, s, mk), "rac_attention softmax launch");
     if (rc) return rc;
-    return check_hip(gemm_launch(0, 0, ws, v, out, t, d, t, 1.0f, 0.0f, iters, mode, s, bh, tt, td, td),
+    // causal: P is exactly 0 above the diagonal, so P V may stop each row
+    // tile's K loop at its last row -- when V is finite (0 * inf is NaN);
+    // the flag lives in the workspace tail and is evaluated on the device
+    int* flag = nullptr;
+    if (causal) {
+        flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + attention_scores_bytes(b, h, t));
+        rc = check_hip(all_finite_launch(v, (long)bh * td, flag, s), "rac_attention finite check");
+        if (rc) return rc;
+    }
+    return check_hip(gemm_launch(0, 0, ws, v, out, t, d, t, 1.0f, 0.0f, iters, mode, s, bh, tt, td, td,
+                                 causal ? 2 : 0, flag),
                      "rac_attention output launch");
 }
 

@@ -54,18 +54,34 @@ __device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc
     }
 }
 
-template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED>
+template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED, int SCHED>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc,
-    GemmEpilogue ep, int skip_upper)
+    GemmEpilogue ep, const int* k_causal)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
-    // Causal attention scores: a tile whose every column lies above the
-    // diagonal (n0 >= m0 + BM) is masked to -inf by the softmax whatever it
-    // holds, so it is not computed (the whole workgroup leaves together).
-    if (skip_upper && (long)blockIdx.x * BN >= (long)blockIdx.y * BM + BM) return;
+    // Tile schedule.  0: tile (blockIdx.y, blockIdx.x).  1 (causal attention
+    // scores, square, BM == BN): only tiles on or below the diagonal, which
+    // the softmax does not overwrite with -inf; workgroup (x, p) takes row p
+    // col x for x <= p, else row nt-1-p col x-p-1, so every workgroup has one
+    // tile and rows p and nt-1-p share a column of the grid (grid nt+1 x
+    // ceil(nt/2)).  2 (causal P V): workgroup p computes row tiles p and
+    // nt-1-p, whose K ranges (below) sum to a constant.
+    int tm = blockIdx.y, tn = blockIdx.x, tm2 = -1;
+    if constexpr (SCHED == 1) {
+        const int nt = (M + BM - 1) / BM, p = blockIdx.y, x = blockIdx.x;
+        if (x > p) {
+            tm = nt - 1 - p;
+            tn = x - p - 1;
+            if (tm == p) return;     // middle row of an odd tile count: covered by x <= p
+        }
+    } else if constexpr (SCHED == 2) {
+        const int nt = (M + BM - 1) / BM, p = blockIdx.y;
+        if (nt - 1 - p != p) tm2 = nt - 1 - p;
+    }
+    const long m0a = (long)tm * BM, m0b = tm2 < 0 ? -1L : (long)tm2 * BM, n0 = (long)tn * BN;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
@@ -74,114 +90,147 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
-    const long m0 = (long)blockIdx.y * BM, n0 = (long)blockIdx.x * BN;
 
-    float acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+    constexpr int kPasses = SCHED == 2 ? 2 : 1;
+    for (int pass = 0; pass < kPasses; pass++) {
+        const long m0 = pass ? m0b : m0a;
+        if (m0 < 0) break;
 
-    float ra[Cfg::kALoads], rb[Cfg::kBLoads];
+        float acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
 
-    // Global -> register staging of one K-tile; element (m, k) of op(A) and
-    // (k, n) of op(B), zero outside the matrix.  Index order is chosen so
-    // consecutive lanes read consecutive addresses.
-    auto load_tile = [&](int k0) {
-#pragma unroll
-        for (int r = 0; r < Cfg::kALoads; r++) {
-            const int idx = tid + r * 256;
-            int mm, kk;
-            if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
-            else { mm = idx / BK; kk = idx % BK; }
-            const long gm = m0 + mm, gk = (long)k0 + kk;
-            float v = 0.0f;
-            if (gm < M && gk < K) v = TA ? A[gk * M + gm] : A[gm * K + gk];
-            ra[r] = v;
-        }
-#pragma unroll
-        for (int r = 0; r < Cfg::kBLoads; r++) {
-            const int idx = tid + r * 256;
-            int nn, kk;
-            if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
-            else { kk = idx / BN; nn = idx % BN; }
-            const long gn = n0 + nn, gk = (long)k0 + kk;
-            float v = 0.0f;
-            if (gn < N && gk < K) v = TB ? B[gn * K + gk] : B[gk * N + gn];
-            rb[r] = v;
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int r = 0; r < Cfg::kALoads; r++) {
-            const int idx = tid + r * 256;
-            int mm, kk;
-            if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
-            else { mm = idx / BK; kk = idx % BK; }
-            sA[kk][mm] = ra[r];
-        }
-#pragma unroll
-        for (int r = 0; r < Cfg::kBLoads; r++) {
-            const int idx = tid + r * 256;
-            int nn, kk;
-            if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
-            else { kk = idx / BN; nn = idx % BN; }
-            sB[kk][nn] = rb[r];
-        }
-    };
+        float ra[Cfg::kALoads], rb[Cfg::kBLoads];
 
-    load_tile(0);
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        __syncthreads();            // previous tile fully consumed
-        store_tile();
-        __syncthreads();
-        if (k0 + BK < K) load_tile(k0 + BK);   // prefetch overlaps the MACs
+        // Global -> register staging of one K-tile; element (m, k) of op(A) and
+        // (k, n) of op(B), zero outside the matrix.  Index order is chosen so
+        // consecutive lanes read consecutive addresses.
+        auto load_tile = [&](int k0) {
+#pragma unroll
+            for (int r = 0; r < Cfg::kALoads; r++) {
+                const int idx = tid + r * 256;
+                int mm, kk;
+                if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
+                else { mm = idx / BK; kk = idx % BK; }
+                const long gm = m0 + mm, gk = (long)k0 + kk;
+                float v = 0.0f;
+                if (gm < M && gk < K) v = TA ? A[gk * M + gm] : A[gm * K + gk];
+                ra[r] = v;
+            }
+#pragma unroll
+            for (int r = 0; r < Cfg::kBLoads; r++) {
+                const int idx = tid + r * 256;
+                int nn, kk;
+                if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
+                else { kk = idx / BN; nn = idx % BN; }
+                const long gn = n0 + nn, gk = (long)k0 + kk;
+                float v = 0.0f;
+                if (gn < N && gk < K) v = TB ? B[gn * K + gk] : B[gk * N + gn];
+                rb[r] = v;
+            }
+        };
+        auto store_tile = [&]() {
+#pragma unroll
+            for (int r = 0; r < Cfg::kALoads; r++) {
+                const int idx = tid + r * 256;
+                int mm, kk;
+                if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
+                else { mm = idx / BK; kk = idx % BK; }
+                sA[kk][mm] = ra[r];
+            }
+#pragma unroll
+            for (int r = 0; r < Cfg::kBLoads; r++) {
+                const int idx = tid + r * 256;
+                int nn, kk;
+                if constexpr (TB) { nn = idx / BK; kk = idx % BK; }
+                else { kk = idx / BN; nn = idx % BN; }
+                sB[kk][nn] = rb[r];
+            }
+        };
+
+        // Causal P V: row t of P is exactly 0 beyond column t, and with every v
+        // finite (*k_causal == 1, checked on the device) fma(0, v, acc) == acc
+        // (acc starts at +0 and can never become -0), so the K loop stops after
+        // the tile's last row.
+        int kend = K;
+        if (k_causal && *k_causal == 1) kend = (int)min((long)K, m0 + BM);
+        load_tile(0);
+        for (int k0 = 0; k0 < kend; k0 += BK) {
+            __syncthreads();            // previous tile fully consumed
+            store_tile();
+            __syncthreads();
+            if (k0 + BK < kend) load_tile(k0 + BK);   // prefetch overlaps the MACs
 #pragma unroll 1
-        for (int kk = 0; kk < BK; kk++) {
-            float a[TM], b[TN];
-            uint32_t bs[TN];
+            for (int kk = 0; kk < BK; kk++) {
+                float a[TM], b[TN];
+                uint32_t bs[TN];
 #pragma unroll
-            for (int i = 0; i < TM; i += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
-                a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+                for (int i = 0; i < TM; i += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
+                    a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+                }
+#pragma unroll
+                for (int j = 0; j < TN; j += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
+                    b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
+                }
+#pragma unroll
+                for (int j = 0; j < TN; j++) bs[j] = as_u(b[j]) & 0x80000000u;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
             }
-#pragma unroll
-            for (int j = 0; j < TN; j += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
-                b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
-            }
-#pragma unroll
-            for (int j = 0; j < TN; j++) bs[j] = as_u(b[j]) & 0x80000000u;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
         }
-    }
 
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const long gm = m0 + ty * TM + i;
-        if (gm >= M) continue;
+        for (int i = 0; i < TM; i++) {
+            const long gm = m0 + ty * TM + i;
+            if (gm >= M) continue;
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const long gn = n0 + tx * TN + j;
-            if (gn >= N) continue;
-            float* cp = C + gm * N + gn;
-            // rac_kernels.hip:267-272
-            float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc[i][j], beta * *cp)
-                                     : alpha * acc[i][j];
-            if constexpr (FUSED) {
-                // rac_torch.cu:770-775: + bias, then the activation in
-                // registers (the pre-activation is kept when asked for)
-                if (ep.bias) v = v + ep.bias[gn];
-                if (ep.pre) ep.pre[gm * N + gn] = v;
-                v = act_rt(v, ep.act, iters, ep.khinv);
+            for (int j = 0; j < TN; j++) {
+                const long gn = n0 + tx * TN + j;
+                if (gn >= N) continue;
+                float* cp = C + gm * N + gn;
+                // rac_kernels.hip:267-272
+                float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc[i][j], beta * *cp)
+                                         : alpha * acc[i][j];
+                if constexpr (FUSED) {
+                    // rac_torch.cu:770-775: + bias, then the activation in
+                    // registers (the pre-activation is kept when asked for)
+                    if (ep.bias) v = v + ep.bias[gn];
+                    if (ep.pre) ep.pre[gm * N + gn] = v;
+                    v = act_rt(v, ep.act, iters, ep.khinv);
+                }
+                *cp = v;
             }
-            *cp = v;
         }
-    }
+    }   // pass
+}
+
+// flag = 1 unless some x[i] is inf or NaN (flag must be 1 on entry; lanes
+// only ever store 0, so concurrent stores agree).
+__global__ __launch_bounds__(256) void all_finite_kernel(const float* __restrict__ x, long n,
+                                                         int* __restrict__ flag) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    bool ok = true;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        ok &= __builtin_isfinite(x[i]);
+    if (!ok) *flag = 0;
+}
+
+__global__ void set_flag_kernel(int* flag, int v) { *flag = v; }
+
+hipError_t all_finite_launch(const float* x, long n, int* flag, hipStream_t s) {
+    hipLaunchKernelGGL(set_flag_kernel, dim3(1), dim3(1), 0, s, flag, 1);
+    long blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(all_finite_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, flag);
+    return hipGetLastError();
 }
 
 struct GemmArgs {
@@ -195,28 +244,35 @@ struct GemmArgs {
     long sa, sb, sc;
     GemmEpilogue ep;
     bool fused;
-    int skip_upper;
+    int sched;
+    const int* k_causal;
 };
 
-template <int MODE, int NITER, bool TA, bool TB, bool FUSED>
+template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED = 0>
 static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     constexpr int TM = (MODE == kModeFast) ? 8 : 4;
     constexpr int TN = TM;
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     const float kinv = cordic_kinv(g.iters);
-    dim3 grid((unsigned)((g.N + Cfg::kBN - 1) / Cfg::kBN), (unsigned)((g.M + Cfg::kBM - 1) / Cfg::kBM),
-              (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED>), grid, dim3(256), 0, stream,
+    const unsigned nt = (unsigned)((g.M + Cfg::kBM - 1) / Cfg::kBM);
+    dim3 grid((unsigned)((g.N + Cfg::kBN - 1) / Cfg::kBN), nt, (unsigned)g.batch);
+    if (g.sched == 1) grid = dim3(nt + 1, (nt + 1) / 2, (unsigned)g.batch);
+    if (g.sched == 2) grid.y = (nt + 1) / 2;
+    hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED, SCHED>), grid, dim3(256), 0, stream,
                        g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
-                       g.ep, g.skip_upper);
+                       g.ep, g.k_causal);
     return hipGetLastError();
 }
 
 // The fused epilogue exists for the NT layout only (input @ weight^T, the
-// linear layer); gemm_fused_launch never asks for another.
+// linear layer), the triangular schedule for NT only (causal Q K^T) and the
+// paired-row schedule for NN only (causal P V); their callers never ask for
+// another layout.
 template <int MODE, int NITER>
 static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s) {
     if (g.fused) return launch_cfg<MODE, NITER, false, true, true>(g, s);
+    if (g.sched == 1) return launch_cfg<MODE, NITER, false, true, false, 1>(g, s);   // NT only
+    if (g.sched == 2) return launch_cfg<MODE, NITER, false, false, false, 2>(g, s);  // NN only
     if (!ta && !tb) return launch_cfg<MODE, NITER, false, false, false>(g, s);
     if (!ta && tb) return launch_cfg<MODE, NITER, false, true, false>(g, s);
     if (ta && !tb) return launch_cfg<MODE, NITER, true, false, false>(g, s);
@@ -236,15 +292,16 @@ static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStrea
 
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
-                       hipStream_t s, int batch, long sa, long sb, long sc, int skip_upper) {
+                       hipStream_t s, int batch, long sa, long sb, long sc, int sched,
+                       const int* k_causal) {
     const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc,
-                     GemmEpilogue(), false, skip_upper};
+                     GemmEpilogue(), false, sched, k_causal};
     return dispatch(ta, tb, mode, g, s);
 }
 
 hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
                              const GemmEpilogue& ep, int iters, int mode, hipStream_t s) {
-    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0};
+    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0, nullptr};
     return dispatch(0, 1, mode, g, s);
 }
 

@@ -39,12 +39,18 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 
 // batch > 1: C_z = alpha op(A_z) op(B_z) + beta C_z for z < batch, with
 // A_z = A + z*sa, B_z = B + z*sb, C_z = C + z*sc (element strides).
-// skip_upper: output tiles entirely above the diagonal (every column index
-// > every row index) are left unwritten (causal attention scores).
+// sched 1 (square M == N): only output tiles on or below the diagonal are
+// computed (causal attention scores; the tiles above are left unwritten).
+// sched 2: each workgroup computes row tiles p and nt-1-p (balances the
+// causal P V below).  k_causal: device flag; when it holds 1, row tile m
+// sums k only up to its last row (causal P V with a lower-triangular P and
+// finite V).
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch = 1, long sa = 0, long sb = 0, long sc = 0,
-                       int skip_upper = 0);
+                       int sched = 0, const int* k_causal = nullptr);
+// *flag = 1 if every x[i] is finite, else 0 (stream-ordered).
+hipError_t all_finite_launch(const float* x, long n, int* flag, hipStream_t s);
 
 // Optional attention masking of each row r (position t = r % seq, column j):
 // causal -> x = -inf for j > t; then x += mask[t*seq + j] when mask != null.

@@ -553,10 +553,11 @@ def attention_scale(head_dim: int) -> float:
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
               is_causal: bool = False, iters: int = 0, mode: int = -1,
               return_probs: bool = False):
-    """rac_attention (rac.h:323-335) on [B, H, T, D] tensors: scores =
-    Q K^T / sqrt(D) by the RAC matmul, causal/additive mask, CORDIC softmax,
-    out = P V by the RAC matmul.  With return_probs, also returns P
-    [B, H, T, T] (what the backward pass needs)."""
+    """rac_attention (rac.h:323-335) on [B, H, T, D] tensors through
+    rac_attention_dev: scores = Q K^T / sqrt(D) by the RAC matmul,
+    causal/additive [T, T] mask, CORDIC softmax, out = P V by the RAC
+    matmul.  With return_probs, also returns P [B, H, T, T] (what the
+    backward pass needs)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _require_f32(t, n)
         if t.dim() != 4:
@@ -564,15 +565,23 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
     if q.shape != k.shape or q.shape != v.shape:
         raise RuntimeError("RAC: q, k, v must have the same shape")
     B, H, T, D = q.shape
-    q3 = q.contiguous().view(B * H, T, D)
-    k3 = k.contiguous().view(B * H, T, D)
-    v3 = v.contiguous().view(B * H, T, D)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     iters, mode = _resolve(iters, mode)
-    P = bmm(q3, k3, trans_b=True, alpha=attention_scale(D), iters=iters, mode=mode)
-    softmax_masked_(P, mask, is_causal, iters)
-    out = bmm(P, v3, iters=iters, mode=mode).view(B, H, T, D)
+    mptr = None
+    if mask is not None:
+        _require_f32(mask, "mask")
+        if tuple(mask.shape) != (T, T):
+            raise RuntimeError("RAC: attention mask must be [T, T]")
+        mask = mask.contiguous()
+        mptr = mask.data_ptr()
+    out = torch.empty_like(q)
+    lib = _lib.load()
+    ws = torch.empty(lib.rac_attention_workspace_bytes(B, H, T) // 4, device=q.device, dtype=torch.float32)
+    check(lib.rac_attention_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), mptr, int(bool(is_causal)),
+                                out.data_ptr(), B, H, T, D, ws.data_ptr(), iters, mode, _stream(out)),
+          "rac_attention_dev")
     if return_probs:
-        return out, P.view(B, H, T, T)
+        return out, ws[:B * H * T * T].view(B, H, T, T)
     return out
 
 

@@ -204,7 +204,8 @@ def _qkv(shape, seed):
 
 
 @pytest.mark.parametrize("iters,mode", [(16, 1), (8, 1), (24, 1), (16, 0)])
-@pytest.mark.parametrize("shape", [(2, 3, 16, 8), (1, 2, 33, 64), (1, 4, 128, 128), (2, 2, 67, 40)])
+@pytest.mark.parametrize("shape", [(2, 3, 16, 8), (1, 2, 33, 64), (1, 4, 128, 128), (2, 2, 67, 40),
+                                   (1, 2, 200, 32), (1, 1, 300, 64)])
 def test_attention_vs_oracle(shape, iters, mode):
     e = ext()
     q, k, v = _qkv(shape, seed=sum(shape))
@@ -220,6 +221,24 @@ def test_attention_vs_oracle(shape, iters, mode):
         # same scores bit for bit; the softmax row sum is a tree on the GPU and
         # left-to-right in the checker: each p moves by <= T * 2^-24 relative
         assert np.max(np.abs(got - ref)) <= Tn * ULP * vmax + 1e-7
+
+
+def test_attention_causal_nonfinite_v_keeps_full_products():
+    """Causal P V stops each row tile at its last row only when V is finite:
+    with an inf in V, 0 * inf = NaN must reach the earlier rows, as in the
+    reference's full sum."""
+    e = ext()
+    shape = (1, 2, 130, 16)
+    q, k, v = _qkv(shape, seed=321)
+    v[0, 1, 129, 3] = np.inf
+    v[0, 0, 70, 5] = np.nan
+    for iters, mode in ((16, 1), (24, 0)):
+        got = H(e.attention(T(q), T(k), T(v), None, True, iters=iters, mode=mode))
+        ref = rl.orc_attention(q, k, v, None, True, iters, mode)
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        assert np.isnan(got[0, 1, :129, 3]).all() and np.isnan(got[0, 0, :70, 5]).all()
+        fin = np.isfinite(ref)
+        assert np.max(np.abs(got[fin] - ref[fin])) <= 130 * ULP * np.abs(v[np.isfinite(v)]).max() + 1e-7
 
 
 def test_attention_golden_and_rac_h():
