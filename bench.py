@@ -277,6 +277,46 @@ def bench_hbm_ops(torch, ext, dev, g):
         record(f"q8_0_gemv_{Nq}x{Kq}", wbytes + 4 * (Kq + Nq), _events_time(q8, reps, torch))
         del wsets
 
+    # RAC-DSP fixed-point engine (Q32.32 / Q0.63 int64): 2^24 evaluations of
+    # rotate (x, y, z in and out: 48 B each) and of project (x, z in, x out:
+    # 24 B, the rac_dsp_project_batch form); the 256 x 256 systolic product of
+    # 256 activation vectors (2^24 projections, outputs K x N)
+    nd = 1 << 24
+    xd, yd, zd = (torch.randint(-2 ** 62, 2 ** 62, (nd,), device=dev, dtype=torch.int64, generator=g)
+                  for _ in range(3))
+    od = [torch.empty_like(xd) for _ in range(3)]
+    for opd, name, nbytes in ((0, "rotate", 48), (1, "project", 24)):
+        def dsp():
+            if opd == 0:
+                chk(lib.rac_dsp_eval_dev(0, nd, xd.data_ptr(), yd.data_ptr(), zd.data_ptr(), od[0].data_ptr(),
+                                         od[1].data_ptr(), od[2].data_ptr(), stream))
+            else:
+                chk(lib.rac_dsp_eval_dev(1, nd, xd.data_ptr(), None, zd.data_ptr(), od[0].data_ptr(), None, None,
+                                         stream))
+
+        dsp()
+        torch.cuda.synchronize()
+        t = _events_time(dsp, reps, torch)
+        out[f"dsp_{name}_16M"] = {"us": round(t * 1e6, 2), "Geval_per_s": round(nd / t / 1e9, 2),
+                                  "GBps": round(nbytes * nd / t / 1e9, 1),
+                                  "frac_of_hbm_peak": round(nbytes * nd / t / 1e9 / PEAK_HBM_GBPS, 4)}
+        print(f"# dsp {name}: {t * 1e6:.1f} us, {nd / t / 1e9:.1f} G-evals/s", file=sys.stderr, flush=True)
+    del xd, yd, zd, od
+    Ns = Ks = 256
+    Wd = torch.randint(-2 ** 63, 2 ** 63 - 1, (Ns, Ns), device=dev, dtype=torch.int64, generator=g)
+    Xd = torch.randint(-2 ** 40, 2 ** 40, (Ks, Ns), device=dev, dtype=torch.int64, generator=g)
+    Yd = torch.empty_like(Xd)
+
+    def sysd():
+        chk(lib.rac_dsp_systolic_dev(Ns, Ks, Wd.data_ptr(), Xd.data_ptr(), Yd.data_ptr(), stream))
+
+    sysd()
+    torch.cuda.synchronize()
+    t = _events_time(sysd, reps, torch)
+    out["dsp_systolic_256x256_k256"] = {"us": round(t * 1e6, 2), "Geval_per_s": round(Ns * Ns * Ks / t / 1e9, 2)}
+    print(f"# dsp systolic: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
+    del Wd, Xd, Yd
+
     # SiLU 16384 x 11008 (n = 16)
     xsilu = torch.randn((16384, 11008), device=dev, generator=g)
     ysilu = torch.empty_like(xsilu)
@@ -357,6 +397,21 @@ def cpu_baseline_child():
     yv = np.zeros(11008, np.float32)
     t = timeit(lambda: r.rac_q8_0_gemv(rl.p(xv), rl.p(wq), None, rl.p(yv), 11008, 4096, 0), 20)
     res["q8_0_gemv_11008x4096"] = {"seconds": t, "GBps": wq.nbytes / t / 1e9}
+    del wq
+    # RAC-DSP project batch, 2^20 evaluations (reference sim/rac_dsp_core.c,
+    # ROMs generated by the rtl/gen_coarse_lut.py rule)
+    lut, at, ath = np.zeros(1024, np.uint64), np.zeros(17, np.int64), np.zeros(9, np.int64)
+    rl.oracle().orc_dsp_gen_roms(rl.p(lut), rl.p(at), rl.p(ath))
+    ctypes.memmove(ctypes.addressof(ctypes.c_uint64.in_dll(r, "rac_coarse_lut")), lut.ctypes.data, lut.nbytes)
+    ctypes.memmove(ctypes.addressof(ctypes.c_int64.in_dll(r, "rac_atan_rom")), at.ctypes.data, at.nbytes)
+    ctypes.memmove(ctypes.addressof(ctypes.c_int64.in_dll(r, "rac_atanh_tab")), ath.ctypes.data, ath.nbytes)
+    nd = 1 << 20
+    rng = np.random.default_rng(4)
+    xs = rng.integers(-2 ** 62, 2 ** 62, nd, dtype=np.int64)
+    zs = rng.integers(-2 ** 63, 2 ** 63 - 1, nd, dtype=np.int64)
+    xo = np.zeros(nd, np.int64)
+    t = timeit(lambda: r.rac_dsp_project_batch(nd, rl.p(xs), rl.p(zs), rl.p(xo)), 3)
+    res["dsp_project"] = {"seconds": t, "evals": nd, "Geval_per_s": nd / t / 1e9}
     print(json.dumps(res))
 
 

@@ -1101,3 +1101,135 @@ ORC_API int orc_q8_0_gemv(const float *x, const uint8_t *w, const float *bias, f
     }
     return 0;
 }
+
+/* ── RAC-DSP fixed-point CORDIC engine (sim/rac_dsp_core.c) ──────────────
+ * Integer model of the RTL datapath: x, y in Q32.32, z in Q0.63 fractions
+ * of pi; 64-bit two's-complement arithmetic (computed here in uint64_t so
+ * overflow wraps as the hardware does).  ROMs: a 1024-entry coarse LUT of
+ * 10-bit direction words, atan(2^-i) for i = 0..16 and atanh(2^-s) for
+ * s = 8..16, both in Q0.63 fractions of pi. */
+
+#define ORC_DSP_LUT_BITS 10
+#define ORC_DSP_LUT 1024
+#define ORC_DSP_RES 9
+#define ORC_DSP_RES_START 8
+#define ORC_DSP_ATAN (ORC_DSP_RES_START + ORC_DSP_RES)
+
+static uint64_t orc_dsp_lut[ORC_DSP_LUT];
+static int64_t orc_dsp_atan[ORC_DSP_ATAN];
+static int64_t orc_dsp_atanh[ORC_DSP_RES];
+static int orc_dsp_ready = 0;
+
+/* round(v / pi * 2^63) as rtl/gen_coarse_lut.py computes it in doubles
+ * (round half to even), as a 64-bit pattern. */
+static int64_t q063_frac_pi(double v)
+{
+    double s = nearbyint(v / M_PI * 9223372036854775808.0);
+    return (int64_t)s;
+}
+
+/* The ROMs by the generation rule of rtl/gen_coarse_lut.py:27-123: LUT
+ * entry k holds the direction bits of a double-precision circular CORDIC
+ * driving z = (k - 512 + 0.5) pi / 1024 to zero over 10 steps (bit i set
+ * for d_i = +1). */
+ORC_API void orc_dsp_gen_roms(uint64_t *lut, int64_t *atan_rom, int64_t *atanh_rom)
+{
+    for (int k = 0; k < ORC_DSP_LUT; k++) {
+        double z = (k - ORC_DSP_LUT / 2 + 0.5) * M_PI / ORC_DSP_LUT;
+        uint64_t bits = 0;
+        for (int i = 0; i < ORC_DSP_LUT_BITS; i++) {
+            double step = atan(ldexp(1.0, -i));
+            if (z >= 0.0) { z -= step; bits |= (uint64_t)1 << i; }
+            else z += step;
+        }
+        lut[k] = bits;
+    }
+    for (int i = 0; i < ORC_DSP_ATAN; i++) atan_rom[i] = q063_frac_pi(atan(ldexp(1.0, -i)));
+    for (int i = 0; i < ORC_DSP_RES; i++)
+        atanh_rom[i] = q063_frac_pi(atanh(ldexp(1.0, -(ORC_DSP_RES_START + i))));
+}
+
+static void dsp_init(void)
+{
+    if (!orc_dsp_ready) {
+        orc_dsp_gen_roms(orc_dsp_lut, orc_dsp_atan, orc_dsp_atanh);
+        orc_dsp_ready = 1;
+    }
+}
+
+/* Use the given ROM contents instead of the generated ones. */
+ORC_API void orc_dsp_set_roms(const uint64_t *lut, const int64_t *atan_rom, const int64_t *atanh_rom)
+{
+    memcpy(orc_dsp_lut, lut, sizeof(orc_dsp_lut));
+    memcpy(orc_dsp_atan, atan_rom, sizeof(orc_dsp_atan));
+    memcpy(orc_dsp_atanh, atanh_rom, sizeof(orc_dsp_atanh));
+    orc_dsp_ready = 1;
+}
+
+static inline uint64_t dsp_asr(uint64_t v, int n)          /* arithmetic shift right */
+{
+    return (uint64_t)((int64_t)v >> n);
+}
+
+/* rac_dsp_eval, sim/rac_dsp_core.c:95-149: quadrant fold (|z| >= pi/2 ->
+ * z + pi, (x, y) negated), then for op != 2 (vectoring) a coarse stage of
+ * 10 circular micro-rotations whose directions come from the LUT indexed by
+ * the top bits of 2z, then 9 residual micro-rotations at shifts 8..16
+ * (hyperbolic for op 3; vectoring directions from sign(y) for op 2). */
+ORC_API void orc_dsp_eval(int64_t xi, int64_t yi, int64_t zi, int op, int64_t *xo, int64_t *yo, int64_t *zo)
+{
+    dsp_init();
+    uint64_t x = (uint64_t)xi, y = (uint64_t)yi, z = (uint64_t)zi;
+    if (((z >> 63) ^ (z >> 62)) & 1u) {
+        z ^= (uint64_t)1 << 63;
+        x = (uint64_t)0 - x;
+        y = (uint64_t)0 - y;
+    }
+    const int hyper = (op == 3), vect = (op == 2);
+    if (!vect) {
+        const int idx = (int)(((int64_t)(z << 1) >> (64 - ORC_DSP_LUT_BITS)) + ORC_DSP_LUT / 2) & (ORC_DSP_LUT - 1);
+        const uint64_t dv = orc_dsp_lut[idx];
+        uint64_t za = 0;
+        for (int i = 0; i < ORC_DSP_LUT_BITS; i++) {
+            const uint64_t ys = dsp_asr(y, i), xs = dsp_asr(x, i);
+            if ((dv >> i) & 1u) { x = x - ys; y = y + xs; za += (uint64_t)orc_dsp_atan[i]; }
+            else { x = x + ys; y = y - xs; za -= (uint64_t)orc_dsp_atan[i]; }
+        }
+        z = z - za;
+    }
+    for (int i = 0; i < ORC_DSP_RES; i++) {
+        const int ph = ORC_DSP_RES_START + i;
+        const int dpos = vect ? ((int64_t)y < 0) : ((int64_t)z >= 0);
+        const uint64_t xs = dsp_asr(x, ph), ys = dsp_asr(y, ph);
+        const uint64_t c = (uint64_t)(hyper ? orc_dsp_atanh[i] : orc_dsp_atan[ph]);
+        uint64_t xn;
+        if (hyper) xn = dpos ? x + ys : x - ys;
+        else xn = dpos ? x - ys : x + ys;
+        const uint64_t yn = dpos ? y + xs : y - xs;
+        const uint64_t zn = dpos ? z - c : z + c;
+        x = xn; y = yn; z = zn;
+    }
+    *xo = (int64_t)x; *yo = (int64_t)y; *zo = (int64_t)z;
+}
+
+ORC_API void orc_dsp_eval_batch(int op, long n, const int64_t *x, const int64_t *y, const int64_t *z,
+                                int64_t *xo, int64_t *yo, int64_t *zo)
+{
+    for (long i = 0; i < n; i++) orc_dsp_eval(x[i], y[i], z[i], op, &xo[i], &yo[i], &zo[i]);
+}
+
+/* sim/rac_systolic_ref.c:40-55: Y[k][c] = sum_r project(X[k][r], 0,
+ * W[r][c]).x over a weight-stationary N x N array, for K input vectors. */
+ORC_API void orc_dsp_systolic(int N, int K, const int64_t *W, const int64_t *X, int64_t *Y)
+{
+    for (int k = 0; k < K; k++)
+        for (int c = 0; c < N; c++) {
+            uint64_t sum = 0;
+            for (int r = 0; r < N; r++) {
+                int64_t xo, yo, zo;
+                orc_dsp_eval(X[(size_t)k * N + r], 0, W[(size_t)r * N + c], 1, &xo, &yo, &zo);
+                sum += (uint64_t)xo;
+            }
+            Y[(size_t)k * N + c] = (int64_t)sum;
+        }
+}

@@ -70,6 +70,16 @@ _SIGNATURES = {
     "rac_q8_0_quantize_row": (None, [_vp, _vp, _i]),
     "rac_q8_0_quantize_matrix": (None, [_vp, _vp, _i, _i]),
     "rac_q8_0_dequantize_row": (None, [_vp, _vp, _i]),
+    # rac_dsp.h — the fixed-point RAC-DSP engine (int64 operands)
+    "rac_load_hex_lut": (_i, [ctypes.c_char_p, _vp, _i]),
+    "rac_load_all_roms": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
+    "rac_dsp_set_roms": (None, [_vp, _vp, _vp]),
+    "rac_dsp_get_roms": (None, [_vp, _vp, _vp]),
+    "rac_dsp_eval": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i, _vp, _vp, _vp]),
+    "rac_dsp_project_batch": (None, [_i, _vp, _vp, _vp]),
+    "rac_dsp_project_sum": (ctypes.c_int64, [_i, _vp, _vp]),
+    "rac_dsp_eval_dev": (_i, [_i, _l, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "rac_dsp_systolic_dev": (_i, [_i, _i, _vp, _vp, _vp, _vp]),
     "rac_fp16_to_fp32": (_f, [ctypes.c_uint16]),
     "rac_fp32_to_fp16": (ctypes.c_uint16, [_f]),
     "rac_last_error": (ctypes.c_char_p, []),

@@ -571,6 +571,167 @@ RAC_EXPORT int rac_q8_0_dequantize_dev(const void* src, float* dst, long rows, i
                      "rac_q8_0_dequantize_dev launch");
 }
 
+// ── RAC-DSP integer CORDIC engine (sim/rac_dsp_core.h) ──────────────────
+
+// ROM contents: generated by the rule of rtl/gen_coarse_lut.py:27-123 (LUT
+// entry k = direction bits of a 10-step double-precision circular CORDIC
+// driving (k - 512 + 0.5) pi / 1024 to zero; atan / atanh constants
+// round(v / pi * 2^63)), or replaced by rac_load_all_roms.  A copy lives
+// in device memory per GPU, refreshed when the host contents change.
+static std::mutex g_dsp_mutex;
+static DspRoms g_dsp_roms;
+static int g_dsp_version = 0;            // 0: not generated yet
+struct DspDeviceRoms {
+    DspRoms* ptr = nullptr;
+    int version = -1;
+};
+static DspDeviceRoms g_dsp_dev[64];
+
+static int64_t q063_frac_pi(double v) { return (int64_t)nearbyint(v / M_PI * 9223372036854775808.0); }
+
+static void dsp_derive(DspRoms& r);
+
+static void dsp_generate_roms(DspRoms& r) {
+    for (int k = 0; k < kDspLut; k++) {
+        double z = (k - kDspLut / 2 + 0.5) * M_PI / kDspLut;
+        unsigned bits = 0;
+        for (int i = 0; i < kDspLutBits; i++) {
+            const double step = atan(ldexp(1.0, -i));
+            if (z >= 0.0) { z -= step; bits |= 1u << i; }
+            else z += step;
+        }
+        r.lut[k] = (uint16_t)bits;
+    }
+    for (int i = 0; i < kDspAtan; i++) r.atan_rom[i] = q063_frac_pi(atan(ldexp(1.0, -i)));
+    for (int i = 0; i < kDspRes; i++) r.atanh_rom[i] = q063_frac_pi(atanh(ldexp(1.0, -(kDspResStart + i))));
+    dsp_derive(r);
+}
+
+// The coarse stage's z bookkeeping depends only on the LUT word and the atan
+// ROM; sums wrap modulo 2^64, so the table equals the step-by-step update.
+static void dsp_derive(DspRoms& r) {
+    for (int k = 0; k < kDspLut; k++) {
+        uint64_t za = 0;
+        for (int i = 0; i < kDspLutBits; i++)
+            za = ((r.lut[k] >> i) & 1u) ? za + (uint64_t)r.atan_rom[i] : za - (uint64_t)r.atan_rom[i];
+        r.coarse_z[k] = (int64_t)za;
+    }
+}
+
+// Device copy of the current ROMs for the current device (allocated once per
+// device and kept for the life of the process).
+static int dsp_device_roms(const DspRoms** out, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_dsp_mutex);
+    if (g_dsp_version == 0) {
+        dsp_generate_roms(g_dsp_roms);
+        g_dsp_version = 1;
+    }
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= 64) return fail(RAC_ERR_DEVICE, "RAC-DSP: device index %d out of range", dev);
+    DspDeviceRoms& d = g_dsp_dev[dev];
+    if (!d.ptr) {
+        if (hipMalloc(&d.ptr, sizeof(DspRoms)) != hipSuccess) {
+            (void)hipGetLastError();
+            d.ptr = nullptr;
+            return fail(RAC_ERR_ALLOC, "RAC-DSP: ROM buffer allocation failed");
+        }
+    }
+    if (d.version != g_dsp_version) {
+        rc = check_hip(hipMemcpyAsync(d.ptr, &g_dsp_roms, sizeof(DspRoms), hipMemcpyHostToDevice, s),
+                       "RAC-DSP ROM upload");
+        if (!rc) rc = check_hip(hipStreamSynchronize(s), "RAC-DSP ROM upload");
+        if (rc) return rc;
+        d.version = g_dsp_version;
+    }
+    *out = d.ptr;
+    return RAC_OK;
+}
+
+// rac_load_hex_lut (sim/rac_dsp_core.c:56-72): $readmemh-style lines; blank
+// lines and // comments skipped; returns the count parsed or -1.
+RAC_EXPORT int rac_load_hex_lut(const char* path, uint64_t* out, int expected) {
+    if (!path || !out) return fail(RAC_ERR_NULL_PTR, "rac_load_hex_lut: null argument");
+    FILE* f = fopen(path, "r");
+    if (!f) return fail(-1, "rac_load_hex_lut: cannot open %s", path);
+    char line[256];
+    int n = 0;
+    while (fgets(line, sizeof(line), f)) {
+        const char* p = line;
+        while (*p == ' ' || *p == '\t') p++;
+        if (*p == '\0' || *p == '\n' || (*p == '/' && p[1] == '/')) continue;
+        unsigned long long v = 0;
+        if (sscanf(p, "%llx", &v) != 1) continue;
+        if (n < expected) out[n++] = (uint64_t)v;
+    }
+    fclose(f);
+    return n;
+}
+
+// rac_load_all_roms (sim/rac_dsp_core.c:74-89): replaces the ROMs used by
+// every later RAC-DSP call; 0 on success, 1/2/3 for the LUT/atan/atanh file.
+RAC_EXPORT int rac_load_all_roms(const char* coarse_lut_path, const char* atan_path, const char* atanh_path) {
+    uint64_t lut[kDspLut] = {0}, at[kDspAtan] = {0}, ath[kDspRes] = {0};
+    if (rac_load_hex_lut(coarse_lut_path, lut, kDspLut) < 0) return 1;
+    if (rac_load_hex_lut(atan_path, at, kDspAtan) < 0) return 2;
+    if (rac_load_hex_lut(atanh_path, ath, kDspRes) < 0) return 3;
+    std::lock_guard<std::mutex> lock(g_dsp_mutex);
+    for (int i = 0; i < kDspLut; i++) g_dsp_roms.lut[i] = (uint16_t)(lut[i] & 0x3ffu);
+    for (int i = 0; i < kDspAtan; i++) g_dsp_roms.atan_rom[i] = (int64_t)at[i];
+    for (int i = 0; i < kDspRes; i++) g_dsp_roms.atanh_rom[i] = (int64_t)ath[i];
+    dsp_derive(g_dsp_roms);
+    g_dsp_version = g_dsp_version + 1 + (g_dsp_version == 0);
+    return 0;
+}
+
+// Replaces the ROMs from memory (the reference lets callers assign its ROM
+// globals directly, sim/rac_dsp_core.h:23-27).  Any pointer may be null to
+// keep that ROM.
+RAC_EXPORT void rac_dsp_set_roms(const uint64_t* lut, const int64_t* atan_rom, const int64_t* atanh_rom) {
+    std::lock_guard<std::mutex> lock(g_dsp_mutex);
+    if (g_dsp_version == 0) dsp_generate_roms(g_dsp_roms);
+    if (lut) for (int i = 0; i < kDspLut; i++) g_dsp_roms.lut[i] = (uint16_t)(lut[i] & 0x3ffu);
+    if (atan_rom) for (int i = 0; i < kDspAtan; i++) g_dsp_roms.atan_rom[i] = atan_rom[i];
+    if (atanh_rom) for (int i = 0; i < kDspRes; i++) g_dsp_roms.atanh_rom[i] = atanh_rom[i];
+    dsp_derive(g_dsp_roms);
+    g_dsp_version = g_dsp_version + 1 + (g_dsp_version == 0);
+}
+
+// Host copy of the ROMs in use (generated ones unless replaced).
+RAC_EXPORT void rac_dsp_get_roms(uint64_t* lut, int64_t* atan_rom, int64_t* atanh_rom) {
+    std::lock_guard<std::mutex> lock(g_dsp_mutex);
+    if (g_dsp_version == 0) {
+        dsp_generate_roms(g_dsp_roms);
+        g_dsp_version = 1;
+    }
+    if (lut) for (int i = 0; i < kDspLut; i++) lut[i] = g_dsp_roms.lut[i];
+    if (atan_rom) for (int i = 0; i < kDspAtan; i++) atan_rom[i] = g_dsp_roms.atan_rom[i];
+    if (atanh_rom) for (int i = 0; i < kDspRes; i++) atanh_rom[i] = g_dsp_roms.atanh_rom[i];
+}
+
+RAC_EXPORT int rac_dsp_eval_dev(int op, long n, const int64_t* x, const int64_t* y, const int64_t* z, int64_t* xo,
+                                int64_t* yo, int64_t* zo, void* stream) {
+    if (!x || !z || !xo) return fail(RAC_ERR_NULL_PTR, "rac_dsp_eval_dev: x, z and xo are required");
+    if (n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_dsp_eval_dev: negative count");
+    if (n == 0) return RAC_OK;
+    const DspRoms* roms = nullptr;
+    int rc = dsp_device_roms(&roms, (hipStream_t)stream);
+    if (rc) return rc;
+    return check_hip(dsp_eval_launch(op, n, x, y, z, xo, yo, zo, roms, (hipStream_t)stream),
+                     "rac_dsp_eval_dev launch");
+}
+
+RAC_EXPORT int rac_dsp_systolic_dev(int N, int K, const int64_t* W, const int64_t* X, int64_t* Y, void* stream) {
+    if (!W || !X || !Y) return fail(RAC_ERR_NULL_PTR, "rac_dsp_systolic_dev: null buffer");
+    if (N <= 0 || K <= 0 || (long)N * N > 2147483647L || (long)N * K > 2147483647L)
+        return fail(RAC_ERR_INVALID_DIM, "rac_dsp_systolic_dev: need N, K > 0 and N*N, N*K < 2^31");
+    const DspRoms* roms = nullptr;
+    int rc = dsp_device_roms(&roms, (hipStream_t)stream);
+    if (rc) return rc;
+    return check_hip(dsp_systolic_launch(N, K, W, X, Y, roms, (hipStream_t)stream), "rac_dsp_systolic_dev launch");
+}
+
 // ═════════════════ reference launcher ABI (rac_kernels.hip) ═══════════════
 
 RAC_EXPORT void rac_launch_nn_iters(const float* A, const float* B, float* C, int M, int N, int K,
@@ -979,6 +1140,70 @@ RAC_EXPORT int rac_q8_0_gemv(const float* input, const void* weight, const float
     if (!rc) rc = rac_q8_0_gemv_dev(a.f(), w.dev, bb.f(), o.f(), 1, N, K, act, s);
     if (!rc) rc = o.copy_out(s);
     return finish_sync(s, rc);
+}
+
+// ── RAC-DSP with the sim/rac_dsp_core.h signatures (host or device) ─────
+
+static int dsp_sync(int op, long n, const int64_t* x, const int64_t* y, const int64_t* z, int64_t* xo, int64_t* yo,
+                    int64_t* zo) {
+    if (n <= 0) return RAC_OK;
+    hipStream_t s = g_stream.load();
+    const size_t b = sizeof(int64_t) * (size_t)n;
+    Staged sx, sy, sz, ox, oy, oz;
+    int rc = sx.bind(x, b, true, s);
+    if (!rc) rc = sy.bind(y, b, true, s);
+    if (!rc) rc = sz.bind(z, b, true, s);
+    if (!rc) rc = ox.bind(xo, b, false, s);
+    if (!rc) rc = oy.bind(yo, b, false, s);
+    if (!rc) rc = oz.bind(zo, b, false, s);
+    if (!rc) rc = rac_dsp_eval_dev(op, n, static_cast<const int64_t*>(sx.dev), static_cast<const int64_t*>(sy.dev),
+                                   static_cast<const int64_t*>(sz.dev), static_cast<int64_t*>(ox.dev),
+                                   static_cast<int64_t*>(oy.dev), static_cast<int64_t*>(oz.dev), s);
+    if (!rc) rc = ox.copy_out(s);
+    if (!rc) rc = oy.copy_out(s);
+    if (!rc) rc = oz.copy_out(s);
+    return finish_sync(s, rc);
+}
+
+// sim/rac_dsp_core.h:41-42
+RAC_EXPORT void rac_dsp_eval(int64_t x_in, int64_t y_in, int64_t z_in, int op, int64_t* x_out, int64_t* y_out,
+                             int64_t* z_out) {
+    if (!x_out || !y_out || !z_out) { fail(RAC_ERR_NULL_PTR, "rac_dsp_eval: null output"); return; }
+    int64_t xo = 0, yo = 0, zo = 0;
+    if (dsp_sync(op, 1, &x_in, &y_in, &z_in, &xo, &yo, &zo) == RAC_OK) {
+        *x_out = xo;
+        *y_out = yo;
+        *z_out = zo;
+    }
+}
+
+// sim/rac_dsp_core.h:48-50: x_out[i] = project(xs[i], 0, zs[i]).x
+RAC_EXPORT void rac_dsp_project_batch(int n, const int64_t* xs, const int64_t* zs, int64_t* x_out) {
+    if (!xs || !zs || !x_out) { fail(RAC_ERR_NULL_PTR, "rac_dsp_project_batch: null buffer"); return; }
+    (void)dsp_sync(1, n, xs, nullptr, zs, x_out, nullptr, nullptr);
+}
+
+// sim/rac_dsp_core.h:57-58: sum of the n projections (wrapping int64)
+RAC_EXPORT int64_t rac_dsp_project_sum(int n, const int64_t* xs, const int64_t* zs) {
+    if (!xs || !zs) { fail(RAC_ERR_NULL_PTR, "rac_dsp_project_sum: null buffer"); return 0; }
+    if (n <= 0) return 0;
+    hipStream_t s = g_stream.load();
+    const size_t b = sizeof(int64_t) * (size_t)n;
+    // the n projections run on the GPU; their wrapping sum is taken here
+    std::string buf(b, '\0');
+    Staged sx, sz, ox;
+    int rc = sx.bind(xs, b, true, s);
+    if (!rc) rc = sz.bind(zs, b, true, s);
+    if (!rc) rc = ox.bind(&buf[0], b, false, s);
+    if (!rc) rc = rac_dsp_eval_dev(1, n, static_cast<const int64_t*>(sx.dev), nullptr,
+                                   static_cast<const int64_t*>(sz.dev), static_cast<int64_t*>(ox.dev), nullptr,
+                                   nullptr, s);
+    if (!rc) rc = ox.copy_out(s);
+    if (finish_sync(s, rc) != RAC_OK) return 0;
+    uint64_t sum = 0;
+    const int64_t* v = reinterpret_cast<const int64_t*>(buf.data());
+    for (int i = 0; i < n; i++) sum += (uint64_t)v[i];
+    return (int64_t)sum;
 }
 
 // ── context (rac.h:85-88; the reference's HIP backend is a stub,

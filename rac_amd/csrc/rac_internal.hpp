@@ -3,6 +3,7 @@
 // arguments before calling and returns the launch status.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace rac {
 
@@ -96,6 +97,23 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
                           int K, int act, hipStream_t s);
 hipError_t q8_quantize_launch(const float* src, uint8_t* dst, long nblocks, hipStream_t s);
 hipError_t q8_dequantize_launch(const uint8_t* src, float* dst, long nblocks, hipStream_t s);
+// RAC-DSP integer CORDIC engine (sim/rac_dsp_core.h geometry).
+constexpr int kDspLutBits = 10;
+constexpr int kDspLut = 1 << kDspLutBits;
+constexpr int kDspRes = 9;
+constexpr int kDspResStart = 8;
+constexpr int kDspAtan = kDspResStart + kDspRes;
+struct DspRoms {
+    uint16_t lut[kDspLut];        // 10-bit direction words
+    int64_t coarse_z[kDspLut];    // angle the coarse stage applies for each word:
+                                  // wrapping sum of +-atan_rom[i] by its bits
+    int64_t atan_rom[kDspAtan];   // atan(2^-i), Q0.63 fractions of pi
+    int64_t atanh_rom[kDspRes];   // atanh(2^-(8+i)), same units
+};
+hipError_t dsp_eval_launch(int op, long n, const int64_t* x, const int64_t* y, const int64_t* z, int64_t* xo,
+                           int64_t* yo, int64_t* zo, const DspRoms* roms, hipStream_t s);
+hipError_t dsp_systolic_launch(int N, int K, const int64_t* W, const int64_t* X, int64_t* Y, const DspRoms* roms,
+                               hipStream_t s);
 hipError_t sincos_launch(const float* theta, float* s_out, float* c_out, long count,
                          hipStream_t s);
 

@@ -725,6 +725,55 @@ def q8_gemv(x: torch.Tensor, wq: torch.Tensor, bias: Optional[torch.Tensor] = No
     return out.reshape(*lead, N)
 
 
+# ── RAC-DSP fixed-point engine (sim/rac_dsp_core.h) ──────────────────────
+
+DSP_OPS = {"rotate": 0, "project": 1, "vectoring": 2, "hyperbolic": 3}
+
+
+def _require_i64(t: torch.Tensor, what: str) -> None:
+    _require_gpu(t, what)
+    if t.dtype != torch.int64:
+        raise RuntimeError(f"RAC: {what} must be int64 (Q32.32 / Q0.63 fixed point)")
+
+
+def dsp_eval(op, x: torch.Tensor, z: torch.Tensor, y: Optional[torch.Tensor] = None
+             ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(x, y, z) outputs of the RAC-DSP engine (rac_dsp_core.c:95-149) for
+    every element: x, y in Q32.32, z in Q0.63 fractions of pi (int64); y
+    defaults to 0.  op: 0..3 or a DSP_OPS name."""
+    op = DSP_OPS[op] if isinstance(op, str) else int(op)
+    _require_i64(x, "x")
+    _require_i64(z, "z")
+    if y is not None:
+        _require_i64(y, "y")
+        if y.shape != x.shape:
+            raise RuntimeError("RAC: x, y, z shapes differ")
+        y = y.contiguous()
+    if z.shape != x.shape:
+        raise RuntimeError("RAC: x, y, z shapes differ")
+    x, z = x.contiguous(), z.contiguous()
+    xo, yo, zo = (torch.empty_like(x) for _ in range(3))
+    check(_lib.load().rac_dsp_eval_dev(op, x.numel(), x.data_ptr(), y.data_ptr() if y is not None else None,
+                                       z.data_ptr(), xo.data_ptr(), yo.data_ptr(), zo.data_ptr(), _stream(x)),
+          "rac_dsp_eval_dev")
+    return xo, yo, zo
+
+
+def dsp_systolic(W: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
+    """Weight-stationary systolic product of rac_systolic_ref.c:40-55 for a
+    batch of activations: Y[k, c] = sum_r project(X[k, r], 0, W[r, c]).x
+    (W [N, N] angles in Q0.63, X [K, N] in Q32.32, wrapping int64 sums)."""
+    _require_i64(W, "W")
+    _require_i64(X, "X")
+    if W.dim() != 2 or W.size(0) != W.size(1) or X.dim() != 2 or X.size(1) != W.size(0):
+        raise RuntimeError("RAC: systolic shapes must be W [N, N], X [K, N]")
+    W, X = W.contiguous(), X.contiguous()
+    Y = torch.empty_like(X)
+    check(_lib.load().rac_dsp_systolic_dev(W.size(0), X.size(0), W.data_ptr(), X.data_ptr(), Y.data_ptr(),
+                                           _stream(X)), "rac_dsp_systolic_dev")
+    return Y
+
+
 __all__ = [
     "MODE_FAST", "MODE_CORDIC", "MODE_SHIFTADD", "RACError",
     "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
@@ -734,4 +783,5 @@ __all__ = [
     "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
     "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
     "q8_quantize", "q8_dequantize", "q8_gemv", "Q8_BLOCK_BYTES",
+    "dsp_eval", "dsp_systolic", "DSP_OPS",
 ]

@@ -7,7 +7,7 @@ oracle/ref_probe.c.  Every value below is produced by reference code; the
 inputs come from tests/raclib.py's seeded generator and are stored too, so
 the fixtures are self-contained data (nothing of the reference's source).
 
-    python tests/golden/make_golden.py [core] [prims] [attention] [q8]
+    python tests/golden/make_golden.py [core] [prims] [attention] [q8] [dsp]
 
 Outputs (tests/golden/):
   tables.json            reference CORDIC tables (rac_cpu.c:20-52)
@@ -26,6 +26,9 @@ Outputs (tests/golden/):
                          rac_inner, rac_outer, rac_dct
   attention.npz          rac_scaled_dot_attention on [2,3,16,8], with and
                          without causal / additive mask
+  dsp.npz                RAC-DSP integer CORDIC (sim/rac_dsp_core.c with the
+                         rtl/*.mem ROMs): ROM contents, rac_dsp_eval for
+                         ops 0-3, a 16x16 systolic product
   q8.npz                 rac_fp16_to_fp32 / rac_fp32_to_fp16 samples,
                          rac_q8_0_quantize_matrix of a 40x512 matrix, and
                          rac_q8_0_gemv with each activation, +- bias
@@ -56,6 +59,8 @@ def main(sections) -> None:
         write_attention(r)
     if "q8" in sections:
         write_q8(r)
+    if "dsp" in sections:
+        write_dsp(r)
     print("golden fixtures written to", HERE)
 
 
@@ -263,5 +268,47 @@ def write_q8(r) -> None:
                         x=x, bias=bias, **outs)
 
 
+def write_dsp(r) -> None:
+    """RAC-DSP integer CORDIC model (sim/rac_dsp_core.c) with the ROMs of
+    rtl/*.mem: the ROM contents, rac_dsp_eval on 1500 vectors per op, and a
+    16 x 16 weight-stationary systolic product (sim/rac_systolic_ref.c) of
+    3 input vectors through rac_dsp_project_sum."""
+    rtl = "/root/reference/rtl"
+    assert r.rac_load_all_roms(*(os.path.join(rtl, f).encode() for f in
+                                 ("cordic_coarse_lut.mem", "cordic_atan.mem", "cordic_atanh.mem"))) == 0
+    lib = C.CDLL(rl.REF_SO)
+    lut = np.ctypeslib.as_array((C.c_uint64 * 1024).in_dll(lib, "rac_coarse_lut")).copy()
+    atan_rom = np.ctypeslib.as_array((C.c_int64 * 17).in_dll(lib, "rac_atan_rom")).copy()
+    atanh_rom = np.ctypeslib.as_array((C.c_int64 * 9).in_dll(lib, "rac_atanh_tab")).copy()
+    rng = np.random.default_rng(20261204)
+    n = 1500
+    x = rng.integers(-2 ** 40, 2 ** 40, n, dtype=np.int64)
+    y = rng.integers(-2 ** 40, 2 ** 40, n, dtype=np.int64)
+    z = rng.integers(-2 ** 63, 2 ** 63 - 1, n, dtype=np.int64)
+    # quadrant boundaries, zero, and extreme magnitudes
+    z[:8] = [0, 2 ** 62, -2 ** 62, 2 ** 62 - 1, -2 ** 62 - 1, -2 ** 63, 2 ** 63 - 1, 1]
+    x[8:16] = [2 ** 62, -2 ** 62, 2 ** 63 - 1, -2 ** 63, 0, 1, -1, 2 ** 32]
+    y[8:16] = [0, 2 ** 61, -2 ** 63, 2 ** 63 - 1, 0, -1, 1, 0]
+    outs = {}
+    a, b, c = C.c_int64(), C.c_int64(), C.c_int64()
+    for op in range(4):
+        res = np.zeros((n, 3), np.int64)
+        for i in range(n):
+            r.rac_dsp_eval(int(x[i]), int(y[i]), int(z[i]), op, C.byref(a), C.byref(b), C.byref(c))
+            res[i] = (a.value, b.value, c.value)
+        outs[f"op{op}"] = res
+    N, K = 16, 3
+    W = rng.integers(-2 ** 63, 2 ** 63 - 1, (N, N), dtype=np.int64)
+    X = rng.integers(-2 ** 34, 2 ** 34, (K, N), dtype=np.int64)
+    Y = np.zeros((K, N), np.int64)
+    for k in range(K):
+        for col in range(N):
+            zc = np.ascontiguousarray(W[:, col])
+            xk = np.ascontiguousarray(X[k])
+            Y[k, col] = r.rac_dsp_project_sum(N, rl.p(xk), rl.p(zc))
+    np.savez_compressed(os.path.join(HERE, "dsp.npz"), lut=lut, atan=atan_rom, atanh=atanh_rom, x=x, y=y, z=z,
+                        W=W, X=X, Y=Y, **outs)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1:] or ["core", "prims", "attention", "q8"])
+    main(sys.argv[1:] or ["core", "prims", "attention", "q8", "dsp"])

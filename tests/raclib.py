@@ -71,6 +71,11 @@ _ORACLE_SIGS = {
     "orc_q8_0_dequantize": (None, [_vp, _vp, _l, _i]),
     "orc_q8_0_block_dot": (_f, [_vp, _vp]),
     "orc_q8_0_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i]),
+    "orc_dsp_gen_roms": (None, [_vp, _vp, _vp]),
+    "orc_dsp_set_roms": (None, [_vp, _vp, _vp]),
+    "orc_dsp_eval": (None, [C.c_int64, C.c_int64, C.c_int64, _i, _vp, _vp, _vp]),
+    "orc_dsp_eval_batch": (None, [_i, _l, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "orc_dsp_systolic": (None, [_i, _i, _vp, _vp, _vp]),
     "orc_check_chain_all_mantissas": (_l, [_i, _i]),
     "orc_check_projection_identity": (_l, [_i, _l, C.c_uint64]),
 }
@@ -110,6 +115,10 @@ _REF_SIGS = {
     "rac_inner": (_f, [_vp, _vp, _i]),
     "rac_outer": (None, [_vp, _vp, _vp, _i, _i]),
     "rac_scaled_dot_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "rac_load_all_roms": (_i, [C.c_char_p, C.c_char_p, C.c_char_p]),
+    "rac_dsp_eval": (None, [C.c_int64, C.c_int64, C.c_int64, _i, _vp, _vp, _vp]),
+    "rac_dsp_project_sum": (C.c_int64, [_i, _vp, _vp]),
+    "rac_dsp_project_batch": (None, [_i, _vp, _vp, _vp]),
     "rac_fp16_to_fp32": (_f, [C.c_uint16]),
     "rac_fp32_to_fp16": (C.c_uint16, [_f]),
     "rac_q8_0_quantize_matrix": (None, [_vp, _vp, _i, _i]),
@@ -326,3 +335,11 @@ def orc_q8_gemv(x, wq, bias, act, contract=1):
     assert oracle().orc_q8_0_gemv(p(x), p(np.ascontiguousarray(wq)), p(b) if b is not None else None, p(out),
                                   M, N, K, act, contract) == 0
     return out
+
+
+def orc_dsp_batch(op, x, y, z):
+    x, y, z = (np.ascontiguousarray(t, np.int64) for t in (x, y, z))
+    n = x.size
+    xo, yo, zo = (np.zeros(n, np.int64) for _ in range(3))
+    oracle().orc_dsp_eval_batch(op, n, p(x), p(y), p(z), p(xo), p(yo), p(zo))
+    return xo, yo, zo

@@ -16,7 +16,7 @@ import pytest
 import raclib as rl
 
 ROOT = rl.ROOT
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h", "rac_dsp.h")]
 
 
 def declared_functions():
@@ -54,7 +54,7 @@ def test_python_binding_covers_headers():
 
 def test_headers_compile_and_link_as_c(tmp_path):
     src = tmp_path / "t.c"
-    src.write_text('#include "rac.h"\n#include "rac_ext.h"\n#include "rac_q8_0.h"\n'
+    src.write_text('#include "rac.h"\n#include "rac_ext.h"\n#include "rac_q8_0.h"\n#include "rac_dsp.h"\n'
                    "int main(void){ rac_set_cordic_iters(8); return rac_get_cordic_iters() == 8 ? 0 : 1; }\n")
     exe = tmp_path / "t"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
@@ -188,3 +188,72 @@ def test_q8_argument_errors_before_device(lib):
     assert lib.rac_q8_0_gemv(None, a, None, a, 4, 64, 0) == -1
     assert lib.rac_q8_0_gemv_dev(a, a, None, a, 1, 4, 64, 9, None) == -2   # act
     assert lib.rac_q8_0_quantize_dev(a, a, 0, 64, None) == -2
+
+
+def _dsp_roms(lib):
+    lut, at, ath = np.zeros(1024, np.uint64), np.zeros(17, np.int64), np.zeros(9, np.int64)
+    lib.rac_dsp_get_roms(rl.p(lut), rl.p(at), rl.p(ath))
+    return lut, at, ath
+
+
+def _write_mem(path, values, comment=True):
+    with open(path, "w") as f:
+        if comment:
+            f.write("// generated for the test\n\n")
+        for v in values:
+            f.write("%016x\n" % (int(v) & (2 ** 64 - 1)))
+
+
+def test_dsp_generated_roms_equal_rtl_mem_golden(lib):
+    d = np.load(os.path.join(rl.GOLDEN, "dsp.npz"))
+    lut, at, ath = _dsp_roms(lib)
+    assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"]) and np.array_equal(ath, d["atanh"])
+
+
+def test_dsp_rom_loaders(lib, tmp_path):
+    d = np.load(os.path.join(rl.GOLDEN, "dsp.npz"))
+    paths = [str(tmp_path / n) for n in ("lut.mem", "atan.mem", "atanh.mem")]
+    lut2 = d["lut"][::-1].copy()
+    at2 = d["atan"] + 3
+    _write_mem(paths[0], lut2)
+    _write_mem(paths[1], at2)
+    _write_mem(paths[2], d["atanh"], comment=False)
+    buf = np.zeros(1024, np.uint64)
+    assert lib.rac_load_hex_lut(paths[0].encode(), rl.p(buf), 1024) == 1024
+    assert np.array_equal(buf, lut2)
+    assert lib.rac_load_hex_lut(paths[1].encode(), rl.p(buf), 5) == 5           # capped at `expected`
+    assert lib.rac_load_hex_lut(str(tmp_path / "absent").encode(), rl.p(buf), 4) == -1
+    try:
+        missing = str(tmp_path / "absent").encode()
+        assert lib.rac_load_all_roms(missing, paths[1].encode(), paths[2].encode()) == 1
+        assert lib.rac_load_all_roms(paths[0].encode(), missing, paths[2].encode()) == 2
+        assert lib.rac_load_all_roms(paths[0].encode(), paths[1].encode(), missing) == 3
+        lut, at, ath = _dsp_roms(lib)                     # failed loads change nothing
+        assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"])
+        assert lib.rac_load_all_roms(*(p.encode() for p in paths)) == 0
+        lut, at, ath = _dsp_roms(lib)
+        assert np.array_equal(lut, lut2) and np.array_equal(at, at2) and np.array_equal(ath, d["atanh"])
+        g_lut, g_at, g_ath = d["lut"], d["atan"], d["atanh"]       # held: rl.p does not own the memory
+        lib.rac_dsp_set_roms(None, rl.p(g_at), None)
+        lut, at, _ = _dsp_roms(lib)
+        assert np.array_equal(lut, lut2) and np.array_equal(at, g_at)
+    finally:
+        g_lut, g_at, g_ath = d["lut"], d["atan"], d["atanh"]
+        lib.rac_dsp_set_roms(rl.p(g_lut), rl.p(g_at), rl.p(g_ath))
+    lut, at, ath = _dsp_roms(lib)
+    assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"]) and np.array_equal(ath, d["atanh"])
+
+
+def test_dsp_argument_errors_before_device(lib):
+    buf = (ctypes.c_int64 * 16)()
+    a = ctypes.addressof(buf)
+    assert lib.rac_dsp_eval_dev(0, 4, None, None, a, a, None, None, None) == -1
+    assert lib.rac_dsp_eval_dev(0, -1, a, None, a, a, None, None, None) == -2
+    assert lib.rac_dsp_eval_dev(0, 0, a, None, a, a, None, None, None) == 0
+    assert lib.rac_dsp_systolic_dev(0, 1, a, a, a, None) == -2
+    assert lib.rac_dsp_systolic_dev(4, 1, None, a, a, None) == -1
+    assert lib.rac_dsp_systolic_dev(65536, 1, a, a, a, None) == -2              # N*N >= 2^31
+    lib.rac_clear_error()
+    assert lib.rac_dsp_project_sum(0, a, a) == 0
+    lib.rac_dsp_project_batch(4, None, a, a)
+    assert b"null" in lib.rac_last_error()

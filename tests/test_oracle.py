@@ -522,3 +522,103 @@ def test_q8_closed_forms(o):
     Z = np.zeros((1, 64), np.float32)
     zq = rl.orc_q8_quantize(Z)
     assert not zq.any()
+
+
+# ── RAC-DSP fixed-point engine (sim/rac_dsp_core.c) ──────────────────────
+
+DSP_UNIT = 2.0 ** 63 / math.pi          # Q0.63 fraction-of-pi units per radian
+K_COARSE = math.prod(math.sqrt(1 + 4.0 ** -i) for i in range(10))
+K_RES = math.prod(math.sqrt(1 + 4.0 ** -s) for s in range(8, 17))
+K_HRES = math.prod(math.sqrt(1 - 4.0 ** -s) for s in range(8, 17))
+
+
+def _coarse_angle(word):
+    """Angle (rad) applied by the 10 coarse micro-rotations of one LUT word."""
+    return sum((1 if (int(word) >> i) & 1 else -1) * math.atan(2.0 ** -i) for i in range(10))
+
+
+def _fold(x, y, theta):
+    """The quadrant fold as geometry: an angle outside [-pi/2, pi/2) is moved
+    by pi and the vector negated (the rotation the pair describes is kept)."""
+    if theta >= math.pi / 2 or theta < -math.pi / 2:
+        theta = theta - math.pi if theta > 0 else theta + math.pi
+        return -x, -y, theta
+    return x, y, theta
+
+
+def test_dsp_roms_vs_rtl_mem_golden(o):
+    d = npz("dsp.npz")
+    lut, at, ath = np.zeros(1024, np.uint64), np.zeros(17, np.int64), np.zeros(9, np.int64)
+    o.orc_dsp_gen_roms(rl.p(lut), rl.p(at), rl.p(ath))
+    assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"]) and np.array_equal(ath, d["atanh"])
+    # every LUT word steers its bin centre to within the last coarse step
+    for k in range(1024):
+        centre = (k - 512 + 0.5) * math.pi / 1024
+        assert abs(_coarse_angle(d["lut"][k]) - centre) <= math.atan(2.0 ** -9) + 1e-12, k
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_dsp_eval_bit_exact_vs_reference_golden(o, op):
+    d = npz("dsp.npz")
+    x, y, z = d["x"], d["y"], d["z"]
+    xo, yo, zo = rl.orc_dsp_batch(op, x, y, z)
+    assert np.array_equal(np.stack([xo, yo, zo], 1), d[f"op{op}"])
+
+
+def test_dsp_systolic_vs_reference_golden(o):
+    d = npz("dsp.npz")
+    W, X = np.ascontiguousarray(d["W"]), np.ascontiguousarray(d["X"])
+    K, N = X.shape
+    Y = np.zeros((K, N), np.int64)
+    o.orc_dsp_systolic(N, K, rl.p(W), rl.p(X), rl.p(Y))
+    assert np.array_equal(Y, d["Y"])
+    # each column sum is K_cordic * sum_r x_r cos(w_rc) up to the residual angle error
+    th = W.astype(np.float64) / DSP_UNIT
+    ref = K_COARSE * K_RES * (X.astype(np.float64) @ np.cos(th))
+    tol = 3e-5 * (np.abs(X).astype(np.float64) @ np.ones_like(th)) + 64 * N
+    assert np.all(np.abs(Y - ref) <= tol)
+
+
+def test_dsp_closed_forms(o):
+    rng = np.random.default_rng(77)
+    n = 3000
+    x = rng.integers(-2 ** 40, 2 ** 40, n, dtype=np.int64)
+    y = rng.integers(-2 ** 40, 2 ** 40, n, dtype=np.int64)
+    z = rng.integers(-2 ** 63, 2 ** 63 - 1, n, dtype=np.int64)
+    xf, yf = x.astype(np.float64), y.astype(np.float64)
+    th = z.astype(np.float64) / DSP_UNIT
+    mag = np.hypot(xf, yf)
+    # rotate / project: K * R(theta) (x, y); z driven to within the last step
+    r0 = rl.orc_dsp_batch(0, x, y, z)
+    r1 = rl.orc_dsp_batch(1, x, y, z)
+    assert all(np.array_equal(a, b) for a, b in zip(r0, r1))
+    K = K_COARSE * K_RES
+    ex, ey = K * (xf * np.cos(th) - yf * np.sin(th)), K * (xf * np.sin(th) + yf * np.cos(th))
+    tol = 3e-5 * mag + 64
+    assert np.all(np.abs(r0[0] - ex) <= tol) and np.all(np.abs(r0[1] - ey) <= tol)
+    assert np.all(np.abs(r0[2] / DSP_UNIT) <= 2 * math.atan(2.0 ** -16))
+    # vectoring (no coarse stage): a vector within the residual range of the
+    # x axis is rotated onto it; z accumulates its angle
+    phi = rng.uniform(-0.007, 0.007, n)
+    xv = rng.integers(2 ** 36, 2 ** 40, n, dtype=np.int64)
+    yv = np.round(xv * np.tan(phi)).astype(np.int64)
+    zv = rng.integers(-2 ** 61, 2 ** 61, n, dtype=np.int64)       # |angle| < pi/4: no fold
+    v = rl.orc_dsp_batch(2, xv, yv, zv)
+    mv = np.hypot(xv.astype(np.float64), yv.astype(np.float64))
+    assert np.all(np.abs(v[0] - K_RES * mv) <= 3e-5 * mv + 64)
+    assert np.all(np.abs(v[1]) <= 3e-5 * mv + 64)
+    assert np.all(np.abs((v[2] - zv) / DSP_UNIT - np.arctan2(yv, xv)) <= 2 * math.atan(2.0 ** -16))
+    # hyperbolic: circular coarse rotation by the LUT angle of the folded z,
+    # then a hyperbolic rotation by the rest of the angle
+    lut = npz("dsp.npz")["lut"]
+    h = rl.orc_dsp_batch(3, x, y, z)
+    for i in range(0, n, 7):
+        a, b, t = _fold(xf[i], yf[i], th[i])
+        k = min(int(math.floor((t + math.pi / 2) / (math.pi / 1024))), 1023)
+        tc = _coarse_angle(lut[k])
+        a, b = K_COARSE * (a * math.cos(tc) - b * math.sin(tc)), K_COARSE * (a * math.sin(tc) + b * math.cos(tc))
+        phi_h = t - tc
+        hx = K_HRES * (a * math.cosh(phi_h) + b * math.sinh(phi_h))
+        hy = K_HRES * (b * math.cosh(phi_h) + a * math.sinh(phi_h))
+        bound = 6e-5 * mag[i] + 64
+        assert abs(h[0][i] - hx) <= bound and abs(h[1][i] - hy) <= bound, i
