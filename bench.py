@@ -317,6 +317,51 @@ def bench_hbm_ops(torch, ext, dev, g):
     print(f"# dsp systolic: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
     del Wd, Xd, Yd
 
+    # safetensors loader: a BF16 [11008, 4096] weight (Llama-7B MLP shape, 90 MB)
+    # in a file in the page cache -> HBM as fp32 and as Q8_0 (wall clock per
+    # call incl. the host copies and PCIe; "GBps" counts file bytes); and the
+    # device-resident conversion kernels alone (bf16 bytes already in HBM:
+    # 2 B read + 4 B written per element for fp32, 2 + 34/32 B for Q8_0)
+    import tempfile
+    Nw, Kw = 11008, 4096
+    wbits = (torch.randn(Nw * Kw, generator=torch.Generator().manual_seed(5)) * 0.02).view(torch.int32)
+    wbits = (wbits >> 16).to(torch.int16)                         # bf16 = top half of the fp32 word
+    raw = wbits.numpy().tobytes()
+    hdr = json.dumps({"w": {"dtype": "BF16", "shape": [Nw, Kw], "data_offsets": [0, len(raw)]}}).encode()
+    tmpd = tempfile.mkdtemp(prefix="rac_st_")
+    pathw = os.path.join(tmpd, "w.safetensors")
+    with open(pathw, "wb") as fh:
+        fh.write(len(hdr).to_bytes(8, "little") + hdr + raw)
+    del raw
+    sfw = ext.SafeTensors(pathw)
+    wf = torch.empty((Nw, Kw), device=dev)
+    wq8 = torch.empty((Nw, Kw // 32, 34), device=dev, dtype=torch.uint8)
+    tw = lib.st_find(sfw._f, b"w")
+    for name, fn in (("st_load_bf16_to_f32_11008x4096",
+                      lambda: chk(lib.rac_st_to_f32_dev(sfw._f, tw, wf.data_ptr(), stream))),
+                     ("st_load_bf16_to_q8_0_11008x4096",
+                      lambda: chk(lib.rac_st_to_q8_0_dev(sfw._f, tw, wq8.data_ptr(), stream)))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / 5
+        out[name] = {"ms": round(t * 1e3, 3), "GBps_file": round(2 * Nw * Kw / t / 1e9, 2)}
+        print(f"# {name}: {t * 1e3:.2f} ms, {2 * Nw * Kw / t / 1e9:.1f} GB/s of file", file=sys.stderr, flush=True)
+    sfw.close()
+    os.remove(pathw)
+    os.rmdir(tmpd)
+    draw = wbits.to(dev)
+    record("st_convert_bf16_to_f32_11008x4096", 6 * Nw * Kw,
+           _events_time(lambda: chk(lib.rac_st_convert_dev(3, draw.data_ptr(), Nw * Kw, wf.data_ptr(), stream)),
+                        reps, torch))
+    record("st_quantize_bf16_to_q8_0_11008x4096", 2 * Nw * Kw + Nw * Kw // 32 * 34,
+           _events_time(lambda: chk(lib.rac_st_quantize_dev(3, draw.data_ptr(), Nw * Kw // 32, wq8.data_ptr(),
+                                                            stream)), reps, torch))
+    del draw, wf, wq8, wbits
+
     # SiLU 16384 x 11008 (n = 16)
     xsilu = torch.randn((16384, 11008), device=dev, generator=g)
     ysilu = torch.empty_like(xsilu)

@@ -1233,3 +1233,37 @@ ORC_API void orc_dsp_systolic(int N, int K, const int64_t *W, const int64_t *X, 
             Y[(size_t)k * N + c] = (int64_t)sum;
         }
 }
+
+/* ── safetensors element conversion (bench/safetensors_reader.c:375-425) ──
+ * dtype codes of safetensors_reader.h:37-49: 1 F32 (copy), 2 F16 (the same
+ * exact widening as rac_fp16_to_fp32, safetensors_reader.c:375-397),
+ * 3 BF16 (bits << 16), 4 F64 ((float) cast on this x86-64 host).  Returns
+ * -1 for any other dtype, as st_to_f32 does. */
+ORC_API int orc_st_to_f32(int dtype, const void *raw, long n, float *out)
+{
+    switch (dtype) {
+    case 1:
+        memcpy(out, raw, (size_t)n * sizeof(float));
+        return 0;
+    case 2: {
+        const uint16_t *h = (const uint16_t *)raw;
+        for (long i = 0; i < n; i++) out[i] = orc_fp16_to_fp32(h[i]);
+        return 0;
+    }
+    case 3: {
+        const uint16_t *h = (const uint16_t *)raw;
+        for (long i = 0; i < n; i++) {
+            uint32_t b = (uint32_t)h[i] << 16;
+            memcpy(&out[i], &b, 4);
+        }
+        return 0;
+    }
+    case 4: {
+        const double *d = (const double *)raw;
+        for (long i = 0; i < n; i++) out[i] = (float)d[i];
+        return 0;
+    }
+    default:
+        return -1;
+    }
+}

@@ -35,6 +35,28 @@ class Vec2(ctypes.Structure):
 
 _v2 = Vec2
 
+ST_MAX_TENSORS, ST_MAX_NAME, ST_MAX_NDIM = 8192, 256, 8
+
+
+class StTensor(ctypes.Structure):
+    """st_tensor (safetensors_reader.h:51-58)."""
+
+    _fields_ = [("name", ctypes.c_char * ST_MAX_NAME), ("dtype", ctypes.c_int), ("ndim", ctypes.c_int),
+                ("shape", ctypes.c_int64 * ST_MAX_NDIM), ("offset", ctypes.c_size_t),
+                ("nbytes", ctypes.c_size_t)]
+
+
+class StFile(ctypes.Structure):
+    """st_file (safetensors_reader.h:60-69)."""
+
+    _fields_ = [("fd", ctypes.c_int), ("mmap_base", ctypes.c_void_p), ("mmap_len", ctypes.c_size_t),
+                ("data_offset", ctypes.c_size_t), ("tensors", ctypes.POINTER(StTensor)),
+                ("n_tensors", ctypes.c_int), ("header_copy", ctypes.c_char_p), ("err", ctypes.c_char * 256)]
+
+
+_stf = ctypes.POINTER(StFile)
+_stt = ctypes.POINTER(StTensor)
+
 # name -> (restype, argtypes)
 _SIGNATURES = {
     # rac_ext.h — device pointers, explicit stream
@@ -80,6 +102,19 @@ _SIGNATURES = {
     "rac_dsp_project_sum": (ctypes.c_int64, [_i, _vp, _vp]),
     "rac_dsp_eval_dev": (_i, [_i, _l, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "rac_dsp_systolic_dev": (_i, [_i, _i, _vp, _vp, _vp, _vp]),
+    # rac_safetensors.h — the reader (safetensors_reader.h:73-96) + device forms
+    "st_open": (_stf, [ctypes.c_char_p, ctypes.c_char_p]),
+    "st_close": (None, [_stf]),
+    "st_find": (_stt, [_stf, ctypes.c_char_p]),
+    "st_data": (_vp, [_stf, _stt]),
+    "st_to_f32": (_i, [_stf, _stt, _vp]),
+    "st_numel": (ctypes.c_size_t, [_stt]),
+    "st_dtype_name": (ctypes.c_char_p, [_i]),
+    "st_dump": (None, [_stf]),
+    "rac_st_to_f32_dev": (_i, [_stf, _stt, _vp, _vp]),
+    "rac_st_to_q8_0_dev": (_i, [_stf, _stt, _vp, _vp]),
+    "rac_st_convert_dev": (_i, [_i, _vp, _l, _vp, _vp]),
+    "rac_st_quantize_dev": (_i, [_i, _vp, _l, _vp, _vp]),
     "rac_fp16_to_fp32": (_f, [ctypes.c_uint16]),
     "rac_fp32_to_fp16": (ctypes.c_uint16, [_f]),
     "rac_last_error": (ctypes.c_char_p, []),

@@ -79,6 +79,17 @@ static int check_hip(hipError_t e, const char* what) {
     return fail(RAC_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
+namespace rac {
+int report(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+int report_hip(hipError_t e, const char* what) { return check_hip(e, what); }
+}  // namespace rac
+
 RAC_EXPORT const char* rac_last_error(void) { return g_last_error; }
 RAC_EXPORT void rac_clear_error(void) { g_last_error[0] = '\0'; }
 
@@ -149,7 +160,8 @@ RAC_EXPORT float rac_rsqrt_gain_inverse(void) { return host_consts().rsqrt_khinv
 
 // ── pointer staging for the synchronous API ──────────────────────────────
 
-static bool is_device_pointer(const void* p) {
+namespace rac {
+bool is_device_ptr(const void* p) {
     if (!p) return false;
     hipPointerAttribute_t attr;
     if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
@@ -158,6 +170,8 @@ static bool is_device_pointer(const void* p) {
     }
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
+}  // namespace rac
+static bool is_device_pointer(const void* p) { return is_device_ptr(p); }
 
 struct Staged {
     void* host = nullptr;     // caller's host pointer (null when device)

@@ -97,6 +97,15 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
                           int K, int act, hipStream_t s);
 hipError_t q8_quantize_launch(const float* src, uint8_t* dst, long nblocks, hipStream_t s);
 hipError_t q8_dequantize_launch(const uint8_t* src, float* dst, long nblocks, hipStream_t s);
+// Error channel of the C ABI (rac_last_error): set the message, return code.
+int report(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int report_hip(hipError_t e, const char* what);     // RAC_ERR_DEVICE (-4) unless hipSuccess
+bool is_device_ptr(const void* p);
+
+// safetensors element conversion (dtype codes of safetensors_reader.h:37-49).
+hipError_t st_convert_launch(int dtype, const void* src, long n, float* dst, hipStream_t s);
+hipError_t st_quantize_launch(int dtype, const void* src, long nblocks, uint8_t* dst, hipStream_t s);
+
 // RAC-DSP integer CORDIC engine (sim/rac_dsp_core.h geometry).
 constexpr int kDspLutBits = 10;
 constexpr int kDspLut = 1 << kDspLutBits;

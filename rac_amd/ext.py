@@ -18,6 +18,8 @@ is no CPU path.
 """
 from __future__ import annotations
 
+import ctypes
+import os
 from typing import List, Optional, Tuple
 
 import numpy as np
@@ -774,6 +776,82 @@ def dsp_systolic(W: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
     return Y
 
 
+# ── safetensors weights into HBM (bench/safetensors_reader.h) ──────────────
+
+class SafeTensors:
+    """A mapped safetensors file whose tensors load straight into device
+    memory: `tensor(name)` as fp32 (F32 / F16 / BF16 / F64 widened on the
+    GPU, bit-exact with the reference reader's st_to_f32), `q8_0(name)` as
+    Q8_0 blocks [rows, K/32, 34] quantized on the GPU in the same pass."""
+
+    def __init__(self, path: str):
+        self._lib = _lib.load()
+        err = ctypes.create_string_buffer(256)
+        self._f = self._lib.st_open(os.fsencode(path), err)
+        if not self._f:
+            raise RACError(f"st_open({path}): {err.value.decode(errors='replace')}")
+        self.path = path
+
+    def close(self) -> None:
+        if self._f:
+            self._lib.st_close(self._f)
+            self._f = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+    def _t(self, name: str):
+        if not self._f:
+            raise RACError("safetensors file is closed")
+        t = self._lib.st_find(self._f, name.encode())
+        if not t:
+            raise KeyError(name)
+        return t
+
+    def names(self) -> List[str]:
+        f = self._f.contents
+        return [f.tensors[i].name.decode() for i in range(f.n_tensors)]
+
+    def shape(self, name: str) -> Tuple[int, ...]:
+        t = self._t(name).contents
+        return tuple(int(t.shape[k]) for k in range(t.ndim))
+
+    def dtype(self, name: str) -> str:
+        return self._lib.st_dtype_name(self._t(name).contents.dtype).decode()
+
+    def tensor(self, name: str, device=None) -> torch.Tensor:
+        t = self._t(name)
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        out = torch.empty(self.shape(name), dtype=torch.float32, device=dev)
+        if out.numel():
+            check(self._lib.rac_st_to_f32_dev(self._f, t, out.data_ptr(), _stream(out)), "rac_st_to_f32_dev")
+        return out
+
+    def q8_0(self, name: str, device=None) -> torch.Tensor:
+        t = self._t(name)
+        shape = self.shape(name)
+        if not shape or shape[-1] % 32:
+            raise RACError(f"{name}: Q8_0 needs a last dimension that is a multiple of 32 (shape {shape})")
+        K = shape[-1]
+        rows = 1
+        for d in shape[:-1]:
+            rows *= d
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        out = torch.empty((rows, K // 32, Q8_BLOCK_BYTES), dtype=torch.uint8, device=dev)
+        if out.numel():
+            check(self._lib.rac_st_to_q8_0_dev(self._f, t, out.data_ptr(), _stream(out)), "rac_st_to_q8_0_dev")
+        return out
+
+
 __all__ = [
     "MODE_FAST", "MODE_CORDIC", "MODE_SHIFTADD", "RACError",
     "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
@@ -783,5 +861,5 @@ __all__ = [
     "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
     "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
     "q8_quantize", "q8_dequantize", "q8_gemv", "Q8_BLOCK_BYTES",
-    "dsp_eval", "dsp_systolic", "DSP_OPS",
+    "dsp_eval", "dsp_systolic", "DSP_OPS", "SafeTensors",
 ]

@@ -61,6 +61,8 @@ def main(sections) -> None:
         write_q8(r)
     if "dsp" in sections:
         write_dsp(r)
+    if "st" in sections:
+        write_st(r)
     print("golden fixtures written to", HERE)
 
 
@@ -310,5 +312,107 @@ def write_dsp(r) -> None:
                         W=W, X=X, Y=Y, **outs)
 
 
+def st_sample():
+    """The sample safetensors file: every dtype the reader converts (with
+    subnormals, infinities, NaN payloads, -0), an integer tensor it refuses,
+    a 0-d and an empty tensor, metadata and an unknown per-tensor field."""
+    rng = np.random.default_rng(20261207)
+    f32 = np.array([1.0, -2.5, 0.0, 0.0, np.inf, 0.0], np.float32)
+    f32.view(np.uint32)[2] = 0x7FA00001            # signalling NaN with payload
+    f32.view(np.uint32)[3] = 0x80000000            # -0
+    f32.view(np.uint32)[5] = 0x00000001            # smallest subnormal
+    h = rng.integers(0, 1 << 16, 64, dtype=np.uint64).astype(np.uint16)
+    h[:12] = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7C01, 0x7E00, 0xFE55, 0x3C00]
+    bf = rng.integers(0, 1 << 16, 64, dtype=np.uint64).astype(np.uint16)
+    bf[:8] = [0x0000, 0x8000, 0x0001, 0x7F80, 0xFF80, 0x7F81, 0x7FC0, 0x3F80]
+    d = rng.normal(0, 1, 64) * np.exp(rng.uniform(-30, 30, 64))
+    d[:14] = [0.0, -0.0, np.inf, -np.inf, 1e300, -1e300, 1e-40, -1e-45, 1e-50, 3.4028235677973366e38,
+              1.0000000596046448, 1.0000001788139343, 0.0, 0.0]
+    dv = d.view(np.uint64)
+    dv[12] = 0x7FF0000000000001                     # signalling NaN, low payload
+    dv[13] = 0xFFF8DEADBEEF1234                     # quiet NaN, high payload, negative
+    i8 = np.array([1, -2, 3, -4], np.int8)
+    w = (rng.normal(0, 0.02, (8, 64)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    scalar = np.array(3.0, np.float32)
+    parts = [("f32", "F32", [6], f32.tobytes()), ("f16", "F16", [64], h.tobytes()),
+             ("bf16", "BF16", [2, 32], bf.tobytes()), ("f64", "F64", [2, 32], d.tobytes()),
+             ("i8", "I8", [4], i8.tobytes()), ("model.layers.0.mlp.up_proj.weight", "BF16", [8, 64], w.tobytes()),
+             ("scalar", "F32", [], scalar.tobytes()), ("empty", "F16", [0, 32], b"")]
+    header = {"__metadata__": {"format": "pt", "note": "keys are not tensors {x: [1]}"}}
+    data = b""
+    for name, dt, shape, raw in parts:
+        header[name] = {"dtype": dt, "shape": shape, "data_offsets": [len(data), len(data) + len(raw)]}
+        data += raw
+    header["f32"]["extra"] = [1, [2, 3], {"a": 4}]
+    return rl.st_bytes(header, data), parts
+
+
+def st_malformed():
+    """(name, file bytes) of headers every reader must refuse."""
+    ok_body = '{"dtype":"F32","shape":[1],"data_offsets":[0,4]}'
+    four = b"\0\0\0\0"
+    return [
+        ("not_an_object", rl.st_bytes("[1,2]", four)),
+        ("missing_offsets", rl.st_bytes('{"a":{"dtype":"F32","shape":[1]}}', four)),
+        ("unterminated_key", rl.st_bytes('{"a', four)),
+        ("garbage_after_body", rl.st_bytes('{"a":' + ok_body + ' x}', four)),
+        ("body_not_object", rl.st_bytes('{"a":[1]}', four)),
+        ("header_too_long", (1000).to_bytes(8, "little") + b"{}"),
+        ("too_small", b"\x02\0\0"),
+    ]
+
+
+def write_st(r) -> None:
+    """The compiled reference reader (bench/safetensors_reader.c) on the
+    sample file: its parse of every tensor, st_to_f32 of each (or its -1),
+    rac_q8_0_quantize_matrix of those with a last dimension that is a
+    multiple of 32, and its verdict on each malformed header."""
+    import tempfile
+    blob, parts = st_sample()
+    out = {"sample": np.frombuffer(blob, np.uint8)}
+    recs = []
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "sample.safetensors")
+        with open(path, "wb") as fh:
+            fh.write(blob)
+        err = C.create_string_buffer(256)
+        f = r.st_open(path.encode(), err)
+        assert f, err.value
+        for i in range(f.contents.n_tensors):
+            t = f.contents.tensors[i]
+            recs.append({"name": t.name.decode(), "dtype": t.dtype, "ndim": t.ndim,
+                         "shape": [t.shape[k] for k in range(t.ndim)], "offset": t.offset, "nbytes": t.nbytes})
+        for name, dt, shape, raw in parts:
+            t = r.st_find(f, name.encode())
+            n = int(r.st_numel(t))
+            buf = np.zeros(max(n, 1), np.float32)
+            rc = r.st_to_f32(f, t, rl.p(buf))
+            out[f"rc_{name}"] = np.array(rc)
+            if rc == 0:
+                out[f"f32_{name}"] = buf[:n].copy()
+                if shape and n and shape[-1] % 32 == 0:
+                    K = shape[-1]
+                    q = np.zeros((n // K, K // 32, 34), np.uint8)
+                    src = np.ascontiguousarray(buf[:n])
+                    r.rac_q8_0_quantize_matrix(rl.p(src), rl.p(q), n // K, K)
+                    out[f"q8_{name}"] = q
+        r.st_close(f)
+        bad = st_malformed()
+        verdict = []
+        for i, (name, b) in enumerate(bad):
+            bp = os.path.join(tmp, f"bad{i}.safetensors")
+            with open(bp, "wb") as fh:
+                fh.write(b)
+            g = r.st_open(bp.encode(), err)
+            verdict.append(bool(g))
+            if g:
+                r.st_close(g)
+            out[f"bad_{i}"] = np.frombuffer(b, np.uint8)
+        out["bad_names"] = np.array(json.dumps([n for n, _ in bad]))
+        out["bad_opened"] = np.array(verdict)
+    out["parse"] = np.array(json.dumps(recs))
+    np.savez_compressed(os.path.join(HERE, "st.npz"), **out)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1:] or ["core", "prims", "attention", "q8", "dsp"])
+    main(sys.argv[1:] or ["core", "prims", "attention", "q8", "dsp", "st"])

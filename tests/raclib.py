@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import hashlib
+import json
 import os
 
 import numpy as np
@@ -28,6 +29,24 @@ class Vec2(C.Structure):
 
     _fields_ = [("x", C.c_float), ("y", C.c_float)]
 
+
+class StTensor(C.Structure):
+    """st_tensor (bench/safetensors_reader.h:51-58)."""
+
+    _fields_ = [("name", C.c_char * 256), ("dtype", C.c_int), ("ndim", C.c_int), ("shape", C.c_int64 * 8),
+                ("offset", C.c_size_t), ("nbytes", C.c_size_t)]
+
+
+class StFile(C.Structure):
+    """st_file (bench/safetensors_reader.h:60-69)."""
+
+    _fields_ = [("fd", C.c_int), ("mmap_base", C.c_void_p), ("mmap_len", C.c_size_t), ("data_offset", C.c_size_t),
+                ("tensors", C.POINTER(StTensor)), ("n_tensors", C.c_int), ("header_copy", C.c_char_p),
+                ("err", C.c_char * 256)]
+
+
+_stf, _stt = C.POINTER(StFile), C.POINTER(StTensor)
+ST_DTYPES = {"F32": 1, "F16": 2, "BF16": 3, "F64": 4, "I8": 5, "U8": 6, "I16": 7, "I32": 8, "I64": 9, "BOOL": 10}
 
 _ORACLE_SIGS = {
     "orc_tables": (None, [_vp, _vp, _vp]),
@@ -77,6 +96,7 @@ _ORACLE_SIGS = {
     "orc_dsp_eval_batch": (None, [_i, _l, _vp, _vp, _vp, _vp, _vp, _vp]),
     "orc_dsp_systolic": (None, [_i, _i, _vp, _vp, _vp]),
     "orc_check_chain_all_mantissas": (_l, [_i, _i]),
+    "orc_st_to_f32": (_i, [_i, _vp, _l, _vp]),
     "orc_check_projection_identity": (_l, [_i, _l, C.c_uint64]),
 }
 
@@ -119,6 +139,11 @@ _REF_SIGS = {
     "rac_dsp_eval": (None, [C.c_int64, C.c_int64, C.c_int64, _i, _vp, _vp, _vp]),
     "rac_dsp_project_sum": (C.c_int64, [_i, _vp, _vp]),
     "rac_dsp_project_batch": (None, [_i, _vp, _vp, _vp]),
+    "st_open": (_stf, [C.c_char_p, C.c_char_p]),
+    "st_close": (None, [_stf]),
+    "st_find": (_stt, [_stf, C.c_char_p]),
+    "st_to_f32": (_i, [_stf, _stt, _vp]),
+    "st_numel": (C.c_size_t, [_stt]),
     "rac_fp16_to_fp32": (_f, [C.c_uint16]),
     "rac_fp32_to_fp16": (C.c_uint16, [_f]),
     "rac_q8_0_quantize_matrix": (None, [_vp, _vp, _i, _i]),
@@ -343,3 +368,20 @@ def orc_dsp_batch(op, x, y, z):
     xo, yo, zo = (np.zeros(n, np.int64) for _ in range(3))
     oracle().orc_dsp_eval_batch(op, n, p(x), p(y), p(z), p(xo), p(yo), p(zo))
     return xo, yo, zo
+
+
+# ── safetensors files ───────────────────────────────────────────────────────
+
+def st_bytes(header, data: bytes) -> bytes:
+    """A safetensors file: u64 little-endian header length, header JSON, data."""
+    h = header if isinstance(header, (bytes, str)) else json.dumps(header, separators=(",", ":"))
+    h = h.encode() if isinstance(h, str) else h
+    return len(h).to_bytes(8, "little") + h + data
+
+
+def orc_st_to_f32(dtype: int, raw: bytes, n: int) -> np.ndarray:
+    """The CPU checker's widening of n raw elements (safetensors_reader.c:406-425)."""
+    src = np.frombuffer(raw, np.uint8).copy()
+    out = np.zeros(max(n, 1), np.float32)
+    assert oracle().orc_st_to_f32(dtype, p(src), n, p(out)) == 0
+    return out[:n]

@@ -16,7 +16,8 @@ import pytest
 import raclib as rl
 
 ROOT = rl.ROOT
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h", "rac_dsp.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h", "rac_dsp.h",
+                                                               "rac_safetensors.h")]
 
 
 def declared_functions():
@@ -26,7 +27,7 @@ def declared_functions():
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b([a-z_][a-z0-9_]*)\s*\(", text):
             name = m.group(1)
-            if name.startswith("rac_") and not name.startswith("rac_context"):
+            if (name.startswith("rac_") or name.startswith("st_")) and not name.startswith("rac_context"):
                 names.add(name)
     return sorted(names)
 
@@ -55,6 +56,7 @@ def test_python_binding_covers_headers():
 def test_headers_compile_and_link_as_c(tmp_path):
     src = tmp_path / "t.c"
     src.write_text('#include "rac.h"\n#include "rac_ext.h"\n#include "rac_q8_0.h"\n#include "rac_dsp.h"\n'
+                   '#include "rac_safetensors.h"\n'
                    "int main(void){ rac_set_cordic_iters(8); return rac_get_cordic_iters() == 8 ? 0 : 1; }\n")
     exe = tmp_path / "t"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
@@ -257,3 +259,162 @@ def test_dsp_argument_errors_before_device(lib):
     assert lib.rac_dsp_project_sum(0, a, a) == 0
     lib.rac_dsp_project_batch(4, None, a, a)
     assert b"null" in lib.rac_last_error()
+
+
+# ── safetensors reader (host side: parsing, lookup, argument checks) ─────
+
+def _st_open(lib, path):
+    err = ctypes.create_string_buffer(256)
+    f = lib.st_open(str(path).encode(), err)
+    return f, err.value.decode()
+
+
+def _st_records(f):
+    out = []
+    for i in range(f.contents.n_tensors):
+        t = f.contents.tensors[i]
+        out.append({"name": t.name.decode(), "dtype": t.dtype, "ndim": t.ndim,
+                    "shape": [t.shape[k] for k in range(t.ndim)], "offset": t.offset, "nbytes": t.nbytes})
+    return out
+
+
+def test_st_parse_matches_reference_reader(lib, tmp_path):
+    import json
+    d = np.load(os.path.join(rl.GOLDEN, "st.npz"))
+    path = tmp_path / "sample.safetensors"
+    blob = d["sample"].tobytes()
+    path.write_bytes(blob)
+    f, err = _st_open(lib, path)
+    assert f, err
+    try:
+        assert _st_records(f) == json.loads(str(d["parse"]))
+        hl = int.from_bytes(blob[:8], "little")
+        assert f.contents.data_offset == 8 + hl and f.contents.mmap_len == len(blob)
+        t = lib.st_find(f, b"model.layers.0.mlp.up_proj.weight")
+        assert t and lib.st_numel(t) == 512
+        assert not lib.st_find(f, b"not_there")
+        raw = ctypes.string_at(lib.st_data(f, t), t.contents.nbytes)
+        assert raw == blob[8 + hl + t.contents.offset: 8 + hl + t.contents.offset + t.contents.nbytes]
+        assert lib.st_dtype_name(3) == b"BF16" and lib.st_dtype_name(0) == b"UNKNOWN"
+        assert lib.st_dtype_name(99) == b"UNKNOWN"
+        scalar = lib.st_find(f, b"scalar")
+        assert scalar.contents.ndim == 0 and lib.st_numel(scalar) == 1
+    finally:
+        lib.st_close(f)
+    lib.st_close(None)
+
+
+def test_st_dump_lists_tensors(lib, tmp_path, capfd):
+    d = np.load(os.path.join(rl.GOLDEN, "st.npz"))
+    path = tmp_path / "sample.safetensors"
+    path.write_bytes(d["sample"].tobytes())
+    f, err = _st_open(lib, path)
+    lib.st_dump(f)
+    lib.st_close(f)
+    text = capfd.readouterr().out
+    assert "8 tensors" in text and "model.layers.0.mlp.up_proj.weight" in text and "[8, 64]" in text
+
+
+def test_st_refuses_what_the_reference_refuses(lib, tmp_path):
+    import json
+    d = np.load(os.path.join(rl.GOLDEN, "st.npz"))
+    names = json.loads(str(d["bad_names"]))
+    assert not d["bad_opened"].any()
+    for i, name in enumerate(names):
+        path = tmp_path / f"bad{i}.safetensors"
+        path.write_bytes(d[f"bad_{i}"].tobytes())
+        f, err = _st_open(lib, path)
+        assert not f and err, name
+        assert b"st_open" in lib.rac_last_error()
+    f, err = _st_open(lib, tmp_path / "absent.safetensors")
+    assert not f and "absent" in err
+
+
+def test_st_validates_ranges_and_sizes(lib, tmp_path):
+    """Stricter than the reference reader, which accepts these and later
+    reads past the tensor or the mapping."""
+    cases = {
+        "past_the_end": ({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 4),
+        "size_mismatch": ({"a": {"dtype": "F16", "shape": [3], "data_offsets": [0, 8]}}, b"\0" * 8),
+        "reversed": ({"a": {"dtype": "F32", "shape": [1], "data_offsets": [4, 0]}}, b"\0" * 8),
+        "nine_dims": ({"a": {"dtype": "U8", "shape": [1] * 9, "data_offsets": [0, 1]}}, b"\0"),
+        "negative_dim": ({"a": {"dtype": "U8", "shape": [-1], "data_offsets": [0, 1]}}, b"\0"),
+    }
+    for name, (hdr, data) in cases.items():
+        path = tmp_path / f"{name}.safetensors"
+        path.write_bytes(rl.st_bytes(hdr, data))
+        f, err = _st_open(lib, path)
+        assert not f, name
+    # unknown dtypes are kept (their size is not checked), escaped names raw
+    path = tmp_path / "odd.safetensors"
+    path.write_bytes(rl.st_bytes('{"q\\"x":{"dtype":"F8_E4M3","shape":[3],"data_offsets":[0,3]},"__metadata__":{}}',
+                                 b"abc"))
+    f, err = _st_open(lib, path)
+    assert f, err
+    assert _st_records(f) == [{"name": 'q\\"x', "dtype": 0, "ndim": 1, "shape": [3], "offset": 0, "nbytes": 3}]
+    lib.st_close(f)
+    path.write_bytes(rl.st_bytes("{}", b""))
+    f, err = _st_open(lib, path)
+    assert f and f.contents.n_tensors == 0
+    lib.st_close(f)
+
+
+def test_st_reads_files_written_by_safetensors(lib, tmp_path):
+    torch = pytest.importorskip("torch")
+    st_torch = pytest.importorskip("safetensors.torch")
+    from safetensors import safe_open
+    g = torch.Generator().manual_seed(0)
+    tensors = {
+        "w_bf16": torch.randn(33, 64, generator=g).to(torch.bfloat16),
+        "w_f16": torch.randn(7, 96, generator=g).to(torch.float16),
+        "w_f32": torch.randn(5, 3, 2, generator=g),
+        "w_f64": torch.randn(4, 32, generator=g, dtype=torch.float64),
+        "ids": torch.arange(10, dtype=torch.int32),
+        "mask": torch.ones(6, dtype=torch.bool),
+        "b": torch.zeros(0),
+    }
+    path = tmp_path / "model.safetensors"
+    st_torch.save_file(tensors, str(path), metadata={"format": "pt"})
+    f, err = _st_open(lib, path)
+    assert f, err
+    try:
+        recs = {r["name"]: r for r in _st_records(f)}
+        assert set(recs) == set(tensors)
+        with safe_open(str(path), framework="pt") as sf:
+            for name in tensors:
+                sl = sf.get_slice(name)
+                assert recs[name]["shape"] == list(sl.get_shape()), name
+                assert recs[name]["dtype"] == rl.ST_DTYPES[sl.get_dtype()], name
+        blob = path.read_bytes()
+        base = f.contents.data_offset
+        for name, t in tensors.items():
+            r = recs[name]
+            raw = blob[base + r["offset"]: base + r["offset"] + r["nbytes"]]
+            assert raw == t.contiguous().view(torch.uint8).numpy().tobytes(), name
+    finally:
+        lib.st_close(f)
+
+
+def test_st_argument_errors_before_device(lib, tmp_path):
+    d = np.load(os.path.join(rl.GOLDEN, "st.npz"))
+    path = tmp_path / "sample.safetensors"
+    path.write_bytes(d["sample"].tobytes())
+    f, err = _st_open(lib, path)
+    f2, _ = _st_open(lib, path)
+    buf = (ctypes.c_float * 1024)()
+    a = ctypes.addressof(buf)
+    try:
+        i8 = lib.st_find(f, b"i8")
+        assert lib.st_to_f32(f, i8, a) == -1                             # integer dtype, as the reference
+        assert lib.rac_st_to_f32_dev(f, i8, a, None) == -5
+        assert lib.rac_st_to_q8_0_dev(f, i8, a, None) == -5
+        assert lib.rac_st_to_f32_dev(f, None, a, None) == -1
+        assert lib.rac_st_to_f32_dev(f, lib.st_find(f2, b"f16"), a, None) == -1   # tensor of another file
+        assert b"another file" in lib.rac_last_error() or b"belong" in lib.rac_last_error()
+        assert lib.rac_st_to_q8_0_dev(f, lib.st_find(f, b"f32"), a, None) == -2   # last dim 6
+        assert lib.rac_st_convert_dev(5, a, 4, a, None) == -5
+        assert lib.rac_st_convert_dev(3, None, 4, a, None) == -1
+        assert lib.rac_st_quantize_dev(3, a, -1, a, None) == -2
+    finally:
+        lib.st_close(f)
+        lib.st_close(f2)

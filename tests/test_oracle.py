@@ -622,3 +622,51 @@ def test_dsp_closed_forms(o):
         hy = K_HRES * (b * math.cosh(phi_h) + a * math.sinh(phi_h))
         bound = 6e-5 * mag[i] + 64
         assert abs(h[0][i] - hx) <= bound and abs(h[1][i] - hy) <= bound, i
+
+
+# ── safetensors element conversion (bench/safetensors_reader.c:375-425) ──
+
+ST_GOLDEN_FLOAT = {"f32": 1, "f16": 2, "bf16": 3, "f64": 4, "model.layers.0.mlp.up_proj.weight": 3, "scalar": 1,
+                   "empty": 2}
+
+
+def _st_raw(d, rec):
+    blob = d["sample"].tobytes()
+    hl = int.from_bytes(blob[:8], "little")
+    return blob[8 + hl + rec["offset"]: 8 + hl + rec["offset"] + rec["nbytes"]]
+
+
+def test_st_to_f32_bit_exact_vs_reference_golden(o):
+    d = npz("st.npz")
+    recs = {r["name"]: r for r in json.loads(str(d["parse"]))}
+    for name, dt in ST_GOLDEN_FLOAT.items():
+        rec = recs[name]
+        n = int(np.prod(rec["shape"])) if rec["shape"] else 1
+        got = rl.orc_st_to_f32(dt, _st_raw(d, rec), n)
+        assert np.array_equal(got.view(np.uint32), d[f"f32_{name}"].view(np.uint32)), name
+        if f"q8_{name}" in d:
+            assert np.array_equal(rl.orc_q8_quantize(got.reshape(-1, rec["shape"][-1])), d[f"q8_{name}"]), name
+    raw = np.zeros(8, np.uint8)
+    out = np.zeros(2, np.float32)
+    assert o.orc_st_to_f32(5, rl.p(raw), 2, rl.p(out)) == -1          # I8: refused, as st_to_f32 does
+    assert int(d["rc_i8"]) == -1
+
+
+def test_st_conversions_closed_forms(o):
+    rng = np.random.default_rng(8)
+    # every half: the IEEE widening (numpy's, which keeps NaN payloads)
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = rl.orc_st_to_f32(2, h.tobytes(), h.size)
+    assert np.array_equal(got.view(np.uint32), h.view(np.float16).astype(np.float32).view(np.uint32))
+    # bf16 is the top half of an fp32 word
+    b = rng.integers(0, 1 << 16, 4096, dtype=np.uint32).astype(np.uint16)
+    got = rl.orc_st_to_f32(3, b.tobytes(), b.size)
+    assert np.array_equal(got.view(np.uint32), b.astype(np.uint32) << 16)
+    # f64 -> f32 rounds to nearest even (numpy's cast), finite and infinite inputs
+    v = rng.normal(0, 1, 4096) * np.exp(rng.uniform(-120, 120, 4096))
+    v[:6] = [np.inf, -np.inf, 0.0, -0.0, 1.0 + 2.0 ** -24, 1.0 + 3 * 2.0 ** -24]
+    with np.errstate(over="ignore"):
+        want = v.astype(np.float32)
+    got = rl.orc_st_to_f32(4, v.tobytes(), v.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert got[4] == 1.0 and got[5] == np.float32(1.0 + 2.0 ** -22)
