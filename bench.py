@@ -140,6 +140,47 @@ def bench_gpu(args):
     }
 
 
+def _llama_breakdown(torch, blk, xb):
+    """Per-op milliseconds of one RACLlamaBlock forward: HIP events recorded by
+    forward hooks around each submodule on the current stream.  attention_core
+    is the attention module minus its QKV / RoPE / output-projection children
+    (Q K^T, causal CORDIC softmax, P V and the head transposes); residual_adds
+    is the block minus its four children."""
+    ev = {}
+
+    def mark(name):
+        def pre(_m, _a):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            ev[name] = [e]
+
+        def post(_m, _a, _o):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            ev[name].append(e)
+        return pre, post
+
+    mods = {"block": blk, "rmsnorm1": blk.norm1, "attention": blk.attn, "qkv_proj": blk.attn.qkv,
+            "rope": blk.attn.rope, "out_proj": blk.attn.out_proj, "rmsnorm2": blk.norm2, "ffn": blk.ffn,
+            "fc1_silu": blk.ffn.fc1, "fc2": blk.ffn.fc2}
+    handles = []
+    for name, m in mods.items():
+        pre, post = mark(name)
+        handles += [m.register_forward_pre_hook(pre), m.register_forward_hook(post)]
+    try:
+        blk(xb, is_causal=True)
+        torch.cuda.synchronize()
+    finally:
+        for h in handles:
+            h.remove()
+    ms = {k: v[0].elapsed_time(v[1]) for k, v in ev.items()}
+    res = {k: round(ms[k], 3) for k in ("rmsnorm1", "qkv_proj", "rope", "out_proj", "rmsnorm2", "fc1_silu", "fc2")}
+    res["attention_core"] = round(ms["attention"] - ms["qkv_proj"] - ms["rope"] - ms["out_proj"], 3)
+    res["residual_adds"] = round(ms["block"] - ms["rmsnorm1"] - ms["attention"] - ms["rmsnorm2"] - ms["ffn"], 3)
+    res["total"] = round(ms["block"], 3)
+    return res
+
+
 def bench_hbm_ops(torch, ext, dev, g):
     lib = ext._lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -169,6 +210,17 @@ def bench_hbm_ops(torch, ext, dev, g):
         sm()
         torch.cuda.synchronize()
         record(f"softmax_4096x4096_n{n}", 2 * 4 * R * Cn, _events_time(sm, reps, torch))
+    # torch's own device copy of the same bytes with the same rotation, for
+    # scale: what a generic streaming kernel achieves at this transfer size
+    st_c = {"i": 0}
+
+    def cp():
+        i = st_c["i"] = (st_c["i"] + 1) % 4
+        ys[i].copy_(xs[i])
+
+    cp()
+    torch.cuda.synchronize()
+    record("torch_copy_4096x4096", 2 * 4 * R * Cn, _events_time(cp, reps, torch))
     del xs, ys
 
     # RoPE: Q and K [8,32,4096,128] in place (2 GiB moved per step)
@@ -202,6 +254,15 @@ def bench_hbm_ops(torch, ext, dev, g):
     rms()
     torch.cuda.synchronize()
     record("rmsnorm_16384x4096", 2 * 4 * R * D + 4 * D, _events_time(rms, reps, torch))
+    st_c = {"i": 0}
+
+    def cp():
+        i = st_c["i"] = (st_c["i"] + 1) % 2
+        yr[i].copy_(xr[i])
+
+    cp()
+    torch.cuda.synchronize()
+    record("torch_copy_16384x4096", 2 * 4 * R * D, _events_time(cp, reps, torch))
     del xr, yr
 
     # RACLlamaBlock forward, d=4096, H=32, ff=11008, batch 1,
@@ -223,8 +284,10 @@ def bench_hbm_ops(torch, ext, dev, g):
                 blk(xb, is_causal=True)
                 torch.cuda.synchronize()
                 t = _events_time(lambda: blk(xb, is_causal=True), 2, torch)
+                parts = _llama_breakdown(torch, blk, xb)
             out[f"llama_block_T2048_n{n}"] = {"ms": round(t * 1e3, 2),
-                                              "linear_equiv_TFLOPs": round(644.2e9 / t / 1e12, 3)}
+                                              "linear_equiv_TFLOPs": round(644.2e9 / t / 1e12, 3),
+                                              "per_op_ms": parts}
             print(f"# llama block n={n}: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
     finally:
         rt.rac_set_mode(prev_mode)
@@ -232,7 +295,7 @@ def bench_hbm_ops(torch, ext, dev, g):
     del blk, xb
 
     # attention core of config 5 through RAC (rac_attention_dev): [1, 32, 2048,
-    # 128], causal, CORDIC mode n = 16; Q K^T and P V are 2 x 34.4 GFLOP
+    # 128], causal, CORDIC mode n = 16; Q K^T and P V each 17.2 G causal MACs
     Ba, Ha, Ta, Da = 1, 32, 2048, 128
     qa, ka, va = (torch.randn((Ba, Ha, Ta, Da), device=dev, generator=g) for _ in range(3))
     oa = torch.empty_like(qa)
@@ -245,9 +308,13 @@ def bench_hbm_ops(torch, ext, dev, g):
     attn()
     torch.cuda.synchronize()
     t = _events_time(attn, 3, torch)
-    macs = 2 * Ba * Ha * Ta * Ta * Da
+    # causal work: query row t needs t+1 scores (Q K^T) and t+1 rows of V
+    # (P V), so each product has B*H*D*T(T+1)/2 MACs; the dense count would
+    # credit the masked half that is never computed
+    macs = 2 * Ba * Ha * Da * Ta * (Ta + 1) // 2
     out["attention_core_1x32x2048x128_n16"] = {
-        "ms": round(t * 1e3, 3), "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
+        "ms": round(t * 1e3, 3), "causal_macs": macs,
+        "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
         "valu_frac_of_fp32_peak": round(macs * 2 * 33 / t / 1e12 / PEAK_FP32_TFLOPS, 4)}
     print(f"# attention core n=16: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del qa, ka, va, oa, wsa
