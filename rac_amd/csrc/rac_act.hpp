@@ -34,7 +34,10 @@ __device__ __forceinline__ float elt(float x, int iters, float khinv) {
 
 // elt<OP, NITER> on E values at once: for the exp-based ops with a
 // compile-time step count the E exps run step-major (exp_cordic_vec);
-// bit-identical to E calls of elt<OP, NITER>.
+// bit-identical to E calls of elt<OP, NITER> (up to NaN payloads).  The
+// activations only use e in 1 + e / 1 - e, so the k <= -127 flush is
+// skipped, and SiLU's x / (1 + e) is NaN through x, so its exp skips the
+// NaN pass-through as well.
 template <int OP, int NITER, int E>
 __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
     if constexpr (NITER > 0 && (OP == kEltExp || OP == kEltSilu || OP == kEltSigmoid || OP == kEltTanh)) {
@@ -45,7 +48,8 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
             else if constexpr (OP == kEltTanh) a[e] = -2.0f * __builtin_fabsf(v[e]);
             else a[e] = -v[e];
         }
-        exp_cordic_vec<NITER, E>(a, khinv);
+        constexpr int kOpt = OP == kEltExp ? kExpFull : (OP == kEltSilu ? 0 : kExpNan);
+        exp_cordic_vec<NITER, E, kOpt>(a, khinv);
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if constexpr (OP == kEltExp) v[e] = a[e];

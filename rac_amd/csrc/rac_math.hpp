@@ -147,11 +147,21 @@ __device__ __forceinline__ float shiftadd_mul(float a, float b, int iters) {
 // (p / K_h(n)) 2^k through the exponent field (rac_alu.c:572-581).
 // t = fma(x, 1/ln2, +-0.5) truncated; (x >= 0 ? 0.5 : -0.5) is written as
 // copysign(0.5, x): they differ only at x = -0, where both truncate to 0.
-// t is clamped to +-2^30 (one v_med3) so the conversion is always defined.
+
+// float -> int32 by v_cvt_i32_f32: truncation toward zero, out-of-range
+// values saturate to INT32_MIN / INT32_MAX, NaN gives 0.  C's (int) cast of
+// such values is undefined, so the instruction is named directly.  For the
+// exp this is exact: |t| >= 2^31 means |x| > 1.4e9, where the result is
+// inf or 0 (k far outside -149..127) whatever the saturated k and r are.
+__device__ __forceinline__ int cvt_i32_sat(float t) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(t));
+    return r;
+}
+
 __device__ __forceinline__ void exp_reduce(float x, int& k, float& r) {
-    float t = __builtin_fmaf(x, kInvLn2, __builtin_copysignf(0.5f, x));
-    t = __builtin_amdgcn_fmed3f(t, -1073741824.0f, 1073741824.0f);
-    k = (int)t;
+    const float t = __builtin_fmaf(x, kInvLn2, __builtin_copysignf(0.5f, x));
+    k = cvt_i32_sat(t);
     r = __builtin_fmaf(-(float)k, kLn2, x);
 }
 
@@ -210,21 +220,44 @@ struct HypStepV {
     }
 };
 
-template <int N, int E>
+//
+// OPT drops stages a caller makes redundant (each saves VALU issue slots;
+// none changes a result the caller keeps):
+//   kExpNan    NaN arguments return themselves.  Without it a NaN argument
+//              gives an unspecified finite value or inf: fine for x / (1 + e)
+//              (SiLU), whose result is NaN through x.
+//   kExpFlush  k <= -127 gives +0 as the reference's exponent field does.
+//              Without it those k give er * 2^k (a subnormal or 0): fine
+//              wherever the exp only enters 1 + e or 1 - e, which round to
+//              1 alike for any e < 2^-24.
+//   kExpNonPos every argument is <= 0 or NaN (softmax's x - max), so the
+//              rounding bias copysign(0.5, x) is the constant -0.5: at x = +0
+//              both biases truncate to k = 0, below 0 they are equal.
+constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4;
+constexpr int kExpFull = kExpNan | kExpFlush;
+
+template <int N, int E, int OPT = kExpFull>
 __device__ __forceinline__ void exp_cordic_vec(float* x, float khinv) {
     static_assert(N >= 1 && N <= kMaxIters, "iteration count");
     int k[E];
     float p[E], z[E];
 #pragma unroll
     for (int e = 0; e < E; e++) {
-        exp_reduce(x[e], k[e], z[e]);
+        if constexpr ((OPT & kExpNonPos) != 0) {
+            k[e] = cvt_i32_sat(__builtin_fmaf(x[e], kInvLn2, -0.5f));
+            z[e] = __builtin_fmaf(-(float)k[e], kLn2, x[e]);
+        } else {
+            exp_reduce(x[e], k[e], z[e]);
+        }
         p[e] = 1.0f;
     }
     HypStepV<N, 0, E>::run(p, z);
 #pragma unroll
     for (int e = 0; e < E; e++) {
-        const float res = exp_scale(p[e] * khinv, k[e]);
-        x[e] = (x[e] != x[e]) ? x[e] : res;
+        const float er = p[e] * khinv;
+        const float res = (OPT & kExpFlush) ? exp_scale(er, k[e]) : __builtin_ldexpf(er, k[e]);
+        if constexpr ((OPT & kExpNan) != 0) x[e] = (x[e] != x[e]) ? x[e] : res;
+        else x[e] = res;
     }
 }
 

@@ -84,12 +84,12 @@ __device__ __forceinline__ float inv_sum(float s, int zero_guard) {
 // counts use the step-major form (all elements advance one step at a time:
 // independent chains interleave and constants are shared); bit-identical
 // to one exp_cordic call per element.
-template <int NITER, int E>
+template <int NITER, int E, int OPT = kExpFull>
 __device__ __forceinline__ void exp_lane(float* v, int iters, float khinv) {
     if constexpr (NITER > 0) {
         constexpr int G = E < 16 ? E : 16;
 #pragma unroll
-        for (int b = 0; b < E; b += G) exp_cordic_vec<NITER, G>(v + b, khinv);
+        for (int b = 0; b < E; b += G) exp_cordic_vec<NITER, G, OPT>(v + b, khinv);
     } else {
 #pragma unroll
         for (int e = 0; e < E; e++) v[e] = exp_cordic_rt(v[e], iters, khinv);
@@ -136,12 +136,27 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     for (int i = 0; i < VPT; i++)
         m = fmaxf(fmaxf(fmaxf(m, v[4 * i]), fmaxf(v[4 * i + 1], v[4 * i + 2])), v[4 * i + 3]);
     m = block_max(m, red);
+    // Unmasked rows with a compile-time step count: every x - max is <= 0
+    // or NaN, and a NaN anywhere (a NaN element, or max = +-inf) makes the
+    // reference's row sum NaN and so every output NaN.  The exps then skip
+    // their per-element NaN test and sign-dependent rounding bias
+    // (kExpNonPos); NaN is found once per lane with a NaN-propagating
+    // maximum and forced into the row sum instead.
+    constexpr bool kLean = !MASKED && NITER > 0;
+    float nanp = -__builtin_inff();
 #pragma unroll
-    for (int e = 0; e < E; e++) v[e] = v[e] - m;
-    exp_lane<NITER, E>(v, iters, khinv);
+    for (int e = 0; e < E; e++) {
+        v[e] = v[e] - m;
+        if constexpr (kLean) nanp = __builtin_elementwise_maximum(nanp, v[e]);
+    }
+    if constexpr (kLean) exp_lane<NITER, E, kExpFlush | kExpNonPos>(v, iters, khinv);
+    else exp_lane<NITER, E>(v, iters, khinv);
     float s = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; e++) s += v[e];
+    if constexpr (kLean) {
+        if (nanp != nanp) s = __builtin_nanf("");
+    }
     s = block_sum(s, red);
     const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
 #pragma unroll

@@ -166,7 +166,9 @@ def test_reference_launcher_abi():
 # ── exp / activations ──────────────────────────────────────────────────────
 
 SPECIAL = np.float32([0.0, -0.0, 1.0, -1.0, 0.5, 88.0, 88.8, 89.0, -87.0, -88.0, -103.0, -104.0,
-                      200.0, -200.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 0.34657359, -0.34657359])
+                      200.0, -200.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 0.34657359, -0.34657359,
+                      # |x| / ln2 >= 2^30 and >= 2^31: the range reduction's integer k saturates
+                      7.5e8, -7.5e8, 1.5e9, -1.5e9, 3e38, -3e38, 1e-45, -1e-45])
 
 
 @pytest.mark.parametrize("iters", [1, 5, 8, 16, 24])
@@ -267,6 +269,45 @@ def test_softmax_shapes(shape):
     got = H(ext().softmax(T(x), iters=16))
     ref = rl.orc_softmax(x, 16)
     assert rl.max_rel(got, ref, 1e-37) <= 1e-5
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24, 5])
+@pytest.mark.parametrize("cols", [4096, 4000])
+def test_softmax_special_rows(iters, cols):
+    """Rows holding NaN, +-inf, only -inf, huge offsets and arguments whose
+    range reduction saturates: NaN exactly where the checker has NaN (a NaN
+    anywhere makes the reference's whole row NaN).  Finite rows are compared
+    with the checker's own exps over their float64 sum: rows of equal values
+    drive the reference's left-to-right float sum to ~4e-5 relative error,
+    which is the checker's rounding, not the kernel's."""
+    x = rl.gen_normal((14, cols), 21, std=3.0)
+    x[0, 5] = np.nan
+    x[1, 0] = np.nan
+    x[2, 77] = np.inf
+    x[3, :] = -np.inf
+    x[4, :100] = -np.inf
+    x[5] -= 200.0
+    x[5, 3] = 0.0
+    x[6] = -np.abs(x[6]) * 40.0
+    x[7] = 0.0
+    x[8] = -1e30
+    x[9] = -np.inf
+    x[9, 4] = 1.0
+    x[10] = -np.inf
+    x[10, 4] = np.nan
+    x[11] = 3e38
+    x[12, ::2] = -2e9
+    x[13] = np.float32(-1e-45)
+    x[13, 7] = 0.0
+    got = H(ext().softmax(T(x), iters=iters))
+    ref = rl.orc_softmax(x, iters)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    nan_rows = np.isnan(ref).any(axis=1)
+    assert nan_rows.tolist() == [True] * 4 + [False] * 6 + [True] + [False] * 3
+    for r in np.flatnonzero(~nan_rows):
+        xm = x[r] - np.max(x[r])                      # float32 subtraction, as the kernel
+        e = rl.orc_unary("orc_exp_batch", xm, iters).astype(np.float64)
+        assert rl.max_rel(got[r], e / e.sum(), 1e-37) <= 1e-5, r
 
 
 def test_softmax_vs_libm_reference_reported():
