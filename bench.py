@@ -7,15 +7,18 @@ CORDIC-16 matmul (rotate-project-accumulate: 16 micro-rotations per MAC)
 over synthetic U[-1,1] operands resident in HBM.  value = 2*4096^3 / t.
 
 Also measured in the same run (fields "ops" and "cpu_baseline"):
-  * the matmul at n = 8 and 24;
+  * the matmul at n = 8 and 24, and config 1 (1024^3, n = 16) both
+    device-resident and through the synchronous rac.h call on host buffers;
+  * the Llama block (config 5) at n = 8/16/24 with a per-op breakdown;
   * the config-5 attention core through RAC ([1,32,2048,128], causal, n=16)
     and the Q8_0 decode GEMV (11008x4096, 32000x4096, 65536x8192; HBM GB/s);
   * softmax 4096x4096 N(0, std 2) at n = 8/16/24, RoPE on Q and K
     [8,32,4096,128], RMSNorm 16384x4096, SiLU 16384x11008 (n=16): HBM GB/s
     of 1 read + 1 write per element, buffers rotated past the 256 MB MALL;
   * the reference lib/c on the host cores (oracle/_ref, compiled from the
-    reference sources): rac_hal_matmul 4096^3 and the row ops, timed in a
-    child process.
+    reference sources): rac_hal_matmul 4096^3 and 1024^3, softmax, RoPE,
+    RMSNorm, SiLU (rac_hal_silu), the Q8_0 GEMV and the RAC-DSP batch,
+    timed in a child process.
 
 Roofline of the dominant kernel (the matmul): VALU-bound; algorithmic work
 per MAC is W(n) = 2n+1 FP32 FMA lane-ops (n micro-rotations on the (x, y)
@@ -111,6 +114,48 @@ def bench_gpu(args):
         }
         print(f"# matmul n={nn}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del A, B, C
+
+    # rac_matmul 1024^3, U[-1,1], CORDIC n = 16.  Device-
+    # resident launch time, and the synchronous rac.h call on host buffers
+    # (rac_matmul(A, B, C, M, N, K) with the knobs at 16 / cordic: staging
+    # over PCIe included, reported only)
+    import numpy as np
+    M1 = 1024
+    A1 = torch.rand((M1, M1), device=dev, generator=g) * 2 - 1
+    B1 = torch.rand((M1, M1), device=dev, generator=g) * 2 - 1
+    C1 = torch.empty((M1, M1), device=dev)
+
+    def mm1():
+        rc = lib.rac_gemm_dev(A1.data_ptr(), B1.data_ptr(), C1.data_ptr(), M1, M1, M1, 0, 0, 1.0, 0.0,
+                              16, ext.MODE_CORDIC, stream)
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    mm1()
+    torch.cuda.synchronize()
+    t1 = _events_time(mm1, 10, torch)
+    Ah, Bh = A1.cpu().numpy(), B1.cpu().numpy()
+    Ch = np.empty_like(Ah)
+    prev = (lib.rac_get_cordic_iters(), lib.rac_get_cordic_mode())
+    lib.rac_set_cordic_iters(16)
+    lib.rac_set_cordic_mode(ext.MODE_CORDIC)
+    try:
+        lib.rac_matmul(Ah.ctypes.data, Bh.ctypes.data, Ch.ctypes.data, M1, M1, M1)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            lib.rac_matmul(Ah.ctypes.data, Bh.ctypes.data, Ch.ctypes.data, M1, M1, M1)
+        th = (time.perf_counter() - t0) / 5
+    finally:
+        lib.rac_set_cordic_iters(prev[0])
+        lib.rac_set_cordic_mode(prev[1])
+    ops["matmul_1024_cordic_n16"] = {
+        "ms": round(t1 * 1e3, 3),
+        "equiv_GFLOPs": round(2 * M1 ** 3 / t1 / 1e9, 1),
+        "frac_of_fp32_peak": round(M1 ** 3 * 2 * 33 / t1 / 1e12 / PEAK_FP32_TFLOPS, 4),
+        "rac_h_host_buffers_ms": round(th * 1e3, 3)}
+    print(f"# matmul 1024^3 n=16: {t1 * 1e3:.3f} ms device, {th * 1e3:.2f} ms rac.h on host buffers",
+          file=sys.stderr, flush=True)
+    del A1, B1, C1
 
     if not args.matmul_only:
         ops.update(bench_hbm_ops(torch, ext, dev, g))
@@ -475,6 +520,18 @@ def cpu_baseline_child():
     t = (time.perf_counter() - t0) / reps
     res["matmul"] = {"seconds": t, "reps": reps, "GFLOPs": 2 * M * N * K / t / 1e9}
     del A, B, Cm
+    # BASELINE config 1 shape on the same path
+    M1 = 1024
+    A1 = rl.gen_uniform((M1, M1), 0)
+    B1 = rl.gen_uniform((M1, M1), 1)
+    C1 = np.zeros((M1, M1), np.float32)
+    r.rac_hal_matmul(rl.p(A1), rl.p(B1), rl.p(C1), M1, M1, M1)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        r.rac_hal_matmul(rl.p(A1), rl.p(B1), rl.p(C1), M1, M1, M1)
+    t = (time.perf_counter() - t0) / 10
+    res["matmul_1024"] = {"seconds": t, "GFLOPs": 2 * M1 ** 3 / t / 1e9}
+    del A1, B1, C1
 
     def timeit(fn, n):
         fn()
@@ -499,6 +556,12 @@ def cpu_baseline_child():
     gam = np.ones(4096, np.float32)
     t = timeit(lambda: r.rac_rmsnorm(rl.p(x), rl.p(y), rl.p(gam), 1e-6, 16384, 4096, None), 2)
     res["rmsnorm"] = {"seconds": t, "GBps": 2 * x.nbytes / t / 1e9}
+    del x, y
+    # SiLU 16384 x 11008 (rac_hal_silu: the reference's AVX2 dispatch)
+    x = np.random.default_rng(5).standard_normal((16384, 11008), dtype=np.float32)
+    y = np.empty_like(x)
+    t = timeit(lambda: r.rac_hal_silu(rl.p(x), rl.p(y), x.size), 2)
+    res["silu"] = {"seconds": t, "GBps": 2 * x.nbytes / t / 1e9}
     del x, y
     # Q8_0 decode GEMV 11008 x 4096 (reference AVX2 path)
     Wf = np.random.default_rng(2).standard_normal((11008, 4096), dtype=np.float32) * np.float32(0.02)

@@ -16,14 +16,24 @@
 // VALU-bound by two orders of magnitude over LDS and HBM traffic.  A 64x64
 // block tile (4x4 outputs per lane, 256 lanes = 4 wave64) staged through LDS
 // with BK = 16 keeps 16 independent MAC chains per lane for latency hiding
-// and reads only 2 ds_read_b128 per 16 MACs.  FAST mode (1 FMA per MAC)
-// uses a 128x128 tile with 8x8 per lane so LDS traffic stays below the VALU
-// rate.  The next K-tile is prefetched into registers while the current one
-// is computed.
+// and reads only 2 ds_read_b128 per 16 MACs; the rotations of those MACs
+// advance step-major, so independent FMA chains interleave in each wave's
+// instruction stream.  FAST mode (1 FMA per MAC) uses a 128x128 tile with
+// 8x8 per lane so LDS traffic stays below the VALU rate.  Launches with
+// fewer than 1024 block tiles step down to 64x64, then 32x32 (2x2 per lane)
+// so every SIMD holds several waves.  The next K-tile is prefetched into
+// registers while the current one is computed.
 #include <hip/hip_runtime.h>
 #include "rac_act.hpp"
 
 namespace rac {
+
+// CORDIC mode: rotations of kGroupRows tile rows (x TN columns) advance
+// step-major (8 interleaved chains in the 4x4 register tile).
+constexpr int kGroupRows = 2;
+// Fewer block tiles than this (4 per CU) leave SIMDs with one wave or none;
+// such launches step down to a smaller tile (64x64, then 32x32).
+constexpr long kMinTiles = 1024;
 
 template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
 struct GemmCfg {
@@ -166,23 +176,56 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             for (int kk = 0; kk < BK; kk++) {
                 float a[TM], b[TN];
                 uint32_t bs[TN];
+                if constexpr (TM % 4 == 0) {
 #pragma unroll
-                for (int i = 0; i < TM; i += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
-                    a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+                    for (int i = 0; i < TM; i += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
+                        a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+                    }
+                } else {
+                    static_assert(TM == 2, "register tile");
+                    const float2 v = *reinterpret_cast<const float2*>(&sA[kk][ty * TM]);
+                    a[0] = v.x; a[1] = v.y;
                 }
+                if constexpr (TN % 4 == 0) {
 #pragma unroll
-                for (int j = 0; j < TN; j += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
-                    b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
+                    for (int j = 0; j < TN; j += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
+                        b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
+                    }
+                } else {
+                    static_assert(TN == 2, "register tile");
+                    const float2 v = *reinterpret_cast<const float2*>(&sB[kk][tx * TN]);
+                    b[0] = v.x; b[1] = v.y;
                 }
 #pragma unroll
                 for (int j = 0; j < TN; j++) bs[j] = as_u(b[j]) & 0x80000000u;
+                if constexpr (MODE == kModeCordic && NITER > 0) {
+                    // the rotations of kGroupRows x TN MACs advance step-major
+                    // (independent chains interleave; same bits as mac<>)
+                    constexpr int G = kGroupRows < TM ? kGroupRows : TM;
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                    for (int i0 = 0; i0 < TM; i0 += G) {
+                        float xr[G * TN];
 #pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
+                        for (int gi = 0; gi < G; gi++)
+#pragma unroll
+                            for (int j = 0; j < TN; j++) xr[gi * TN + j] = as_f(as_u(a[i0 + gi]) ^ bs[j]);
+                        cordic_rot_x_vec<NITER, G * TN>(xr);
+#pragma unroll
+                        for (int gi = 0; gi < G; gi++)
+#pragma unroll
+                            for (int j = 0; j < TN; j++)
+                                acc[i0 + gi][j] = __builtin_fmaf(xr[gi * TN + j] * cordic_kinv(NITER),
+                                                                 __builtin_fabsf(b[j]), acc[i0 + gi][j]);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
+                }
             }
         }
 
@@ -248,9 +291,8 @@ struct GemmArgs {
     const int* k_causal;
 };
 
-template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED = 0>
+template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED, int TM>
 static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
-    constexpr int TM = (MODE == kModeFast) ? 8 : 4;
     constexpr int TN = TM;
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     const float kinv = cordic_kinv(g.iters);
@@ -264,19 +306,39 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Register tile: 8x8 per lane (128x128 block) for FAST, 4x4 (64x64) for the
+// CORDIC and SHIFTADD MACs, stepping down while the launch would have fewer
+// than kMinTiles blocks; the triangular and paired-row schedules keep the
+// 64x64 tile they are written for.  The tile never changes a result: each
+// output is one accumulator over k in order.
+template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED = 0>
+static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
+    constexpr int kBig = (MODE == kModeFast) ? 8 : 4;
+    if constexpr (SCHED != 0) {
+        return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
+    } else {
+        auto tiles = [&](long bm) { return ((g.M + bm - 1) / bm) * ((g.N + bm - 1) / bm) * (long)g.batch; };
+        if (tiles(16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, kBig>(g, s);
+        if constexpr (kBig == 8) {
+            if (tiles(64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 4>(g, s);
+        }
+        return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 2>(g, s);
+    }
+}
+
 // The fused epilogue exists for the NT layout only (input @ weight^T, the
 // linear layer), the triangular schedule for NT only (causal Q K^T) and the
 // paired-row schedule for NN only (causal P V); their callers never ask for
 // another layout.
 template <int MODE, int NITER>
 static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s) {
-    if (g.fused) return launch_cfg<MODE, NITER, false, true, true>(g, s);
-    if (g.sched == 1) return launch_cfg<MODE, NITER, false, true, false, 1>(g, s);   // NT only
-    if (g.sched == 2) return launch_cfg<MODE, NITER, false, false, false, 2>(g, s);  // NN only
-    if (!ta && !tb) return launch_cfg<MODE, NITER, false, false, false>(g, s);
-    if (!ta && tb) return launch_cfg<MODE, NITER, false, true, false>(g, s);
-    if (ta && !tb) return launch_cfg<MODE, NITER, true, false, false>(g, s);
-    return launch_cfg<MODE, NITER, true, true, false>(g, s);
+    if (g.fused) return launch_tiles<MODE, NITER, false, true, true>(g, s);
+    if (g.sched == 1) return launch_tiles<MODE, NITER, false, true, false, 1>(g, s);   // NT only
+    if (g.sched == 2) return launch_tiles<MODE, NITER, false, false, false, 2>(g, s);  // NN only
+    if (!ta && !tb) return launch_tiles<MODE, NITER, false, false, false>(g, s);
+    if (!ta && tb) return launch_tiles<MODE, NITER, false, true, false>(g, s);
+    if (ta && !tb) return launch_tiles<MODE, NITER, true, false, false>(g, s);
+    return launch_tiles<MODE, NITER, true, true, false>(g, s);
 }
 
 static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStream_t s) {

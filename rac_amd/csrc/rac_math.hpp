@@ -62,6 +62,45 @@ __device__ __forceinline__ float cordic_rot_x(float x0) {
     }
 }
 
+// E independent rotations advanced step-major (micro-rotation i of every
+// chain before micro-rotation i+1 of any): the chains interleave in the
+// instruction stream, so even a SIMD holding a single wave has independent
+// FMAs to issue back to back.  Bit-identical to E calls of cordic_rot_x<N>.
+template <int N, int I, int E>
+struct ChainStepV {
+    __device__ __forceinline__ static void run(float* x, float* yh) {
+        constexpr float cx = chain_cx(I);
+        constexpr float cy = chain_cy(I);
+        if constexpr (I + 1 < N) {
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                const float xn = __builtin_fmaf(cx, yh[e], x[e]);
+                yh[e] = __builtin_fmaf(cy, x[e], yh[e]);
+                x[e] = xn;
+            }
+            ChainStepV<N, I + 1, E>::run(x, yh);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; e++) x[e] = __builtin_fmaf(cx, yh[e], x[e]);
+        }
+    }
+};
+
+// x[e] <- R_N(x[e]) for E values at once.
+template <int N, int E>
+__device__ __forceinline__ void cordic_rot_x_vec(float* x) {
+    static_assert(N >= 1 && N <= kMaxIters, "iteration count");
+    if constexpr (N > 1) {
+        float yh[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            yh[e] = x[e];
+            x[e] = x[e] * 1.5f;
+        }
+        if constexpr (N > 2) ChainStepV<N, 2, E>::run(x, yh);
+    }
+}
+
 // Constant tables for the run-time iteration count paths (wave-uniform
 // indices -> scalar loads).  Built from the same constexpr definitions.
 struct StepTables {
