@@ -43,8 +43,24 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBPS = 8000.0
 
 
-def _events_time(fn, reps, torch):
-    """Average time of fn() per call from HIP events on the current stream."""
+def _events_time(fn, reps, torch, warm_s=0.03, min_timed_s=0.02):
+    """Average time of fn() per call from HIP events on the current stream.
+
+    The GPU's clocks drop while it idles (host-side phases of this script)
+    and take milliseconds to recover, so fn() first runs for ~warm_s of
+    wall time; the timed region then repeats it at least `reps` times and
+    for at least ~min_timed_s."""
+    t0 = time.perf_counter()
+    k = 0
+    while True:
+        fn()
+        k += 1
+        if k % 4 == 0 or k == 1:
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= warm_s:
+                break
+    est = (time.perf_counter() - t0) / k
+    reps = max(reps, min(2000, int(min_timed_s / max(est, 1e-7)) + 1))
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     s.record()
