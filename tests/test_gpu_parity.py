@@ -150,6 +150,53 @@ def test_cordic_matmul_4096_sampled(iters):
     assert np.array_equal(got[rows, cols], ref)
 
 
+# Launches pick their register tile from the block count: (4100, 4097) has
+# >= 1024 128x128 blocks (FAST 8x8 per lane, CORDIC / SHIFTADD 4x4), (2050,
+# 2049) >= 1024 64x64 blocks but fewer 128x128 ones (4x4 for every mode), and
+# small shapes take 2x2.  Each is ragged on both edges.
+TILE_SHAPES = [(4100, 4097, 21), (2050, 2049, 37), (90, 70, 50)]
+
+
+@pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24), (2, 8), (1, 5)])
+@pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_every_tile_size_ragged(mode, iters, layout):
+    """Sampled entries (every corner and the last partial tile rows/columns
+    included) bit-exact vs the checker for each register-tile size."""
+    ta, tb = layout
+    rng = np.random.default_rng(mode * 10 + iters)
+    for (M, N, K) in TILE_SHAPES:
+        print(f"tile shapes mode={mode} iters={iters} layout={layout} shape={(M, N, K)}", flush=True)
+        A = rl.gen_uniform((M, K), seed=M + K)
+        B = rl.gen_uniform((K, N), seed=N + 3 * K)
+        As = np.ascontiguousarray(A.T) if ta else A
+        Bs = np.ascontiguousarray(B.T) if tb else B
+        got = gemm(As, Bs, M, N, K, ta, tb, iters, mode)
+        rows = np.concatenate([rng.integers(0, M, 300), rng.integers(max(0, M - 70), M, 100), [0, 0, M - 1, M - 1]])
+        cols = np.concatenate([rng.integers(0, N, 300), rng.integers(max(0, N - 70), N, 100), [0, N - 1, 0, N - 1]])
+        ref = rl.orc_matmul_entries(As, Bs, M, N, K, iters, mode, rows, cols, ta=ta, tb=tb)
+        assert np.array_equal(got[rows, cols], ref), (M, N, K)
+
+
+def test_fused_linear_on_the_64x64_tile():
+    """The fused bias + SiLU epilogue at a shape with >= 1024 blocks of 64x64
+    (the small-shape fused tests run on the 2x2 tile): equal to the unfused
+    GEMM + activation, sampled pre-activations bit-exact vs the checker."""
+    e = ext()
+    M, N, K = 2050, 2049, 37
+    x = rl.gen_normal((M, K), seed=3)
+    w = rl.gen_normal((N, K), seed=4, std=0.2)
+    b = rl.gen_normal(N, seed=5)
+    out, pre = e.fused_linear_forward(T(x), T(w), T(b), 3, iters=16, mode=1, return_pre=True)
+    lin = e.linear_forward(T(x), T(w), T(b), iters=16, mode=1)
+    assert torch.equal(pre, lin)
+    assert torch.equal(out, e.silu(lin, 16))
+    rng = np.random.default_rng(7)
+    rows = np.concatenate([rng.integers(0, M, 400), [0, M - 1]])
+    cols = np.concatenate([rng.integers(0, N, 400), [N - 1, 0]])
+    ref = rl.orc_matmul_entries(x, w, M, N, K, 16, 1, rows, cols, tb=1) + b[cols]
+    assert np.array_equal(H(pre)[rows, cols], ref.astype(np.float32))
+
+
 def test_reference_launcher_abi():
     M, N, K = 48, 40, 56
     A = rl.gen_normal((M, K), 8)
