@@ -129,6 +129,19 @@ def bench_gpu(args):
             "frac_of_fp32_peak": round(M * N * K * 2 * w / t / 1e12 / PEAK_FP32_TFLOPS, 4),
         }
         print(f"# matmul n={nn}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
+
+    # FAST mode (the rac_torch default, rac_kernels.hip:55-62): the plain
+    # fmaf(a, b, acc) MAC, 2 FLOP per MAC against the same FP32 VALU peak
+    def mmf():
+        rc = lib.rac_gemm_dev(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 0, 0, 1.0, 0.0,
+                              24, ext.MODE_FAST, stream)
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    t = _events_time(mmf, 10, torch)
+    ops["matmul_4096_fast"] = {"ms": round(t * 1e3, 3), "GFLOPs": round(2 * M * N * K / t / 1e9, 1),
+                               "frac_of_fp32_peak": round(2 * M * N * K / t / 1e12 / PEAK_FP32_TFLOPS, 4)}
+    print(f"# matmul FAST: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del A, B, C
 
     # rac_matmul 1024^3, U[-1,1], CORDIC n = 16.  Device-

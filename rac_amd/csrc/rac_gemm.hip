@@ -19,7 +19,9 @@
 // and reads only 2 ds_read_b128 per 16 MACs; the rotations of those MACs
 // advance step-major, so independent FMA chains interleave in each wave's
 // instruction stream.  FAST mode (1 FMA per MAC) uses a 128x128 tile with
-// 8x8 per lane so LDS traffic stays below the VALU rate.  Launches with
+// 8x8 per lane (split in 4x4 groups 64 apart, conflict-free LDS reads), the
+// k loop unrolled by 2; at 16 LDS floats per 64 FMAs it is bound by LDS
+// bandwidth (128 B/clk/CU) as much as by the FMA rate.  Launches with
 // fewer than 1024 block tiles step down to 64x64, then 32x32 (2x2 per lane)
 // so every SIMD holds several waves.  The next K-tile is prefetched into
 // registers while the current one is computed.
@@ -34,6 +36,21 @@ constexpr int kGroupRows = 2;
 // Fewer block tiles than this (4 per CU) leave SIMDs with one wave or none;
 // such launches step down to a smaller tile (64x64, then 32x32).
 constexpr long kMinTiles = 1024;
+
+// Offset of a lane's i-th row (or column) inside the block tile, for the
+// lane's 16-way index t.  Register tiles of 4k are split into k groups of 4
+// spaced 64 apart, so a wave's float4 LDS reads of one group cover 256
+// contiguous bytes (no bank conflicts for the 8x8 tile); 2 and 4 are
+// contiguous.  Only the output a lane owns changes, never its arithmetic.
+template <int TT>
+__device__ __forceinline__ int lane_off(int t, int i) {
+    if constexpr (TT % 4 == 0) return (i >> 2) * 64 + t * 4 + (i & 3);
+    else return t * TT + i;
+}
+
+// FAST MACs are one FMA each: the k loop is unrolled by this so the next
+// k-step's LDS reads issue under the current step's FMAs.
+constexpr int kFastKUnroll = 2;
 
 template <int MODE, int NITER, bool TA, bool TB, int TM, int TN>
 struct GemmCfg {
@@ -172,14 +189,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             store_tile();
             __syncthreads();
             if (k0 + BK < kend) load_tile(k0 + BK);   // prefetch overlaps the MACs
+            // CORDIC steps are long VALU chains and stay rolled
+            constexpr int KU = (MODE == kModeFast) ? kFastKUnroll : 1;
 #pragma unroll 1
-            for (int kk = 0; kk < BK; kk++) {
+            for (int kb = 0; kb < BK; kb += KU)
+#pragma unroll
+            for (int ku = 0; ku < KU; ku++) {
+                const int kk = kb + ku;
                 float a[TM], b[TN];
                 uint32_t bs[TN];
                 if constexpr (TM % 4 == 0) {
 #pragma unroll
                     for (int i = 0; i < TM; i += 4) {
-                        const float4 v = *reinterpret_cast<const float4*>(&sA[kk][ty * TM + i]);
+                        const float4 v = *reinterpret_cast<const float4*>(&sA[kk][lane_off<TM>(ty, i)]);
                         a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
                     }
                 } else {
@@ -190,7 +212,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 if constexpr (TN % 4 == 0) {
 #pragma unroll
                     for (int j = 0; j < TN; j += 4) {
-                        const float4 v = *reinterpret_cast<const float4*>(&sB[kk][tx * TN + j]);
+                        const float4 v = *reinterpret_cast<const float4*>(&sB[kk][lane_off<TN>(tx, j)]);
                         b[j] = v.x; b[j + 1] = v.y; b[j + 2] = v.z; b[j + 3] = v.w;
                     }
                 } else {
@@ -231,11 +253,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            const long gm = m0 + ty * TM + i;
+            const long gm = m0 + lane_off<TM>(ty, i);
             if (gm >= M) continue;
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const long gn = n0 + tx * TN + j;
+                const long gn = n0 + lane_off<TN>(tx, j);
                 if (gn >= N) continue;
                 float* cp = C + gm * N + gn;
                 // rac_kernels.hip:267-272
