@@ -26,6 +26,7 @@
 // so every SIMD holds several waves.  The next K-tile is prefetched into
 // registers while the current one is computed.
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include "rac_act.hpp"
 
 namespace rac {
@@ -313,9 +314,8 @@ struct GemmArgs {
     const int* k_causal;
 };
 
-template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED, int TM>
+template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED, int TM, int TN = TM>
 static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
-    constexpr int TN = TM;
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     const float kinv = cordic_kinv(g.iters);
     const unsigned nt = (unsigned)((g.M + Cfg::kBM - 1) / Cfg::kBM);
@@ -328,7 +328,29 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Register tile: 8x8 per lane (128x128 block) for FAST, 4x4 (64x64) for the
+// Compute units of the current device (256 on MI355X), cached per device.
+static long device_cus() {
+    static std::atomic<long> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    long v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        v = n;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// Register tile: 8x8 per lane (128x128 block) for FAST (16x8 when that fills
+// the CUs better), 4x4 (64x64) for the
 // CORDIC and SHIFTADD MACs, stepping down while the launch would have fewer
 // than kMinTiles blocks; the triangular and paired-row schedules keep the
 // 64x64 tile they are written for.  The tile never changes a result: each
@@ -339,10 +361,24 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
     if constexpr (SCHED != 0) {
         return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
     } else {
-        auto tiles = [&](long bm) { return ((g.M + bm - 1) / bm) * ((g.N + bm - 1) / bm) * (long)g.batch; };
-        if (tiles(16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, kBig>(g, s);
+        auto tiles = [&](long bm, long bn) { return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch; };
+        if constexpr (MODE == kModeFast) {
+            // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
+            // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per
+            // CU); it is taken when it fills its rounds of resident blocks
+            // at least as completely as 8x8 does
+            const long cus = device_cus();
+            auto fill = [&](long t, long per_cu) {
+                const long slots = per_cu * cus, rounds = (t + slots - 1) / slots;
+                return (double)t / (double)(rounds * slots);
+            };
+            const long t16 = tiles(256, 128), t8 = tiles(128, 128);
+            if (t16 >= 2 * cus && fill(t16, 2) >= fill(t8, 3))
+                return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 16, 8>(g, s);
+        }
+        if (tiles(16 * kBig, 16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, kBig>(g, s);
         if constexpr (kBig == 8) {
-            if (tiles(64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 4>(g, s);
+            if (tiles(64, 64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 4>(g, s);
         }
         return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 2>(g, s);
     }

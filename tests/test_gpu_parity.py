@@ -150,11 +150,12 @@ def test_cordic_matmul_4096_sampled(iters):
     assert np.array_equal(got[rows, cols], ref)
 
 
-# Launches pick their register tile from the block count: (4100, 4097) has
-# >= 1024 128x128 blocks (FAST 8x8 per lane, CORDIC / SHIFTADD 4x4), (2050,
+# Launches pick their register tile from the block count: (3996, 4000) fills
+# whole rounds of 256x128 blocks on 256 CUs (FAST 16x8 per lane), (4100,
+# 4097) has >= 1024 128x128 blocks (FAST 8x8, CORDIC / SHIFTADD 4x4), (2050,
 # 2049) >= 1024 64x64 blocks but fewer 128x128 ones (4x4 for every mode), and
 # small shapes take 2x2.  Each is ragged on both edges.
-TILE_SHAPES = [(4100, 4097, 21), (2050, 2049, 37), (90, 70, 50)]
+TILE_SHAPES = [(3996, 4000, 19), (4100, 4097, 21), (2050, 2049, 37), (90, 70, 50)]
 
 
 @pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24), (2, 8), (1, 5)])
@@ -177,23 +178,26 @@ def test_gemm_every_tile_size_ragged(mode, iters, layout):
         assert np.array_equal(got[rows, cols], ref), (M, N, K)
 
 
-def test_fused_linear_on_the_64x64_tile():
-    """The fused bias + SiLU epilogue at a shape with >= 1024 blocks of 64x64
-    (the small-shape fused tests run on the 2x2 tile): equal to the unfused
-    GEMM + activation, sampled pre-activations bit-exact vs the checker."""
+@pytest.mark.parametrize("mode,shape", [(1, (2050, 2049, 37)), (0, (3996, 4000, 19)), (0, (4100, 4097, 21))])
+def test_fused_linear_on_large_tiles(mode, shape):
+    """The fused bias + SiLU epilogue on the large register tiles (the
+    small-shape fused tests run on the 2x2 tile): CORDIC on 4x4, FAST on
+    16x8 and 8x8.  Equal to the unfused GEMM + activation, sampled
+    pre-activations bit-exact vs the checker."""
     e = ext()
-    M, N, K = 2050, 2049, 37
+    M, N, K = shape
+    iters = 16 if mode == 1 else 24
     x = rl.gen_normal((M, K), seed=3)
     w = rl.gen_normal((N, K), seed=4, std=0.2)
     b = rl.gen_normal(N, seed=5)
-    out, pre = e.fused_linear_forward(T(x), T(w), T(b), 3, iters=16, mode=1, return_pre=True)
-    lin = e.linear_forward(T(x), T(w), T(b), iters=16, mode=1)
+    out, pre = e.fused_linear_forward(T(x), T(w), T(b), 3, iters=iters, mode=mode, return_pre=True)
+    lin = e.linear_forward(T(x), T(w), T(b), iters=iters, mode=mode)
     assert torch.equal(pre, lin)
-    assert torch.equal(out, e.silu(lin, 16))
+    assert torch.equal(out, e.silu(lin, iters))
     rng = np.random.default_rng(7)
     rows = np.concatenate([rng.integers(0, M, 400), [0, M - 1]])
     cols = np.concatenate([rng.integers(0, N, 400), [N - 1, 0]])
-    ref = rl.orc_matmul_entries(x, w, M, N, K, 16, 1, rows, cols, tb=1) + b[cols]
+    ref = rl.orc_matmul_entries(x, w, M, N, K, iters, mode, rows, cols, tb=1) + b[cols]
     assert np.array_equal(H(pre)[rows, cols], ref.astype(np.float32))
 
 
