@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py — the RAC rotation-accumulate hot path on one MI355X.
 
-Metric: rac_matmul equiv-GFLOP/s at 4096^3 with 16 CORDIC
+Headline metric: rac_matmul equiv-GFLOP/s at 4096^3 with 16 CORDIC
 iterations; RoPE / softmax / RMSNorm HBM GB/s.  A "step" is one 4096^3
 CORDIC-16 matmul (rotate-project-accumulate: 16 micro-rotations per MAC)
 over synthetic U[-1,1] operands resident in HBM.  value = 2*4096^3 / t.
@@ -144,7 +144,7 @@ def bench_gpu(args):
     print(f"# matmul FAST: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del A, B, C
 
-    # rac_matmul 1024^3, U[-1,1], CORDIC n = 16.  Device-
+    # Benchmark config 1: rac_matmul 1024^3, U[-1,1], CORDIC n = 16.  Device-
     # resident launch time, and the synchronous rac.h call on host buffers
     # (rac_matmul(A, B, C, M, N, K) with the knobs at 16 / cordic: staging
     # over PCIe included, reported only)
@@ -339,7 +339,7 @@ def bench_hbm_ops(torch, ext, dev, g):
     record("torch_copy_16384x4096", 2 * 4 * R * D, _events_time(cp, reps, torch))
     del xr, yr
 
-    # RACLlamaBlock forward, d=4096, H=32, ff=11008, batch 1,
+    # Benchmark config 5: RACLlamaBlock forward, d=4096, H=32, ff=11008, batch 1,
     # seq 2048, causal, weights ~ N(0, 0.02), x ~ N(0, 1), CORDIC mode
     from rac_amd import rac_torch as rt
     torch.manual_seed(0)
@@ -549,7 +549,7 @@ def cpu_baseline_child():
     t = (time.perf_counter() - t0) / reps
     res["matmul"] = {"seconds": t, "reps": reps, "GFLOPs": 2 * M * N * K / t / 1e9}
     del A, B, Cm
-    # BASELINE config 1 shape on the same path
+    # benchmark config 1 shape on the same path
     M1 = 1024
     A1 = rl.gen_uniform((M1, M1), 0)
     B1 = rl.gen_uniform((M1, M1), 1)
@@ -661,7 +661,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): this "
-              "build's hot path is single-GPU; see DESIGN.md for how it would shard.", file=sys.stderr)
+              "build's hot path is single-GPU (every op would shard by rows or output columns with at most one all-reduce per block).", file=sys.stderr)
         sys.exit(2)
 
     gpu = bench_gpu(args)

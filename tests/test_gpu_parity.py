@@ -4,7 +4,7 @@ Bars: bit-exact wherever the kernel and the checker evaluate the same
 roundings (CORDIC/FAST/SHIFTADD matmul, exp, SiLU, sigmoid, tanh, rsqrt,
 sin/cos, RoPE table and apply); elementwise relative error <= 1e-5 where a
 row sum is reduced in a different order (softmax, RMSNorm, LayerNorm); matmul
-vs the reference lib/c within 1e-4*|a_i|*|b_j| per element.  Full BASELINE
+vs the reference lib/c within 1e-4*|a_i|*|b_j| per element.  Full benchmark
 sizes are covered through sampled entries and digests.
 """
 import ctypes
@@ -111,7 +111,7 @@ def test_alpha_beta_epilogue():
 
 
 def test_rac_h_matmul_1024_config1_host_pointers():
-    """rac_matmul 1024^3, U[-1,1] seeds 0/1, n=16, through
+    """Benchmark config 1: rac_matmul 1024^3, U[-1,1] seeds 0/1, n=16, through
     the synchronous rac.h entry point with host buffers."""
     M = N = K = 1024
     A = rl.gen_uniform((M, K), seed=0)
@@ -304,7 +304,7 @@ def test_scalar_rac_h_entry_points():
 
 @pytest.mark.parametrize("iters", [8, 16, 24])
 def test_softmax_config2(iters):
-    """4096 x 4096, N(0, std 2)."""
+    """Benchmark config 2: 4096 x 4096, N(0, std 2)."""
     x = rl.gen_normal((4096, 4096), 0, std=2.0)
     got = H(ext().softmax(T(x), iters=iters))
     ref = rl.orc_softmax(x, iters)
@@ -370,7 +370,7 @@ def test_softmax_vs_libm_reference_reported():
 
 @pytest.mark.parametrize("shape", [(16384, 4096), (5, 64), (3, 4099), (4, 1), (2, 40000)])
 def test_rmsnorm_layernorm(shape):
-    """BASELINE config 4 (16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6) and edge shapes."""
+    """Benchmark config 4 (16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6) and edge shapes."""
     x = rl.gen_normal(shape, 1)
     g = rl.gen_normal((shape[1],), 2, mean=1.0, std=0.02)
     b = rl.gen_normal((shape[1],), 3, std=0.1)
@@ -435,7 +435,7 @@ def test_rope_apply_golden_and_rac_h():
 
 
 def test_rope_config3_full_size():
-    """Q and K [8, 32, 4096, 128] (B,H,T,D), tables from
+    """Benchmark config 3: Q and K [8, 32, 4096, 128] (B,H,T,D), tables from
     rac_rope_cache(4096, 128, 10000): bit-exact over the full tensors."""
     shape = (8, 32, 4096, 128)
     c, s = ext().rope_cache(4096, 128, device=DEV)
