@@ -27,7 +27,7 @@ kernel's average launch time (HIP events on the launch stream); peak =
 MI355X FP32 vector 157.3 TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--iters 16]
-                       [--no-cpu-baseline] [--matmul-only]
+                       [--no-cpu-baseline] [--matmul-only] [--rowops-only]
 """
 from __future__ import annotations
 
@@ -187,7 +187,8 @@ def bench_gpu(args):
     del A1, B1, C1
 
     if not args.matmul_only:
-        ops.update(bench_hbm_ops(torch, ext, dev, g))
+        ops.update(bench_row_ops(torch, ext, dev, g))
+        ops.update(bench_block_ops(torch, ext, dev, g))
 
     w = 2 * n + 1
     achieved = M * N * K * 2 * w / launch_s / 1e12
@@ -255,7 +256,9 @@ def _llama_breakdown(torch, blk, xb):
     return res
 
 
-def bench_hbm_ops(torch, ext, dev, g):
+def bench_row_ops(torch, ext, dev, g):
+    """Softmax, RoPE, RMSNorm and SiLU at the benchmark shapes (HBM-bound row and
+    elementwise kernels), with torch copies of the same bytes for scale."""
     lib = ext._lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
     out = {}
@@ -339,6 +342,36 @@ def bench_hbm_ops(torch, ext, dev, g):
     record("torch_copy_16384x4096", 2 * 4 * R * D, _events_time(cp, reps, torch))
     del xr, yr
 
+    # SiLU 16384 x 11008 (n = 16)
+    xsilu = torch.randn((16384, 11008), device=dev, generator=g)
+    ysilu = torch.empty_like(xsilu)
+
+    def silu():
+        chk(lib.rac_silu_dev(xsilu.data_ptr(), ysilu.data_ptr(), xsilu.numel(), 16, stream))
+
+    silu()
+    torch.cuda.synchronize()
+    record("silu_16384x11008_n16", 2 * 4 * xsilu.numel(), _events_time(silu, 10, torch))
+    del xsilu, ysilu
+    return out
+
+
+def bench_block_ops(torch, ext, dev, g):
+    """Llama block, attention core, Q8_0 GEMV, RAC-DSP and the safetensors loader."""
+    lib = ext._lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+
+    def chk(rc):
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    def record(name, nbytes, t):
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4)}
+        print(f"# {name}: {t * 1e6:.1f} us, {nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+
+    reps = 20
     # Benchmark config 5: RACLlamaBlock forward, d=4096, H=32, ff=11008, batch 1,
     # seq 2048, causal, weights ~ N(0, 0.02), x ~ N(0, 1), CORDIC mode
     from rac_amd import rac_torch as rt
@@ -503,17 +536,6 @@ def bench_hbm_ops(torch, ext, dev, g):
                                                             stream)), reps, torch))
     del draw, wf, wq8, wbits
 
-    # SiLU 16384 x 11008 (n = 16)
-    xsilu = torch.randn((16384, 11008), device=dev, generator=g)
-    ysilu = torch.empty_like(xsilu)
-
-    def silu():
-        chk(lib.rac_silu_dev(xsilu.data_ptr(), ysilu.data_ptr(), xsilu.numel(), 16, stream))
-
-    silu()
-    torch.cuda.synchronize()
-    record("silu_16384x11008_n16", 2 * 4 * xsilu.numel(), _events_time(silu, 10, torch))
-    del xsilu, ysilu
     return out
 
 
@@ -640,6 +662,9 @@ def main():
     ap.add_argument("--iters", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--matmul-only", action="store_true")
+    ap.add_argument("--rowops-only", action="store_true",
+                    help="only time softmax, RoPE, RMSNorm and SiLU and print their figures "
+                         "(a short run for rocprofv3 --pmc passes; not the benchmark line)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device tensor copy 3 times (scales the "
                          "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc runs)")
@@ -664,6 +689,16 @@ def main():
               "build's hot path is single-GPU (every op would shard by rows or output columns with at most one all-reduce per block).", file=sys.stderr)
         sys.exit(2)
 
+    if args.rowops_only:
+        import torch
+        sys.path.insert(0, ROOT)
+        from rac_amd import ext
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        print(json.dumps({"ops": bench_row_ops(torch, ext, dev, g)}), flush=True)
+        return
     gpu = bench_gpu(args)
     cpu = None if args.no_cpu_baseline else run_cpu_baseline()
     line = {
