@@ -20,6 +20,11 @@ Also measured in the same run (fields "ops" and "cpu_baseline"):
     RMSNorm, SiLU (rac_hal_silu), the Q8_0 GEMV and the RAC-DSP batch,
     timed in a child process.
 
+Each "ms"/"us" figure is the average over back-to-back calls (HIP events
+on the launch stream); p10 / median / p90 are of separately bracketed calls,
+which also carry each launch's ramp-up and drain, so for kernels of tens of
+microseconds they sit above the back-to-back average.
+
 Roofline of the dominant kernel (the matmul): VALU-bound; algorithmic work
 per MAC is W(n) = 2n+1 FP32 FMA lane-ops (n micro-rotations on the (x, y)
 pair plus the projecting FMA), i.e. 2*(2n+1) FLOP; achieved = that over the
@@ -43,13 +48,26 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBPS = 8000.0
 
 
-def _events_time(fn, reps, torch, warm_s=0.03, min_timed_s=0.02):
+class Timing(float):
+    """Seconds per call, averaged over back-to-back calls, carrying the
+    10th / 50th / 90th percentiles of separately bracketed calls."""
+    p10 = p50 = p90 = None
+
+
+def _percentiles(vals):
+    v = sorted(vals)
+    pick = lambda q: v[min(len(v) - 1, int(round(q * (len(v) - 1))))]  # noqa: E731
+    return pick(0.1), pick(0.5), pick(0.9)
+
+
+def _events_time(fn, reps, torch, warm_s=0.03, min_timed_s=0.02, dist_calls=20):
     """Average time of fn() per call from HIP events on the current stream.
 
     The GPU's clocks drop while it idles (host-side phases of this script)
     and take milliseconds to recover, so fn() first runs for ~warm_s of
     wall time; the timed region then repeats it at least `reps` times and
-    for at least ~min_timed_s."""
+    for at least ~min_timed_s.  Then `dist_calls` more calls, each between
+    its own pair of events, give the per-call percentiles."""
     t0 = time.perf_counter()
     k = 0
     while True:
@@ -68,7 +86,25 @@ def _events_time(fn, reps, torch, warm_s=0.03, min_timed_s=0.02):
         fn()
     e.record()
     e.synchronize()
-    return s.elapsed_time(e) / reps / 1e3
+    out = Timing(s.elapsed_time(e) / reps / 1e3)
+    if dist_calls:
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(dist_calls)]
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        out.p10, out.p50, out.p90 = _percentiles([a.elapsed_time(b) / 1e3 for a, b in ev])
+    return out
+
+
+def _dist_fields(t, scale, unit):
+    """p10 / median / p90 of a Timing in `unit` (empty if it has none)."""
+    if getattr(t, "p50", None) is None:
+        return {}
+    return {f"p10_{unit}": round(t.p10 * scale, 3), f"median_{unit}": round(t.p50 * scale, 3),
+            f"p90_{unit}": round(t.p90 * scale, 3)}
 
 
 def bench_gpu(args):
@@ -108,7 +144,8 @@ def bench_gpu(args):
         b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    launch_s = sum(a.elapsed_time(b) for a, b in ev) / len(ev) / 1e3
+    launch_s = Timing(sum(a.elapsed_time(b) for a, b in ev) / len(ev) / 1e3)
+    launch_s.p10, launch_s.p50, launch_s.p90 = _percentiles([a.elapsed_time(b) / 1e3 for a, b in ev])
     ms_per_step = wall / args.steps * 1e3
     print(f"# matmul 4096^3 CORDIC n={n}: {launch_s * 1e3:.2f} ms/launch, wall {ms_per_step:.2f} ms/step",
           file=sys.stderr, flush=True)
@@ -127,6 +164,7 @@ def bench_gpu(args):
             "equiv_GFLOPs": round(2 * M * N * K / t / 1e9, 1),
             "valu_TFLOPs": round(M * N * K * 2 * w / t / 1e12, 2),
             "frac_of_fp32_peak": round(M * N * K * 2 * w / t / 1e12 / PEAK_FP32_TFLOPS, 4),
+            **_dist_fields(t, 1e3, "ms"),
         }
         print(f"# matmul n={nn}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
 
@@ -140,7 +178,8 @@ def bench_gpu(args):
 
     t = _events_time(mmf, 10, torch)
     ops["matmul_4096_fast"] = {"ms": round(t * 1e3, 3), "GFLOPs": round(2 * M * N * K / t / 1e9, 1),
-                               "frac_of_fp32_peak": round(2 * M * N * K / t / 1e12 / PEAK_FP32_TFLOPS, 4)}
+                               "frac_of_fp32_peak": round(2 * M * N * K / t / 1e12 / PEAK_FP32_TFLOPS, 4),
+                               **_dist_fields(t, 1e3, "ms")}
     print(f"# matmul FAST: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del A, B, C
 
@@ -181,7 +220,8 @@ def bench_gpu(args):
         "ms": round(t1 * 1e3, 3),
         "equiv_GFLOPs": round(2 * M1 ** 3 / t1 / 1e9, 1),
         "frac_of_fp32_peak": round(M1 ** 3 * 2 * 33 / t1 / 1e12 / PEAK_FP32_TFLOPS, 4),
-        "rac_h_host_buffers_ms": round(th * 1e3, 3)}
+        "rac_h_host_buffers_ms": round(th * 1e3, 3),
+        **_dist_fields(t1, 1e3, "ms")}
     print(f"# matmul 1024^3 n=16: {t1 * 1e3:.3f} ms device, {th * 1e3:.2f} ms rac.h on host buffers",
           file=sys.stderr, flush=True)
     del A1, B1, C1
@@ -210,6 +250,7 @@ def bench_gpu(args):
                                      "profiles/gemm_cordic16_4096_pmc.md); algorithmic A+B+C = 2.01e8",
                      "kernel": f"gemm_kernel<CORDIC,{n},NN> 64x64 tile, 4x4 per lane",
                      "avg_launch_ms": round(launch_s * 1e3, 3),
+                     **{f"launch_{k}": v for k, v in _dist_fields(launch_s, 1e3, "ms").items()},
                      "work_per_mac": f"{w} FMA lane-ops (2n+1)"},
         "ops": ops,
     }
@@ -269,7 +310,8 @@ def bench_row_ops(torch, ext, dev, g):
 
     def record(name, nbytes, t):
         out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
-                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4)}
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4),
+                     **_dist_fields(t, 1e6, "us")}
         print(f"# {name}: {t * 1e6:.1f} us, {nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
 
     reps = 20
@@ -368,7 +410,8 @@ def bench_block_ops(torch, ext, dev, g):
 
     def record(name, nbytes, t):
         out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
-                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4)}
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4),
+                     **_dist_fields(t, 1e6, "us")}
         print(f"# {name}: {t * 1e6:.1f} us, {nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
 
     reps = 20
@@ -390,11 +433,11 @@ def bench_block_ops(torch, ext, dev, g):
             with torch.no_grad():
                 blk(xb, is_causal=True)
                 torch.cuda.synchronize()
-                t = _events_time(lambda: blk(xb, is_causal=True), 2, torch)
+                t = _events_time(lambda: blk(xb, is_causal=True), 2, torch, dist_calls=5)
                 parts = _llama_breakdown(torch, blk, xb)
             out[f"llama_block_T2048_n{n}"] = {"ms": round(t * 1e3, 2),
                                               "linear_equiv_TFLOPs": round(644.2e9 / t / 1e12, 3),
-                                              "per_op_ms": parts}
+                                              "per_op_ms": parts, **_dist_fields(t, 1e3, "ms")}
             print(f"# llama block n={n}: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
     finally:
         rt.rac_set_mode(prev_mode)
@@ -422,7 +465,8 @@ def bench_block_ops(torch, ext, dev, g):
     out["attention_core_1x32x2048x128_n16"] = {
         "ms": round(t * 1e3, 3), "causal_macs": macs,
         "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
-        "valu_frac_of_fp32_peak": round(macs * 2 * 33 / t / 1e12 / PEAK_FP32_TFLOPS, 4)}
+        "valu_frac_of_fp32_peak": round(macs * 2 * 33 / t / 1e12 / PEAK_FP32_TFLOPS, 4),
+        **_dist_fields(t, 1e3, "ms")}
     print(f"# attention core n=16: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del qa, ka, va, oa, wsa
 
@@ -473,7 +517,8 @@ def bench_block_ops(torch, ext, dev, g):
         t = _events_time(dsp, reps, torch)
         out[f"dsp_{name}_16M"] = {"us": round(t * 1e6, 2), "Geval_per_s": round(nd / t / 1e9, 2),
                                   "GBps": round(nbytes * nd / t / 1e9, 1),
-                                  "frac_of_hbm_peak": round(nbytes * nd / t / 1e9 / PEAK_HBM_GBPS, 4)}
+                                  "frac_of_hbm_peak": round(nbytes * nd / t / 1e9 / PEAK_HBM_GBPS, 4),
+                                  **_dist_fields(t, 1e6, "us")}
         print(f"# dsp {name}: {t * 1e6:.1f} us, {nd / t / 1e9:.1f} G-evals/s", file=sys.stderr, flush=True)
     del xd, yd, zd, od
     Ns = Ks = 256
@@ -487,7 +532,8 @@ def bench_block_ops(torch, ext, dev, g):
     sysd()
     torch.cuda.synchronize()
     t = _events_time(sysd, reps, torch)
-    out["dsp_systolic_256x256_k256"] = {"us": round(t * 1e6, 2), "Geval_per_s": round(Ns * Ns * Ks / t / 1e9, 2)}
+    out["dsp_systolic_256x256_k256"] = {"us": round(t * 1e6, 2), "Geval_per_s": round(Ns * Ns * Ks / t / 1e9, 2),
+                                        **_dist_fields(t, 1e6, "us")}
     print(f"# dsp systolic: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
     del Wd, Xd, Yd
 

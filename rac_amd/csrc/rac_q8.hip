@@ -6,8 +6,8 @@
 // reference's AVX2 build (rac_q8_0.c:128-211): each block's 32 products
 // combine in the order of its 8-lane vector tree, and the block terms of a
 // row accumulate in block order as acc = fma(d_b, dot_b, acc).  The fast
-// kernel keeps that serial order while the loads of a whole chunk (16 rows
-// x up to 128 blocks) are in flight at once; shapes it does not cover
+// kernel keeps that serial order while the loads of a whole chunk (16 or 32
+// rows x 32 blocks) are in flight at once; shapes it does not cover
 // (K % 256 != 0, unaligned weights) take a generic kernel with the same
 // arithmetic.
 #include <hip/hip_runtime.h>
@@ -48,40 +48,40 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
     }
 }
 
-// Fast path (K % 256 == 0, 16-byte aligned buffers).  A workgroup owns
-// kQ8R = 16 consecutive weight rows and walks K in chunks of up to CB
-// blocks (64 for one input row: 16 x 2176 bytes, all requested at once, so
-// the whole chunk is in flight before any of it is used; LDS leaves room
-// for 3 workgroups per CU):
+// Fast path (K % 256 == 0, 16-byte aligned buffers).  A workgroup owns R
+// consecutive weight rows (16 or 32) and walks K in chunks of up to CB
+// blocks (R x CB x 34 bytes, all requested at once, so the whole chunk is
+// in flight before any of it is used):
 //   1. 16-byte loads of the chunk (contiguous per row) -> registers -> LDS;
 //   2. every lane computes block dots, lane-fast along a row (consecutive
 //      lanes read consecutive blocks, the x slice is padded to 33 floats
 //      per block, so LDS reads do not collide), and stores (d, dot);
 //   3. lane (m, r) folds its row's terms in block order.
 // Up to 4 input rows (batched decode) share one pass over the weights.
-constexpr int kQ8R = 16;
+// The shape only decides which lane computes what; every output is the
+// same serial fold, so all shapes give identical bits.
 constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
 
-template <int MX, int CB>
+template <int MX, int CB, int R>
 __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ x,
                                                       const uint8_t* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ out, int M, int N, int K,
                                                       int act) {
-    static_assert(256 % CB == 0 && CB % 8 == 0, "chunk shape");
+    static_assert(256 % CB == 0 && CB % 8 == 0 && R * CB >= 256 && MX * R <= 256, "chunk shape");
     constexpr int kRowLds = CB * kQ8Bytes + 16;                       // row stride in LDS (16-byte multiple)
-    constexpr int kVPT = (kQ8R * CB * kQ8Bytes / 16 + 255) / 256;     // weight vectors per lane
+    constexpr int kVPT = (R * CB * kQ8Bytes / 16 + 255) / 256;     // weight vectors per lane
     constexpr int kXPT = MX * CB * kQ8Block / 4 / 256;                // x float4 per lane
-    constexpr int kRPT = kQ8R * CB / 256;                             // rows per lane in the dot phase
+    constexpr int kRPT = R * CB / 256;                             // rows per lane in the dot phase
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    __shared__ __attribute__((aligned(16))) uint8_t sw[kQ8R * kRowLds];
+    __shared__ __attribute__((aligned(16))) uint8_t sw[R * kRowLds];
     __shared__ float sx[MX][CB * kQ8XPad];
-    __shared__ float sdot[MX][kQ8R][CB + 1];
-    __shared__ float sd[kQ8R][CB + 1];
+    __shared__ float sdot[MX][R][CB + 1];
+    __shared__ float sd[R][CB + 1];
 
     const int tid = threadIdx.x;
-    const long j0 = (long)blockIdx.x * kQ8R;
-    const int nrows = (int)min((long)kQ8R, (long)N - j0);
+    const long j0 = (long)blockIdx.x * R;
+    const int nrows = (int)min((long)R, (long)N - j0);
     const int nb = K / kQ8Block;
     const long rowB = (long)nb * kQ8Bytes;
 
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
 #pragma unroll
     for (int i = 0; i < kVPT; i++) {
         const int v = tid + i * 256;
-        const bool live = v < kQ8R * kVrow;
+        const bool live = v < R * kVrow;
         const int r = live ? v / kVrow : 0, o = live ? v % kVrow : 0;
         gfull[i] = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
         sfull[i] = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
         }
         const int vrow = cb * kQ8Bytes / 16;
         const int v = tid + i * 256;
-        const bool live = v < kQ8R * vrow;
+        const bool live = v < R * vrow;
         const int r = live ? v / vrow : 0, o = live ? v % vrow : 0;
         goff = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
         soff = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
@@ -192,8 +192,8 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
         }
         __syncthreads();
         // ordered fold of this chunk's terms
-        if (tid < MX * kQ8R) {
-            const int m = tid / kQ8R, r = tid % kQ8R;
+        if (tid < MX * R) {
+            const int m = tid / R, r = tid % R;
             if (m < M && r < nrows) {
                 for (int kk = 0; kk < cb; kk += 8) {
                     float dv[8], tv[8];
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
             }
         }
     }
-    if (tid < MX * kQ8R) {
-        const int m = tid / kQ8R, r = tid % kQ8R;
+    if (tid < MX * R) {
+        const int m = tid / R, r = tid % R;
         if (m < M && r < nrows) out[(long)m * N + j0 + r] = q8_finish(acc, bias, j0 + r, act);
     }
 }
@@ -249,15 +249,21 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
                           int K, int act, hipStream_t s) {
     const bool fast = (K % (8 * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
     if (fast) {
-        const dim3 grid((unsigned)((N + kQ8R - 1) / kQ8R));
+        // one input row: chunks of 32 blocks; 32 rows per workgroup once
+        // that still gives >= 1.5 workgroups per CU, else 16 (measured on
+        // N x 4096 and 65536 x 8192: within 2% of the best of 6 shapes)
+        const bool wide = N >= 12288;
+        const dim3 g16((unsigned)((N + 15) / 16)), g32((unsigned)((N + 31) / 32));
         for (int m0 = 0; m0 < M; m0 += 4) {
             const int mm = min(4, M - m0);
             const float* xg = x + (long)m0 * K;
             float* og = out + (long)m0 * N;
-            if (mm == 1)
-                hipLaunchKernelGGL((q8_gemv_kernel<1, 64>), grid, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+            if (mm > 1)
+                hipLaunchKernelGGL((q8_gemv_kernel<4, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+            else if (wide)
+                hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
             else
-                hipLaunchKernelGGL((q8_gemv_kernel<4, 32>), grid, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
         }
     } else {
         const long outs = (long)M * N;

@@ -114,6 +114,26 @@ def test_gemv_llama_shapes_bit_exact():
         assert np.array_equal(got, rl.orc_q8_gemv(x, wq, None, 0)[0])
 
 
+@pytest.mark.parametrize("N,K", [(12301, 256), (14336, 4096), (12288, 2048)])
+def test_gemv_wide_launch_bit_exact(N, K):
+    """N >= 12288 takes 32 rows per workgroup: full and ragged last
+    workgroups, one and several chunks along K, bias and activations."""
+    e = ext()
+    W = _weights(N, K, N + K)
+    wq = rl.orc_q8_quantize(W)
+    rng = np.random.default_rng(N)
+    x = rng.normal(0, 1, K).astype(np.float32)
+    bias = rng.normal(0, 1, N).astype(np.float32)
+    for act, b in ((0, None), (1, bias), (3, bias)):
+        print(f"q8 gemv wide N={N} K={K} act={act}", flush=True)
+        got = H(e.q8_gemv(T(x), T(wq), T(b) if b is not None else None, act))
+        ref = rl.orc_q8_gemv(x, wq, b, act)[0]
+        if act in (0, 1):
+            assert np.array_equal(got, ref)
+        else:
+            assert np.all(np.abs(got - ref) <= 1e-6 * (np.abs(ref) + 1.0)), float(np.max(np.abs(got - ref)))
+
+
 def test_reference_api_golden_host_pointers():
     import os
     import rac_amd
