@@ -64,11 +64,17 @@ struct GemmCfg {
     static constexpr int kBLoads = kBN * kBK / kThreads;
 };
 
-template <int MODE, int NITER>
+template <int MODE, int NITER, bool LIT = false>
 __device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc,
                                      int iters, float kinv) {
     if constexpr (MODE == kModeFast) {
         return __builtin_fmaf(a, b, acc);
+    } else if constexpr (MODE == kModeCordic && LIT) {
+        // the rotation as rac_kernels.hip:152-163 writes it, for inputs
+        // outside the strength-reduced chain's range (cordic_needs_literal)
+        const float x0 = as_f(as_u(a) ^ bsign);
+        const float xr = cordic_rot_x_literal_rt(x0, NITER > 0 ? NITER : iters);
+        return __builtin_fmaf(xr * kinv, __builtin_fabsf(b), acc);
     } else if constexpr (MODE == kModeCordic) {
         if constexpr (NITER > 0) {
             return mac_cordic<NITER>(a, b, bsign, acc);
@@ -115,9 +121,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     C += (long)blockIdx.z * sc;
     __shared__ __attribute__((aligned(16))) float sA[BK][BM + PAD];
     __shared__ __attribute__((aligned(16))) float sB[BK][BN + PAD];
+    // CORDIC mode: lit_pass[pass] is set when some A element of the output
+    // tile's row panel lies outside the strength-reduced chain's range
+    // (cordic_needs_literal); the tile is then recomputed on the literal
+    // chain.  One flag per pass, so no flag is cleared while being read.
+    __shared__ int lit_pass[2];
 
     const int tid = threadIdx.x;
     const int tx = tid % 16, ty = tid / 16;
+    if constexpr (MODE == kModeCordic) {
+        if (tid == 0) lit_pass[0] = lit_pass[1] = 0;   // ordered before any set by the K loop's barriers
+    }
 
     constexpr int kPasses = SCHED == 2 ? 2 : 1;
     for (int pass = 0; pass < kPasses; pass++) {
@@ -131,6 +145,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
 
         float ra[Cfg::kALoads], rb[Cfg::kBLoads];
+        // Range of the A elements this lane staged, as |a| bit patterns: the
+        // largest, and the smallest minus one (unsigned, so +-0 never counts).
+        uint32_t a_hi = 0u, a_lo_m1 = 0xffffffffu;
 
         // Global -> register staging of one K-tile; element (m, k) of op(A) and
         // (k, n) of op(B), zero outside the matrix.  Index order is chosen so
@@ -167,6 +184,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 if constexpr (TA) { kk = idx / BM; mm = idx % BM; }
                 else { mm = idx / BK; kk = idx % BK; }
                 sA[kk][mm] = ra[r];
+                if constexpr (MODE == kModeCordic) {
+                    const uint32_t u = as_u(ra[r]) & 0x7fffffffu;
+                    a_hi = max(a_hi, u);
+                    a_lo_m1 = min(a_lo_m1, u - 1u);
+                }
             }
 #pragma unroll
             for (int r = 0; r < Cfg::kBLoads; r++) {
@@ -248,6 +270,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 #pragma unroll
                         for (int j = 0; j < TN; j++)
                             acc[i][j] = mac<MODE, NITER>(a[i], b[j], bs[j], acc[i][j], iters, kinv);
+                }
+            }
+        }
+
+        if constexpr (MODE == kModeCordic) {
+            if (cordic_range_needs_literal(a_lo_m1, a_hi)) lit_pass[pass] = 1;
+            __syncthreads();
+            if (lit_pass[pass]) {
+                // Rare: the tile's A panel holds subnormal, tiny (< 2^-105),
+                // top-binade, infinite or NaN elements.  Recompute it on the
+                // literal chain, straight from global memory (zero outside
+                // the matrix, as the staged tiles are).
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+#pragma unroll 1
+                for (int k = 0; k < kend; k++) {
+                    float a[TM], b[TN];
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        const long gm = m0 + lane_off<TM>(ty, i);
+                        a[i] = gm < M ? (TA ? A[(long)k * M + gm] : A[gm * K + k]) : 0.0f;
+                    }
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const long gn = n0 + lane_off<TN>(tx, j);
+                        b[j] = gn < N ? (TB ? B[gn * K + k] : B[(long)k * N + gn]) : 0.0f;
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = mac<MODE, NITER, true>(a[i], b[j], as_u(b[j]) & 0x80000000u, acc[i][j],
+                                                               iters, NITER > 0 ? cordic_kinv(NITER > 0 ? NITER : 1)
+                                                                                : kinv);
                 }
             }
         }

@@ -106,6 +106,7 @@ __device__ __forceinline__ void cordic_rot_x_vec(float* x) {
 struct StepTables {
     float cx[kMaxIters];
     float cy[kMaxIters];
+    float dir[kMaxIters];
     float hS[kMaxIters];
     float hC[kMaxIters];
 };
@@ -114,6 +115,7 @@ constexpr StepTables make_step_tables() {
     for (int i = 0; i < kMaxIters; i++) {
         t.cx[i] = chain_cx(i);
         t.cy[i] = chain_cy(i);
+        t.dir[i] = (float)cordic_dir(i);
         t.hS[i] = hyp_S(i);
         t.hC[i] = hyp_C(i);
     }
@@ -133,6 +135,59 @@ __device__ __forceinline__ float cordic_rot_x_rt(float x0, int n) {
         x = xn;
     }
     return x;
+}
+
+// The micro-rotation chain exactly as rac_kernels.hip:152-163 writes it:
+// x' = x - d*y*scale, y' = y + d*x*scale, every product and sum rounded on
+// its own (d*y is exact, (d*y)*scale may round once it is subnormal).  The
+// strength-reduced chain above equals it bit for bit whenever
+// 2^-105 <= |x0| < 2^127 (exhaustive over every float in that range, n = 1..24);
+// outside it (subnormal and tiny inputs, the top binade, inf, NaN) the GEMM
+// runs this form instead.  Here on E values one after the other (the GEMM
+// takes it only for rare tiles, so it is written for few live registers, not
+// for speed): x[e] <- x output of rotating (x[e], 0).
+template <int N, int E>
+__device__ __forceinline__ void cordic_rot_x_literal_vec(float* x) {
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        float xv = x[e], y = 0.0f, scale = 1.0f;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const float d = (float)cordic_dir(i);
+            const float xn = xv - (d * y) * scale;
+            const float yn = y + (d * xv) * scale;
+            xv = xn;
+            y = yn;
+            scale *= 0.5f;
+        }
+        x[e] = xv;
+        __builtin_amdgcn_sched_barrier(0);   // keep the chains apart: no interleaving
+    }
+}
+
+__device__ __forceinline__ float cordic_rot_x_literal_rt(float x0, int n) {
+    float x = x0, y = 0.0f, scale = 1.0f;
+    for (int i = 0; i < n; i++) {
+        const float d = g_steps.dir[i];
+        const float xn = x - (d * y) * scale;
+        const float yn = y + (d * x) * scale;
+        x = xn;
+        y = yn;
+        scale *= 0.5f;
+    }
+    return x;
+}
+
+// The inputs whose rotation must take the literal chain: nonzero with
+// |x0| < 2^-105 or |x0| >= 2^127 (inf and NaN included).  For a set of
+// inputs given by lo_m1 = min(|x|bits - 1) (unsigned: zeros wrap to the
+// top) and hi = max(|x|bits): true when any member needs it.
+__device__ __forceinline__ bool cordic_range_needs_literal(uint32_t lo_m1, uint32_t hi) {
+    return lo_m1 < (22u << 23) - 1u || hi >= (254u << 23);
+}
+__device__ __forceinline__ bool cordic_needs_literal(float x0) {
+    const uint32_t u = as_u(x0) & 0x7fffffffu;
+    return cordic_range_needs_literal(u - 1u, u);
 }
 
 // One CORDIC-mode multiply-accumulate: b is the angle index (sign -> 0 or pi,

@@ -80,6 +80,41 @@ def test_cordic_matmul_bit_exact(iters, layout):
         assert np.array_equal(got, ref), (M, N, K, float(np.max(np.abs(got - ref))))
 
 
+SPECIALS = np.array([0.0, -0.0, 1e-45, -3e-39, 2.0 ** -126, -(2.0 ** -110), 1.5 * 2.0 ** -106, 2.0 ** -105,
+                     -(2.0 ** -104), 1.9 * 2.0 ** 126, -(2.0 ** 127), 3e38, np.inf, -np.inf, np.nan, 1.0, -0.75],
+                    np.float32)
+
+
+def _sprinkle(A, B, seed):
+    """Special values in a few rows of A (their tiles take the literal
+    rotation chain, the others stay on the strength-reduced one) and a few
+    finite ones in B."""
+    rng = np.random.default_rng(seed)
+    M, K = A.shape
+    for r in rng.integers(0, M, 6):
+        A[r, rng.integers(0, K, 5)] = rng.choice(SPECIALS, 5)
+    B[rng.integers(0, B.shape[0], 4), rng.integers(0, B.shape[1], 4)] = rng.choice(SPECIALS[:12], 4)
+    return A, B
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24, 5])
+@pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_cordic_matmul_special_values(iters, layout):
+    """Subnormal, tiny (< 2^-105), top-binade, infinite and NaN operands:
+    bit-exact with the literal rotation chain of the reference, NaN exactly
+    where the checker has NaN; 2x2 tiles (small shapes) and 4x4 tiles."""
+    ta, tb = layout
+    for (M, N, K) in [(67, 45, 83), (130, 129, 64), (2100, 2100, 20)]:
+        print(f"cordic specials iters={iters} layout={layout} shape={(M, N, K)}", flush=True)
+        A, B = _sprinkle(rl.gen_uniform((M, K), seed=M + 11 * K), rl.gen_uniform((K, N), seed=N + K), M + iters)
+        As = np.ascontiguousarray(A.T) if ta else A
+        Bs = np.ascontiguousarray(B.T) if tb else B
+        got = gemm(As, Bs, M, N, K, ta, tb, iters, 1)
+        ref = rl.orc_matmul(As, Bs, M, N, K, iters, 1, ta=ta, tb=tb)
+        assert np.array_equal(got, ref, equal_nan=True), (M, N, K)
+        assert np.isnan(ref).any() and np.isfinite(ref).sum() > ref.size // 2
+
+
 @pytest.mark.parametrize("mode", [0, 2])
 def test_fast_and_shiftadd_bit_exact(mode):
     for (M, N, K) in [(3, 5, 7), (67, 45, 83), (130, 129, 40)]:

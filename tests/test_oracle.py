@@ -114,10 +114,23 @@ def test_direction_sequence(o):
 
 @pytest.mark.parametrize("iters", [1, 2, 3, 4, 8, 12, 16, 20, 24])
 def test_fast_chain_exhaustive(o, iters):
-    # all 2^23 mantissas at exponent 0; scaling by 2^e is exact, so spot
-    # exponents -60 and +60 as well
+    # all 2^23 mantissas at exponent 0 and at spot exponents inside the
+    # range where every intermediate of both chains stays normal
     for e in (0, -60, 60):
         assert o.orc_check_chain_all_mantissas(iters, e) == 0
+
+
+def test_fast_chain_range_boundary(o):
+    """The GEMM runs the strength-reduced chain only for 2^-105 <= |a| < 2^127
+    and the literal one elsewhere.  Both edge binades of that range agree
+    for every mantissa and step count; the binades just outside it do not
+    (subnormal products round differently from the fused form below, the
+    doubled y overflows above), which is why the range ends there."""
+    for e in (-105, 126):
+        for n in range(1, 25):
+            assert o.orc_check_chain_all_mantissas(n, e) == 0, (e, n)
+    assert o.orc_check_chain_all_mantissas(24, -106) > 0
+    assert o.orc_check_chain_all_mantissas(24, 127) > 0
 
 
 @pytest.mark.parametrize("iters", [1, 5, 8, 16, 24])
