@@ -115,6 +115,20 @@ def test_cordic_matmul_special_values(iters, layout):
         assert np.isnan(ref).any() and np.isfinite(ref).sum() > ref.size // 2
 
 
+@pytest.mark.parametrize("mode,iters", [(0, 24), (2, 8), (2, 24)])
+def test_fast_shiftadd_special_values(mode, iters):
+    """The same special operands through the FAST and SHIFTADD MACs."""
+    for (M, N, K) in [(67, 45, 83), (130, 129, 64)]:
+        for ta, tb in [(0, 0), (1, 1)]:
+            print(f"mode={mode} specials iters={iters} shape={(M, N, K)} layout={(ta, tb)}", flush=True)
+            A, B = _sprinkle(rl.gen_uniform((M, K), seed=M), rl.gen_uniform((K, N), seed=N), M + mode)
+            As = np.ascontiguousarray(A.T) if ta else A
+            Bs = np.ascontiguousarray(B.T) if tb else B
+            got = gemm(As, Bs, M, N, K, ta, tb, iters, mode)
+            ref = rl.orc_matmul(As, Bs, M, N, K, iters, mode, ta=ta, tb=tb, literal=1)
+            assert np.array_equal(got, ref, equal_nan=True), (mode, iters, (M, N, K))
+
+
 @pytest.mark.parametrize("mode", [0, 2])
 def test_fast_and_shiftadd_bit_exact(mode):
     for (M, N, K) in [(3, 5, 7), (67, 45, 83), (130, 129, 40)]:
