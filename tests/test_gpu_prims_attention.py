@@ -223,6 +223,23 @@ def test_attention_vs_oracle(shape, iters, mode):
         assert np.max(np.abs(got - ref)) <= Tn * ULP * vmax + 1e-7
 
 
+@pytest.mark.parametrize("shape", [(16, 64, 256, 64), (1, 4, 256, 64)])
+def test_attention_causal_many_heads_sampled(shape):
+    """Causal attention over 1024 and 4 heads (the paired-row P V launch at
+    2048 and 8 workgroups); sampled heads against the checker."""
+    e = ext()
+    q, k, v = _qkv(shape, seed=sum(shape) + 1)
+    Bn, Hn, Tn, _ = shape
+    vmax = float(np.abs(v).max())
+    for iters, mode in ((16, 1), (24, 0)):
+        print(f"attention causal heads shape={shape} iters={iters} mode={mode}", flush=True)
+        got = H(e.attention(T(q), T(k), T(v), None, True, iters=iters, mode=mode))
+        for b, h in {(0, 0), (Bn - 1, Hn - 1), (Bn // 2, Hn // 3)}:
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            ref = rl.orc_attention(q[sl], k[sl], v[sl], None, True, iters, mode)
+            assert np.max(np.abs(got[sl] - ref)) <= Tn * ULP * vmax + 1e-7, (b, h)
+
+
 def test_attention_causal_nonfinite_v_keeps_full_products():
     """Causal P V stops each row tile at its last row only when V is finite:
     with an inf in V, 0 * inf = NaN must reach the earlier rows, as in the
