@@ -357,6 +357,17 @@ def bench_row_ops(torch, ext, dev, g):
     rope()
     torch.cuda.synchronize()
     record("rope_qk_8x32x4096x128", 2 * 2 * 4 * q.numel(), _events_time(rope, reps, torch))
+
+    # the same tensors read as [B, T, H, D] (the layout a fused QKV projection
+    # produces): position stride H*D, head stride D
+    def rope_bthd():
+        for t in (q, k):
+            chk(lib.rac_rope_apply_dev(t.data_ptr(), cos.data_ptr(), sin.data_ptr(), Bq, Hq, Tq, Dq,
+                                       Tq * Hq * Dq, Dq, Hq * Dq, stream))
+
+    rope_bthd()
+    torch.cuda.synchronize()
+    record("rope_qk_bthd_8x4096x32x128", 2 * 2 * 4 * q.numel(), _events_time(rope_bthd, reps, torch))
     del q, k
 
     # RMSNorm 16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6; 2 sets (1 GiB)
