@@ -368,6 +368,22 @@ def bench_row_ops(torch, ext, dev, g):
     rope_bthd()
     torch.cuda.synchronize()
     record("rope_qk_bthd_8x4096x32x128", 2 * 2 * 4 * q.numel(), _events_time(rope_bthd, reps, torch))
+
+    # the table itself: rac_rope_cache(4096, 128, 10000) on the device, 16
+    # circular CORDIC steps per entry after the reference's sequential wrap
+    # of theta (inv_freq from the host's powf, already in device memory)
+    inv = ext.rope_inv_freq(Dq, 10000.0).to(dev)
+    ct, stb = torch.empty_like(cos), torch.empty_like(sin)
+
+    def rope_tab():
+        chk(lib.rac_rope_cache_dev(ct.data_ptr(), stb.data_ptr(), Tq, Dq, 10000.0, inv.data_ptr(), stream))
+
+    rope_tab()
+    torch.cuda.synchronize()
+    t = _events_time(rope_tab, reps, torch)
+    out["rope_cache_4096x128"] = {"us": round(t * 1e6, 2), "entries": Tq * Dq // 2,
+                                  "Gentries_per_s": round(Tq * Dq // 2 / t / 1e9, 2), **_dist_fields(t, 1e6, "us")}
+    print(f"# rope_cache_4096x128: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
     del q, k
 
     # RMSNorm 16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6; 2 sets (1 GiB)
