@@ -512,8 +512,12 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
     // causal: score tiles wholly above the diagonal are masked by the
     // softmax regardless of their contents, so the scores GEMM schedules only
     // the tiles on or below it
+    // Both products keep the strength-reduced rotation chain for every input
+    // (exact_specials off): the attention's parity bar is the row-sum bound,
+    // and peaked softmax rows are full of probabilities below 2^-105, which
+    // would otherwise send most P V tiles through the literal-chain recompute.
     int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt,
-                                   causal ? 1 : 0),
+                                   causal ? 1 : 0, nullptr, false),
                        "rac_attention scores launch");
     if (rc) return rc;
     SoftmaxMask mk;
@@ -533,7 +537,7 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
         if (rc) return rc;
     }
     return check_hip(gemm_launch(0, 0, ws, v, out, t, d, t, 1.0f, 0.0f, iters, mode, s, bh, tt, td, td,
-                                 causal ? 2 : 0, flag),
+                                 causal ? 2 : 0, flag, false),
                      "rac_attention output launch");
 }
 

@@ -92,7 +92,7 @@ template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED, int
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc,
-    GemmEpilogue ep, const int* k_causal)
+    GemmEpilogue ep, const int* k_causal, int exact_specials)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
         }
 
         if constexpr (MODE == kModeCordic) {
-            if (cordic_range_needs_literal(a_lo_m1, a_hi)) lit_pass[pass] = 1;
+            if (exact_specials && cordic_range_needs_literal(a_lo_m1, a_hi)) lit_pass[pass] = 1;
             __syncthreads();
             if (lit_pass[pass]) {
                 // Rare: the tile's A panel holds subnormal, tiny (< 2^-105),
@@ -370,6 +370,7 @@ struct GemmArgs {
     bool fused;
     int sched;
     const int* k_causal;
+    int exact_specials;
 };
 
 template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED, int TM, int TN = TM>
@@ -382,7 +383,7 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     if (g.sched == 2) grid.y = (nt + 1) / 2;
     hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED, SCHED>), grid, dim3(256), 0, stream,
                        g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
-                       g.ep, g.k_causal);
+                       g.ep, g.k_causal, g.exact_specials);
     return hipGetLastError();
 }
 
@@ -471,15 +472,15 @@ static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStrea
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch, long sa, long sb, long sc, int sched,
-                       const int* k_causal) {
+                       const int* k_causal, bool exact_specials) {
     const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc,
-                     GemmEpilogue(), false, sched, k_causal};
+                     GemmEpilogue(), false, sched, k_causal, exact_specials ? 1 : 0};
     return dispatch(ta, tb, mode, g, s);
 }
 
 hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
                              const GemmEpilogue& ep, int iters, int mode, hipStream_t s) {
-    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0, nullptr};
+    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0, nullptr, 1};
     return dispatch(0, 1, mode, g, s);
 }
 

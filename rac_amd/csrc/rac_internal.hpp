@@ -45,11 +45,16 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 // sched 2: each workgroup computes row tiles p and nt-1-p (balances the
 // causal P V below).  k_causal: device flag; when it holds 1, row tile m
 // sums k only up to its last row (causal P V with a lower-triangular P and
-// finite V).
+// finite V).  exact_specials (CORDIC mode): tiles whose A panel holds
+// values outside the strength-reduced rotation chain's range are recomputed
+// on the literal chain, so every input gives the reference's bits; false
+// keeps the strength-reduced chain for every input (callers whose parity
+// bar is a summation bound, where subnormal-rounding differences of tiny
+// products are far below it).
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch = 1, long sa = 0, long sb = 0, long sc = 0,
-                       int sched = 0, const int* k_causal = nullptr);
+                       int sched = 0, const int* k_causal = nullptr, bool exact_specials = true);
 // *flag = 1 if every x[i] is finite, else 0 (stream-ordered).
 hipError_t all_finite_launch(const float* x, long n, int* flag, hipStream_t s);
 
