@@ -279,9 +279,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             __syncthreads();
             if (lit_pass[pass]) {
                 // Rare: the tile's A panel holds subnormal, tiny (< 2^-105),
-                // top-binade, infinite or NaN elements.  Recompute it on the
-                // literal chain, straight from global memory (zero outside
-                // the matrix, as the staged tiles are).
+                // top-binade, infinite or NaN elements.  Recompute it straight
+                // from global memory (zero outside the matrix, as the staged
+                // tiles are): those elements' MACs on the literal chain, all
+                // others on the strength-reduced one (the same bits there).
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -300,12 +301,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                         b[j] = gn < N ? (TB ? B[gn * K + k] : B[(long)k * N + gn]) : 0.0f;
                     }
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                    for (int i = 0; i < TM; i++) {
+                        if (cordic_needs_literal(a[i])) {
 #pragma unroll
-                        for (int j = 0; j < TN; j++)
-                            acc[i][j] = mac<MODE, NITER, true>(a[i], b[j], as_u(b[j]) & 0x80000000u, acc[i][j],
-                                                               iters, NITER > 0 ? cordic_kinv(NITER > 0 ? NITER : 1)
-                                                                                : kinv);
+                            for (int j = 0; j < TN; j++)
+                                acc[i][j] = mac<MODE, NITER, true>(a[i], b[j], as_u(b[j]) & 0x80000000u, acc[i][j],
+                                                                   iters, NITER > 0 ? cordic_kinv(NITER > 0 ? NITER : 1)
+                                                                                    : kinv);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < TN; j++)
+                                acc[i][j] = mac<MODE, NITER>(a[i], b[j], as_u(b[j]) & 0x80000000u, acc[i][j],
+                                                             iters, kinv);
+                        }
+                    }
                 }
             }
         }
