@@ -260,12 +260,13 @@ __device__ __forceinline__ void exp_reduce(float x, int& k, float& r) {
 }
 
 // er * 2^k with the reference's exponent-field semantics (k + 127 <= 0 ->
-// 0; k + 127 > 254 -> er * inf; otherwise the product er * 2^k, rounded
-// once).  v_ldexp_f32 computes er * 2^k with one rounding for every k, so
-// only the flush of k <= -127 needs a select.
+// 0; k + 127 > 254 -> er * inf = +inf, er being positive; otherwise the
+// product er * 2^k, rounded once).  v_ldexp_f32 computes er * 2^k with one
+// rounding for every k; the two ends need selects: k <= -127 flushes, and
+// k = 128 with er < 1 (x in [127.5 ln2, 88.72)) would still be finite.
 __device__ __forceinline__ float exp_scale(float er, int k) {
     const float res = __builtin_ldexpf(er, k);
-    return (k <= -127) ? 0.0f : res;
+    return (k <= -127) ? 0.0f : (k > 127 ? __builtin_inff() : res);
 }
 
 // Step J of the product-register exp, constants forced to compile time.
@@ -326,7 +327,8 @@ struct HypStepV {
 //              1 alike for any e < 2^-24.
 //   kExpNonPos every argument is <= 0 or NaN (softmax's x - max), so the
 //              rounding bias copysign(0.5, x) is the constant -0.5: at x = +0
-//              both biases truncate to k = 0, below 0 they are equal.
+//              both biases truncate to k = 0, below 0 they are equal; and
+//              k <= 0, so the overflow select (k > 127 -> inf) is dropped.
 constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4;
 constexpr int kExpFull = kExpNan | kExpFlush;
 
@@ -349,7 +351,9 @@ __device__ __forceinline__ void exp_cordic_vec(float* x, float khinv) {
 #pragma unroll
     for (int e = 0; e < E; e++) {
         const float er = p[e] * khinv;
-        const float res = (OPT & kExpFlush) ? exp_scale(er, k[e]) : __builtin_ldexpf(er, k[e]);
+        float res = __builtin_ldexpf(er, k[e]);
+        if constexpr ((OPT & kExpFlush) != 0) res = (k[e] <= -127) ? 0.0f : res;
+        if constexpr ((OPT & kExpNonPos) == 0) res = (k[e] > 127) ? __builtin_inff() : res;
         if constexpr ((OPT & kExpNan) != 0) x[e] = (x[e] != x[e]) ? x[e] : res;
         else x[e] = res;
     }

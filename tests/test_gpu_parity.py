@@ -268,7 +268,10 @@ def test_reference_launcher_abi():
 SPECIAL = np.float32([0.0, -0.0, 1.0, -1.0, 0.5, 88.0, 88.8, 89.0, -87.0, -88.0, -103.0, -104.0,
                       200.0, -200.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 0.34657359, -0.34657359,
                       # |x| / ln2 >= 2^30 and >= 2^31: the range reduction's integer k saturates
-                      7.5e8, -7.5e8, 1.5e9, -1.5e9, 3e38, -3e38, 1e-45, -1e-45])
+                      7.5e8, -7.5e8, 1.5e9, -1.5e9, 3e38, -3e38, 1e-45, -1e-45,
+                      # k = 128 with a reduced factor below 1: the exponent field
+                      # overflows (inf) although er * 2^128 would still be finite
+                      88.38, 88.5, 88.7, -88.38, -88.5, -88.7, 88.376, 88.721])
 
 
 @pytest.mark.parametrize("iters", [1, 5, 8, 16, 24])
@@ -279,6 +282,22 @@ def test_exp_and_activations_bit_exact(iters):
     for name, oname in (("exp", "orc_exp_batch"), ("silu", "orc_silu"),
                         ("sigmoid", "orc_sigmoid"), ("tanh", "orc_tanh")):
         print(f"{name} iters={iters}", flush=True)
+        got = H(getattr(e, name)(xd, iters=iters))
+        ref = rl.orc_unary(oname, x, iters)
+        assert np.array_equal(got, ref, equal_nan=True), (name, iters)
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24])
+def test_exp_family_over_all_float_classes(iters):
+    """Every 1009th 32-bit pattern (4.26 M floats: both signs, subnormals,
+    every exponent, inf and NaN payloads): exp, SiLU, sigmoid and tanh
+    bit-exact with the checker."""
+    x = (np.arange(0, 2 ** 32, 1009, dtype=np.uint64) & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    e = ext()
+    xd = T(x)
+    for name, oname in (("exp", "orc_exp_batch"), ("silu", "orc_silu"),
+                        ("sigmoid", "orc_sigmoid"), ("tanh", "orc_tanh")):
+        print(f"{name} all float classes iters={iters}", flush=True)
         got = H(getattr(e, name)(xd, iters=iters))
         ref = rl.orc_unary(oname, x, iters)
         assert np.array_equal(got, ref, equal_nan=True), (name, iters)
