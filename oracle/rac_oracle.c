@@ -365,6 +365,13 @@ ORC_API void orc_sincos(float theta, float *s, float *c)
     *s = y;
 }
 
+/* orc_sincos over an array (test sweeps). */
+ORC_API void orc_sincos_batch(const float *theta, float *s, float *c, long count)
+{
+    #pragma omp parallel for schedule(dynamic, 4096)
+    for (long i = 0; i < count; i++) orc_sincos(theta[i], &s[i], &c[i]);
+}
+
 /* rac_rope_cache, rac_cpu.c:576-598 (angle = (float)p * inv_freq[i]). */
 ORC_API int orc_rope_cache(float *cos_out, float *sin_out, int max_seq,
                            int head_dim, float base)
@@ -605,6 +612,13 @@ ORC_API float orc_rsqrt(float v)
     float root = X * orc_hyp_kinv(ORC_RSQRT_STEPS);
     float r = 1.0f / root;
     return ldexpf(r, -e);
+}
+
+/* orc_rsqrt over an array (test sweeps). */
+ORC_API void orc_rsqrt_batch(const float *x, float *y, long count)
+{
+    #pragma omp parallel for schedule(static)
+    for (long i = 0; i < count; i++) y[i] = orc_rsqrt(x[i]);
 }
 
 /* rac_rmsnorm, rac_cpu.c:548-574: ms = sequential fmaf(x,x,ms), ms /= d,

@@ -62,6 +62,7 @@ _ORACLE_SIGS = {
     "orc_matmul_entries": (_i, [_i, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "orc_rope_inv_freq": (None, [_vp, _i, _f]),
     "orc_sincos": (None, [_f, _fp, _fp]),
+    "orc_sincos_batch": (None, [_vp, _vp, _vp, _l]),
     "orc_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
     "orc_rope_apply": (_i, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "orc_rope_apply_strided": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l]),
@@ -72,6 +73,7 @@ _ORACLE_SIGS = {
     "orc_exp_batch": (None, [_vp, _vp, _l, _i]),
     "orc_softmax_rows": (None, [_vp, _vp, _i, _i, _i]),
     "orc_rsqrt": (_f, [_f]),
+    "orc_rsqrt_batch": (None, [_vp, _vp, _l]),
     "orc_rmsnorm": (_i, [_vp, _vp, _vp, _f, _i, _i, _i]),
     "orc_layernorm": (_i, [_vp, _vp, _vp, _vp, _f, _i, _i, _i]),
     "orc_silu": (None, [_vp, _vp, _l, _i]),

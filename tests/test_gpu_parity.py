@@ -342,6 +342,46 @@ def test_rsqrt_sincos_bit_exact():
     assert np.isnan(s[-3]) and np.isnan(s[-2])   # wrap-loop guard
 
 
+def _float_sweep(stride):
+    """Every stride-th 32-bit pattern as float32 (both signs, subnormals,
+    every exponent, infinities, NaN payloads)."""
+    return (np.arange(0, 2 ** 32, stride, dtype=np.uint64) & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+
+
+def test_rsqrt_sincos_over_float_classes():
+    """rsqrt on every 1009th bit pattern; sin/cos on every 1009th pattern
+    with |theta| < 2^14 (the reference's wrap loop runs |theta| / 2 pi
+    times), plus the NaN/inf angles: bit-exact with the checker."""
+    x = _float_sweep(1009)
+    got = H(ext().rsqrt(T(x)))
+    ref = np.empty_like(x)
+    rl.oracle().orc_rsqrt_batch(rl.p(x), rl.p(ref), x.size)
+    assert np.array_equal(got, ref, equal_nan=True)
+    th = x[~(np.abs(x) >= 16384.0)]              # keeps NaN
+    th = np.concatenate([th, np.float32([np.inf, -np.inf])])
+    s, c = ext().sincos(T(th))
+    so, co = np.empty_like(th), np.empty_like(th)
+    rl.oracle().orc_sincos_batch(rl.p(th), rl.p(so), rl.p(co), th.size)
+    assert np.array_equal(H(s), so, equal_nan=True) and np.array_equal(H(c), co, equal_nan=True)
+
+
+@pytest.mark.parametrize("mode,iters", [(1, 8), (1, 16), (1, 24), (1, 5), (2, 8), (2, 24), (0, 24)])
+def test_mac_over_float_classes(mode, iters):
+    """The GEMM's MAC on every 65521st bit pattern of a against 40 values
+    of b (a K = 1 product C = A B: one MAC per output), literal per-MAC
+    checker; the CORDIC tiles holding out-of-range a take the literal
+    rotation chain."""
+    a = _float_sweep(65521).reshape(-1, 1)
+    b = np.concatenate([rl.gen_normal(28, seed=9, std=3.0),
+                        np.float32([0.0, -0.0, 1.0, -1.0, 1e-40, -2.0 ** -120, 3e38, -1.7e38, np.inf, -np.inf,
+                                    np.nan, 2.0 ** -100])]).astype(np.float32).reshape(1, -1)
+    M, N = a.shape[0], b.shape[1]
+    print(f"mac sweep mode={mode} iters={iters} M={M} N={N}", flush=True)
+    got = gemm(a, b, M, N, 1, 0, 0, iters, mode)
+    ref = rl.orc_matmul(a, b, M, N, 1, iters, mode, literal=1)
+    assert np.array_equal(got, ref, equal_nan=True)
+
+
 def test_scalar_rac_h_entry_points():
     L = lib()
     L.rac_set_cordic_iters(16)
