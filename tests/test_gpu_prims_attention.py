@@ -83,6 +83,30 @@ def test_cordic_prims_bit_exact(name):
     assert np.array_equal(got, ref, equal_nan=True), float(np.nanmax(np.abs(got - ref)))
 
 
+def _float_sweep(stride):
+    return (np.arange(0, 2 ** 32, stride, dtype=np.uint64) & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("name", EXACT + ["rotate_n"])
+def test_cordic_prims_over_float_classes(name):
+    """Vector components from every 2039th bit pattern (subnormals, huge,
+    inf, NaN) paired with shuffled partners, angles from every 2039th
+    pattern with |theta| < 2^14 (the wrap loop's bound) plus inf / NaN:
+    bit-exact with the checker."""
+    v = _float_sweep(2039)
+    rng = np.random.default_rng(7)
+    a = np.stack([v, rng.permutation(v)], axis=1)
+    b = np.stack([rng.permutation(v), rng.permutation(v)], axis=1)
+    th = v[~(np.abs(v) >= 16384.0)]
+    th = np.resize(np.concatenate([th, np.float32([np.inf, -np.inf, np.nan])]), len(v))
+    _, _, nb, nt = rl.PRIM_OPS[name]
+    print(f"prim sweep {name} n={len(a)}", flush=True)
+    iarg = 12 if name == "rotate_n" else 0
+    got = _gpu_prim(name, a, b if nb else None, th if nt else None, iarg)
+    ref = rl.orc_prim(name, a, b if nb else None, th if nt else None, iarg)
+    assert np.array_equal(got, ref, equal_nan=True)
+
+
 @pytest.mark.parametrize("iters", [1, 4, 8, 13, 16, 24, 30])
 def test_precision_prims_bit_exact(iters):
     a, _, th = _inputs(1024)
