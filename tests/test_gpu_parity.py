@@ -496,6 +496,40 @@ def test_rmsnorm_layernorm(shape):
         assert np.max(np.abs(z - zr) / np.maximum(np.abs(zr), 1.0)) <= 1e-5
 
 
+@pytest.mark.parametrize("cols", [4096, 1000])
+def test_norm_special_rows(cols):
+    """Rows holding NaN, +-inf, all zeros, only subnormals, huge values whose
+    squares overflow, tiny and mixed magnitudes: NaN exactly where the
+    checker has NaN, zeros where it has zeros, the rest within the row-sum
+    bar."""
+    x = rl.gen_normal((12, cols), 31)
+    x[0, 7] = np.nan
+    x[1, 3] = np.inf
+    x[2, 5] = -np.inf
+    x[3] = 0.0
+    x[4] = np.float32(1e-41) * np.sign(x[4])
+    x[5] = x[5] * np.float32(3e19)                # squares overflow: mean square = inf
+    x[6] = x[6] * np.float32(1e-20)               # squares underflow to ~0: eps dominates
+    x[7, ::3] = np.float32(1e18)
+    x[8] = x[8] * np.float32(1e15)
+    x[9, 0] = np.float32(3e38)
+    g = rl.gen_normal((cols,), 32, mean=1.0, std=0.02)
+    b = rl.gen_normal((cols,), 33, std=0.1)
+    e = ext()
+    for eps in (1e-6, 0.0):
+        y = H(e.rmsnorm(T(x), T(g), eps))
+        r = rl.orc_rmsnorm(x, g, eps)
+        assert np.array_equal(np.isnan(y), np.isnan(r)), eps
+        assert np.array_equal(y == 0, r == 0), eps
+        fin = np.isfinite(r) & (r != 0)
+        assert np.all(np.abs(y[fin] - r[fin]) <= 1e-5 * np.abs(r[fin])), eps
+        z = H(e.layernorm(T(x), T(g), T(b), eps))
+        zr = rl.orc_layernorm(x, g, b, eps)
+        assert np.array_equal(np.isnan(z), np.isnan(zr)), eps
+        fin = np.isfinite(zr)
+        assert np.max(np.abs(z[fin] - zr[fin]) / np.maximum(np.abs(zr[fin]), 1.0)) <= 1e-5, eps
+
+
 def test_norms_vs_reference_golden():
     d = np.load(os.path.join(rl.GOLDEN, "norms.npz"))
     e = ext()
