@@ -92,6 +92,29 @@ def test_gemv_vs_oracle(K, M):
                 assert np.all(np.abs(got - ref) <= 1e-6 * (np.abs(ref) + 1.0)), float(np.max(np.abs(got - ref)))
 
 
+def test_gemv_every_fp16_scale():
+    """Row r's first block carries the fp16 scale with bit pattern r (all
+    65536: zeros, subnormal halves, infinities, NaN payloads), the other
+    blocks scale 0: the device fp16 decode and the block-order fold
+    bit-exact with the checker, fast and generic kernels."""
+    N, K = 65536, 256
+    rng = np.random.default_rng(5)
+    wq = np.zeros((N, K // 32, 34), np.uint8)
+    wq[:, :, 2:] = rng.integers(0, 256, (N, K // 32, 32), dtype=np.uint8)
+    r = np.arange(N, dtype=np.uint32)
+    wq[:, 0, 0] = (r & 0xFF).astype(np.uint8)
+    wq[:, 0, 1] = (r >> 8).astype(np.uint8)
+    x = rng.normal(0, 1, K).astype(np.float32)
+    e = ext()
+    ref = rl.orc_q8_gemv(x, wq, None, 0)[0]
+    got = H(e.q8_gemv(T(x), T(wq), None, 0))
+    assert np.array_equal(got, ref, equal_nan=True)
+    K2 = 224                                      # K % 256 != 0: generic kernel
+    ref2 = rl.orc_q8_gemv(x[:K2], np.ascontiguousarray(wq[:, :K2 // 32]), None, 0)[0]
+    got2 = H(e.q8_gemv(T(x[:K2]), T(np.ascontiguousarray(wq[:, :K2 // 32])), None, 0))
+    assert np.array_equal(got2, ref2, equal_nan=True)
+
+
 def test_gemv_unaligned_input_takes_generic_path():
     e = ext()
     N, K = 70, 512
