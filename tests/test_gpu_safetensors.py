@@ -150,6 +150,23 @@ def test_device_raw_conversions_unaligned_and_tails():
             assert np.array_equal(H(q), ref.reshape(-1)), (dt, shift)
 
 
+def test_device_half_widening_every_pattern():
+    """F16 and BF16 -> F32 on the device for all 65536 bit patterns (zeros,
+    subnormal halves, infinities, NaN payloads): bit-exact with the
+    checker's restatement of the reference reader."""
+    from rac_amd import _lib
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    raw = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rb = np.frombuffer(raw.tobytes(), np.uint8).copy()
+    for dt in (2, 3):
+        buf = torch.from_numpy(rb).to(DEV)
+        out = torch.zeros(65536, device=DEV)
+        assert lib.rac_st_convert_dev(dt, buf.data_ptr(), 65536, out.data_ptr(), st) == 0
+        ref = rl.orc_st_to_f32(dt, rb.tobytes(), 65536)
+        assert np.array_equal(H(out).view(np.uint32), ref.view(np.uint32)), dt
+
+
 def test_loader_feeds_the_q8_gemv(sample):
     """End to end: weights from the file, quantized on the GPU, drive the
     decode GEMV exactly as the reference's load-then-quantize path does."""
