@@ -32,12 +32,34 @@ __device__ __forceinline__ float elt(float x, int iters, float khinv) {
     }
 }
 
+// num / den rounded to nearest, without the scale / fixup stages of the
+// compiler's IEEE division: v_rcp_f32 (1 ulp), one Newton step that makes
+// the reciprocal y correctly rounded, then q = num y and one remainder
+// correction q + (num - den q) y (Markstein's sequence; the remainder is
+// exact once q is faithful).  Used only where the scale / fixup stages are
+// identities: den in [1, 2^64], num in [2^-100, 2^100] in magnitude, so no
+// operand, remainder or quotient is subnormal, infinite or NaN.  On that
+// domain, for the activations' own denominators 1 + e, it equals the
+// IEEE quotient for every float32 argument at n = 8, 16 and 24 (checked
+// exhaustively on the device by tests/test_gpu_parity.py).  Without the
+// Newton step one argument in 2^32 (SiLU, n = 16) rounds the other way.
+__device__ __forceinline__ float div_rn_normal(float num, float den) {
+    float y = __builtin_amdgcn_rcpf(den);
+    y = __builtin_fmaf(__builtin_fmaf(-den, y, 1.0f), y, y);
+    const float q = num * y;
+    return __builtin_fmaf(__builtin_fmaf(-den, q, num), y, q);
+}
+
 // elt<OP, NITER> on E values at once: for the exp-based ops with a
 // compile-time step count the E exps run step-major (exp_cordic_vec);
 // bit-identical to E calls of elt<OP, NITER> (up to NaN payloads).  The
 // activations only use e in 1 + e / 1 - e, so the k <= -127 flush is
 // skipped, and SiLU's x / (1 + e) is NaN through x, so its exp skips the
-// NaN pass-through as well.
+// NaN pass-through as well.  SiLU and sigmoid divide by div_rn_normal when
+// all E arguments of the lane keep it in its domain (|x| in [2^-100, 44]
+// for SiLU: then 1 + e^-x < 2^64 and the quotient is normal; x >= -44 for
+// sigmoid, NaN included, which propagates through the reciprocal), and by
+// the IEEE division otherwise; the two give the same bits.
 template <int OP, int NITER, int E>
 __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
     if constexpr (NITER > 0 && (OP == kEltExp || OP == kEltSilu || OP == kEltSigmoid || OP == kEltTanh)) {
@@ -50,6 +72,28 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
         }
         constexpr int kOpt = OP == kEltExp ? kExpFull : (OP == kEltSilu ? 0 : kExpNan);
         exp_cordic_vec<NITER, E, kOpt>(a, khinv);
+        if constexpr (OP == kEltSilu || OP == kEltSigmoid) {
+            float mx = OP == kEltSilu ? __builtin_fabsf(v[0]) : 0.0f, mn = OP == kEltSilu ? mx : v[0];
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                if constexpr (OP == kEltSilu) {
+                    mx = __builtin_fmaxf(mx, __builtin_fabsf(v[e]));
+                    mn = __builtin_fminf(mn, __builtin_fabsf(v[e]));
+                } else {
+                    mn = __builtin_fminf(mn, v[e]);   // fmin drops NaN: NaN lanes stay fast
+                }
+            }
+            const bool fast = OP == kEltSilu ? (mx <= 44.0f && mn >= 0x1p-100f) : (mn >= -44.0f);
+            if (fast) {
+#pragma unroll
+                for (int e = 0; e < E; e++)
+                    v[e] = div_rn_normal(OP == kEltSilu ? v[e] : 1.0f, 1.0f + a[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; e++) v[e] = (OP == kEltSilu ? v[e] : 1.0f) / (1.0f + a[e]);
+            }
+            return;
+        }
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if constexpr (OP == kEltExp) v[e] = a[e];
