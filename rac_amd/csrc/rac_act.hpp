@@ -37,8 +37,9 @@ __device__ __forceinline__ float elt(float x, int iters, float khinv) {
 // the reciprocal y correctly rounded, then q = num y and one remainder
 // correction q + (num - den q) y (Markstein's sequence; the remainder is
 // exact once q is faithful).  Used only where the scale / fixup stages are
-// identities: den in [1, 2^64], num in [2^-100, 2^100] in magnitude, so no
-// operand, remainder or quotient is subnormal, infinite or NaN.  On that
+// identities: den in [1, 2^64], num = 0 or in [2^-100, 2^100] in magnitude,
+// so no operand, remainder or quotient is subnormal, infinite or NaN (a
+// zero num gives +0 at every step, as the IEEE quotient does).  On that
 // domain, for the activations' own denominators 1 + e, it equals the
 // IEEE quotient for every float32 argument at n = 8, 16 and 24 (checked
 // exhaustively on the device by tests/test_gpu_parity.py).  Without the
@@ -59,7 +60,10 @@ __device__ __forceinline__ float div_rn_normal(float num, float den) {
 // all E arguments of the lane keep it in its domain (|x| in [2^-100, 44]
 // for SiLU: then 1 + e^-x < 2^64 and the quotient is normal; x >= -44 for
 // sigmoid, NaN included, which propagates through the reciprocal), and by
-// the IEEE division otherwise; the two give the same bits.
+// the IEEE division otherwise; the two give the same bits.  tanh always
+// takes it: (1 - e) / (1 + e) with e = e^-2|x| in [0, 1.01) (the CORDIC
+// error at n >= 8 is below 2^-7) has a numerator 0 or of magnitude >= 2^-24
+// (1 - e is exact for e in [0.5, 2)) and a denominator in [1, 2.01].
 template <int OP, int NITER, int E>
 __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
     if constexpr (NITER > 0 && (OP == kEltExp || OP == kEltSilu || OP == kEltSigmoid || OP == kEltTanh)) {
@@ -99,7 +103,7 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
             if constexpr (OP == kEltExp) v[e] = a[e];
             else if constexpr (OP == kEltSilu) v[e] = v[e] / (1.0f + a[e]);
             else if constexpr (OP == kEltSigmoid) v[e] = 1.0f / (1.0f + a[e]);
-            else v[e] = __builtin_copysignf((1.0f - a[e]) / (1.0f + a[e]), v[e]);
+            else v[e] = __builtin_copysignf(div_rn_normal(1.0f - a[e], 1.0f + a[e]), v[e]);
         }
     } else {
 #pragma unroll

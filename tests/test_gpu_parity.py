@@ -304,12 +304,13 @@ def test_exp_family_over_all_float_classes(iters):
 
 
 @pytest.mark.parametrize("iters", [8, 16, 24])
-def test_silu_sigmoid_division_every_float(iters):
-    """SiLU and sigmoid on all 2^32 bit patterns against x / (1 + e) and
-    1 / (1 + e) formed with torch's IEEE division on the device from the
-    library's own e = exp(-x) (the same e the activations use, pinned to the
-    checker by the tests above; the activations skip its k <= -127 flush,
-    which 1 + e cannot see).  Pins the kernels' shortened division
+def test_activation_division_every_float(iters):
+    """SiLU, sigmoid and tanh on all 2^32 bit patterns against x / (1 + e),
+    1 / (1 + e) and copysign((1 - e2) / (1 + e2), x) formed with torch's IEEE
+    division on the device from the library's own e = exp(-x) and
+    e2 = exp(-2|x|) (the exps the activations use, pinned to the checker by
+    the tests above; the activations skip its k <= -127 flush, which 1 + e
+    and 1 - e cannot see).  Pins the kernels' shortened division
     (reciprocal, Newton step, one remainder correction, taken when a lane's
     arguments stay in its range) to the IEEE quotient on every input.
     torch's device division is itself checked against numpy's float32
@@ -319,13 +320,19 @@ def test_silu_sigmoid_division_every_float(iters):
     rng = np.random.default_rng(iters)
     for c in range(16):
         lo = -(1 << 31) + c * CH
-        print(f"silu/sigmoid every float iters={iters} chunk {c}", flush=True)
+        print(f"silu/sigmoid/tanh every float iters={iters} chunk {c}", flush=True)
         x = torch.arange(lo, lo + CH, dtype=torch.int32, device=DEV).view(torch.float32)
         d = 1.0 + e.exp(-x, iters=iters)
-        for name in ("silu", "sigmoid"):
-            num = x if name == "silu" else torch.ones_like(x)
+        e2 = e.exp(-2.0 * x.abs(), iters=iters)
+        for name in ("silu", "sigmoid", "tanh"):
+            if name == "tanh":
+                num, d = 1.0 - e2, 1.0 + e2
+            else:
+                num = x if name == "silu" else torch.ones_like(x)
             got = getattr(e, name)(x, iters=iters)
             ref = torch.div(num, d)
+            if name == "tanh":
+                ref = torch.copysign(ref, x)
             bad = (got.view(torch.int32) != ref.view(torch.int32)) & ~(torch.isnan(got) & torch.isnan(ref))
             n_bad = int(bad.sum())
             if n_bad:
@@ -333,11 +340,11 @@ def test_silu_sigmoid_division_every_float(iters):
                 pytest.fail(f"{name} iters={iters}: {n_bad} mismatches, first x bits "
                             f"{int(x.view(torch.int32)[i]) & 0xFFFFFFFF:#010x}: {float(got[i])!r} vs {float(ref[i])!r}")
             idx = torch.from_numpy(rng.integers(0, CH, 4096)).to(DEV)
-            q = H(ref[idx])
+            q = H(torch.div(num, d)[idx])
             with np.errstate(all="ignore"):
                 assert np.array_equal(q, H(num[idx]) / H(d[idx]), equal_nan=True), name
             del got, ref, bad, num
-        del x, d
+        del x, d, e2
 
 
 def test_elementwise_odd_length_and_offsets():
