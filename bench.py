@@ -671,7 +671,8 @@ def cpu_baseline_child():
     q = np.random.default_rng(0).standard_normal((8, 32, 4096, 128), dtype=np.float32)
     c = np.zeros((4096, 64), np.float32)
     s = np.zeros((4096, 64), np.float32)
-    r.rac_rope_cache(rl.p(c), rl.p(s), 4096, 128, 10000.0)
+    t = timeit(lambda: r.rac_rope_cache(rl.p(c), rl.p(s), 4096, 128, 10000.0), 3)
+    res["rope_cache_4096x128"] = {"seconds": t, "Gentries_per_s": 4096 * 64 / t / 1e9}
     t = timeit(lambda: r.rac_rope_apply(rl.p(q), rl.p(c), rl.p(s), 8, 32, 4096, 128, None), 2)
     res["rope_per_tensor"] = {"seconds": t, "GBps": 2 * q.nbytes / t / 1e9}
     del q
