@@ -418,3 +418,49 @@ def test_st_argument_errors_before_device(lib, tmp_path):
     finally:
         lib.st_close(f)
         lib.st_close(f2)
+
+
+def test_dimension_guards_match_reference(lib):
+    """Non-positive dimensions are refused with RAC_ERR_INVALID_DIM before any
+    device work, as the reference's guards do (rac_cpu.c:393, 482, 515, 556,
+    581, 608, 646); an odd head_dim is refused by the RoPE entry points; an
+    empty elementwise batch is a no-op and a negative one an error."""
+    buf = (ctypes.c_float * 64)()
+    a = ctypes.addressof(buf)
+    bad = (0, -3)
+    for v in bad:
+        for M, N, K in ((v, 4, 4), (4, v, 4), (4, 4, v)):
+            assert lib.rac_gemm_dev(a, a, a, M, N, K, 0, 0, 1.0, 0.0, 16, 1, None) == -2, (M, N, K)
+            assert lib.rac_gemm_batched_dev(a, a, a, M, N, K, 0, 0, 1.0, 0.0, 16, 1, 1, 16, 16, 16,
+                                            None) == -2, (M, N, K)
+        assert lib.rac_gemm_batched_dev(a, a, a, 4, 4, 4, 0, 0, 1.0, 0.0, 16, 1, v, 16, 16, 16, None) == -2
+        for rows, n in ((v, 4), (4, v)):
+            assert lib.rac_softmax_dev(a, a, rows, n, 16, None) == -2, (rows, n)
+            assert lib.rac_rmsnorm_dev(a, a, a, 1e-6, rows, n, None) == -2, (rows, n)
+            assert lib.rac_layernorm_dev(a, a, a, a, 1e-5, rows, n, None) == -2, (rows, n)
+        assert lib.rac_softmax_masked_dev(a, a, v, 4, None, 1, 16, None) == -2
+        assert lib.rac_softmax_masked_dev(a, a, 4, v, None, 1, 16, None) == -2
+        for ms, hd in ((v, 4), (4, v), (4, 5)):
+            assert lib.rac_rope_cache_dev(a, a, ms, hd, 1e4, a, None) == -2, (ms, hd)
+        for dims in ((v, 1, 4, 4), (1, v, 4, 4), (1, 1, v, 4), (1, 1, 4, v), (1, 1, 4, 5)):
+            assert lib.rac_rope_apply_dev(a, a, a, *dims, 16, 16, 4, None) == -2, dims
+        for dims in ((v, 1, 4, 4), (1, v, 4, 4), (1, 1, v, 4), (1, 1, 4, v)):
+            assert lib.rac_attention_dev(a, a, a, None, 0, a, *dims, a, 16, 1, None) == -2, dims
+        for name in ("rac_exp_dev", "rac_silu_dev", "rac_sigmoid_dev", "rac_tanh_dev"):
+            rc = getattr(lib, name)(a, a, v, 16, None)
+            assert rc == (0 if v == 0 else -2), (name, v)
+        for name in ("rac_gelu_dev", "rac_relu_dev", "rac_rsqrt_dev"):
+            assert getattr(lib, name)(a, a, v, None) == (0 if v == 0 else -2), (name, v)
+    # the reference-style void entry points record the same refusal
+    lib.rac_clear_error()
+    lib.rac_layernorm(a, a, None, None, 1e-5, 4, 0)
+    assert b"must be > 0" in lib.rac_last_error()
+    lib.rac_clear_error()
+    lib.rac_rope_cache(a, a, 4, 0, 1e4)
+    assert lib.rac_last_error() != b""
+    lib.rac_clear_error()
+    lib.rac_rope_apply(a, a, a, 1, 1, 0, 4)
+    assert lib.rac_last_error() != b""
+    lib.rac_clear_error()
+    lib.rac_attention(a, a, a, None, 0, a, 1, 1, 0, 4)
+    assert lib.rac_last_error() != b""
