@@ -75,26 +75,39 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
             else a[e] = -v[e];
         }
         constexpr int kOpt = OP == kEltExp ? kExpFull : (OP == kEltSilu ? 0 : kExpNan);
-        exp_cordic_vec<NITER, E, kOpt>(a, khinv);
-        if constexpr (OP == kEltSilu || OP == kEltSigmoid) {
-            float mx = OP == kEltSilu ? __builtin_fabsf(v[0]) : 0.0f, mn = OP == kEltSilu ? mx : v[0];
+        if constexpr (OP == kEltSilu) {
+            // |x| in [2^-100, 44] on every argument of the lane: the exp of -x
+            // cannot overflow (so it drops that select) and the quotient
+            // x / (1 + e) is in div_rn_normal's domain; else the full exp
+            // and the IEEE division.
+            float mx = __builtin_fabsf(v[0]), mn = mx;
 #pragma unroll
-            for (int e = 0; e < E; e++) {
-                if constexpr (OP == kEltSilu) {
-                    mx = __builtin_fmaxf(mx, __builtin_fabsf(v[e]));
-                    mn = __builtin_fminf(mn, __builtin_fabsf(v[e]));
-                } else {
-                    mn = __builtin_fminf(mn, v[e]);   // fmin drops NaN: NaN lanes stay fast
-                }
+            for (int e = 1; e < E; e++) {
+                mx = __builtin_fmaxf(mx, __builtin_fabsf(v[e]));
+                mn = __builtin_fminf(mn, __builtin_fabsf(v[e]));
             }
-            const bool fast = OP == kEltSilu ? (mx <= 44.0f && mn >= 0x1p-100f) : (mn >= -44.0f);
-            if (fast) {
+            if (mx <= 44.0f && mn >= 0x1p-100f) {
+                exp_cordic_vec<NITER, E, kExpNoOvf>(a, khinv);
 #pragma unroll
-                for (int e = 0; e < E; e++)
-                    v[e] = div_rn_normal(OP == kEltSilu ? v[e] : 1.0f, 1.0f + a[e]);
+                for (int e = 0; e < E; e++) v[e] = div_rn_normal(v[e], 1.0f + a[e]);
+            } else {
+                exp_cordic_vec<NITER, E, kOpt>(a, khinv);
+#pragma unroll
+                for (int e = 0; e < E; e++) v[e] = v[e] / (1.0f + a[e]);
+            }
+            return;
+        }
+        exp_cordic_vec<NITER, E, kOpt>(a, khinv);
+        if constexpr (OP == kEltSigmoid) {
+            float mn = v[0];
+#pragma unroll
+            for (int e = 1; e < E; e++) mn = __builtin_fminf(mn, v[e]);   // drops NaN: NaN lanes stay fast
+            if (mn >= -44.0f) {
+#pragma unroll
+                for (int e = 0; e < E; e++) v[e] = div_rn_normal(1.0f, 1.0f + a[e]);
             } else {
 #pragma unroll
-                for (int e = 0; e < E; e++) v[e] = (OP == kEltSilu ? v[e] : 1.0f) / (1.0f + a[e]);
+                for (int e = 0; e < E; e++) v[e] = 1.0f / (1.0f + a[e]);
             }
             return;
         }

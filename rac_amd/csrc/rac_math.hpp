@@ -329,7 +329,9 @@ struct HypStepV {
 //              rounding bias copysign(0.5, x) is the constant -0.5: at x = +0
 //              both biases truncate to k = 0, below 0 they are equal; and
 //              k <= 0, so the overflow select (k > 127 -> inf) is dropped.
-constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4;
+//   kExpNoOvf  every argument is below 88 (k <= 127), so the overflow
+//              select is dropped; the rounding bias keeps its sign.
+constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4, kExpNoOvf = 8;
 constexpr int kExpFull = kExpNan | kExpFlush;
 
 template <int N, int E, int OPT = kExpFull>
@@ -353,7 +355,7 @@ __device__ __forceinline__ void exp_cordic_vec(float* x, float khinv) {
         const float er = p[e] * khinv;
         float res = __builtin_ldexpf(er, k[e]);
         if constexpr ((OPT & kExpFlush) != 0) res = (k[e] <= -127) ? 0.0f : res;
-        if constexpr ((OPT & kExpNonPos) == 0) res = (k[e] > 127) ? __builtin_inff() : res;
+        if constexpr ((OPT & (kExpNonPos | kExpNoOvf)) == 0) res = (k[e] > 127) ? __builtin_inff() : res;
         if constexpr ((OPT & kExpNan) != 0) x[e] = (x[e] != x[e]) ? x[e] : res;
         else x[e] = res;
     }
