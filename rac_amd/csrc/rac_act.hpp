@@ -114,9 +114,7 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if constexpr (OP == kEltExp) v[e] = a[e];
-            else if constexpr (OP == kEltSilu) v[e] = v[e] / (1.0f + a[e]);
-            else if constexpr (OP == kEltSigmoid) v[e] = 1.0f / (1.0f + a[e]);
-            else v[e] = __builtin_copysignf(div_rn_normal(1.0f - a[e], 1.0f + a[e]), v[e]);
+            else v[e] = __builtin_copysignf(div_rn_normal(1.0f - a[e], 1.0f + a[e]), v[e]);   // tanh
         }
     } else {
 #pragma unroll
