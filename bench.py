@@ -251,7 +251,12 @@ def bench_gpu(args):
                      "kernel": f"gemm_kernel<CORDIC,{n},NN> 64x64 tile, 4x4 per lane",
                      "avg_launch_ms": round(launch_s * 1e3, 3),
                      **{f"launch_{k}": v for k, v in _dist_fields(launch_s, 1e3, "ms").items()},
-                     "work_per_mac": f"{w} FMA lane-ops (2n+1)"},
+                     "work_per_mac": f"{w} FMA lane-ops (2n+1)",
+                     # the kernel executes 2n-1 VALU lane-ops per MAC (x0 sign flip,
+                     # x0 * 1.5, 2(n-3)+1 chain FMAs, the gain multiply and the
+                     # accumulate FMA), two fewer than the 2n+1 the roofline counts
+                     "executed_lane_ops_per_mac": 2 * n - 1,
+                     "executed_frac": round(achieved * (2 * n - 1) / w / PEAK_FP32_TFLOPS, 4)},
         "ops": ops,
     }
 
@@ -626,6 +631,10 @@ def cpu_baseline_child():
     if not rl.have_ref():
         print(json.dumps({"error": "oracle/_ref/librac_ref.so not present"}))
         return
+    cpus = os.environ.get("RAC_BENCH_CPUS", "")
+    if cpus:
+        # before the reference's OpenMP runtime starts: its threads inherit this
+        os.sched_setaffinity(0, [int(c) for c in cpus.split(",")])
     r = rl.ref()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     res = {"threads": threads}
@@ -715,17 +724,91 @@ def cpu_baseline_child():
     print(json.dumps(res))
 
 
+def _cpu_list(text):
+    """'0-3,8,10-11' -> [0, 1, 2, 3, 8, 10, 11]."""
+    cpus = []
+    for part in text.strip().split(","):
+        if not part:
+            continue
+        lo, _, hi = part.partition("-")
+        cpus.extend(range(int(lo), int(hi or lo) + 1))
+    return cpus
+
+
+def _read(path):
+    try:
+        with open(path) as f:
+            return f.read().strip()
+    except OSError:
+        return None
+
+
+def _gpu0_host_placement():
+    """Where the CPU baseline runs: the host CPU model, GPU 0's PCI address
+    and NUMA node (sysfs), and one logical CPU per physical core of that node
+    among the CPUs this process may use (all allowed cores when the node is
+    unknown or none of its cores are allowed)."""
+    info = {"cpu_model": None, "gpu_pci_bus": None, "numa_node": None}
+    for line in (_read("/proc/cpuinfo") or "").splitlines():
+        if line.startswith("model name"):
+            info["cpu_model"] = line.split(":", 1)[1].strip()
+            break
+    try:
+        import ctypes
+        hip = ctypes.CDLL("libamdhip64.so.7")       # the runtime torch already loaded
+        buf = ctypes.create_string_buffer(64)
+        if hip.hipDeviceGetPCIBusId(buf, 64, 0) == 0:
+            info["gpu_pci_bus"] = buf.value.decode().lower()
+    except Exception:  # noqa: BLE001
+        pass
+    allowed = sorted(os.sched_getaffinity(0))
+    local = allowed
+    if info["gpu_pci_bus"]:
+        dev = f"/sys/bus/pci/devices/{info['gpu_pci_bus']}"
+        node = _read(dev + "/numa_node")
+        if node is not None and node.lstrip("-").isdigit():
+            info["numa_node"] = int(node)
+        lst = _read(dev + "/local_cpulist")
+        if lst and info["numa_node"] is not None and info["numa_node"] >= 0:
+            local = sorted(set(_cpu_list(lst)) & set(allowed)) or allowed
+    cores = {}
+    for c in local:
+        key = (_read(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id"),
+               _read(f"/sys/devices/system/cpu/cpu{c}/topology/core_id") or str(c))
+        cores.setdefault(key, c)
+    info["allowed_logical_cpus"] = len(allowed)
+    info["node_local_allowed_logical_cpus"] = len(local)
+    info["cpus"] = sorted(cores.values())
+    info["physical_cores"] = len(info["cpus"])
+    return info
+
+
 def run_cpu_baseline():
+    """Times the reference lib/c in a child process pinned to GPU 0's NUMA
+    node: one OpenMP thread per physical core of that node (at most the
+    environment's OMP_NUM_THREADS, which the GPU boxes cap)."""
+    place = _gpu0_host_placement()
+    threads = place["physical_cores"]
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        threads = min(threads, int(cap))
+    cpus = place["cpus"][:threads]
     env = dict(os.environ)
-    env.setdefault("OMP_PROC_BIND", "close")
-    env.setdefault("OMP_PLACES", "cores")
+    env["OMP_NUM_THREADS"] = str(threads)
+    env["OMP_PROC_BIND"] = "close"
+    env["OMP_PLACES"] = ",".join("{%d}" % c for c in cpus)
+    env["RAC_BENCH_CPUS"] = ",".join(str(c) for c in cpus)
     try:
         out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-child"],
                              capture_output=True, text=True, env=env, timeout=240)
         line = [ln for ln in out.stdout.splitlines() if ln.startswith("{")][-1]
-        return json.loads(line)
+        res = json.loads(line)
     except Exception as e:  # noqa: BLE001
-        return {"error": f"cpu baseline failed: {e}"}
+        res = {"error": f"cpu baseline failed: {e}"}
+    res["placement"] = {k: place[k] for k in ("cpu_model", "gpu_pci_bus", "numa_node", "allowed_logical_cpus",
+                                              "node_local_allowed_logical_cpus", "physical_cores")}
+    res["placement"]["cpus_used"] = env["RAC_BENCH_CPUS"]
+    return res
 
 
 def main():
@@ -794,13 +877,17 @@ def main():
         "ops": gpu["ops"],
     }
     if cpu is not None and "matmul" in cpu:
+        pl = cpu.get("placement", {})
         line["cpu_baseline"] = {
             "value": round(cpu["matmul"]["GFLOPs"], 1), "unit": "GFLOP/s", "cores": cpu["threads"],
             "kind": "reference",
             "sample": f"reference lib/c rac_hal_matmul (AVX2 GotoBLAS, FMA; ignores n) 4096^3 x "
-                      f"{cpu['matmul']['reps']} reps, {cpu['threads']} OpenMP threads",
+                      f"{cpu['matmul']['reps']} reps, {cpu['threads']} OpenMP threads, one per physical core "
+                      f"of GPU 0's NUMA node {pl.get('numa_node')} ({pl.get('cpu_model')})",
+            "cpu_model": pl.get("cpu_model"), "numa_node": pl.get("numa_node"),
+            "placement": pl,
             "ops": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in cpu.items()
-                    if isinstance(v, dict) and k != "matmul"},
+                    if isinstance(v, dict) and k not in ("matmul", "placement")},
         }
     elif cpu is not None:
         line["cpu_baseline"] = {"value": None, "unit": "GFLOP/s", "cores": 0, "kind": "reference",

@@ -486,8 +486,9 @@ static int check_attention(const void* q, const void* k, const void* v, const vo
     if (!q || !k || !v || !out) return fail(RAC_ERR_NULL_PTR, "rac_attention: null buffer");
     if (b <= 0 || h <= 0 || t <= 0 || d <= 0) return fail(RAC_ERR_INVALID_DIM, "rac_attention: dims must be > 0");
     if (b * h > 65535L) return fail(RAC_ERR_INVALID_DIM, "rac_attention: batch*n_heads must be <= 65535");
-    if (b * h * t > 2147483647L || t > 2147483647L / 16)
-        return fail(RAC_ERR_INVALID_DIM, "rac_attention: batch*n_heads*seq too large");
+    // one softmax workgroup per score row: at most 16777215 rows per launch
+    if (b * h * t > 16777215L || t > 2147483647L / 16)
+        return fail(RAC_ERR_INVALID_DIM, "rac_attention: batch*n_heads*seq must be <= 16777215");
     return RAC_OK;
 }
 
@@ -657,6 +658,10 @@ static int dsp_device_roms(const DspRoms** out, hipStream_t s) {
         }
     }
     if (d.version != g_dsp_version) {
+        // The buffer is rewritten in place: RAC-DSP kernels queued earlier on
+        // any stream of this device must finish reading the old ROMs first.
+        rc = check_hip(hipDeviceSynchronize(), "RAC-DSP ROM upload (wait for earlier users)");
+        if (rc) return rc;
         rc = check_hip(hipMemcpyAsync(d.ptr, &g_dsp_roms, sizeof(DspRoms), hipMemcpyHostToDevice, s),
                        "RAC-DSP ROM upload");
         if (!rc) rc = check_hip(hipStreamSynchronize(s), "RAC-DSP ROM upload");
@@ -689,17 +694,35 @@ RAC_EXPORT int rac_load_hex_lut(const char* path, uint64_t* out, int expected) {
 
 // rac_load_all_roms (sim/rac_dsp_core.c:74-89): replaces the ROMs used by
 // every later RAC-DSP call; 0 on success, 1/2/3 for the LUT/atan/atanh file.
+// As in the reference the three files are applied one after the other: a
+// file that cannot be opened stops the load with the earlier ROMs already
+// replaced, and a file with fewer entries than its ROM replaces only those
+// entries.  (The reference keeps the previous entries for a short LUT file
+// but copies uninitialised stack words for a short atan or atanh file; here
+// every short file keeps the previous entries.)
 RAC_EXPORT int rac_load_all_roms(const char* coarse_lut_path, const char* atan_path, const char* atanh_path) {
-    uint64_t lut[kDspLut] = {0}, at[kDspAtan] = {0}, ath[kDspRes] = {0};
-    if (rac_load_hex_lut(coarse_lut_path, lut, kDspLut) < 0) return 1;
-    if (rac_load_hex_lut(atan_path, at, kDspAtan) < 0) return 2;
-    if (rac_load_hex_lut(atanh_path, ath, kDspRes) < 0) return 3;
     std::lock_guard<std::mutex> lock(g_dsp_mutex);
-    for (int i = 0; i < kDspLut; i++) g_dsp_roms.lut[i] = (uint16_t)(lut[i] & 0x3ffu);
-    for (int i = 0; i < kDspAtan; i++) g_dsp_roms.atan_rom[i] = (int64_t)at[i];
-    for (int i = 0; i < kDspRes; i++) g_dsp_roms.atanh_rom[i] = (int64_t)ath[i];
-    dsp_derive(g_dsp_roms);
-    g_dsp_version = g_dsp_version + 1 + (g_dsp_version == 0);
+    if (g_dsp_version == 0) {
+        dsp_generate_roms(g_dsp_roms);
+        g_dsp_version = 1;
+    }
+    auto publish = [] {
+        dsp_derive(g_dsp_roms);
+        g_dsp_version = g_dsp_version + 1;
+    };
+    uint64_t words[kDspLut];
+    for (int i = 0; i < kDspLut; i++) words[i] = g_dsp_roms.lut[i];
+    if (rac_load_hex_lut(coarse_lut_path, words, kDspLut) < 0) return 1;
+    for (int i = 0; i < kDspLut; i++) g_dsp_roms.lut[i] = (uint16_t)(words[i] & 0x3ffu);
+    publish();
+    for (int i = 0; i < kDspAtan; i++) words[i] = (uint64_t)g_dsp_roms.atan_rom[i];
+    if (rac_load_hex_lut(atan_path, words, kDspAtan) < 0) return 2;
+    for (int i = 0; i < kDspAtan; i++) g_dsp_roms.atan_rom[i] = (int64_t)words[i];
+    publish();
+    for (int i = 0; i < kDspRes; i++) words[i] = (uint64_t)g_dsp_roms.atanh_rom[i];
+    if (rac_load_hex_lut(atanh_path, words, kDspRes) < 0) return 3;
+    for (int i = 0; i < kDspRes; i++) g_dsp_roms.atanh_rom[i] = (int64_t)words[i];
+    publish();
     return 0;
 }
 

@@ -106,6 +106,104 @@ def _kw():
     return dict(iters=_RAC_CORDIC_ITERS, mode=_RAC_CORDIC_MODE)
 
 
+# ── torch.library ops: the kernels as torch.compile sees them ──────────────
+#
+# The autograd Functions call the GEMM kernels through these ops.  Run
+# eagerly they launch the kernel on the current stream; under torch.compile,
+# tracing with fake tensors uses the shape functions registered beside them
+# (a kernel cannot run on a fake tensor), and the compiled program calls the
+# kernel.  Optional outputs come back as empty tensors.
+
+Tensor = torch.Tensor
+
+
+@torch.library.custom_op("rac_amd::matmul", mutates_args=())
+def _op_matmul(A: Tensor, B: Tensor, iters: int, mode: int) -> Tensor:
+    return _rac.matmul_forward(A, B, iters=iters, mode=mode)
+
+
+@_op_matmul.register_fake
+def _(A, B, iters, mode):
+    return A.new_empty((A.shape[0], B.shape[1]), dtype=torch.float32)
+
+
+@torch.library.custom_op("rac_amd::matmul_backward", mutates_args=())
+def _op_matmul_backward(grad_C: Tensor, A: Tensor, B: Tensor, need_a: bool, need_b: bool,
+                        iters: int, mode: int) -> tuple[Tensor, Tensor]:
+    gA, gB = _rac.matmul_backward(grad_C, A, B, need_a, need_b, iters=iters, mode=mode)
+    return (gA if gA is not None else A.new_empty(0)), (gB if gB is not None else B.new_empty(0))
+
+
+@_op_matmul_backward.register_fake
+def _(grad_C, A, B, need_a, need_b, iters, mode):
+    return (A.new_empty(A.shape) if need_a else A.new_empty(0)), (B.new_empty(B.shape) if need_b else B.new_empty(0))
+
+
+def _no_bias(x: Tensor) -> Tensor:
+    return x.new_empty(0, dtype=torch.float32)
+
+
+@torch.library.custom_op("rac_amd::linear", mutates_args=())
+def _op_linear(input: Tensor, weight: Tensor, bias: Optional[Tensor], iters: int, mode: int) -> Tensor:
+    return _rac.linear_forward(input, weight, bias if bias is not None else _no_bias(input), iters=iters, mode=mode)
+
+
+@_op_linear.register_fake
+def _(input, weight, bias, iters, mode):
+    return input.new_empty((*input.shape[:-1], weight.shape[0]))
+
+
+@torch.library.custom_op("rac_amd::linear_backward", mutates_args=())
+def _op_linear_backward(grad_output: Tensor, input: Tensor, weight: Tensor, need_bias_grad: bool,
+                        iters: int, mode: int) -> tuple[Tensor, Tensor, Tensor]:
+    gi, gw, gb = _rac.linear_backward(grad_output, input, weight, need_bias_grad, iters=iters, mode=mode)
+    return gi, gw, (gb if gb is not None else _no_bias(grad_output))
+
+
+@_op_linear_backward.register_fake
+def _(grad_output, input, weight, need_bias_grad, iters, mode):
+    out_f, in_f = weight.shape
+    f32 = torch.float32
+    gb = grad_output.new_empty((out_f,), dtype=f32) if need_bias_grad else grad_output.new_empty(0, dtype=f32)
+    return (input.new_empty((*input.shape[:-1], in_f), dtype=f32), weight.new_empty((out_f, in_f), dtype=f32), gb)
+
+
+@torch.library.custom_op("rac_amd::fused_linear", mutates_args=())
+def _op_fused_linear(input: Tensor, weight: Tensor, bias: Optional[Tensor], act: int, need_pre: bool,
+                     iters: int, mode: int) -> tuple[Tensor, Tensor]:
+    b = bias if bias is not None else _no_bias(input)
+    if need_pre:
+        out, pre = _rac.fused_linear_forward(input, weight, b, act, return_pre=True, iters=iters, mode=mode)
+        return out, pre
+    return _rac.fused_linear_forward(input, weight, b, act, iters=iters, mode=mode), _no_bias(input)
+
+
+@_op_fused_linear.register_fake
+def _(input, weight, bias, act, need_pre, iters, mode):
+    shape = (*input.shape[:-1], weight.shape[0])
+    pre = input.new_empty(shape, dtype=torch.float32) if need_pre else input.new_empty(0, dtype=torch.float32)
+    return input.new_empty(shape), pre
+
+
+@torch.library.custom_op("rac_amd::fused_linear_backward", mutates_args=())
+def _op_fused_linear_backward(grad_output: Tensor, input: Tensor, weight: Tensor, bias: Optional[Tensor],
+                              pre: Tensor, act: int, need_bias_grad: bool, iters: int,
+                              mode: int) -> tuple[Tensor, Tensor, Tensor]:
+    b = bias if bias is not None else _no_bias(input)
+    gi, gw, gb = _rac.fused_linear_backward(grad_output, input, weight, b, pre, act, need_bias_grad,
+                                            iters=iters, mode=mode)
+    return gi, gw, (gb if gb is not None else _no_bias(grad_output))
+
+
+@_op_fused_linear_backward.register_fake
+def _(grad_output, input, weight, bias, pre, act, need_bias_grad, iters, mode):
+    out_f, in_f = weight.shape
+    dt = grad_output.dtype
+    gb = grad_output.new_empty((out_f,)) if need_bias_grad else grad_output.new_empty(0, dtype=torch.float32)
+    return (grad_output.new_empty((*grad_output.shape[:-1], in_f), dtype=dt),
+            grad_output.new_empty((out_f, in_f), dtype=dt), gb)
+
+
 # ── autograd: matmul / linear (rac_torch.py:163-258) ──────────────────────
 
 class RACMatmulFunction(Function):
@@ -116,19 +214,16 @@ class RACMatmulFunction(Function):
         _need_gpu(A, "A")
         ctx.save_for_backward(A, B)
         dtype = A.dtype
-        C = _rac.matmul_forward(A.float(), B.float(), **_kw())
+        C = _op_matmul(A.float(), B.float(), _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
         return C if dtype == torch.float32 else C.to(dtype)
 
     @staticmethod
     def backward(ctx, grad_C):
         A, B = ctx.saved_tensors
-        gA, gB = _rac.matmul_backward(grad_C.float().contiguous(), A.float(), B.float(),
-                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1], **_kw())
-        if gA is not None:
-            gA = gA.to(A.dtype)
-        if gB is not None:
-            gB = gB.to(B.dtype)
-        return gA, gB
+        need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gA, gB = _op_matmul_backward(grad_C.float().contiguous(), A.float(), B.float(), need_a, need_b,
+                                     _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
+        return (gA.to(A.dtype) if need_a else None), (gB.to(B.dtype) if need_b else None)
 
 
 class RACLinearFunction(Function):
@@ -139,13 +234,13 @@ class RACLinearFunction(Function):
         _need_gpu(input, "input")
         ctx.save_for_backward(input, weight, bias)
         ctx.has_bias = bias is not None
-        b = bias if bias is not None else torch.empty(0, device=input.device)
-        return _rac.linear_forward(input, weight, b, **_kw())
+        return _op_linear(input, weight, bias, _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
 
     @staticmethod
     def backward(ctx, grad_output):
         input, weight, bias = ctx.saved_tensors
-        gi, gw, gb = _rac.linear_backward(grad_output.contiguous(), input, weight, ctx.has_bias, **_kw())
+        gi, gw, gb = _op_linear_backward(grad_output.contiguous(), input, weight, ctx.has_bias,
+                                         _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
         grad_input = gi.to(input.dtype) if ctx.needs_input_grad[0] else None
         grad_weight = gw.to(weight.dtype) if ctx.needs_input_grad[1] else None
         grad_bias = gb.to(bias.dtype) if ctx.has_bias else None
@@ -276,22 +371,16 @@ class RACFusedLinearFunction(Function):
         _need_gpu(input, "input")
         ctx.act_id = act_id
         ctx.has_bias = bias is not None
-        b = bias if bias is not None else torch.empty(0, device=input.device)
         need_pre = act_id != ACT_NONE and any(ctx.needs_input_grad[:3])
-        if need_pre:
-            out, pre = _rac.fused_linear_forward(input, weight, b, act_id, return_pre=True, **_kw())
-        else:
-            out = _rac.fused_linear_forward(input, weight, b, act_id, **_kw())
-            pre = out
-        ctx.save_for_backward(input, weight, bias, pre)
+        out, pre = _op_fused_linear(input, weight, bias, act_id, need_pre, _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
+        ctx.save_for_backward(input, weight, bias, pre if need_pre else out)
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
         input, weight, bias, pre = ctx.saved_tensors
-        b = bias if bias is not None else torch.empty(0, device=input.device)
-        gi, gw, gb = _rac.fused_linear_backward(grad_output.contiguous(), input, weight, b, pre, ctx.act_id,
-                                                ctx.has_bias, **_kw())
+        gi, gw, gb = _op_fused_linear_backward(grad_output.contiguous(), input, weight, bias, pre, ctx.act_id,
+                                               ctx.has_bias, _RAC_CORDIC_ITERS, _RAC_CORDIC_MODE)
         grad_input = gi.to(input.dtype) if ctx.needs_input_grad[0] else None
         grad_weight = gw.to(weight.dtype) if ctx.needs_input_grad[1] else None
         grad_bias = gb.to(bias.dtype) if ctx.has_bias else None
@@ -363,13 +452,24 @@ class RACFusedQKV(nn.Module):
 
     @classmethod
     def from_qkv_linears(cls, q_linear, k_linear, v_linear):
+        """One fused module from three d_model -> d_model projections: rows
+        [0, d), [d, 2d), [2d, 3d) of the fused weight (and bias) are Q's, K's
+        and V's, so chunk(3) in forward hands each projection back."""
+        parts = (q_linear, k_linear, v_linear)
         d_model = q_linear.in_features
-        has_bias = q_linear.bias is not None
-        fused = cls(d_model, bias=has_bias, device=q_linear.weight.device, dtype=q_linear.weight.dtype)
+        if any(p.in_features != d_model or p.out_features != d_model for p in parts):
+            raise ValueError("from_qkv_linears: Q, K and V must all map d_model -> d_model")
+        with_bias = q_linear.bias is not None
+        if any((p.bias is not None) != with_bias for p in parts):
+            raise ValueError("from_qkv_linears: Q, K and V must all have a bias or none")
+        ref = q_linear.weight
+        fused = cls(d_model, bias=with_bias, device=ref.device, dtype=ref.dtype)
         with torch.no_grad():
-            fused.qkv.weight.copy_(torch.cat([q_linear.weight, k_linear.weight, v_linear.weight], dim=0))
-            if has_bias:
-                fused.qkv.bias.copy_(torch.cat([q_linear.bias, k_linear.bias, v_linear.bias], dim=0))
+            for slot, p in enumerate(parts):
+                rows = slice(slot * d_model, (slot + 1) * d_model)
+                fused.qkv.weight[rows].copy_(p.weight)
+                if with_bias:
+                    fused.qkv.bias[rows].copy_(p.bias)
         return fused
 
     def extra_repr(self):
@@ -827,83 +927,96 @@ class RACLlamaBlock(nn.Module):
                 f'ff_dim={self.ffn.fc1.out_features}')
 
 
-# ── model patching (rac_torch.py:865-940) ──────────────────────────────────
+# ── model patching (rac_torch.py:865-985) ──────────────────────────────────
+#
+# The interface fixes the names, the arguments, the min_features rule (both
+# dimensions at least min_features), exact weight preservation and the keys
+# of benchmark_model's result.  The traversal works on a snapshot of
+# (owner, attribute) slots taken before anything is replaced, so swapping a
+# child never disturbs the walk.
+
+def _child_slots(model: nn.Module):
+    """Every (dotted name, owner module, attribute, child) of the tree."""
+    slots = []
+    for owner_name, owner in model.named_modules():
+        for attr, child in owner.named_children():
+            slots.append((f'{owner_name}.{attr}' if owner_name else attr, owner, attr, child))
+    return slots
+
+
+def _copy_params(dst: nn.Module, src: nn.Module) -> nn.Module:
+    """dst.weight/bias := src.weight/bias, bit for bit."""
+    with torch.no_grad():
+        dst.weight.copy_(src.weight)
+        if src.bias is not None:
+            dst.bias.copy_(src.bias)
+    return dst
+
 
 def patch_model(model: nn.Module, verbose: bool = True, min_features: int = 64) -> nn.Module:
-    """Replace every nn.Linear (both dims >= min_features) with RACLinear."""
-    replaced = []
-
-    def _replace(module: nn.Module, prefix: str = ''):
-        for name, child in module.named_children():
-            full = f'{prefix}.{name}' if prefix else name
-            if isinstance(child, nn.Linear) and not isinstance(child, RACLinear):
-                if child.in_features >= min_features and child.out_features >= min_features:
-                    setattr(module, name, RACLinear.from_linear(child))
-                    replaced.append((full, child.in_features, child.out_features))
-                elif verbose:
-                    print(f'  skip  {full}: {child.in_features}->{child.out_features} (below min_features)')
-            else:
-                _replace(child, full)
-
-    _replace(model)
+    """Swap every plain nn.Linear whose in and out features are both at least
+    min_features for a RACLinear holding the same parameters; smaller layers
+    stay as they are.  Returns the model (modified in place)."""
+    swapped, kept = [], []
+    for name, owner, attr, child in _child_slots(model):
+        if not isinstance(child, nn.Linear):    # RACLinear is not an nn.Linear subclass
+            continue
+        shape = (child.in_features, child.out_features)
+        if min(shape) < min_features:
+            kept.append((name, shape))
+            continue
+        setattr(owner, attr, RACLinear.from_linear(child))
+        swapped.append((name, shape))
     if verbose:
-        print(f'patch_model: replaced {len(replaced)} Linear layers with RACLinear')
-        for name, inf, outf in replaced:
-            print(f'  +  {name}: {inf}->{outf}')
+        for name, (fi, fo) in kept:
+            print(f'patch_model: {name} stays nn.Linear ({fi} x {fo} is below min_features={min_features})')
+        print(f'patch_model: {len(swapped)} of {len(swapped) + len(kept)} nn.Linear layers now run through RAC')
+        for name, (fi, fo) in swapped:
+            print(f'    {name:<40s} {fi:>6d} -> {fo:<6d}')
     return model
 
 
 def unpatch_model(model: nn.Module, verbose: bool = True) -> nn.Module:
-    """Reverse patch_model."""
-    restored = []
-
-    def _restore(module: nn.Module, prefix: str = ''):
-        for name, child in module.named_children():
-            full = f'{prefix}.{name}' if prefix else name
-            if isinstance(child, RACLinear):
-                lin = nn.Linear(child.in_features, child.out_features, bias=child.bias is not None,
-                                device=child.weight.device, dtype=child.weight.dtype)
-                with torch.no_grad():
-                    lin.weight.copy_(child.weight)
-                    if child.bias is not None:
-                        lin.bias.copy_(child.bias)
-                setattr(module, name, lin)
-                restored.append(full)
-            else:
-                _restore(child, full)
-
-    _restore(model)
+    """Undo patch_model: every RACLinear (not the fused variants) becomes an
+    nn.Linear with the same parameters, device and dtype."""
+    count = 0
+    for name, owner, attr, child in _child_slots(model):
+        if type(child) is not RACLinear:
+            continue
+        plain = nn.Linear(child.in_features, child.out_features, bias=child.bias is not None,
+                          device=child.weight.device, dtype=child.weight.dtype)
+        setattr(owner, attr, _copy_params(plain, child))
+        count += 1
     if verbose:
-        print(f'unpatch_model: restored {len(restored)} RACLinear -> Linear')
+        print(f'unpatch_model: {count} RACLinear layer(s) turned back into nn.Linear')
     return model
 
 
 def benchmark_model(model: nn.Module, input_shape: tuple, n_warmup: int = 10, n_iters: int = 100,
                     device: str = 'cuda') -> dict:
-    """Time a model before and after patch_model (rac_torch.py:945-985)."""
-    import time
-
+    """Mean forward time of `model` on one random input as given, then with
+    its linear layers on RAC (patch_model), then restored (unpatch_model).
+    Times come from device events on the current stream."""
     model = model.to(device).eval()
-    x = torch.randn(*input_shape, device=device)
+    sample = torch.randn(*input_shape, device=device)
 
-    def _time(m):
-        with torch.no_grad():
+    def mean_ms(m):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.inference_mode():
             for _ in range(n_warmup):
-                m(x)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        with torch.no_grad():
+                m(sample)
+            start.record()
             for _ in range(n_iters):
-                m(x)
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / n_iters * 1000
+                m(sample)
+            stop.record()
+        stop.synchronize()
+        return start.elapsed_time(stop) / max(n_iters, 1)
 
-    base = _time(model)
-    patched = patch_model(model, verbose=False)
-    rac_ms = _time(patched)
-    unpatch_model(patched, verbose=False)
-    return {'baseline_ms': base, 'rac_ms': rac_ms,
-            'speedup': base / rac_ms if rac_ms > 0 else float('inf'), 'n_iters': n_iters}
+    torch_ms = mean_ms(model)
+    rac_ms = mean_ms(patch_model(model, verbose=False))
+    unpatch_model(model, verbose=False)
+    return {'baseline_ms': torch_ms, 'rac_ms': rac_ms,
+            'speedup': (torch_ms / rac_ms) if rac_ms > 0 else float('inf'), 'n_iters': n_iters}
 
 
 def rac_info():
@@ -923,11 +1036,3 @@ def rac_info():
     print("  kernels:               matmul/linear (FAST/CORDIC/SHIFTADD), softmax + SiLU + sigmoid "
           "(hyperbolic CORDIC exp), RMSNorm/LayerNorm (CORDIC rsqrt), RoPE (circular CORDIC)")
     print(f"  adaptive threshold:    {_RAC_MIN_ELEMENTS} elements (RAC_MIN_ELEMENTS)")
-
-
-try:
-    if hasattr(torch, '_dynamo') and hasattr(torch._dynamo, 'allow_in_graph'):
-        for _fn in (RACMatmulFunction, RACLinearFunction, RACFusedLinearFunction):
-            torch._dynamo.allow_in_graph(_fn)
-except Exception:  # noqa: BLE001
-    warnings.warn("torch.compile registration of RAC functions failed; eager mode only", RuntimeWarning)

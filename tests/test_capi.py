@@ -225,23 +225,46 @@ def test_dsp_rom_loaders(lib, tmp_path):
     assert np.array_equal(buf, lut2)
     assert lib.rac_load_hex_lut(paths[1].encode(), rl.p(buf), 5) == 5           # capped at `expected`
     assert lib.rac_load_hex_lut(str(tmp_path / "absent").encode(), rl.p(buf), 4) == -1
+    g_lut, g_at, g_ath = d["lut"], d["atan"], d["atanh"]       # held: rl.p does not own the memory
+
+    def restore():
+        lib.rac_dsp_set_roms(rl.p(g_lut), rl.p(g_at), rl.p(g_ath))
+
     try:
         missing = str(tmp_path / "absent").encode()
+        # the files are applied in order and a failure stops there, with the
+        # earlier ROMs already replaced (sim/rac_dsp_core.c:74-89)
         assert lib.rac_load_all_roms(missing, paths[1].encode(), paths[2].encode()) == 1
+        lut, at, ath = _dsp_roms(lib)
+        assert np.array_equal(lut, g_lut) and np.array_equal(at, g_at)
         assert lib.rac_load_all_roms(paths[0].encode(), missing, paths[2].encode()) == 2
+        lut, at, ath = _dsp_roms(lib)
+        assert np.array_equal(lut, lut2) and np.array_equal(at, g_at)
+        restore()
         assert lib.rac_load_all_roms(paths[0].encode(), paths[1].encode(), missing) == 3
-        lut, at, ath = _dsp_roms(lib)                     # failed loads change nothing
-        assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"])
+        lut, at, ath = _dsp_roms(lib)
+        assert np.array_equal(lut, lut2) and np.array_equal(at, at2) and np.array_equal(ath, g_ath)
+        restore()
         assert lib.rac_load_all_roms(*(p.encode() for p in paths)) == 0
         lut, at, ath = _dsp_roms(lib)
-        assert np.array_equal(lut, lut2) and np.array_equal(at, at2) and np.array_equal(ath, d["atanh"])
-        g_lut, g_at, g_ath = d["lut"], d["atan"], d["atanh"]       # held: rl.p does not own the memory
+        assert np.array_equal(lut, lut2) and np.array_equal(at, at2) and np.array_equal(ath, g_ath)
         lib.rac_dsp_set_roms(None, rl.p(g_at), None)
         lut, at, _ = _dsp_roms(lib)
         assert np.array_equal(lut, lut2) and np.array_equal(at, g_at)
+        # a short file replaces only the entries it holds; the rest keep
+        # their previous values (for the LUT exactly as the reference does)
+        restore()
+        short = [str(tmp_path / n) for n in ("lut_short.mem", "atan_short.mem", "atanh_short.mem")]
+        _write_mem(short[0], lut2[:10])
+        _write_mem(short[1], at2[:5])
+        _write_mem(short[2], g_ath[:2] + 7)
+        assert lib.rac_load_all_roms(*(p.encode() for p in short)) == 0
+        lut, at, ath = _dsp_roms(lib)
+        assert np.array_equal(lut[:10], lut2[:10]) and np.array_equal(lut[10:], g_lut[10:])
+        assert np.array_equal(at[:5], at2[:5]) and np.array_equal(at[5:], g_at[5:])
+        assert np.array_equal(ath[:2], g_ath[:2] + 7) and np.array_equal(ath[2:], g_ath[2:])
     finally:
-        g_lut, g_at, g_ath = d["lut"], d["atan"], d["atanh"]
-        lib.rac_dsp_set_roms(rl.p(g_lut), rl.p(g_at), rl.p(g_ath))
+        restore()
     lut, at, ath = _dsp_roms(lib)
     assert np.array_equal(lut, d["lut"]) and np.array_equal(at, d["atan"]) and np.array_equal(ath, d["atanh"])
 
@@ -451,6 +474,10 @@ def test_dimension_guards_match_reference(lib):
             assert rc == (0 if v == 0 else -2), (name, v)
         for name in ("rac_gelu_dev", "rac_relu_dev", "rac_rsqrt_dev"):
             assert getattr(lib, name)(a, a, v, None) == (0 if v == 0 else -2), (name, v)
+    # one softmax workgroup per score row: more than 16777215 rows is refused
+    # before the scores product runs
+    assert lib.rac_attention_dev(a, a, a, None, 1, a, 1, 4096, 4097, 4, a, 16, 1, None) == -2
+    assert b"16777215" in lib.rac_last_error()
     # the reference-style void entry points record the same refusal
     lib.rac_clear_error()
     lib.rac_layernorm(a, a, None, None, 1e-5, 4, 0)
@@ -464,3 +491,50 @@ def test_dimension_guards_match_reference(lib):
     lib.rac_clear_error()
     lib.rac_attention(a, a, a, None, 0, a, 1, 1, 0, 4)
     assert lib.rac_last_error() != b""
+
+
+def test_rac_cuda_ext_exports_the_reference_surface():
+    """The reference's extension module name (rac_torch_bind.cpp:223-258)
+    resolves to rac_amd.ext's objects (no compute calls here)."""
+    import rac_cuda_ext
+    from rac_amd import ext
+    for name in ("matmul_forward", "matmul_backward", "linear_forward", "linear_backward", "set_cordic_iters",
+                 "get_cordic_iters", "set_cordic_mode", "get_cordic_mode", "MODE_FAST", "MODE_CORDIC",
+                 "MODE_SHIFTADD", "fused_linear_forward", "fused_linear_backward", "softmax", "rmsnorm",
+                 "rope_apply_", "attention"):
+        assert getattr(rac_cuda_ext, name) is getattr(ext, name), name
+    assert set(rac_cuda_ext.__all__) == set(ext.__all__)
+
+
+def test_patch_helpers_and_qkv_fusion_on_cpu(capsys):
+    """patch_model / unpatch_model keep parameters bit for bit and follow the
+    min_features rule through nested modules; from_qkv_linears stacks Q, K, V
+    rows in that order and refuses mismatched projections."""
+    import torch
+    import torch.nn as nn
+    from rac_amd import rac_torch as rt
+
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(96, 128), nn.Sequential(nn.ReLU(), nn.Linear(128, 80)), nn.Linear(80, 8))
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    rt.patch_model(model, verbose=True, min_features=64)
+    out = capsys.readouterr().out
+    assert isinstance(model[0], rt.RACLinear) and isinstance(model[1][1], rt.RACLinear)
+    assert type(model[2]) is nn.Linear                                   # 80 -> 8 is below 64
+    assert "2 of 3" in out and "1.1" in out and "min_features=64" in out
+    assert all(torch.equal(before[k], v) for k, v in model.state_dict().items())
+    rt.unpatch_model(model, verbose=True)
+    assert "2 RACLinear" in capsys.readouterr().out
+    assert type(model[0]) is nn.Linear and type(model[1][1]) is nn.Linear
+    assert all(torch.equal(before[k], v) for k, v in model.state_dict().items())
+
+    lq, lk, lv = (nn.Linear(16, 16) for _ in range(3))
+    fused = rt.RACFusedQKV.from_qkv_linears(lq, lk, lv)
+    w = fused.qkv.weight.detach()
+    assert torch.equal(w[:16], lq.weight) and torch.equal(w[16:32], lk.weight) and torch.equal(w[32:], lv.weight)
+    b = fused.qkv.bias.detach()
+    assert torch.equal(b[:16], lq.bias) and torch.equal(b[32:], lv.bias)
+    with pytest.raises(ValueError):
+        rt.RACFusedQKV.from_qkv_linears(lq, nn.Linear(16, 8), lv)
+    with pytest.raises(ValueError):
+        rt.RACFusedQKV.from_qkv_linears(lq, nn.Linear(16, 16, bias=False), lv)
