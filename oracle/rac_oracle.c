@@ -683,6 +683,162 @@ ORC_API int orc_layernorm(const float *x, float *y, const float *gamma,
     return 0;
 }
 
+/* ── Row sums in the gfx950 row kernels' order ────────────────────────────
+ * orc_rmsnorm, orc_layernorm and orc_softmax_rows add a row left to right,
+ * as rac_cpu.c does.  The device row kernels add it as a tree: 256 lanes,
+ * lane l owning the float4 groups l, l + 256, l + 512, ... (VPT groups, VPT
+ * the smallest of 1, 2, 4, 8, 16 with n/4 <= 256 VPT; rows with n % 4 != 0
+ * or n/4 > 4096 are owned element-wise, lane l taking elements l, l + 256,
+ * ...), each lane adding its own elements in that order; then the 64 lanes
+ * of each wave combine by a butterfly (lane l adds lane l ^ 32, then l ^ 16,
+ * ..., l ^ 1; IEEE addition commutes, so both partners hold the same sum)
+ * and the four wave sums are added in wave order.  The *_lanes functions
+ * below are the same computations as their left-to-right counterparts with
+ * only the row sums regrouped that way, so the GPU kernels can be checked
+ * bit for bit instead of within a reordering bound.  Every other rounding
+ * (max, CORDIC exp, rsqrt, the output products) is the one of the
+ * counterpart.  Pinned in tests/test_oracle.py: equal to the left-to-right
+ * versions where every partial sum is exact, and within the reordering
+ * bound of them otherwise. */
+
+#define ORC_ROW_LANES 256
+
+/* Number of elements (slots) each lane owns in a row of n (the owner map
+ * above). */
+static int row_slots(int n)
+{
+    int n4 = n / 4;
+    if (n % 4 == 0) {
+        for (int vpt = 1; vpt <= 16; vpt *= 2)
+            if (n4 <= ORC_ROW_LANES * vpt) return 4 * vpt;
+    }
+    return (n + ORC_ROW_LANES - 1) / ORC_ROW_LANES;
+}
+
+/* Butterfly within each wave of 64 lanes, then the 4 wave sums in order. */
+static float lanes_combine(const float *lane)
+{
+    float red[ORC_ROW_LANES / 64];
+    for (int w = 0; w < ORC_ROW_LANES / 64; w++) {
+        float v[64], t[64];
+        memcpy(v, lane + 64 * w, sizeof v);
+        for (int off = 32; off > 0; off >>= 1) {
+            for (int l = 0; l < 64; l++) t[l] = v[l] + v[l ^ off];
+            memcpy(v, t, sizeof v);
+        }
+        red[w] = v[0];
+    }
+    float r = red[0];
+    for (int w = 1; w < ORC_ROW_LANES / 64; w++) r += red[w];
+    return r;
+}
+
+/* The element index held in (lane, slot), or -1 past the row end. */
+static int row_elem(int n, int lane, int slot)
+{
+    int n4 = n / 4;
+    if (n % 4 == 0 && n4 <= ORC_ROW_LANES * 16) {
+        int g = lane + ORC_ROW_LANES * (slot / 4);
+        return g < n4 ? 4 * g + slot % 4 : -1;
+    }
+    int i = lane + ORC_ROW_LANES * slot;
+    return i < n ? i : -1;
+}
+
+/* sum over the row of f(i) in lane order; f(i) of a missing element
+ * contributes nothing (the kernels' padding adds +0 or is skipped). */
+#define ROW_LANE_SUM(n, result, ACC_INIT, ACC_STEP)                           \
+    do {                                                                      \
+        float lane_[ORC_ROW_LANES];                                           \
+        int slots_ = row_slots(n);                                            \
+        for (int l_ = 0; l_ < ORC_ROW_LANES; l_++) {                          \
+            float acc = ACC_INIT;                                             \
+            for (int s_ = 0; s_ < slots_; s_++) {                             \
+                int i = row_elem(n, l_, s_);                                  \
+                if (i >= 0) { ACC_STEP; }                                     \
+            }                                                                 \
+            lane_[l_] = acc;                                                  \
+        }                                                                     \
+        result = lanes_combine(lane_);                                        \
+    } while (0)
+
+/* rac_rmsnorm (rac_cpu.c:548-574) with the lane-order sum of squares. */
+ORC_API int orc_rmsnorm_lanes(const float *x, float *y, const float *gamma, float eps, int rows, int d)
+{
+    if (!x || !y) return -1;
+    if (rows <= 0 || d <= 0) return -2;
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * d;
+        float *yr = y + (size_t)r * d;
+        float ss;
+        ROW_LANE_SUM(d, ss, 0.0f, acc = fmaf(xr[i], xr[i], acc));
+        float inv = rsqrt_sel(ss / (float)d + eps, 1);
+        for (int i = 0; i < d; i++) {
+            float g = gamma ? gamma[i] : 1.0f;
+            yr[i] = xr[i] * inv * g;
+        }
+    }
+    return 0;
+}
+
+/* rac_layernorm (rac_cpu.c:507-546) with lane-order sums. */
+ORC_API int orc_layernorm_lanes(const float *x, float *y, const float *gamma, const float *beta, float eps,
+                                int rows, int d)
+{
+    if (!x || !y) return -1;
+    if (rows <= 0 || d <= 0) return -2;
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * d;
+        float *yr = y + (size_t)r * d;
+        float sm, sv;
+        ROW_LANE_SUM(d, sm, 0.0f, acc += xr[i]);
+        float mean = sm / (float)d;
+        ROW_LANE_SUM(d, sv, 0.0f, { float z = xr[i] - mean; acc = fmaf(z, z, acc); });
+        float inv = rsqrt_sel(sv / (float)d + eps, 1);
+        for (int i = 0; i < d; i++) {
+            float z = (xr[i] - mean) * inv;
+            float g = gamma ? gamma[i] : 1.0f;
+            float b = beta ? beta[i] : 0.0f;
+            yr[i] = fmaf(g, z, b);
+        }
+    }
+    return 0;
+}
+
+/* Row softmax (rac_cpu.c:258-271; CORDIC exp of `iters` steps) with the
+ * lane-order row sum.  With masking on (causal, an additive [seq, seq] mask
+ * or the zero-sum guard, the attention form of rac_cpu.c:668-689), row r is
+ * query position t = r % seq: causal sets -inf above the diagonal, then the
+ * mask is added, and a non-positive sum gives inv = 0 when zero_guard. */
+ORC_API int orc_softmax_lanes(const float *x, float *out, int rows, int n, int iters, int causal,
+                              const float *mask, int zero_guard)
+{
+    if (!x || !out) return -1;
+    if (rows <= 0 || n <= 0) return -2;
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * n;
+        float *o = out + (size_t)r * n;
+        int t = r % n;
+        for (int i = 0; i < n; i++) {
+            float v = xr[i];
+            if (causal && i > t) v = -INFINITY;
+            if (mask) v += mask[(size_t)t * n + i];
+            o[i] = v;
+        }
+        float m = o[0];
+        for (int i = 1; i < n; i++) if (o[i] > m) m = o[i];
+        for (int i = 0; i < n; i++) o[i] = orc_exp_n(o[i] - m, iters);
+        float s;
+        ROW_LANE_SUM(n, s, 0.0f, acc += o[i]);
+        float inv = (zero_guard && !(s > 0.0f)) ? 0.0f : 1.0f / s;
+        for (int i = 0; i < n; i++) o[i] *= inv;
+    }
+    return 0;
+}
+
 /* ── Activations (A12) ──────────────────────────────────────────────────── */
 
 /* rac_silu, rac_cpu.c:453-457: x / (1 + e^-x), with e^-x from the n-step

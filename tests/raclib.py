@@ -77,6 +77,9 @@ _ORACLE_SIGS = {
     "orc_rmsnorm": (_i, [_vp, _vp, _vp, _f, _i, _i, _i]),
     "orc_layernorm": (_i, [_vp, _vp, _vp, _vp, _f, _i, _i, _i]),
     "orc_silu": (None, [_vp, _vp, _l, _i]),
+    "orc_rmsnorm_lanes": (_i, [_vp, _vp, _vp, _f, _i, _i]),
+    "orc_layernorm_lanes": (_i, [_vp, _vp, _vp, _vp, _f, _i, _i]),
+    "orc_softmax_lanes": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _i]),
     "orc_sigmoid": (None, [_vp, _vp, _l, _i]),
     "orc_gelu": (None, [_vp, _vp, _l]),
     "orc_tanh": (None, [_vp, _vp, _l, _i]),
@@ -296,6 +299,34 @@ def orc_layernorm(x, g, b, eps, use_cordic=1):
     return y
 
 
+def orc_rmsnorm_lanes(x, g, eps):
+    """RMSNorm with the row kernels' lane-order sum (bit-exact checker)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    assert oracle().orc_rmsnorm_lanes(p(x), p(y), p(g) if g is not None else None, eps,
+                                      x.shape[0], x.shape[1]) == 0
+    return y
+
+
+def orc_layernorm_lanes(x, g, b, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    assert oracle().orc_layernorm_lanes(p(x), p(y), p(g) if g is not None else None,
+                                        p(b) if b is not None else None, eps, x.shape[0], x.shape[1]) == 0
+    return y
+
+
+def orc_softmax_lanes(x, iters, causal=False, mask=None, zero_guard=False):
+    """Row softmax with the row kernels' lane-order sum; with masking, row r
+    is query position r % n (the attention layout)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    assert oracle().orc_softmax_lanes(p(x), p(y), x.shape[0], x.shape[1], iters, int(causal),
+                                      p(m) if m is not None else None, int(zero_guard)) == 0
+    return y
+
+
 def orc_rope_cache(max_seq, head_dim, base=10000.0):
     half = head_dim // 2
     c = np.empty((max_seq, half), np.float32)
@@ -338,6 +369,21 @@ def orc_attention(q, k, v, mask, causal, iters, mode):
     m = None if mask is None else np.ascontiguousarray(mask, np.float32)
     assert oracle().orc_attention(p(q), p(k), p(v), p(m) if m is not None else None, int(causal),
                                   p(out), B, H, T, D, iters, mode) == 0
+    return out
+
+
+def orc_attention_lanes(q, k, v, mask, causal, iters, mode):
+    """rac_attention composed from the checker's products and the lane-order
+    masked softmax (zero-sum guard on), head by head: the GPU's bits."""
+    q, k, v = (np.ascontiguousarray(t, np.float32) for t in (q, k, v))
+    B, Hh, Tn, D = q.shape
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = np.empty_like(q)
+    for b in range(B):
+        for h in range(Hh):
+            sc = orc_matmul(q[b, h], k[b, h], Tn, Tn, D, iters, mode, tb=1, alpha=scale)
+            pr = orc_softmax_lanes(sc, iters, causal=causal, mask=mask, zero_guard=True)
+            out[b, h] = orc_matmul(pr, v[b, h], Tn, D, Tn, iters, mode)
     return out
 
 

@@ -9,15 +9,21 @@ the stage is checked on its own GPU input against the CPU checker:
     checker's CORDIC SiLU);
   * RoPE on the full Q and K: bit-exact with orc_rope_apply on the CORDIC-16
     table;
-  * RMSNorm on 256 sampled rows of each norm: <= 1e-5 relative;
+  * RMSNorm on 256 sampled rows of each norm: bit-exact with
+    orc_rmsnorm_lanes (the kernel's row-sum order) and <= 1e-5 relative to
+    the left-to-right orc_rmsnorm;
   * the causal attention core on 256 sampled (head, query) rows: scores
-    bit-exact from orc_matmul_entries, probabilities from orc_softmax, output
-    row from orc_matmul_entries on those probabilities, within the row-sum
-    order bound T * 2^-24 * max|v|;
+    from orc_matmul_entries, probabilities from orc_softmax_lanes, output
+    row from orc_matmul_entries on those probabilities, bit-exact (and
+    within the row-sum order bound T * 2^-24 * max|v| of the left-to-right
+    softmax);
   * both residual adds, exact.
 Then rows 0..3 of the block output are recomputed end to end from x by the
-checker's composition (causality makes them depend on rows 0..3 only) and
-compared at max|y - ref| / max(|ref|, 1) < 1e-4.
+checker's composition (causality makes them depend on rows 0..3 only):
+bit-exact with the lane-order sums, and within max|y - ref| / max(|ref|, 1)
+< 1e-4 at n = 16, 24 with the left-to-right sums (at n = 8 a one-ulp change
+of an exp argument can flip a CORDIC direction and move e^x by ~2^-6, so
+only the bit-exact comparison is meaningful there).
 Templates: reference lib/c/test_rac_lib_e2e.c:313-378 (block composition
 from library ops) and rac_torch/rac_torch.py:1348-1383 (the block).
 """
@@ -135,8 +141,8 @@ def _check_rms(name, x, gamma, got, rng):
     x = x.reshape(-1, D_MODEL)
     got = got.reshape(-1, D_MODEL)
     r = np.sort(rng.choice(x.shape[0], 256, replace=False))
-    ref = rl.orc_rmsnorm(x[r], gamma, 1e-6)
-    err = rl.max_rel(got[r], ref, 1e-6)
+    assert np.array_equal(got[r], rl.orc_rmsnorm_lanes(x[r], gamma, 1e-6)), name
+    err = rl.max_rel(got[r], rl.orc_rmsnorm(x[r], gamma, 1e-6), 1e-6)
     assert err < 1e-5, f"{name}: max relative error {err:.3e}"
 
 
@@ -181,12 +187,18 @@ def test_llama_block_config5_sampled(block, n):
         qh, kh, vh = np.ascontiguousarray(q[0, hh]), np.ascontiguousarray(k[0, hh]), v[0, hh]
         ks = np.arange(t + 1, dtype=np.int32)
         acc = rl.orc_matmul_entries(qh, kh, SEQ, SEQ, HD, n, 1, np.full(t + 1, t, np.int32), ks, tb=1)
-        sc = (acc * scale).astype(np.float32)
-        prob = rl.orc_softmax(sc[None, :], n)
+        row = np.full((1, SEQ), -np.inf, np.float32)
+        row[0, :t + 1] = acc * scale
+        prob = rl.orc_softmax_lanes(row, n, zero_guard=True)
+        assert not prob[0, t + 1:].any()
         vt = np.ascontiguousarray(vh[:t + 1])
-        ref = rl.orc_matmul_entries(prob, vt, 1, HD, t + 1, n, 1, np.zeros(HD, np.int32),
-                                    np.arange(HD, dtype=np.int32))
-        err = float(np.max(np.abs(o[0, hh, t] - ref)))
+        cols = np.arange(HD, dtype=np.int32)
+        ref = rl.orc_matmul_entries(np.ascontiguousarray(prob[:, :t + 1]), vt, 1, HD, t + 1, n, 1,
+                                    np.zeros(HD, np.int32), cols)
+        assert np.array_equal(o[0, hh, t], ref), (n, int(hh), int(t))
+        prob_seq = rl.orc_softmax(row[:, :t + 1], n)
+        ref_seq = rl.orc_matmul_entries(prob_seq, vt, 1, HD, t + 1, n, 1, np.zeros(HD, np.int32), cols)
+        err = float(np.max(np.abs(o[0, hh, t] - ref_seq)))
         assert err <= (t + 1) * 2.0 ** -24 * vmax + 1e-6 * vmax, (n, int(hh), int(t), err)
 
     print(f"config5 n={n}: residuals", flush=True)
@@ -202,24 +214,36 @@ def test_llama_block_config5_sampled(block, n):
         return rl.orc_matmul(np.ascontiguousarray(a, np.float32), np.ascontiguousarray(w), a.shape[0],
                              w.shape[0], a.shape[1], n, 1, tb=1)
 
-    h = rl.orc_rmsnorm(xn[:R], P["norm1.weight"], 1e-6)
-    qkv = lin(h, P["attn.qkv.weight"])
-    qe, ke, ve = (qkv[:, i * D_MODEL:(i + 1) * D_MODEL].reshape(1, R, N_HEADS, HD).transpose(0, 2, 1, 3)
-                  for i in range(3))
-    qe = rl.orc_rope_apply(qe, c[:R], s[:R])
-    ke = rl.orc_rope_apply(ke, c[:R], s[:R])
-    ve = np.ascontiguousarray(ve)
-    oe = np.zeros((1, N_HEADS, R, HD), np.float32)
-    for hh in range(N_HEADS):
-        sc = rl.orc_matmul(np.ascontiguousarray(qe[0, hh]), np.ascontiguousarray(ke[0, hh]), R, R, HD, n, 1,
-                           tb=1, alpha=float(scale))
+    def composed(rms, softmax_rows):
+        h = rms(xn[:R], P["norm1.weight"], 1e-6)
+        qkv = lin(h, P["attn.qkv.weight"])
+        qe, ke, ve = (qkv[:, i * D_MODEL:(i + 1) * D_MODEL].reshape(1, R, N_HEADS, HD).transpose(0, 2, 1, 3)
+                      for i in range(3))
+        qe = rl.orc_rope_apply(qe, c[:R], s[:R])
+        ke = rl.orc_rope_apply(ke, c[:R], s[:R])
+        ve = np.ascontiguousarray(ve)
+        oe = np.zeros((1, N_HEADS, R, HD), np.float32)
+        for hh in range(N_HEADS):
+            sc = rl.orc_matmul(np.ascontiguousarray(qe[0, hh]), np.ascontiguousarray(ke[0, hh]), R, R, HD, n, 1,
+                               tb=1, alpha=float(scale))
+            oe[0, hh] = rl.orc_matmul(softmax_rows(sc), ve[0, hh], R, HD, R, n, 1)
+        x1e = xn[:R] + lin(oe.transpose(0, 2, 1, 3).reshape(R, D_MODEL), P["attn.out_proj.weight"])
+        h2 = rms(x1e, P["norm2.weight"], 1e-6)
+        f1 = rl.orc_unary("orc_silu", lin(h2, P["ffn.fc1.weight"]), n)
+        return x1e + lin(f1, P["ffn.fc2.weight"])
+
+    def causal_lanes(sc):
+        return rl.orc_softmax_lanes(sc, n, causal=True, zero_guard=True)
+
+    def causal_seq(sc):
         pr = np.zeros((R, R), np.float32)
         for t in range(R):
             pr[t, :t + 1] = rl.orc_softmax(sc[t:t + 1, :t + 1], n)[0]
-        oe[0, hh] = rl.orc_matmul(pr, ve[0, hh], R, HD, R, n, 1)
-    x1e = xn[:R] + lin(oe.transpose(0, 2, 1, 3).reshape(R, D_MODEL), P["attn.out_proj.weight"])
-    h2 = rl.orc_rmsnorm(x1e, P["norm2.weight"], 1e-6)
-    f1 = rl.orc_unary("orc_silu", lin(h2, P["ffn.fc1.weight"]), n)
-    ref = x1e + lin(f1, P["ffn.fc2.weight"])
-    err = np.abs(y[:R] - ref) / np.maximum(np.abs(ref), 1.0)
-    assert err.max() < 1e-4, (n, float(err.max()))
+        return pr
+
+    ref = composed(rl.orc_rmsnorm_lanes, causal_lanes)
+    assert np.array_equal(y[:R], ref), (n, float(np.max(np.abs(y[:R] - ref))))
+    if n >= 16:
+        ref = composed(rl.orc_rmsnorm, causal_seq)
+        err = np.abs(y[:R] - ref) / np.maximum(np.abs(ref), 1.0)
+        assert err.max() < 1e-4, (n, float(err.max()))

@@ -461,6 +461,7 @@ def test_softmax_config2(iters):
     got = H(ext().softmax(T(x), iters=iters))
     ref = rl.orc_softmax(x, iters)
     assert rl.max_rel(got, ref, 1e-37) <= 1e-5
+    assert np.array_equal(got, rl.orc_softmax_lanes(x, iters))     # the kernel's row-sum order
     assert np.allclose(got.sum(1), 1.0, atol=2e-5)
 
 
@@ -472,6 +473,7 @@ def test_softmax_shapes(shape):
     got = H(ext().softmax(T(x), iters=16))
     ref = rl.orc_softmax(x, 16)
     assert rl.max_rel(got, ref, 1e-37) <= 1e-5
+    assert np.array_equal(got, rl.orc_softmax_lanes(x, 16))
 
 
 @pytest.mark.parametrize("iters", [8, 16, 24, 5])
@@ -529,10 +531,13 @@ def test_rmsnorm_layernorm(shape):
     e = ext()
     y = H(e.rmsnorm(T(x), T(g), 1e-6))
     assert rl.max_rel(y, rl.orc_rmsnorm(x, g, 1e-6), 1e-30) <= 1e-5
+    assert np.array_equal(y, rl.orc_rmsnorm_lanes(x, g, 1e-6))     # the kernel's row-sum order
     y0 = H(e.rmsnorm(T(x), None, 1e-6))
     assert rl.max_rel(y0, rl.orc_rmsnorm(x, None, 1e-6), 1e-30) <= 1e-5
+    assert np.array_equal(y0, rl.orc_rmsnorm_lanes(x, None, 1e-6))
     if shape[0] <= 16:
         z = H(e.layernorm(T(x), T(g), T(b), 1e-5))
+        assert np.array_equal(z, rl.orc_layernorm_lanes(x, g, b, 1e-5))
         zr = rl.orc_layernorm(x, g, b, 1e-5)
         # LayerNorm outputs are unit-scale; a different order of the mean's
         # sum moves every output by the same ~1e-7, so the bar is relative

@@ -245,6 +245,8 @@ def test_attention_vs_oracle(shape, iters, mode):
         # same scores bit for bit; the softmax row sum is a tree on the GPU and
         # left-to-right in the checker: each p moves by <= T * 2^-24 relative
         assert np.max(np.abs(got - ref)) <= Tn * ULP * vmax + 1e-7
+        # with the kernel's row-sum order the whole core is bit-exact
+        assert np.array_equal(got, rl.orc_attention_lanes(q, k, v, mk, causal, iters, mode))
 
 
 @pytest.mark.parametrize("shape", [(16, 64, 256, 64), (1, 4, 256, 64)])

@@ -36,6 +36,13 @@ exhaustive enumeration, or libm within an analytic bound.  Map:
                           rac_scaled_dot_attention) bit-exact with expf and
                           FAST products; float64 softmax attention within the
                           CORDIC bound
+  orc_rmsnorm_lanes /     the left-to-right functions above with the row
+  orc_layernorm_lanes /   sums regrouped: equal to them where every partial
+  orc_softmax_lanes       sum is exact (integer-valued rows, rows of <= 4
+                          live elements), within the reordering bound
+                          otherwise; a row where the order decides the sum
+                          (the lane map, butterfly and wave order of the
+                          row kernels) against its hand-derived value
 """
 import json
 import math
@@ -683,3 +690,52 @@ def test_st_conversions_closed_forms(o):
     got = rl.orc_st_to_f32(4, v.tobytes(), v.size)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert got[4] == 1.0 and got[5] == np.float32(1.0 + 2.0 ** -22)
+
+
+def test_lane_order_row_sums_pinned():
+    """orc_*_lanes regroup only the row sums of orc_rmsnorm / orc_layernorm /
+    orc_softmax_rows."""
+    rng = np.random.default_rng(11)
+    g = rl.gen_normal((4096,), 4, 1.0, 0.02)
+    b = rl.gen_normal((4096,), 5, std=0.1)
+    # integer-valued rows of zero sum (+-v pairs): every partial sum, the mean
+    # (0) and every partial sum of squares are exact, so any order gives the
+    # same bits
+    for d in (4096, 1000, 4099, 64):
+        half = rng.integers(-8, 9, (6, d // 2))
+        xi = np.concatenate([half, -half, np.zeros((6, d % 2), half.dtype)], axis=1)
+        xi = rng.permuted(xi, axis=1).astype(np.float32)
+        assert np.array_equal(rl.orc_rmsnorm_lanes(xi, g[:d], 1e-6), rl.orc_rmsnorm(xi, g[:d], 1e-6)), d
+        assert np.array_equal(rl.orc_layernorm_lanes(xi, g[:d], b[:d], 1e-5),
+                              rl.orc_layernorm(xi, g[:d], b[:d], 1e-5, use_cordic=1)), d
+    # random rows: within the reordering bound of the left-to-right sums
+    x = rl.gen_normal((32, 4096), 6)
+    assert rl.max_rel(rl.orc_rmsnorm_lanes(x, g, 1e-6), rl.orc_rmsnorm(x, g, 1e-6), 1e-6) < 4e-6
+    s = rl.gen_normal((32, 4096), 7, std=2.0)
+    for iters in (8, 16, 24):
+        assert rl.max_rel(rl.orc_softmax_lanes(s, iters), rl.orc_softmax(s, iters), 1e-37) < 4e-6
+    # causal rows with at most 4 live elements sit in lane 0's first float4,
+    # summed left to right: equal to the left-to-right softmax of the prefix
+    sc = rl.gen_normal((16, 16), 8)
+    pl = rl.orc_softmax_lanes(sc, 16, causal=True, zero_guard=True)
+    for t_ in range(4):
+        assert np.array_equal(pl[t_, :t_ + 1], rl.orc_softmax(sc[t_:t_ + 1, :t_ + 1], 16)[0])
+        assert not pl[t_, t_ + 1:].any()
+    # the order itself: a row of 1024 (256 lanes x one float4) with 2^24 in
+    # element 0 and 1.0 everywhere else.  Left to right every 1.0 is lost
+    # (2^24 + 1 rounds to 2^24), sum = 2^24.  In lane order lane 0 holds
+    # ((2^24 + 1) + 1) + 1 = 2^24 and lanes 1..63 hold 4; the butterfly adds
+    # lane 0's 2^24 to partial sums 4, 8, 16, ..., 128 of the other lanes in
+    # turn (each exactly representable above 2^24 at spacing 2), giving
+    # 2^24 + 252 for wave 0, and waves 1..3 hold 256 each: total
+    # 2^24 + 252 + 768 = 2^24 + 1020.  mean square = that / 1024 exactly.
+    row = np.ones((1, 1024), np.float32)
+    row[0, 0] = np.float32(4096.0)                     # 4096^2 = 2^24 as the square
+    ms_lanes = np.float32(2 ** 24 + 1020) / np.float32(1024)
+    ms_seq = np.float32(2 ** 24) / np.float32(1024)
+    got_l = rl.orc_rmsnorm_lanes(row, None, 0.0)
+    got_s = rl.orc_rmsnorm(row, None, 0.0)
+    inv_l = rl.orc_unary("orc_rsqrt_batch", np.array([ms_lanes], np.float32))[0]
+    inv_s = rl.orc_unary("orc_rsqrt_batch", np.array([ms_seq], np.float32))[0]
+    assert got_l[0, 1] == np.float32(1.0) * inv_l and got_s[0, 1] == np.float32(1.0) * inv_s
+    assert inv_l != inv_s
