@@ -146,15 +146,35 @@ int rac_inner_dev(const float *a, const float *b, long n, float *out, void *stre
 int rac_outer_dev(const float *a, const float *b, float *C, int m, int n, void *stream);
 /* X = rac_dct(x) (rac.h:189), one lane per output k. */
 int rac_dct_dev(const float *x, float *X, int n, void *stream);
-/* rac_attention (rac.h:330) on device buffers [batch, n_heads, seq, head_dim]:
- * scores = Q K^T / sqrt(head_dim) by the RAC matmul (mode, iters), causal
- * and additive [seq, seq] mask, CORDIC softmax in place, out = P V by the RAC
- * matmul.  workspace: rac_attention_workspace_bytes(batch, n_heads, seq)
- * bytes of device memory owned by the caller (the scores, and a flag). */
+/* rac_attention (rac.h:330; CPU definition rac_cpu.c:637-703) on device
+ * buffers [batch, n_heads, seq, head_dim]: scores = Q K^T / sqrt(head_dim) by
+ * the RAC matmul (mode, iters), causal and additive [seq, seq] mask, CORDIC
+ * softmax, out = P V by the RAC matmul.  The core runs over chunks of query
+ * rows, so the workspace holds the scores of one chunk (at most 128 MiB, or
+ * 64 query rows of every head when one row of every head needs more than
+ * 2 MiB), not the [batch*n_heads, seq, seq] matrix the reference
+ * materialises; results do not depend on the chunk.  workspace:
+ * rac_attention_workspace_bytes(batch, n_heads, seq) bytes of device memory
+ * owned by the caller. */
 long rac_attention_workspace_bytes(int batch, int n_heads, int seq);
 int rac_attention_dev(const float *q, const float *k, const float *v, const float *mask,
                       int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
                       float *workspace, int iters, int mode, void *stream);
+/* rac_attention_dev with the workspace's size in bytes: the chunk is the
+ * largest that workspace_bytes holds (at least one query row of every head,
+ * 4*batch*n_heads*seq + 256 bytes).  Same output bits for every size. */
+int rac_attention_ws_dev(const float *q, const float *k, const float *v, const float *mask,
+                         int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
+                         float *workspace, long workspace_bytes, int iters, int mode, void *stream);
+/* The same attention in one chunk, keeping every probability: on return the
+ * first batch*n_heads*seq*seq floats of the workspace (of
+ * rac_attention_probs_workspace_bytes bytes) hold P, what the backward pass
+ * (dV = P^T dO, dS = P (dP - rowsum(dP P))) reads.  Same output bits as
+ * rac_attention_dev. */
+long rac_attention_probs_workspace_bytes(int batch, int n_heads, int seq);
+int rac_attention_probs_dev(const float *q, const float *k, const float *v, const float *mask,
+                            int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
+                            float *workspace, int iters, int mode, void *stream);
 
 /* ── reference launcher ABI (rac_kernels.hip:822-909; bound by
  *    rac_torch_bind.cpp:16-45 with the stream as void*) ──────────────────── */

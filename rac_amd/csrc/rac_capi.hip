@@ -492,54 +492,96 @@ static int check_attention(const void* q, const void* k, const void* v, const vo
     return RAC_OK;
 }
 
-// Bytes of the workspace rac_attention_dev needs: the batch*n_heads*seq*seq
-// float scores plus 256 bytes for a device flag.
-static long attention_scores_bytes(long batch, long n_heads, long seq) {
-    return (long)sizeof(float) * batch * n_heads * seq * seq;
+// The attention core runs over chunks of `chunk` query rows: per chunk the
+// scores of those rows against every key, [batch*n_heads, chunk, seq] in the
+// workspace, the masked softmax of those full-length rows in place, and
+// their P V rows.  Every score, probability and output element is computed
+// exactly as with one chunk of all seq rows (each score row keeps its full
+// length, so the softmax's row sum has the same order), so the chunk size
+// never changes a result; it only bounds the workspace by
+// 4 * batch*n_heads * chunk * seq bytes instead of 4 * batch*n_heads * seq^2.
+// The workspace ends with 256 bytes for a device flag.
+static constexpr long kAttnChunkBudget = 128L << 20;
+
+static long attention_scores_bytes(long bh, long seq, long chunk) {
+    return (long)sizeof(float) * bh * chunk * seq;
 }
+
+// Query rows per chunk for a workspace budget: all seq rows when their
+// scores fit it, else the largest multiple of 64 rows that does (64 at
+// least, or seq when shorter).
+static long attention_chunk_rows(long bh, long seq, long budget) {
+    const long per_row = attention_scores_bytes(bh, seq, 1);
+    long c = budget / per_row;
+    if (c >= seq) return seq;
+    c = (c / 64) * 64;
+    return c >= 64 ? c : (seq < 64 ? seq : 64);
+}
+
 RAC_EXPORT long rac_attention_workspace_bytes(int batch, int n_heads, int seq) {
     if (batch <= 0 || n_heads <= 0 || seq <= 0) return 0;
-    return attention_scores_bytes(batch, n_heads, seq) + 256;
+    const long bh = (long)batch * n_heads;
+    return attention_scores_bytes(bh, seq, attention_chunk_rows(bh, seq, kAttnChunkBudget)) + 256;
+}
+
+// The workspace of rac_attention_probs_dev: all [batch*n_heads, seq, seq]
+// probabilities (what the backward pass reads) plus the flag.
+RAC_EXPORT long rac_attention_probs_workspace_bytes(int batch, int n_heads, int seq) {
+    if (batch <= 0 || n_heads <= 0 || seq <= 0) return 0;
+    return attention_scores_bytes((long)batch * n_heads, seq, seq) + 256;
 }
 
 // scores = (Q K^T) / sqrt(D) by the RAC matmul (batched over b*h), masked
-// row softmax with CORDIC exp in place, out = P V by the RAC matmul.
+// row softmax with CORDIC exp in place, out = P V by the RAC matmul; over
+// query chunks of `chunk` rows (see above).
 static int attention_launch(const float* q, const float* k, const float* v, const float* mask, int causal,
-                            float* out, int b, int h, int t, int d, float* ws, int iters, int mode,
+                            float* out, int b, int h, int t, int d, float* ws, long chunk, int iters, int mode,
                             hipStream_t s) {
     const int bh = b * h;
-    const long td = (long)t * d, tt = (long)t * t;
+    const long td = (long)t * d;
     const float scale = 1.0f / sqrtf((float)d);
-    // causal: score tiles wholly above the diagonal are masked by the
-    // softmax regardless of their contents, so the scores GEMM schedules only
-    // the tiles on or below it
-    // Both products keep the strength-reduced rotation chain for every input
-    // (exact_specials off): the attention's parity bar is the row-sum bound,
-    // and peaked softmax rows are full of probabilities below 2^-105, which
-    // would otherwise send most P V tiles through the literal-chain recompute.
-    int rc = check_hip(gemm_launch(0, 1, q, k, ws, t, t, d, scale, 0.0f, iters, mode, s, bh, td, td, tt,
-                                   causal ? 1 : 0, nullptr, false),
-                       "rac_attention scores launch");
-    if (rc) return rc;
-    SoftmaxMask mk;
-    mk.mask = mask;
-    mk.causal = causal != 0;
-    mk.seq = t;
-    mk.zero_guard = 1;
-    rc = check_hip(softmax_launch(ws, ws, (long)bh * t, t, iters, s, mk), "rac_attention softmax launch");
-    if (rc) return rc;
     // causal: P is exactly 0 above the diagonal, so P V may stop each row
-    // tile's K loop at its last row -- when V is finite (0 * inf is NaN);
-    // the flag lives in the workspace tail and is evaluated on the device
+    // tile's K loop at its last query position -- when V is finite (0 * inf
+    // is NaN); the flag lives in the workspace tail, evaluated on the device
     int* flag = nullptr;
+    int rc = RAC_OK;
     if (causal) {
-        flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + attention_scores_bytes(b, h, t));
+        flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + attention_scores_bytes(bh, t, chunk));
         rc = check_hip(all_finite_launch(v, (long)bh * td, flag, s), "rac_attention finite check");
         if (rc) return rc;
     }
-    return check_hip(gemm_launch(0, 0, ws, v, out, t, d, t, 1.0f, 0.0f, iters, mode, s, bh, tt, td, td,
-                                 causal ? 2 : 0, flag, false),
-                     "rac_attention output launch");
+    for (long t0 = 0; t0 < t; t0 += chunk) {
+        const int c = (int)(chunk < t - t0 ? chunk : t - t0);
+        const long ct = (long)c * t;
+        // causal: score tiles wholly above the diagonal are masked by the
+        // softmax regardless of their contents, so the scores GEMM schedules
+        // only the tiles on or below it (one chunk: the square triangular
+        // schedule; several: each chunk's trapezoid).  Both products keep
+        // the strength-reduced rotation chain for every input (exact_specials
+        // off): the attention's parity bar is the row-sum bound, and peaked
+        // softmax rows are full of probabilities below 2^-105, which would
+        // otherwise send most P V tiles through the literal-chain recompute.
+        const int ssched = !causal ? 0 : (c == t ? 1 : 3);
+        rc = check_hip(gemm_launch(0, 1, q + t0 * d, k, ws, c, t, d, scale, 0.0f, iters, mode, s, bh, td, td, ct,
+                                   ssched, nullptr, false, (int)t0),
+                       "rac_attention scores launch");
+        if (rc) return rc;
+        SoftmaxMask mk;
+        mk.mask = mask;
+        mk.causal = causal != 0;
+        mk.seq = c;
+        mk.row0 = t0;
+        mk.mask_ld = t;
+        mk.zero_guard = 1;
+        rc = check_hip(softmax_launch(ws, ws, (long)bh * c, t, iters, s, mk), "rac_attention softmax launch");
+        if (rc) return rc;
+        const int psched = (causal && c == t) ? 2 : 0;
+        rc = check_hip(gemm_launch(0, 0, ws, v, out + t0 * d, c, d, t, 1.0f, 0.0f, iters, mode, s, bh, ct, td, td,
+                                   psched, flag, false, (int)t0),
+                       "rac_attention output launch");
+        if (rc) return rc;
+    }
+    return RAC_OK;
 }
 
 RAC_EXPORT int rac_attention_dev(const float* q, const float* k, const float* v, const float* mask,
@@ -549,7 +591,52 @@ RAC_EXPORT int rac_attention_dev(const float* q, const float* k, const float* v,
     if (rc) return rc;
     if (!workspace) return fail(RAC_ERR_NULL_PTR, "rac_attention_dev: null workspace");
     if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_dev: mode must be 0, 1 or 2");
+    const long bh = (long)batch * n_heads;
     return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, workspace,
+                            attention_chunk_rows(bh, seq, kAttnChunkBudget), clamp_iters(iters), mode,
+                            (hipStream_t)stream);
+}
+
+// Query rows per chunk that a workspace of `bytes` holds: all seq rows when
+// they fit, else the largest multiple of 64 rows that fits, else as many
+// rows as fit (0 when not even one row does).
+static long attention_chunk_for_bytes(long bh, long seq, long bytes) {
+    const long per_row = attention_scores_bytes(bh, seq, 1);
+    const long c = (bytes - 256) / per_row;
+    if (c >= seq) return seq;
+    if (c >= 64) return (c / 64) * 64;
+    return c > 0 ? c : 0;
+}
+
+// rac_attention_dev with the workspace size given: the chunk is the largest
+// the workspace holds (results do not depend on it).
+RAC_EXPORT int rac_attention_ws_dev(const float* q, const float* k, const float* v, const float* mask,
+                                    int is_causal, float* out, int batch, int n_heads, int seq, int head_dim,
+                                    float* workspace, long workspace_bytes, int iters, int mode, void* stream) {
+    int rc = check_attention(q, k, v, out, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (!workspace) return fail(RAC_ERR_NULL_PTR, "rac_attention_ws_dev: null workspace");
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_ws_dev: mode must be 0, 1 or 2");
+    const long bh = (long)batch * n_heads;
+    const long chunk = attention_chunk_for_bytes(bh, seq, workspace_bytes);
+    if (chunk < 1)
+        return fail(RAC_ERR_INVALID_DIM, "rac_attention_ws_dev: workspace of %ld bytes is below the %ld one query "
+                    "row of every head needs", workspace_bytes, attention_scores_bytes(bh, seq, 1) + 256);
+    return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, workspace, chunk,
+                            clamp_iters(iters), mode, (hipStream_t)stream);
+}
+
+// rac_attention_dev in one chunk: the workspace (of
+// rac_attention_probs_workspace_bytes) keeps every probability P [batch,
+// n_heads, seq, seq] in its first batch*n_heads*seq*seq floats.
+RAC_EXPORT int rac_attention_probs_dev(const float* q, const float* k, const float* v, const float* mask,
+                                       int is_causal, float* out, int batch, int n_heads, int seq,
+                                       int head_dim, float* workspace, int iters, int mode, void* stream) {
+    int rc = check_attention(q, k, v, out, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (!workspace) return fail(RAC_ERR_NULL_PTR, "rac_attention_probs_dev: null workspace");
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_probs_dev: mode must be 0, 1 or 2");
+    return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, workspace, seq,
                             clamp_iters(iters), mode, (hipStream_t)stream);
 }
 
@@ -1078,8 +1165,10 @@ RAC_EXPORT void rac_attention(const float* q, const float* k, const float* v, co
     if (!rc) rc = sv.bind(v, xb, true, s);
     if (!rc) rc = sm.bind(mask, sizeof(float) * (size_t)seq * seq, true, s);
     if (!rc) rc = so.bind(out, xb, false, s);
+    const long bh = (long)batch * n_heads;
+    const long chunk = attention_chunk_rows(bh, seq, kAttnChunkBudget);
     if (!rc) {
-        const size_t wb = (size_t)rac_attention_workspace_bytes(batch, n_heads, seq);
+        const size_t wb = (size_t)attention_scores_bytes(bh, seq, chunk) + 256;
         if (hipMalloc(&ws.dev, wb) != hipSuccess) {
             (void)hipGetLastError();
             ws.dev = nullptr;
@@ -1089,7 +1178,7 @@ RAC_EXPORT void rac_attention(const float* q, const float* k, const float* v, co
         }
     }
     if (!rc) rc = attention_launch(sq.f(), sk.f(), sv.f(), sm.f(), is_causal, so.f(), batch, n_heads, seq,
-                                   head_dim, ws.f(), rac_get_cordic_iters(), rac_get_cordic_mode(), s);
+                                   head_dim, ws.f(), chunk, rac_get_cordic_iters(), rac_get_cordic_mode(), s);
     if (!rc) rc = so.copy_out(s);
     (void)finish_sync(s, rc);
 }

@@ -92,7 +92,7 @@ template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED, int
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, float kinv, long sa, long sb, long sc,
-    GemmEpilogue ep, const int* k_causal, int exact_specials)
+    GemmEpilogue ep, const int* k_causal, int exact_specials, int row0)
 {
     using Cfg = GemmCfg<MODE, NITER, TA, TB, TM, TN>;
     constexpr int BM = Cfg::kBM, BN = Cfg::kBN, BK = Cfg::kBK, PAD = Cfg::kPad;
@@ -102,8 +102,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     // col x for x <= p, else row nt-1-p col x-p-1, so every workgroup has one
     // tile and rows p and nt-1-p share a column of the grid (grid nt+1 x
     // ceil(nt/2)).  2 (causal P V): workgroup p computes row tiles p and
-    // nt-1-p, whose K ranges (below) sum to a constant.
+    // nt-1-p, whose K ranges (below) sum to a constant.  3 (causal attention
+    // scores of query rows row0.. row0+M-1 against keys 0..N-1): tile (y, x)
+    // as in 0, skipped when it lies wholly above the diagonal (every column
+    // past every row's query position).
     int tm = blockIdx.y, tn = blockIdx.x, tm2 = -1;
+    if constexpr (SCHED == 3) {
+        if ((long)tn * BN > (long)row0 + (long)tm * BM + BM - 1) return;
+    }
     if constexpr (SCHED == 1) {
         const int nt = (M + BM - 1) / BM, p = blockIdx.y, x = blockIdx.x;
         if (x > p) {
@@ -203,9 +209,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(
         // Causal P V: row t of P is exactly 0 beyond column t, and with every v
         // finite (*k_causal == 1, checked on the device) fma(0, v, acc) == acc
         // (acc starts at +0 and can never become -0), so the K loop stops after
-        // the tile's last row.
+        // the tile's last row (query position row0 + m0 + BM - 1).
         int kend = K;
-        if (k_causal && *k_causal == 1) kend = (int)min((long)K, m0 + BM);
+        if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + m0 + BM);
         load_tile(0);
         for (int k0 = 0; k0 < kend; k0 += BK) {
             __syncthreads();            // previous tile fully consumed
@@ -380,6 +386,7 @@ struct GemmArgs {
     int sched;
     const int* k_causal;
     int exact_specials;
+    int row0;
 };
 
 template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED, int TM, int TN = TM>
@@ -392,7 +399,7 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     if (g.sched == 2) grid.y = (nt + 1) / 2;
     hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED, SCHED>), grid, dim3(256), 0, stream,
                        g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
-                       g.ep, g.k_causal, g.exact_specials);
+                       g.ep, g.k_causal, g.exact_specials, g.row0);
     return hipGetLastError();
 }
 
@@ -426,11 +433,11 @@ static long device_cus() {
 template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED = 0>
 static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
     constexpr int kBig = (MODE == kModeFast) ? 8 : 4;
-    if constexpr (SCHED != 0) {
+    if constexpr (SCHED == 1 || SCHED == 2) {
         return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
     } else {
         auto tiles = [&](long bm, long bn) { return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch; };
-        if constexpr (MODE == kModeFast) {
+        if constexpr (MODE == kModeFast && SCHED == 0) {
             // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
             // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per
             // CU); it is taken when it fills its rounds of resident blocks
@@ -444,23 +451,24 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
             if (t16 >= 2 * cus && fill(t16, 2) >= fill(t8, 3))
                 return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 16, 8>(g, s);
         }
-        if (tiles(16 * kBig, 16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, kBig>(g, s);
+        if (tiles(16 * kBig, 16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, kBig>(g, s);
         if constexpr (kBig == 8) {
-            if (tiles(64, 64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 4>(g, s);
+            if (tiles(64, 64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
         }
-        return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 2>(g, s);
+        return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 2>(g, s);
     }
 }
 
 // The fused epilogue exists for the NT layout only (input @ weight^T, the
-// linear layer), the triangular schedule for NT only (causal Q K^T) and the
-// paired-row schedule for NN only (causal P V); their callers never ask for
-// another layout.
+// linear layer), the triangular and trapezoidal schedules for NT only
+// (causal Q K^T) and the paired-row schedule for NN only (causal P V);
+// their callers never ask for another layout.
 template <int MODE, int NITER>
 static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s) {
     if (g.fused) return launch_tiles<MODE, NITER, false, true, true>(g, s);
     if (g.sched == 1) return launch_tiles<MODE, NITER, false, true, false, 1>(g, s);   // NT only
     if (g.sched == 2) return launch_tiles<MODE, NITER, false, false, false, 2>(g, s);  // NN only
+    if (g.sched == 3) return launch_tiles<MODE, NITER, false, true, false, 3>(g, s);   // NT only
     if (!ta && !tb) return launch_tiles<MODE, NITER, false, false, false>(g, s);
     if (!ta && tb) return launch_tiles<MODE, NITER, false, true, false>(g, s);
     if (ta && !tb) return launch_tiles<MODE, NITER, true, false, false>(g, s);
@@ -481,15 +489,15 @@ static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStrea
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch, long sa, long sb, long sc, int sched,
-                       const int* k_causal, bool exact_specials) {
+                       const int* k_causal, bool exact_specials, int row0) {
     const GemmArgs g{A, B, C, M, N, K, alpha, beta, clamp_iters(iters), batch, sa, sb, sc,
-                     GemmEpilogue(), false, sched, k_causal, exact_specials ? 1 : 0};
+                     GemmEpilogue(), false, sched, k_causal, exact_specials ? 1 : 0, row0};
     return dispatch(ta, tb, mode, g, s);
 }
 
 hipError_t gemm_fused_launch(const float* A, const float* W, float* C, int M, int N, int K,
                              const GemmEpilogue& ep, int iters, int mode, hipStream_t s) {
-    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0, nullptr, 1};
+    const GemmArgs g{A, W, C, M, N, K, 1.0f, 0.0f, clamp_iters(iters), 1, 0, 0, 0, ep, true, 0, nullptr, 1, 0};
     return dispatch(0, 1, mode, g, s);
 }
 

@@ -43,9 +43,12 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 // sched 1 (square M == N): only output tiles on or below the diagonal are
 // computed (causal attention scores; the tiles above are left unwritten).
 // sched 2: each workgroup computes row tiles p and nt-1-p (balances the
-// causal P V below).  k_causal: device flag; when it holds 1, row tile m
-// sums k only up to its last row (causal P V with a lower-triangular P and
-// finite V).  exact_specials (CORDIC mode): tiles whose A panel holds
+// causal P V below).  sched 3 (NT): output rows are query positions
+// row0 .. row0+M-1 and columns key positions; tiles wholly above the
+// diagonal are skipped (left unwritten).  k_causal: device flag; when it
+// holds 1, row tile m sums k only up to its last query position
+// row0 + m*BM + BM - 1 (causal P V with a lower-triangular P and finite V).
+// exact_specials (CORDIC mode): tiles whose A panel holds
 // values outside the strength-reduced rotation chain's range are recomputed
 // on the literal chain, so every input gives the reference's bits; false
 // keeps the strength-reduced chain for every input (callers whose parity
@@ -54,19 +57,23 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch = 1, long sa = 0, long sb = 0, long sc = 0,
-                       int sched = 0, const int* k_causal = nullptr, bool exact_specials = true);
+                       int sched = 0, const int* k_causal = nullptr, bool exact_specials = true,
+                       int row0 = 0);
 // *flag = 1 if every x[i] is finite, else 0 (stream-ordered).
 hipError_t all_finite_launch(const float* x, long n, int* flag, hipStream_t s);
 
-// Optional attention masking of each row r (position t = r % seq, column j):
-// causal -> x = -inf for j > t; then x += mask[t*seq + j] when mask != null.
-// zero_guard: 1/sum replaced by 0 when sum is not > 0 (rac_cpu.c:687).
-// x and y may be the same buffer (in-place softmax).
+// Optional attention masking of each row r (query position t = row0 +
+// r % seq, column j): causal -> x = -inf for j > t; then x += mask[t*ld + j]
+// when mask != null (ld = mask_ld, or the row length when 0).  zero_guard:
+// 1/sum replaced by 0 when sum is not > 0 (rac_cpu.c:687).  x and y may be
+// the same buffer (in-place softmax).
 struct SoftmaxMask {
     const float* mask = nullptr;
     int causal = 0;
     long seq = 0;
     int zero_guard = 0;
+    long row0 = 0;
+    long mask_ld = 0;
 };
 hipError_t softmax_launch(const float* x, float* y, long rows, long n, int iters,
                           hipStream_t s, const SoftmaxMask& mk = SoftmaxMask());

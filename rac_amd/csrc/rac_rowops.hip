@@ -68,10 +68,10 @@ __device__ __forceinline__ float exp_n(float x, int iters, float khinv) {
 
 // Attention masking of score x at (query position t, key column j), in the
 // order of rac_cpu.c:668-670: causal sets -inf above the diagonal, then the
-// additive mask is added.
+// additive mask is added (mask_ld set by the dispatcher).
 __device__ __forceinline__ float mask_score(float x, long t, long j, const SoftmaxMask& mk) {
     if (mk.causal && j > t) x = -__builtin_inff();
-    if (mk.mask) x += mk.mask[t * mk.seq + j];
+    if (mk.mask) x += mk.mask[t * mk.mask_ld + j];
     return x;
 }
 
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
         v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
     if constexpr (MASKED) {
-        const long t = row % mk.seq;
+        const long t = mk.row0 + row % mk.seq;
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const long idx = threadIdx.x + (long)i * kRowThreads;
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
 {
     __shared__ float red[kRowWaves];
     const long row = blockIdx.x;
-    const long t = MASKED ? row % mk.seq : 0;
+    const long t = MASKED ? mk.row0 + row % mk.seq : 0;
     const float* xr = x + row * n;
     float* yr = y + row * n;
     float m = -__builtin_inff();
@@ -239,6 +239,7 @@ static hipError_t softmax_mask_dispatch(const float* x, float* y, long rows, lon
     if (mk.mask || mk.causal || mk.zero_guard) {
         SoftmaxMask m2 = mk;
         if (m2.seq <= 0) m2.seq = n;   // square scores: row length = sequence length
+        if (m2.mask_ld <= 0) m2.mask_ld = n;
         return softmax_dispatch<NITER, true>(x, y, rows, n, iters, khinv, s, m2);
     }
     return softmax_dispatch<NITER, false>(x, y, rows, n, iters, khinv, s, mk);

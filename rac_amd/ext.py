@@ -578,12 +578,19 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
         mptr = mask.data_ptr()
     out = torch.empty_like(q)
     lib = _lib.load()
+    if return_probs:
+        # one chunk: the workspace keeps every probability for the backward pass
+        ws = torch.empty(lib.rac_attention_probs_workspace_bytes(B, H, T) // 4, device=q.device,
+                         dtype=torch.float32)
+        check(lib.rac_attention_probs_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), mptr, int(bool(is_causal)),
+                                          out.data_ptr(), B, H, T, D, ws.data_ptr(), iters, mode, _stream(out)),
+              "rac_attention_probs_dev")
+        return out, ws[:B * H * T * T].view(B, H, T, T)
+    # chunks of query rows: the workspace holds one chunk's scores
     ws = torch.empty(lib.rac_attention_workspace_bytes(B, H, T) // 4, device=q.device, dtype=torch.float32)
     check(lib.rac_attention_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), mptr, int(bool(is_causal)),
                                 out.data_ptr(), B, H, T, D, ws.data_ptr(), iters, mode, _stream(out)),
           "rac_attention_dev")
-    if return_probs:
-        return out, ws[:B * H * T * T].view(B, H, T, T)
     return out
 
 

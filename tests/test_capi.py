@@ -538,3 +538,20 @@ def test_patch_helpers_and_qkv_fusion_on_cpu(capsys):
         rt.RACFusedQKV.from_qkv_linears(lq, nn.Linear(16, 8), lv)
     with pytest.raises(ValueError):
         rt.RACFusedQKV.from_qkv_linears(lq, nn.Linear(16, 16, bias=False), lv)
+
+
+def test_attention_workspace_sizes(lib):
+    """The attention workspace holds one chunk of query rows (at most 128 MiB
+    of scores, or 64 rows of every head), plus 256 bytes for a flag; the
+    probability-keeping form holds the whole [B*H, T, T] matrix.  A
+    workspace below one row of every head is refused before device work."""
+    MiB = 2 ** 20
+    assert lib.rac_attention_workspace_bytes(1, 32, 2048) == 128 * MiB + 256      # 512 rows per chunk
+    assert lib.rac_attention_workspace_bytes(2, 3, 200) == 4 * 6 * 200 * 200 + 256  # one chunk
+    assert lib.rac_attention_workspace_bytes(1, 64, 65536) == 4 * 64 * 64 * 65536 + 256   # floor of 64 rows
+    assert lib.rac_attention_probs_workspace_bytes(1, 32, 2048) == 512 * MiB + 256
+    assert lib.rac_attention_workspace_bytes(0, 1, 1) == 0
+    buf = (ctypes.c_float * 64)()
+    a = ctypes.addressof(buf)
+    assert lib.rac_attention_ws_dev(a, a, a, None, 1, a, 1, 2, 16, 4, a, 4 * 2 * 16 + 255, 16, 1, None) == -2
+    assert b"below" in lib.rac_last_error()

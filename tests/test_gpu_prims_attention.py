@@ -389,3 +389,68 @@ def test_rope_attention_module_uses_rac_core():
     assert torch.allclose(y, y2, rtol=1e-3, atol=1e-4)
     y.sum().backward()
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in m.parameters())
+
+
+def _attention_ws(q, k, v, mask, causal, iters, mode, chunk_rows=None, probs=False):
+    """rac_attention_ws_dev with a workspace for `chunk_rows` query rows per
+    chunk (or rac_attention_probs_dev in one chunk)."""
+    L = lib()
+    B, Hh, Tn, D = q.shape
+    qt, kt, vt = T(q), T(k), T(v)
+    mt = T(mask) if mask is not None else None
+    out = torch.empty_like(qt)
+    stream = torch.cuda.current_stream().cuda_stream
+    mp = mt.data_ptr() if mt is not None else None
+    if probs:
+        nbytes = L.rac_attention_probs_workspace_bytes(B, Hh, Tn)
+        ws = torch.empty(nbytes // 4, device=DEV)
+        rc = L.rac_attention_probs_dev(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), mp, int(causal), out.data_ptr(),
+                                       B, Hh, Tn, D, ws.data_ptr(), iters, mode, stream)
+    else:
+        nbytes = 4 * B * Hh * chunk_rows * Tn + 256
+        ws = torch.full((nbytes // 4,), float("nan"), device=DEV)
+        rc = L.rac_attention_ws_dev(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), mp, int(causal), out.data_ptr(),
+                                    B, Hh, Tn, D, ws.data_ptr(), nbytes, iters, mode, stream)
+    assert rc == 0, L.rac_last_error()
+    return H(out)
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 200, 32), (1, 4, 256, 64), (1, 2, 333, 48)])
+@pytest.mark.parametrize("iters,mode", [(16, 1), (8, 1), (24, 0)])
+def test_attention_query_chunks_bit_identical(shape, iters, mode):
+    """The core over chunks of query rows (workspace of one chunk's scores)
+    gives the one-chunk bits for every chunk size: 1 row, 7 rows, 64, 130
+    and the whole sequence; causal, additive mask, both, neither.  The
+    workspace starts as NaN, so a chunk that read scores it had not written
+    would show."""
+    q, k, v = _qkv(shape, seed=sum(shape) + 7)
+    Tn = shape[2]
+    mask = (rl.gen_normal((Tn, Tn), seed=78) * np.float32(0.5)).astype(np.float32)
+    mask[3, Tn - 2] = -np.inf
+    for mk, causal in ((None, True), (mask, False), (mask, True), (None, False)):
+        print(f"attention chunks shape={shape} iters={iters} mode={mode} mask={mk is not None} causal={causal}",
+              flush=True)
+        ref = _attention_ws(q, k, v, mk, causal, iters, mode, probs=True)
+        for rows in (1, 7, 64, 130, Tn):
+            got = _attention_ws(q, k, v, mk, causal, iters, mode, chunk_rows=rows)
+            assert np.array_equal(got, ref, equal_nan=True), (rows, mk is not None, causal)
+        if shape == (2, 3, 200, 32):
+            assert np.array_equal(ref, rl.orc_attention_lanes(q, k, v, mk, causal, iters, mode))
+
+
+def test_attention_config5_default_chunks_equal_one_chunk():
+    """At config 5 ([1, 32, 2048, 128], causal, n = 16) rac_attention_dev's
+    workspace holds 512 of the 2048 query rows per chunk (128 MiB instead of
+    the 512 MiB score matrix); its output equals the one-chunk output bit
+    for bit, and two sampled heads equal the checker's composition."""
+    L = lib()
+    assert L.rac_attention_workspace_bytes(1, 32, 2048) == 128 * 2 ** 20 + 256
+    assert L.rac_attention_probs_workspace_bytes(1, 32, 2048) == 512 * 2 ** 20 + 256
+    shape = (1, 32, 2048, 128)
+    q, k, v = _qkv(shape, seed=611)
+    got = H(ext().attention(T(q), T(k), T(v), None, True, iters=16, mode=1))
+    one, _ = ext().attention(T(q), T(k), T(v), None, True, iters=16, mode=1, return_probs=True)
+    assert np.array_equal(got, H(one))
+    for h in (0, 31):
+        sl = (slice(0, 1), slice(h, h + 1))
+        assert np.array_equal(got[sl], rl.orc_attention_lanes(q[sl], k[sl], v[sl], None, True, 16, 1)), h
