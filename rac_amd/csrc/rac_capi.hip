@@ -626,6 +626,60 @@ RAC_EXPORT int rac_attention_ws_dev(const float* q, const float* k, const float*
                             clamp_iters(iters), mode, (hipStream_t)stream);
 }
 
+// ── allocation-free attention ────────────────────────────────────────────
+//
+// For callers that cannot allocate device memory (code under stream or
+// graph capture, serving loops that forbid allocation): the chunk workspace
+// lives in this file-scope device array, kScratchBytes per GPU, held by
+// each GPU the library runs on until the process ends.  Every call on one
+// GPU shares that GPU's array: calls that overlap on one GPU (other
+// streams, other host threads) race and must be serialised by the caller.
+// The array's device address is looked up once per device (the host-side
+// name is only a stand-in for it) and used from then on.
+static constexpr long kScratchBytes = 32L << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[64];
+
+static int scratch_for_current_device(void** out) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= 64) return fail(RAC_ERR_DEVICE, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch address");
+        if (rc) return rc;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return RAC_OK;
+}
+
+// rac_attention_dev without a workspace argument and without allocating:
+// the chunks of query rows are sized to the library's 32 MiB scratch array
+// (results equal rac_attention_dev's).  Refuses, before any device work,
+// shapes whose one query row of every head does not fit it
+// (4*batch*n_heads*seq + 256 > 32 MiB, i.e. batch*n_heads*seq > 8388544).
+RAC_EXPORT int rac_attention_noalloc_dev(const float* q, const float* k, const float* v, const float* mask,
+                                         int is_causal, float* out, int batch, int n_heads, int seq,
+                                         int head_dim, int iters, int mode, void* stream) {
+    int rc = check_attention(q, k, v, out, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_noalloc_dev: mode must be 0, 1 or 2");
+    const long bh = (long)batch * n_heads;
+    const long chunk = attention_chunk_for_bytes(bh, seq, kScratchBytes);
+    if (chunk < 1)
+        return fail(RAC_ERR_INVALID_DIM, "rac_attention_noalloc_dev: batch*n_heads*seq = %ld exceeds the %ld the "
+                    "%ld-byte scratch holds", bh * seq, (kScratchBytes - 256) / (long)sizeof(float), kScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+    return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, static_cast<float*>(ws),
+                            chunk, clamp_iters(iters), mode, (hipStream_t)stream);
+}
+
 // rac_attention_dev in one chunk: the workspace (of
 // rac_attention_probs_workspace_bytes) keeps every probability P [batch,
 // n_heads, seq, seq] in its first batch*n_heads*seq*seq floats.
