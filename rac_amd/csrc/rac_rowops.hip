@@ -34,7 +34,10 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Block-wide reductions; `red` holds kRowWaves floats.  The result is the
-// same value in every lane (fixed combination order).
+// same value in every lane (fixed combination order).  TRAIL: end with a
+// barrier, so that `red` may be rewritten at once; callers that give each
+// reduction of a row its own `red` leave it off.
+template <bool TRAIL = true>
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int w = threadIdx.x / 64;
@@ -43,9 +46,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     float r = red[0];
 #pragma unroll
     for (int i = 1; i < kRowWaves; i++) r += red[i];
-    __syncthreads();
+    if constexpr (TRAIL) __syncthreads();
     return r;
 }
+template <bool TRAIL = true>
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
     const int w = threadIdx.x / 64;
@@ -54,7 +58,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     float r = red[0];
 #pragma unroll
     for (int i = 1; i < kRowWaves; i++) r = fmaxf(r, red[i]);
-    __syncthreads();
+    if constexpr (TRAIL) __syncthreads();
     return r;
 }
 
@@ -96,32 +100,15 @@ __device__ __forceinline__ void exp_lane(float* v, int iters, float khinv) {
     }
 }
 
-// The row is read once into registers (16-byte loads), reduced, exponentiated
-// and written once.  Lanes past the row end hold -inf, whose exp is +0, so
-// the max, the lane sums (s + 0 == s) and the output are those of the
-// elements that exist.
-// FULL: n == 1024 * VPT exactly, so no lane needs a bounds check.
-template <int VPT, int NITER, bool MASKED, bool FULL>
-__global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
-    const float* x, float* y, long n, int iters, float khinv,
-    SoftmaxMask mk)
-{
-    __shared__ float red[kRowWaves];
-    const long row = blockIdx.x;
-    const float4* xr = reinterpret_cast<const float4*>(x + row * n);
-    float4* yr = reinterpret_cast<float4*>(y + row * n);
-    const long n4 = n / 4;
-    constexpr int E = 4 * VPT;
-    float v[E];
-#pragma unroll
-    for (int i = 0; i < VPT; i++) {
-        const long idx = threadIdx.x + (long)i * kRowThreads;
-        float4 t = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
-        if (FULL || idx < n4) t = ld4_stream(&xr[idx]);
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
+// Softmax of the row a workgroup holds in registers: lane l holds the float4
+// groups l, l + 256, ... of the row (E = 4 VPT values, -inf past the row
+// end, whose exp is +0, so the max, the lane sums (s + 0 == s) and the
+// outputs are those of the elements that exist).  On return v holds the
+// outputs.  t is the row's query position (masked rows only).
+// First stage: masking (masked rows) and the lane's maximum.
+template <int VPT, bool MASKED, bool FULL>
+__device__ __forceinline__ float softmax_lane_max(float* v, long n4, long t, const SoftmaxMask& mk) {
     if constexpr (MASKED) {
-        const long t = mk.row0 + row % mk.seq;
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const long idx = threadIdx.x + (long)i * kRowThreads;
@@ -135,7 +122,17 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
 #pragma unroll
     for (int i = 0; i < VPT; i++)
         m = fmaxf(fmaxf(fmaxf(m, v[4 * i]), fmaxf(v[4 * i + 1], v[4 * i + 2])), v[4 * i + 3]);
-    m = block_max(m, red);
+    return m;
+}
+
+// Second stage: row max, exps, row sum, scaling (m: the lane's maximum).
+// red: 2 kRowWaves floats (max and sum partials apart, so neither reduction
+// needs a trailing barrier; a kernel handles one row per workgroup).
+template <int VPT, int NITER, bool MASKED>
+__device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters, float khinv,
+                                                   const SoftmaxMask& mk, float* red) {
+    constexpr int E = 4 * VPT;
+    m = block_max<false>(m, red);
     // Unmasked rows with a compile-time step count: every x - max is <= 0
     // or NaN, and a NaN anywhere (a NaN element, or max = +-inf) makes the
     // reference's row sum NaN and so every output NaN.  The exps then skip
@@ -157,17 +154,57 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     if constexpr (kLean) {
         if (nanp != nanp) s = __builtin_nanf("");
     }
-    s = block_sum(s, red);
+    s = block_sum<false>(s, red + kRowWaves);
     const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
+#pragma unroll
+    for (int e = 0; e < E; e++) v[e] = v[e] * inv;
+}
+
+template <int VPT, int NITER, bool MASKED, bool FULL>
+__device__ __forceinline__ void softmax_row_regs(float* v, long n4, long t, int iters, float khinv,
+                                                 const SoftmaxMask& mk, float* red) {
+    const float m = softmax_lane_max<VPT, MASKED, FULL>(v, n4, t, mk);
+    softmax_row_finish<VPT, NITER, MASKED>(v, m, iters, khinv, mk, red);
+}
+
+template <int VPT, bool FULL>
+__device__ __forceinline__ void load_row_regs(const float* xrow, long n4, float* v) {
+    const float4* xr = reinterpret_cast<const float4*>(xrow);
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const long idx = threadIdx.x + (long)i * kRowThreads;
-        if (FULL || idx < n4) {
-            float4 o;
-            o.x = v[4 * i] * inv; o.y = v[4 * i + 1] * inv; o.z = v[4 * i + 2] * inv; o.w = v[4 * i + 3] * inv;
-            st4_stream(&yr[idx], o);
-        }
+        float4 t = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+        if (FULL || idx < n4) t = ld4_stream(&xr[idx]);
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
+}
+
+template <int VPT, bool FULL>
+__device__ __forceinline__ void store_row_regs(float* yrow, long n4, const float* v) {
+    float4* yr = reinterpret_cast<float4*>(yrow);
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const long idx = threadIdx.x + (long)i * kRowThreads;
+        if (FULL || idx < n4) st4_stream(&yr[idx], make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]));
+    }
+}
+
+// One workgroup per row: the row is read once into registers (16-byte
+// loads), reduced, exponentiated and written once.
+// FULL: n == 1024 * VPT exactly, so no lane needs a bounds check.
+template <int VPT, int NITER, bool MASKED, bool FULL>
+__global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
+    const float* x, float* y, long n, int iters, float khinv,
+    SoftmaxMask mk)
+{
+    __shared__ float red[2 * kRowWaves];
+    const long row = blockIdx.x;
+    const long n4 = n / 4;
+    float v[4 * VPT];
+    load_row_regs<VPT, FULL>(x + row * n, n4, v);
+    softmax_row_regs<VPT, NITER, MASKED, FULL>(v, n4, MASKED ? mk.row0 + row % mk.seq : 0, iters, khinv, mk,
+                                               red);
+    store_row_regs<VPT, FULL>(y + row * n, n4, v);
 }
 
 template <int NITER, bool MASKED>

@@ -452,6 +452,20 @@ def test_scalar_rac_h_entry_points():
     assert np.array_equal(so, rl.orc_unary("orc_silu", xs, 16))
 
 
+@pytest.mark.parametrize("iters", [8, 16, 24])
+def test_silu_config4b_full_size(iters):
+    """Benchmark config 4b: SiLU over [16384 x 11008] N(0, 1) (44 M float4
+    groups, 176 k workgroups), bit-exact with the checker's CORDIC SiLU on
+    every element; plus counts that end inside a workgroup's groups and
+    inside a float4 (the scalar path)."""
+    x = np.random.default_rng(31).standard_normal((16384, 11008), dtype=np.float32)
+    got = H(ext().silu(T(x), iters=iters))
+    assert np.array_equal(got, rl.orc_unary("orc_silu", x, iters))
+    for count in (4 * 256 * 7 + 4 * 129, 4 * 256 + 4, 4 * 3, 4099, 1):
+        xs = rl.gen_normal((count,), 32 + count % 7, std=3.0)
+        assert np.array_equal(H(ext().silu(T(xs), iters=iters)), rl.orc_unary("orc_silu", xs, iters)), count
+
+
 # ── softmax / norms ────────────────────────────────────────────────────────
 
 @pytest.mark.parametrize("iters", [8, 16, 24])
