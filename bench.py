@@ -374,6 +374,20 @@ def bench_row_ops(torch, ext, dev, g):
     torch.cuda.synchronize()
     record("rope_qk_bthd_8x4096x32x128", 2 * 2 * 4 * q.numel(), _events_time(rope_bthd, reps, torch))
 
+    # the operator surface: RACRoPE forward on the same Q and K (out of place:
+    # each output is a new tensor, one read and one write per element)
+    from rac_amd import rac_torch as rt
+    rope_mod = rt.RACRoPE(Dq, max_seq_len=Tq).to(dev)
+
+    def rope_module():
+        with torch.no_grad():
+            rope_mod(q, k)
+
+    rope_module()
+    torch.cuda.synchronize()
+    record("rope_module_qk_8x32x4096x128", 2 * 2 * 4 * q.numel(), _events_time(rope_module, reps, torch))
+    del rope_mod
+
     # the table itself: rac_rope_cache(4096, 128, 10000) on the device, 16
     # circular CORDIC steps per entry after the reference's sequential wrap
     # of theta (inv_freq from the host's powf, already in device memory)

@@ -109,6 +109,14 @@ int rac_rope_cache_dev(float *cos_out, float *sin_out, int max_seq, int head_dim
 int rac_rope_apply_dev(float *x, const float *cos_tab, const float *sin_tab, int batch,
                        int n_heads, int seq, int head_dim, long stride_b, long stride_h,
                        long stride_t, void *stream);
+/* The same rotation out of place (rac_cpu.c:600-635 on a copy): rows read
+ * at x with strides (stride_b, stride_h, stride_t), written at y with
+ * (out_b, out_h, out_t); x and y must not overlap.  One read and one write
+ * per element. */
+int rac_rope_apply_out_dev(const float *x, float *y, const float *cos_tab, const float *sin_tab,
+                           int batch, int n_heads, int seq, int head_dim, long stride_b,
+                           long stride_h, long stride_t, long out_b, long out_h, long out_t,
+                           void *stream);
 
 /* Vector primitives over n items of interleaved (x, y) pairs.  `op` selects
  * the rac.h primitive evaluated per item i (rac.h:101-250, 345-346, with the

@@ -78,6 +78,7 @@ _SIGNATURES = {
     "rac_layernorm_dev": (_i, [_vp, _vp, _vp, _vp, _f, _l, _l, _vp]),
     "rac_rope_cache_dev": (_i, [_vp, _vp, _i, _i, _f, _vp, _vp]),
     "rac_rope_inv_freq": (_i, [_vp, _i, _f]),
+    "rac_rope_apply_out_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l, _l, _l, _l, _vp]),
     "rac_rope_apply_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _l, _l, _l, _vp]),
     "rac_vec2_dev": (_i, [_i, _l, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "rac_inner_dev": (_i, [_vp, _vp, _l, _vp, _vp]),

@@ -419,6 +419,22 @@ RAC_EXPORT int rac_rope_apply_dev(float* x, const float* cos_tab, const float* s
                      "rac_rope_apply_dev launch");
 }
 
+// rac_rope_apply (rac_cpu.c:600-635) out of place: rows read at x with
+// strides (stride_b, stride_h, stride_t), the rotated rows written at y with
+// (out_b, out_h, out_t); x and y must not overlap.  One read and one write
+// per element, where a copy followed by the in-place call moves twice that.
+RAC_EXPORT int rac_rope_apply_out_dev(const float* x, float* y, const float* cos_tab, const float* sin_tab,
+                                      int batch, int n_heads, int seq, int head_dim, long stride_b,
+                                      long stride_h, long stride_t, long out_b, long out_h, long out_t,
+                                      void* stream) {
+    int rc = check_rope(x, cos_tab, sin_tab, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (!y) return fail(RAC_ERR_NULL_PTR, "rac_rope_apply_out_dev: null output");
+    return check_hip(rope_apply_out_launch(x, y, cos_tab, sin_tab, batch, n_heads, seq, head_dim, stride_b,
+                                           stride_h, stride_t, out_b, out_h, out_t, (hipStream_t)stream),
+                     "rac_rope_apply_out_dev launch");
+}
+
 // ── vector primitives on device buffers ──────────────────────────────────
 
 // Which operands each primitive op reads / writes (see PrimOp).

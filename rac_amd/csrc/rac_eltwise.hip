@@ -190,10 +190,18 @@ hipError_t rope_cache_launch(float* cos_out, float* sin_out, const float* inv_fr
 // the number of workgroups in flight and lost bandwidth (16 rows: 394 us).
 constexpr int kRopeRslice = 2;
 
+// Row (b, h, t) is read at x + b*sb + h*sh + t*st and written at
+// y + b*ob + h*oh + t*ot: in place when y == x with the same strides,
+// out of place otherwise (the two must then not overlap).
+struct RopeOut {
+    float* y;
+    long ob, oh, ot;
+};
+
 template <int LPR>   // lanes per row = head_dim / 4, a power of two <= 256
 __global__ __launch_bounds__(256) void rope_apply_vec_kernel(
-    float* __restrict__ x, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
-    int heads, int seq, int head_dim, long sb, long sh, long st, long bh_total)
+    const float* x, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+    int heads, int seq, int head_dim, long sb, long sh, long st, long bh_total, RopeOut out)
 {
     constexpr int RPB = 256 / LPR;
     const int lane_in_row = threadIdx.x % LPR;
@@ -213,8 +221,8 @@ __global__ __launch_bounds__(256) void rope_apply_vec_kernel(
         const long bh = bh0 + r;
         if (bh < bh_end) {
             const long b = bh / heads, h = bh % heads;
-            p[r] = reinterpret_cast<float4*>(x + b * sb + h * sh + (long)t * st) + lane_in_row;
-            v[r] = ld4_stream(p[r]);
+            v[r] = ld4_stream(reinterpret_cast<const float4*>(x + b * sb + h * sh + (long)t * st) + lane_in_row);
+            p[r] = reinterpret_cast<float4*>(out.y + b * out.ob + h * out.oh + (long)t * out.ot) + lane_in_row;
         }
     }
 #pragma unroll
@@ -231,8 +239,8 @@ __global__ __launch_bounds__(256) void rope_apply_vec_kernel(
 }
 
 __global__ __launch_bounds__(256) void rope_apply_scalar_kernel(
-    float* __restrict__ x, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
-    int heads, int seq, int head_dim, long sb, long sh, long st, long total_pairs)
+    const float* x, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+    int heads, int seq, int head_dim, long sb, long sh, long st, long total_pairs, RopeOut out)
 {
     const int half = head_dim / 2;
     const long stride = (long)gridDim.x * blockDim.x;
@@ -242,22 +250,32 @@ __global__ __launch_bounds__(256) void rope_apply_scalar_kernel(
         const long t = r % seq;
         r /= seq;
         const long h = r % heads, b = r / heads;
-        float* row = x + b * sb + h * sh + t * st;
+        const float* row = x + b * sb + h * sh + t * st;
+        float* orow = out.y + b * out.ob + h * out.oh + t * out.ot;
         const float a = row[2 * i], b2 = row[2 * i + 1];
         const float c = cos_tab[t * half + i], s = sin_tab[t * half + i];
-        row[2 * i] = __builtin_fmaf(a, c, -(b2 * s));
-        row[2 * i + 1] = __builtin_fmaf(a, s, b2 * c);
+        orow[2 * i] = __builtin_fmaf(a, c, -(b2 * s));
+        orow[2 * i + 1] = __builtin_fmaf(a, s, b2 * c);
     }
 }
 
 hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_tab, int batch,
                              int heads, int seq, int head_dim, long sb, long sh, long st,
                              hipStream_t s) {
+    return rope_apply_out_launch(x, x, cos_tab, sin_tab, batch, heads, seq, head_dim, sb, sh, st, sb, sh, st, s);
+}
+
+hipError_t rope_apply_out_launch(const float* x, float* y, const float* cos_tab, const float* sin_tab, int batch,
+                                 int heads, int seq, int head_dim, long sb, long sh, long st, long ob, long oh,
+                                 long ot, hipStream_t s) {
     const long bh_total = (long)batch * heads;
     const int lpr = head_dim / 4;
+    const RopeOut out{y, ob, oh, ot};
     const bool pow2_lpr = (head_dim % 4 == 0) && lpr >= 1 && lpr <= 256 && (lpr & (lpr - 1)) == 0;
     const bool aligned = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (sb % 4 == 0) &&
                          (sh % 4 == 0) && (st % 4 == 0) &&
+                         ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ob % 4 == 0) &&
+                         (oh % 4 == 0) && (ot % 4 == 0) &&
                          ((reinterpret_cast<uintptr_t>(cos_tab) & 7) == 0) &&
                          ((reinterpret_cast<uintptr_t>(sin_tab) & 7) == 0);
     const long grid_y = (bh_total + kRopeRslice - 1) / kRopeRslice;
@@ -267,7 +285,7 @@ hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_ta
 #define RAC_ROPE_CASE(L)                                                                          \
     case L:                                                                                       \
         hipLaunchKernelGGL((rope_apply_vec_kernel<L>), grid, dim3(256), 0, s, x, cos_tab, sin_tab, \
-                           heads, seq, head_dim, sb, sh, st, bh_total);                          \
+                           heads, seq, head_dim, sb, sh, st, bh_total, out);                     \
         break;
         switch (lpr) {
             RAC_ROPE_CASE(1) RAC_ROPE_CASE(2) RAC_ROPE_CASE(4) RAC_ROPE_CASE(8)
@@ -279,7 +297,7 @@ hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_ta
     } else {
         const long pairs = bh_total * seq * (head_dim / 2);
         hipLaunchKernelGGL(rope_apply_scalar_kernel, dim3(stream_grid(pairs)), dim3(256), 0, s, x,
-                           cos_tab, sin_tab, heads, seq, head_dim, sb, sh, st, pairs);
+                           cos_tab, sin_tab, heads, seq, head_dim, sb, sh, st, pairs, out);
     }
     return hipGetLastError();
 }

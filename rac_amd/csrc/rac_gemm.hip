@@ -88,6 +88,16 @@ __device__ __forceinline__ float mac(float a, float b, uint32_t bsign, float acc
     }
 }
 
+// Column tiles of row tile r in a causal score trapezoid (query rows
+// row0 + r*BM .. row0 + r*BM + BM - 1, keys 0 .. N-1): those holding a key
+// position not past the row tile's last query position.
+__host__ __device__ __forceinline__ int trap_cols(int row0, int r, int BM, int BN, int N) {
+    const long last = (long)row0 + (long)(r + 1) * BM - 1;
+    const long c = last / BN + 1;
+    const long ntn = (N + BN - 1) / BN;
+    return (int)(c < ntn ? c : ntn);
+}
+
 template <int MODE, int NITER, bool TA, bool TB, int TM, int TN, bool FUSED, int SCHED>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
@@ -103,12 +113,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     // tile and rows p and nt-1-p share a column of the grid (grid nt+1 x
     // ceil(nt/2)).  2 (causal P V): workgroup p computes row tiles p and
     // nt-1-p, whose K ranges (below) sum to a constant.  3 (causal attention
-    // scores of query rows row0.. row0+M-1 against keys 0..N-1): tile (y, x)
-    // as in 0, skipped when it lies wholly above the diagonal (every column
-    // past every row's query position).
+    // scores of query rows row0.. row0+M-1 against keys 0..N-1): only the
+    // tiles on or below the diagonal, numbered row by row (row tile r has
+    // trap_cols(r) of them), one workgroup each; consecutive workgroups go to
+    // consecutive XCDs, so the trapezoid's work spreads over all of them (a
+    // rectangular grid with the upper tiles skipped leaves the live ones on
+    // a few XCDs).
     int tm = blockIdx.y, tn = blockIdx.x, tm2 = -1;
     if constexpr (SCHED == 3) {
-        if ((long)tn * BN > (long)row0 + (long)tm * BM + BM - 1) return;
+        int l = blockIdx.x;
+        tm = 0;
+        for (;;) {
+            const int c = trap_cols(row0, tm, BM, BN, N);
+            if (l < c) break;
+            l -= c;
+            tm++;
+        }
+        tn = l;
     }
     if constexpr (SCHED == 1) {
         const int nt = (M + BM - 1) / BM, p = blockIdx.y, x = blockIdx.x;
@@ -397,6 +418,11 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     dim3 grid((unsigned)((g.N + Cfg::kBN - 1) / Cfg::kBN), nt, (unsigned)g.batch);
     if (g.sched == 1) grid = dim3(nt + 1, (nt + 1) / 2, (unsigned)g.batch);
     if (g.sched == 2) grid.y = (nt + 1) / 2;
+    if (g.sched == 3) {
+        long tiles = 0;
+        for (unsigned r = 0; r < nt; r++) tiles += trap_cols(g.row0, (int)r, Cfg::kBM, Cfg::kBN, g.N);
+        grid = dim3((unsigned)tiles, 1, (unsigned)g.batch);
+    }
     hipLaunchKernelGGL((gemm_kernel<MODE, NITER, TA, TB, TM, TN, FUSED, SCHED>), grid, dim3(256), 0, stream,
                        g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, kinv, g.sa, g.sb, g.sc,
                        g.ep, g.k_causal, g.exact_specials, g.row0);
@@ -436,7 +462,14 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
     if constexpr (SCHED == 1 || SCHED == 2) {
         return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
     } else {
-        auto tiles = [&](long bm, long bn) { return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch; };
+        auto tiles = [&](long bm, long bn) {
+            if constexpr (SCHED == 3) {      // the causal trapezoid's tiles only
+                long t = 0;
+                for (long r = 0; r < (g.M + bm - 1) / bm; r++) t += trap_cols(g.row0, (int)r, (int)bm, (int)bn, g.N);
+                return t * (long)g.batch;
+            }
+            return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch;
+        };
         if constexpr (MODE == kModeFast && SCHED == 0) {
             // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
             // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per

@@ -91,6 +91,10 @@ hipError_t rope_cache_launch(float* cos_out, float* sin_out, const float* inv_fr
 hipError_t rope_apply_launch(float* x, const float* cos_tab, const float* sin_tab,
                              int batch, int heads, int seq, int head_dim,
                              long sb, long sh, long st, hipStream_t s);
+// Out of place: rows read at x (strides sb, sh, st), written at y (ob, oh, ot).
+hipError_t rope_apply_out_launch(const float* x, float* y, const float* cos_tab, const float* sin_tab,
+                                 int batch, int heads, int seq, int head_dim, long sb, long sh, long st,
+                                 long ob, long oh, long ot, hipStream_t s);
 hipError_t rsqrt_launch(const float* x, float* y, long count, hipStream_t s);
 
 enum PrimOp {

@@ -489,6 +489,33 @@ def rope_apply_(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.
     return x
 
 
+def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Out-of-place rope_apply_: returns a new contiguous [B, H, T, D] tensor
+    holding x rotated (x itself, whose last dim must be contiguous and whose
+    other dims may be strided, is only read): one read and one write per
+    element."""
+    _require_f32(x, "x")
+    if x.dim() != 4:
+        raise RuntimeError("RAC: rope_apply expects [batch, heads, seq, head_dim]")
+    if x.stride(-1) != 1:
+        raise RuntimeError("RAC: rope_apply needs a contiguous last dim")
+    B, H, T, D = x.shape
+    if D % 2:
+        raise RuntimeError("RAC: head_dim must be even")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _require_f32(t, n)
+        if not t.is_contiguous() or t.dim() != 2 or t.size(1) != D // 2 or t.size(0) < T:
+            raise RuntimeError(f"RAC: {n} must be a contiguous [>= seq, head_dim/2] table")
+    y = torch.empty((B, H, T, D), device=x.device, dtype=torch.float32)
+    if x.numel() == 0:
+        return y
+    check(_lib.load().rac_rope_apply_out_dev(x.data_ptr(), y.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, H, T,
+                                             D, x.stride(0), x.stride(1), x.stride(2), y.stride(0), y.stride(1),
+                                             y.stride(2), _stream(y)),
+          "rac_rope_apply_out_dev")
+    return y
+
+
 # ── batched products and attention ───────────────────────────────────────
 
 def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool = False,
@@ -864,7 +891,7 @@ __all__ = [
     "set_cordic_iters", "get_cordic_iters", "set_cordic_mode", "get_cordic_mode",
     "matmul_forward", "matmul_backward", "linear_forward", "linear_backward",
     "softmax", "rmsnorm", "layernorm", "exp", "silu", "sigmoid", "tanh", "gelu", "relu",
-    "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_",
+    "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_", "rope_apply",
     "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
     "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
     "q8_quantize", "q8_dequantize", "q8_gemv", "Q8_BLOCK_BYTES",

@@ -601,19 +601,26 @@ class RACRoPE(nn.Module):
 
 
 class _RoPEFunction(Function):
+    """Rotation of [B, H, T, D] (strided views allowed) into a new tensor:
+    one read and one write per element (rac_rope_apply_out_dev)."""
+
     @staticmethod
     def forward(ctx, x, cos, sin, nsin):
         ctx.save_for_backward(cos, nsin)
-        out = x.float().clone() if x.dtype != torch.float32 else x.clone()
-        _rac.rope_apply_(out, cos, sin)
-        return out.to(x.dtype)
+        x32 = x if x.dtype == torch.float32 else x.float()
+        if x32.stride(-1) != 1:
+            x32 = x32.contiguous()
+        out = _rac.rope_apply(x32, cos, sin)
+        return out if x.dtype == torch.float32 else out.to(x.dtype)
 
     @staticmethod
     def backward(ctx, g):
         cos, nsin = ctx.saved_tensors
-        gx = g.float().contiguous().clone()
-        _rac.rope_apply_(gx, cos, nsin)      # transpose of a rotation: angle -> -angle
-        return gx.to(g.dtype), None, None, None
+        g32 = g if g.dtype == torch.float32 else g.float()
+        if g32.stride(-1) != 1:
+            g32 = g32.contiguous()
+        gx = _rac.rope_apply(g32, cos, nsin)      # transpose of a rotation: angle -> -angle
+        return gx if g.dtype == torch.float32 else gx.to(g.dtype), None, None, None
 
 
 class RACRMSNorm(nn.Module):

@@ -627,8 +627,13 @@ def test_rope_apply_bit_exact(shape):
     # the [B, T, H, D] storage used by attention projections
     xt = T(np.ascontiguousarray(x.transpose(0, 2, 1, 3)))
     view = xt.transpose(1, 2)
+    # out of place first (reads the view, leaves it untouched), then in place
+    y = ext().rope_apply(view, T(c), T(s))
+    assert y.is_contiguous() and np.array_equal(H(y), ref)
+    assert np.array_equal(H(view), x)
     ext().rope_apply_(view, T(c), T(s))
     assert np.array_equal(H(view), ref)
+    assert np.array_equal(H(ext().rope_apply(T(x), T(c), T(s))), ref)
 
 
 def test_rope_apply_golden_and_rac_h():
@@ -651,8 +656,11 @@ def test_rope_config3_full_size():
         xd = torch.randn(shape, device=DEV, generator=gen)
         x = H(xd)
         ref = rl.orc_rope_apply(x, ch, sh)
-        ext().rope_apply_(xd, c, s)
-        got = H(xd)
+        if seed == 1:        # out of place, through the module's path
+            got = H(ext().rope_apply(xd, c, s))
+        else:
+            ext().rope_apply_(xd, c, s)
+            got = H(xd)
         assert np.array_equal(got, ref)
         del xd, got, ref, x
 
