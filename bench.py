@@ -508,13 +508,37 @@ def bench_block_ops(torch, ext, dev, g):
     # (P V), so each product has B*H*D*T(T+1)/2 MACs; the dense count would
     # credit the masked half that is never computed
     macs = 2 * Ba * Ha * Da * Ta * (Ta + 1) // 2
+    ws_mib = lib.rac_attention_workspace_bytes(Ba, Ha, Ta) / 2 ** 20
     out["attention_core_1x32x2048x128_n16"] = {
         "ms": round(t * 1e3, 3), "causal_macs": macs,
         "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
         "valu_frac_of_fp32_peak": round(macs * 2 * 33 / t / 1e12 / PEAK_FP32_TFLOPS, 4),
+        "workspace_MiB": round(ws_mib, 1), "path": "rac_attention_dev: query-row chunks",
         **_dist_fields(t, 1e3, "ms")}
-    print(f"# attention core n=16: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
-    del qa, ka, va, oa, wsa
+    print(f"# attention core n=16 (chunks, {ws_mib:.0f} MiB workspace): {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    del wsa
+    # the same core in one chunk (the [B*H, T, T] score matrix the reference
+    # materialises; what the autograd path keeps for backward) and through the
+    # allocation-free entry point (32 MiB static scratch): same output bits
+    wsp = torch.empty(lib.rac_attention_probs_workspace_bytes(Ba, Ha, Ta) // 4, device=dev)
+
+    def attn_one():
+        chk(lib.rac_attention_probs_dev(qa.data_ptr(), ka.data_ptr(), va.data_ptr(), None, 1, oa.data_ptr(), Ba, Ha,
+                                        Ta, Da, wsp.data_ptr(), 16, ext.MODE_CORDIC, stream))
+
+    def attn_noalloc():
+        chk(lib.rac_attention_noalloc_dev(qa.data_ptr(), ka.data_ptr(), va.data_ptr(), None, 1, oa.data_ptr(), Ba,
+                                          Ha, Ta, Da, 16, ext.MODE_CORDIC, stream))
+
+    for name, fn, mib in (("attention_core_one_chunk_1x32x2048x128_n16", attn_one, wsp.numel() * 4 / 2 ** 20),
+                          ("attention_core_noalloc_1x32x2048x128_n16", attn_noalloc, 32.0)):
+        fn()
+        torch.cuda.synchronize()
+        t = _events_time(fn, 3, torch)
+        out[name] = {"ms": round(t * 1e3, 3), "equiv_TFLOPs": round(2 * macs / t / 1e12, 3),
+                     "workspace_MiB": round(mib, 1), **_dist_fields(t, 1e3, "ms")}
+        print(f"# {name}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    del qa, ka, va, oa, wsp
 
     # Q8_0 decode GEMV (M = 1): weight bytes N*K/32*34 streamed once; buffer
     # sets rotate past the MALL

@@ -740,6 +740,10 @@ class RACAttentionFunction(Function):
         _need_gpu(q, "q")
         q32, k32, v32 = (t.float().contiguous() for t in (q, k, v))
         m32 = mask.float().contiguous() if mask is not None else None
+        if not any(ctx.needs_input_grad[:3]):
+            # no backward: the core runs over query-row chunks and keeps no
+            # [B, H, T, T] probabilities (same output bits)
+            return _rac.attention(q32, k32, v32, m32, bool(is_causal), **_kw()).to(q.dtype)
         out, P = _rac.attention(q32, k32, v32, m32, bool(is_causal), return_probs=True, **_kw())
         ctx.save_for_backward(q32, k32, v32, P)
         return out.to(q.dtype)
