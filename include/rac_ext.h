@@ -177,12 +177,12 @@ int rac_attention_ws_dev(const float *q, const float *k, const float *v, const f
 /* rac_attention_dev for callers that cannot allocate device memory (code
  * under stream or graph capture, serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  It allocates nothing: its
- * chunk workspace is a 32 MiB device array inside the library, one per GPU,
- * held until the process ends.  Limit: 4*batch*n_heads*seq + 256 bytes must
- * fit that array (batch*n_heads*seq <= 8388544); larger shapes are refused
- * with -2 before any device work.  Every call on one GPU shares that GPU's
- * array, so calls that overlap on one GPU race: serialise them.  Same output
- * bits as rac_attention_dev. */
+ * chunk workspace is a 64 MiB (+ 256 B) device array inside the library, one
+ * per GPU, held until the process ends.  Limit: batch*n_heads*seq <=
+ * 16777215 (one query row of every head must fit the array); larger shapes
+ * are refused with -2 before any device work.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU race: serialise them.
+ * Same output bits as rac_attention_dev. */
 int rac_attention_noalloc_dev(const float *q, const float *k, const float *v, const float *mask,
                               int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
                               int iters, int mode, void *stream);

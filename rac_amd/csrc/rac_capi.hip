@@ -646,13 +646,18 @@ RAC_EXPORT int rac_attention_ws_dev(const float* q, const float* k, const float*
 //
 // For callers that cannot allocate device memory (code under stream or
 // graph capture, serving loops that forbid allocation): the chunk workspace
-// lives in this file-scope device array, kScratchBytes per GPU, held by
-// each GPU the library runs on until the process ends.  Every call on one
-// GPU shares that GPU's array: calls that overlap on one GPU (other
-// streams, other host threads) race and must be serialised by the caller.
+// lives in this file-scope device array, kScratchBytes (64 MiB + 256 B) per
+// GPU, held by each GPU the library runs on until the process ends.  It
+// holds 256 query rows of every head at [1, 32, 2048, 128] (smaller chunks
+// leave the causal P V launches too few workgroups: 64-row chunks took
+// 16.3 ms there against 10.0 ms), and one query row of every head for every
+// shape the argument check accepts (batch*n_heads*seq <= 16777215).  Every
+// call on one GPU shares that GPU's array: calls that overlap on one GPU
+// (other streams, other host threads) race and must be serialised by the
+// caller.
 // The array's device address is looked up once per device (the host-side
 // name is only a stand-in for it) and used from then on.
-static constexpr long kScratchBytes = 32L << 20;
+static constexpr long kScratchBytes = (64L << 20) + 256;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static std::mutex g_scratch_mutex;
 static void* g_scratch_ptr[64];
@@ -674,10 +679,10 @@ static int scratch_for_current_device(void** out) {
 }
 
 // rac_attention_dev without a workspace argument and without allocating:
-// the chunks of query rows are sized to the library's 32 MiB scratch array
-// (results equal rac_attention_dev's).  Refuses, before any device work,
-// shapes whose one query row of every head does not fit it
-// (4*batch*n_heads*seq + 256 > 32 MiB, i.e. batch*n_heads*seq > 8388544).
+// the chunks of query rows are sized to the library's scratch array
+// (results equal rac_attention_dev's).  Shapes beyond the argument check's
+// limit (batch*n_heads*seq > 16777215, whose one query row of every head
+// would not fit the array either) are refused before any device work.
 RAC_EXPORT int rac_attention_noalloc_dev(const float* q, const float* k, const float* v, const float* mask,
                                          int is_causal, float* out, int batch, int n_heads, int seq,
                                          int head_dim, int iters, int mode, void* stream) {

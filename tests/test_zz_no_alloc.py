@@ -1,7 +1,7 @@
 """rac_attention_noalloc_dev, the allocation-free attention entry point,
 against rac_attention_dev (workspace argument): bit-identical outputs on two
-calls in a row, the second with a smaller input, through the C ABI; and the
-size limit of its 32 MiB scratch refused before any device work."""
+calls in a row, the second with a smaller input, through the C ABI; and
+shapes past its limit refused before any device work."""
 import ctypes
 
 import numpy as np
@@ -50,7 +50,7 @@ def _qkv(shape, seed):
 
 def test_noalloc_attention_matches_workspace_entry_twice(lib):
     # call 1: config 5's attention core, [1, 32, 2048, 128] causal, n = 16
-    # (64 query rows per chunk in the 32 MiB scratch)
+    # (256 query rows per chunk in the scratch)
     q, k, v = _qkv((1, 32, 2048, 128), seed=800)
     got = _run(lib, q, k, v, None, True, 16, 1, noalloc=True)
     ref = _run(lib, q, k, v, None, True, 16, 1, noalloc=False)
@@ -72,7 +72,8 @@ def test_noalloc_attention_matches_workspace_entry_twice(lib):
 def test_noalloc_attention_refuses_beyond_scratch(lib):
     buf = (ctypes.c_float * 64)()
     a = ctypes.addressof(buf)
-    # one query row of every head: 4 * 64 * 131072 + 256 bytes > 32 MiB
+    # batch*n_heads*seq = 16777216: one query row of every head is 64 MiB,
+    # past the limit; refused before any device work
     lib.rac_clear_error()
-    assert lib.rac_attention_noalloc_dev(a, a, a, None, 1, a, 1, 64, 131072, 4, 16, 1, None) == -2
-    assert b"scratch" in lib.rac_last_error()
+    assert lib.rac_attention_noalloc_dev(a, a, a, None, 1, a, 1, 64, 262144, 4, 16, 1, None) == -2
+    assert b"16777215" in lib.rac_last_error()
