@@ -48,8 +48,8 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
     }
 }
 
-// Fast path (K % 256 == 0, 16-byte aligned buffers).  A workgroup owns R
-// consecutive weight rows (16 or 32) and walks K in chunks of up to CB
+// Fast path (K % 256 == 0, K >= 32 CB, 16-byte aligned buffers).  A
+// workgroup owns R consecutive weight rows and walks K in chunks of CB
 // blocks (R x CB x 34 bytes, all requested at once, so the whole chunk is
 // in flight before any of it is used):
 //   1. 16-byte loads of the chunk (contiguous per row) -> registers -> LDS;
@@ -57,22 +57,29 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
 //      lanes read consecutive blocks, the x slice is padded to 33 floats
 //      per block, so LDS reads do not collide), and stores (d, dot);
 //   3. lane (m, r) folds its row's terms in block order.
-// Up to 4 input rows (batched decode) share one pass over the weights.
-// The shape only decides which lane computes what; every output is the
-// same serial fold, so all shapes give identical bits.
+// Every chunk is a full CB blocks: when CB does not divide the row, the
+// last chunk starts CB blocks before the row end and its first blocks,
+// already folded, are skipped.  So the loads' placement is one fixed
+// pattern per lane, computed once, and no code depends on a run-time chunk
+// width.  The next chunk's loads are issued before the current chunk's
+// math.  Up to 4 input rows (batched decode) share one pass over the
+// weights.  The shape only decides which lane computes what; every output
+// is the same serial fold, so all shapes give identical bits.
 constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
 
 template <int MX, int CB, int R>
-__global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ x,
+__global__ __launch_bounds__(256, 4) void q8_gemv_kernel(const float* __restrict__ x,
                                                       const uint8_t* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ out, int M, int N, int K,
                                                       int act) {
     static_assert(256 % CB == 0 && CB % 8 == 0 && R * CB >= 256 && MX * R <= 256, "chunk shape");
     constexpr int kRowLds = CB * kQ8Bytes + 16;                       // row stride in LDS (16-byte multiple)
-    constexpr int kVPT = (R * CB * kQ8Bytes / 16 + 255) / 256;     // weight vectors per lane
-    constexpr int kXPT = MX * CB * kQ8Block / 4 / 256;                // x float4 per lane
-    constexpr int kRPT = R * CB / 256;                             // rows per lane in the dot phase
+    constexpr int kVrow = CB * kQ8Bytes / 16;                         // 16-byte vectors per row and chunk
+    constexpr int kVPT = (R * kVrow + 255) / 256;                     // weight vectors per lane
+    constexpr int kXF4 = MX * CB * kQ8Block / 4;                      // x float4 per chunk
+    constexpr int kXPT = (kXF4 + 255) / 256;                          // x float4 per lane
+    constexpr int kRPT = R * CB / 256;                                // rows per lane in the dot phase
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) uint8_t sw[R * kRowLds];
     __shared__ float sx[MX][CB * kQ8XPad];
@@ -82,85 +89,75 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
     const int tid = threadIdx.x;
     const long j0 = (long)blockIdx.x * R;
     const int nrows = (int)min((long)R, (long)N - j0);
-    const int nb = K / kQ8Block;
+    const int nb = K / kQ8Block;                     // >= CB, multiple of 8
     const long rowB = (long)nb * kQ8Bytes;
+    const int nch = (nb + CB - 1) / CB;
 
-    // Chunk staging in registers: every load is unconditional (lanes past
-    // the chunk or past the last row re-read valid bytes and never store
-    // them), so a chunk's loads are all in flight together.
-    u4 rw[kVPT];
-    float4 rx[kXPT];
-    // Per-lane vector placement for a full chunk (the common case), computed
-    // once: global byte offset relative to the chunk start, LDS offset (-1:
-    // nothing to store).  Only a short last chunk re-derives them.
-    constexpr int kVrow = CB * kQ8Bytes / 16;
-    long gfull[kVPT];
-    int sfull[kVPT];
+    // Vector placement, fixed for every chunk: byte offset of this lane's
+    // vector i from the chunk start (rows past the last re-read row 0: every
+    // load is unconditional, so a chunk's loads are all in flight together)
+    // and its LDS offset (-1: nothing to store).  R rows of one chunk span
+    // less than 2^32 bytes (the host checks rows x blocks against 2^31 x 128).
+    unsigned goff[kVPT];
+    int soff[kVPT];
 #pragma unroll
     for (int i = 0; i < kVPT; i++) {
         const int v = tid + i * 256;
-        const bool live = v < R * kVrow;
-        const int r = live ? v / kVrow : 0, o = live ? v % kVrow : 0;
-        gfull[i] = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
-        sfull[i] = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
+        const bool in = v < R * kVrow;
+        const int r = in ? v / kVrow : 0, o = in ? v % kVrow : 0;
+        goff[i] = (unsigned)((r < nrows ? r : 0) * rowB + o * 16);
+        soff[i] = (in && r < nrows) ? r * kRowLds + o * 16 : -1;
     }
-    auto place = [&](int i, int cb, long& goff, int& soff) {
-        if (cb == CB) {
-            goff = gfull[i];
-            soff = sfull[i];
-            return;
-        }
-        const int vrow = cb * kQ8Bytes / 16;
-        const int v = tid + i * 256;
-        const bool live = v < R * vrow;
-        const int r = live ? v / vrow : 0, o = live ? v % vrow : 0;
-        goff = (r < nrows ? (long)r : 0L) * rowB + (long)o * 16;
-        soff = (live && r < nrows) ? r * kRowLds + o * 16 : -1;
-    };
-    auto fetch = [&](int b0, int cb) {
+    u4 rw[kVPT];
+    float4 rx[kXPT];
+    auto chunk_start = [&](int c) { return min(c * CB, nb - CB); };
+    auto fetch = [&](int b0) {
+        const uint8_t* base = w + j0 * rowB + (long)b0 * kQ8Bytes;
 #pragma unroll
-        for (int i = 0; i < kVPT; i++) {
-            long goff;
-            int soff;
-            place(i, cb, goff, soff);
-            rw[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const u4*>(w + j0 * rowB + (long)b0 * kQ8Bytes + goff));
-        }
+        for (int i = 0; i < kVPT; i++)
+            rw[i] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + goff[i]));
 #pragma unroll
         for (int i = 0; i < kXPT; i++) {
-            const int e = (tid + i * 256) * 4;                        // float index in [MX][CB*32]
+            const int e = min(tid + i * 256, kXF4 - 1) * 4;           // float index in [MX][CB*32]
             const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
-            const int qq = q < cb * kQ8Block ? q : 0;
-            rx[i] = *reinterpret_cast<const float4*>(x + (long)min(m, M - 1) * K + (long)b0 * kQ8Block + qq);
+            rx[i] = *reinterpret_cast<const float4*>(x + (long)min(m, M - 1) * K + (long)b0 * kQ8Block + q);
         }
     };
 
-    float acc = 0.0f;          // lane tid < MX * 16 owns output (tid / 16, j0 + tid % 16)
-    fetch(0, min(CB, nb));
-    for (int b0 = 0; b0 < nb; b0 += CB) {
-        const int cb = min(CB, nb - b0);             // multiple of 8
+    float acc = 0.0f;          // lane tid < MX * R owns output (tid / R, j0 + tid % R)
+    fetch(chunk_start(0));
+    for (int c = 0; c < nch; c++) {
+        const int b0 = chunk_start(c);
+        const int k0 = c * CB - b0;                  // blocks of this chunk already folded
         __syncthreads();                             // previous chunk's LDS consumed
 #pragma unroll
-        for (int i = 0; i < kVPT; i++) {
-            long goff;
-            int soff;
-            place(i, cb, goff, soff);
-            if (soff >= 0) *reinterpret_cast<u4*>(&sw[soff]) = rw[i];
-        }
+        for (int i = 0; i < kVPT; i++)
+            if (soff[i] >= 0) *reinterpret_cast<u4*>(&sw[soff[i]]) = rw[i];
 #pragma unroll
         for (int i = 0; i < kXPT; i++) {
             const int e = (tid + i * 256) * 4;
-            const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
-            if (q < cb * kQ8Block) {
+            if (kXF4 % 256 == 0 || e < kXF4 * 4) {
+                const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
                 float* dst = &sx[m][(q / kQ8Block) * kQ8XPad + q % kQ8Block];
                 dst[0] = rx[i].x; dst[1] = rx[i].y; dst[2] = rx[i].z; dst[3] = rx[i].w;
             }
         }
         __syncthreads();
-        if (b0 + CB < nb) fetch(b0 + CB, min(CB, nb - b0 - CB));   // in flight during the math
+        if (c + 1 < nch) fetch(chunk_start(c + 1));  // in flight during the math
         // block dots: lane owns block k = tid % CB of rows tid / CB + (256 / CB) i
         const int k = tid % CB;
-        if (k < cb) {
+        if (k < k0) {
+            // already folded: (0, 0) terms leave the fold unchanged, since
+            // fma(0, 0, acc) == acc for every acc the fold can hold (it
+            // starts at +0 and a sum rounds to -0 only from -0 + -0)
+#pragma unroll
+            for (int i = 0; i < kRPT; i++) {
+                const int r = tid / CB + (256 / CB) * i;
+                sd[r][k] = 0.0f;
+#pragma unroll
+                for (int m = 0; m < MX; m++) sdot[m][r][k] = 0.0f;
+            }
+        } else {
             float xr[kQ8Block];
             if constexpr (MX == 1) {
 #pragma unroll
@@ -195,7 +192,8 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const float* __restrict__ 
         if (tid < MX * R) {
             const int m = tid / R, r = tid % R;
             if (m < M && r < nrows) {
-                for (int kk = 0; kk < cb; kk += 8) {
+#pragma unroll
+                for (int kk = 0; kk < CB; kk += 8) {
                     float dv[8], tv[8];
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
@@ -249,21 +247,24 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
                           int K, int act, hipStream_t s) {
     const bool fast = (K % (8 * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
     if (fast) {
-        // one input row: chunks of 32 blocks; 32 rows per workgroup once
-        // that still gives >= 1.5 workgroups per CU, else 16 (measured on
-        // N x 4096 and 65536 x 8192: within 2% of the best of 6 shapes)
-        const bool wide = N >= 12288;
+        // chunks of 32 blocks, 16 rows per workgroup; rows of fewer than 32
+        // blocks (K < 1024) in chunks of 8 blocks, 32 rows per workgroup
+        const int nb = K / kQ8Block;
         const dim3 g16((unsigned)((N + 15) / 16)), g32((unsigned)((N + 31) / 32));
         for (int m0 = 0; m0 < M; m0 += 4) {
             const int mm = min(4, M - m0);
             const float* xg = x + (long)m0 * K;
             float* og = out + (long)m0 * N;
-            if (mm > 1)
+            if (nb < 32) {
+                if (mm > 1)
+                    hipLaunchKernelGGL((q8_gemv_kernel<4, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                else
+                    hipLaunchKernelGGL((q8_gemv_kernel<1, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+            } else if (mm > 1) {
                 hipLaunchKernelGGL((q8_gemv_kernel<4, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
-            else if (wide)
-                hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
-            else
+            } else {
                 hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+            }
         }
     } else {
         const long outs = (long)M * N;

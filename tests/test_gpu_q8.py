@@ -71,7 +71,10 @@ def test_quantize_dequantize_bit_exact():
     assert np.array_equal(H(e.q8_quantize(T(W))), rl.orc_q8_quantize(W))
 
 
-@pytest.mark.parametrize("K", [256, 4096, 96, 800])
+# K = 256 / 768: rows shorter than one 32-block chunk (8-block chunks);
+# 1280: one full chunk plus a last chunk that overlaps it by 24 blocks;
+# 96 / 800: K % 256 != 0 (generic kernel)
+@pytest.mark.parametrize("K", [256, 768, 1280, 4096, 96, 800])
 @pytest.mark.parametrize("M", [1, 3, 4, 7, 16])
 def test_gemv_vs_oracle(K, M):
     e = ext()
