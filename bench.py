@@ -99,6 +99,55 @@ def _events_time(fn, reps, torch, warm_s=0.03, min_timed_s=0.02, dist_calls=20):
     return out
 
 
+# The configs' seeded generator, evaluated on the device: u =
+# (splitmix64(seed * 0xD1B54A32D192ED03 + i) >> 40) * 2^-24; uniform lo +
+# (hi - lo) u; normal by Box-Muller in float64 from the pairs (u_2i, u_2i+1),
+# cast to float32.  The NumPy twin is tests/raclib.py (gen_u01 / gen_uniform
+# / gen_normal): the same uniforms bit for bit; normals agree but for rare
+# last-bit differences of the device's float64 log and cos.  int64 tensor
+# arithmetic wraps like uint64; logical right shifts are masked.
+_M64 = (1 << 64) - 1
+
+
+def _s64(v):
+    v &= _M64
+    return v - (1 << 64) if v >= (1 << 63) else v
+
+
+def _lsr(x, s):
+    return (x >> s) & ((1 << (64 - s)) - 1)
+
+
+def dev_u01(count, seed, dev):
+    import torch
+    x = torch.arange(count, dtype=torch.int64, device=dev) + _s64(seed * 0xD1B54A32D192ED03)
+    x = x + _s64(0x9E3779B97F4A7C15)
+    x = (x ^ _lsr(x, 30)) * _s64(0xBF58476D1CE4E5B9)
+    x = (x ^ _lsr(x, 27)) * _s64(0x94D049BB133111EB)
+    x = x ^ _lsr(x, 31)
+    return _lsr(x, 40).to(torch.float64) * (1.0 / 16777216.0)
+
+
+def dev_uniform(shape, seed, dev, lo=-1.0, hi=1.0):
+    n = 1
+    for d in shape:
+        n *= d
+    return (lo + (hi - lo) * dev_u01(n, seed, dev)).float().reshape(shape)
+
+
+def dev_normal(shape, seed, dev, mean=0.0, std=1.0):
+    import math
+    import torch
+    n = 1
+    for d in shape:
+        n *= d
+    u = dev_u01(2 * n, seed, dev)
+    r = torch.sqrt(-2.0 * torch.log(1.0 - u[0::2]))
+    out = (mean + std * r * torch.cos(2.0 * math.pi * u[1::2])).float().reshape(shape)
+    del u, r
+    return out
+
+
 def _dist_fields(t, scale, unit):
     """p10 / median / p90 of a Timing in `unit` (empty if it has none)."""
     if getattr(t, "p50", None) is None:
@@ -118,8 +167,8 @@ def bench_gpu(args):
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     M = N = K = 4096
-    A = torch.rand((M, K), device=dev, generator=g) * 2 - 1
-    B = torch.rand((K, N), device=dev, generator=g) * 2 - 1
+    A = dev_uniform((M, K), 0, dev)
+    B = dev_uniform((K, N), 1, dev)
     C = torch.empty((M, N), device=dev)
     lib = ext._lib.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -189,8 +238,8 @@ def bench_gpu(args):
     # over PCIe included, reported only)
     import numpy as np
     M1 = 1024
-    A1 = torch.rand((M1, M1), device=dev, generator=g) * 2 - 1
-    B1 = torch.rand((M1, M1), device=dev, generator=g) * 2 - 1
+    A1 = dev_uniform((M1, M1), 0, dev)
+    B1 = dev_uniform((M1, M1), 1, dev)
     C1 = torch.empty((M1, M1), device=dev)
 
     def mm1():
@@ -322,7 +371,7 @@ def bench_row_ops(torch, ext, dev, g):
     reps = 20
     # softmax 4096 x 4096, N(0, std 2); 4 buffer sets (512 MiB) rotate past MALL
     R, Cn = 4096, 4096
-    xs = [torch.randn((R, Cn), device=dev, generator=g) * 2.0 for _ in range(4)]
+    xs = [dev_normal((R, Cn), i, dev, std=2.0) for i in range(4)]
     ys = [torch.empty_like(xs[0]) for _ in range(4)]
     for n in (8, 16, 24):
         state = {"i": 0}
@@ -349,8 +398,8 @@ def bench_row_ops(torch, ext, dev, g):
 
     # RoPE: Q and K [8,32,4096,128] in place (2 GiB moved per step)
     shape = (8, 32, 4096, 128)
-    q = torch.randn(shape, device=dev, generator=g)
-    k = torch.randn(shape, device=dev, generator=g)
+    q = dev_normal(shape, 0, dev)
+    k = dev_normal(shape, 1, dev)
     cos, sin = ext.rope_cache(4096, 128, 10000.0, device=dev)
     Bq, Hq, Tq, Dq = shape
 
@@ -407,9 +456,9 @@ def bench_row_ops(torch, ext, dev, g):
 
     # RMSNorm 16384 x 4096, gamma ~ N(1, 0.02), eps 1e-6; 2 sets (1 GiB)
     R, D = 16384, 4096
-    xr = [torch.randn((R, D), device=dev, generator=g) for _ in range(2)]
+    xr = [dev_normal((R, D), i, dev) for i in range(2)]
     yr = [torch.empty_like(xr[0]) for _ in range(2)]
-    gam = torch.randn(D, device=dev, generator=g) * 0.02 + 1.0
+    gam = dev_normal((D,), 2, dev, mean=1.0, std=0.02)
     st = {"i": 0}
 
     def rms():
@@ -431,7 +480,7 @@ def bench_row_ops(torch, ext, dev, g):
     del xr, yr
 
     # SiLU 16384 x 11008 (n = 16)
-    xsilu = torch.randn((16384, 11008), device=dev, generator=g)
+    xsilu = dev_normal((16384, 11008), 0, dev)
     ysilu = torch.empty_like(xsilu)
 
     def silu():
@@ -467,10 +516,9 @@ def bench_block_ops(torch, ext, dev, g):
     torch.manual_seed(0)
     blk = rt.RACLlamaBlock(4096, 32, ff_dim=11008, max_seq_len=2048).to(dev)
     with torch.no_grad():
-        for prm in blk.parameters():
-            if prm.dim() == 2:
-                prm.normal_(0.0, 0.02, generator=g)
-    xb = torch.randn((1, 2048, 4096), device=dev, generator=g)
+        for i, prm in enumerate(p for p in blk.parameters() if p.dim() == 2):
+            prm.copy_(dev_normal(tuple(prm.shape), 100 + i, dev, std=0.02))
+    xb = dev_normal((1, 2048, 4096), 0, dev)
     prev_mode, prev_iters = rt.rac_get_mode(), rt.rac_get_precision()
     rt.rac_set_mode("cordic")
     try:
@@ -493,7 +541,7 @@ def bench_block_ops(torch, ext, dev, g):
     # attention core of config 5 through RAC (rac_attention_dev): [1, 32, 2048,
     # 128], causal, CORDIC mode n = 16; Q K^T and P V each 17.2 G causal MACs
     Ba, Ha, Ta, Da = 1, 32, 2048, 128
-    qa, ka, va = (torch.randn((Ba, Ha, Ta, Da), device=dev, generator=g) for _ in range(3))
+    qa, ka, va = (dev_normal((Ba, Ha, Ta, Da), i, dev) for i in range(3))
     oa = torch.empty_like(qa)
     wsa = torch.empty(lib.rac_attention_workspace_bytes(Ba, Ha, Ta) // 4, device=dev)
 
@@ -908,7 +956,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (U[-1,1] operands, torch generator seed 0, resident in HBM)",
+        "data": "synthetic, the configs' splitmix64 generator (A U[-1,1] seed 0, B seed 1), resident in HBM",
         "config": {"workload": f"rac_matmul 4096x4096x4096 fp32 CORDIC mode n={args.iters} (NN, row-major)",
                    "M": 4096, "N": 4096, "K": 4096, "cordic_iters": args.iters, "mode": "cordic"},
         "roofline": gpu["roofline"],
