@@ -555,3 +555,24 @@ def test_attention_workspace_sizes(lib):
     a = ctypes.addressof(buf)
     assert lib.rac_attention_ws_dev(a, a, a, None, 1, a, 1, 2, 16, 4, a, 4 * 2 * 16 + 255, 16, 1, None) == -2
     assert b"below" in lib.rac_last_error()
+
+
+def test_every_device_entry_point_refuses_null_buffers(lib):
+    """Every *_dev entry point, called with null buffers and otherwise valid
+    sizes, returns an error code and sets the error text, without touching
+    the device or crashing (no GPU in this container)."""
+    from rac_amd import _lib as L
+    args_for = {L._vp: None, L._i: 4, L._l: 4, L._f: 1.0}
+    checked = 0
+    for name, (res, argtypes) in L._SIGNATURES.items():
+        if not name.endswith("_dev") or res is not L._i:
+            continue
+        lib.rac_clear_error()
+        args = []
+        for t in argtypes:
+            args.append(args_for.get(t, None))
+        rc = getattr(lib, name)(*args)
+        assert rc < 0, name
+        assert lib.rac_last_error() != b"", name
+        checked += 1
+    assert checked >= 30
