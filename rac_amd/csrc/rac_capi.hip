@@ -23,6 +23,8 @@
 #include <atomic>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 #include "rac_internal.hpp"
 #include "rac_tables.hpp"
 
@@ -173,16 +175,106 @@ bool is_device_ptr(const void* p) {
 }  // namespace rac
 static bool is_device_pointer(const void* p) { return is_device_ptr(p); }
 
+// Device staging buffers of the synchronous API come from a per-device
+// cache instead of a hipMalloc / hipFree pair per call (hipFree also waits
+// for the whole device, and a scalar call such as rac_rotate would otherwise
+// pay for up to five of each).  Every synchronous call synchronises its
+// stream before its Staged objects are destroyed, so a buffer is back in the
+// cache only once no work of the call can touch it.  At most
+// kStageCacheBytes stay cached per device; a release beyond that is freed.
+// Buffers cached at process exit are left to the runtime's teardown.
+namespace {
+struct StageCache {
+    std::mutex mu;
+    std::vector<std::pair<void*, size_t>> free_list[64];
+    size_t cached[64] = {};
+};
+StageCache g_stage_cache;
+constexpr size_t kStageCacheBytes = 512ull << 20;
+constexpr size_t kStageGranule = 64u << 10;
+
+void* stage_take(int dev, size_t want, size_t* got) {
+    {
+        std::lock_guard<std::mutex> lock(g_stage_cache.mu);
+        auto& fl = g_stage_cache.free_list[dev];
+        int best = -1;
+        for (int i = 0; i < (int)fl.size(); i++)
+            if (fl[i].second >= want && (best < 0 || fl[i].second < fl[best].second)) best = i;
+        if (best >= 0) {
+            void* p = fl[best].first;
+            *got = fl[best].second;
+            g_stage_cache.cached[dev] -= *got;
+            fl.erase(fl.begin() + best);
+            return p;
+        }
+    }
+    const size_t sz = (want + kStageGranule - 1) / kStageGranule * kStageGranule;
+    void* p = nullptr;
+    if (hipMalloc(&p, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        // out of memory with buffers cached: release them and try once more
+        std::vector<std::pair<void*, size_t>> drop;
+        {
+            std::lock_guard<std::mutex> lock(g_stage_cache.mu);
+            drop.swap(g_stage_cache.free_list[dev]);
+            g_stage_cache.cached[dev] = 0;
+        }
+        if (drop.empty()) return nullptr;
+        for (auto& e : drop) (void)hipFree(e.first);
+        if (hipMalloc(&p, sz) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    *got = sz;
+    return p;
+}
+
+void stage_give(int dev, void* p, size_t sz) {
+    {
+        std::lock_guard<std::mutex> lock(g_stage_cache.mu);
+        if (g_stage_cache.cached[dev] + sz <= kStageCacheBytes) {
+            g_stage_cache.free_list[dev].push_back({p, sz});
+            g_stage_cache.cached[dev] += sz;
+            return;
+        }
+    }
+    (void)hipFree(p);
+}
+}  // namespace
+
 struct Staged {
     void* host = nullptr;     // caller's host pointer (null when device)
     void* dev = nullptr;      // pointer the kernel uses
     size_t bytes = 0;
     bool owned = false;
+    int cache_dev = -1;       // device whose stage cache owns `dev` (-1: plain hipMalloc)
+    size_t cap = 0;
     Staged() = default;
     Staged(const Staged&) = delete;
     Staged& operator=(const Staged&) = delete;
     ~Staged() {
-        if (owned && dev) (void)hipFree(dev);
+        if (!owned || !dev) return;
+        if (cache_dev >= 0) stage_give(cache_dev, dev, cap);
+        else (void)hipFree(dev);
+    }
+    // Device memory of at least nbytes owned by this object.
+    int alloc(size_t nbytes, const char* what) {
+        int d = -1;
+        if (hipGetDevice(&d) != hipSuccess) {
+            (void)hipGetLastError();
+            d = -1;
+        }
+        if (d >= 0 && d < 64) {
+            dev = stage_take(d, nbytes, &cap);
+            if (dev) cache_dev = d;
+        } else if (hipMalloc(&dev, nbytes) != hipSuccess) {
+            (void)hipGetLastError();
+            dev = nullptr;
+        }
+        if (!dev) return fail(RAC_ERR_ALLOC, "%s of %zu bytes failed", what, nbytes);
+        owned = true;
+        return RAC_OK;
     }
     // Make `p` (bytes long) visible to the device; copy host contents in when
     // `copy_in`.
@@ -195,12 +287,8 @@ struct Staged {
         }
         host = const_cast<void*>(p);
         if (nbytes == 0) return RAC_OK;
-        if (hipMalloc(&dev, nbytes) != hipSuccess) {
-            (void)hipGetLastError();
-            dev = nullptr;
-            return fail(RAC_ERR_ALLOC, "device staging allocation of %zu bytes failed", nbytes);
-        }
-        owned = true;
+        const int rc = alloc(nbytes, "device staging allocation");
+        if (rc) return rc;
         if (copy_in)
             return check_hip(hipMemcpyAsync(dev, p, nbytes, hipMemcpyHostToDevice, s), "staging copy in");
         return RAC_OK;
@@ -1242,16 +1330,7 @@ RAC_EXPORT void rac_attention(const float* q, const float* k, const float* v, co
     if (!rc) rc = so.bind(out, xb, false, s);
     const long bh = (long)batch * n_heads;
     const long chunk = attention_chunk_rows(bh, seq, kAttnChunkBudget);
-    if (!rc) {
-        const size_t wb = (size_t)attention_scores_bytes(bh, seq, chunk) + 256;
-        if (hipMalloc(&ws.dev, wb) != hipSuccess) {
-            (void)hipGetLastError();
-            ws.dev = nullptr;
-            rc = fail(RAC_ERR_ALLOC, "rac_attention: score workspace of %zu bytes failed", wb);
-        } else {
-            ws.owned = true;
-        }
-    }
+    if (!rc) rc = ws.alloc((size_t)attention_scores_bytes(bh, seq, chunk) + 256, "rac_attention: score workspace");
     if (!rc) rc = attention_launch(sq.f(), sk.f(), sv.f(), sm.f(), is_causal, so.f(), batch, n_heads, seq,
                                    head_dim, ws.f(), chunk, rac_get_cordic_iters(), rac_get_cordic_mode(), s);
     if (!rc) rc = so.copy_out(s);
