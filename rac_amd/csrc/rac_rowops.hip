@@ -10,9 +10,12 @@
 // the row (from L2 for rows up to a few MB).
 //
 // Arithmetic follows rac_cpu.c:258-271 (softmax), :548-574 (RMSNorm) and
-// :507-546 (LayerNorm) rounding for rounding, except that row sums are
-// reduced as a tree instead of left to right (differences are O(1e-7)
-// relative; every per-element stage is bit-exact with the CPU checker).
+// :507-546 (LayerNorm) rounding for rounding, except the order of the row
+// sums: each lane adds its own values in order (lane l holds the float4
+// groups l, l + 256, ...), lanes combine by a wave64 XOR butterfly (offsets
+// 32 .. 1) and the four wave partials in order, instead of one left-to-right
+// sum (differences O(1e-7) relative).  That order is fixed, so results do
+// not depend on scheduling and a CPU model of it matches bit for bit.
 #include <hip/hip_runtime.h>
 #include "rac_math.hpp"
 #include "rac_internal.hpp"
