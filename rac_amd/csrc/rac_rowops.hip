@@ -11,11 +11,12 @@
 //
 // Arithmetic follows rac_cpu.c:258-271 (softmax), :548-574 (RMSNorm) and
 // :507-546 (LayerNorm) rounding for rounding, except the order of the row
-// sums: each lane adds its own values in order (lane l holds the float4
-// groups l, l + 256, ...), lanes combine by a wave64 XOR butterfly (offsets
-// 32 .. 1) and the four wave partials in order, instead of one left-to-right
-// sum (differences O(1e-7) relative).  That order is fixed, so results do
-// not depend on scheduling and a CPU model of it matches bit for bit.
+// sums: each lane adds its own values in order (the register path's lane l
+// holds the float4 groups l, l + 256, ...; the strided loop's, the elements
+// l, l + 256, ...), lanes combine by a wave64 XOR butterfly (offsets 32 ..
+// 1) and the four wave partials in order, instead of one left-to-right sum
+// (differences O(1e-7) relative).  That order is fixed, so results do not
+// depend on scheduling and a CPU model of it matches bit for bit.
 #include <hip/hip_runtime.h>
 #include "rac_math.hpp"
 #include "rac_internal.hpp"
