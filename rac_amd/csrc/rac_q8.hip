@@ -65,10 +65,12 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
 // math.  Up to 4 input rows (batched decode) share one pass over the
 // weights.  The shape only decides which lane computes what; every output
 // is the same serial fold, so all shapes give identical bits.
+// One input row asks for 4 workgroups per CU (at most 128 VGPRs; the
+// kernel needs 119), several rows for 2.
 constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
 
 template <int MX, int CB, int R>
-__global__ __launch_bounds__(256, 4) void q8_gemv_kernel(const float* __restrict__ x,
+__global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const float* __restrict__ x,
                                                       const uint8_t* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ out, int M, int N, int K,
