@@ -196,6 +196,18 @@ int rac_attention_probs_dev(const float *q, const float *k, const float *v, cons
                             int is_causal, float *out, int batch, int n_heads, int seq, int head_dim,
                             float *workspace, int iters, int mode, void *stream);
 
+/* The probabilities of query rows row0 .. row0+rows-1 of every head into P
+ * [batch*n_heads, rows, seq], equal bit for bit to those rows of the P that
+ * rac_attention_probs_dev leaves in its workspace (the attention core's
+ * scores and masked CORDIC softmax, rac_cpu.c:651-690).  For a backward
+ * pass that recomputes P one chunk of query rows at a time instead of
+ * keeping the [batch*n_heads, seq, seq] matrix (what the reference's
+ * autograd of its composition keeps, rac_torch.py:1327-1337).  Same
+ * argument checks as rac_attention_dev, plus 0 <= row0 < row0 + rows <= seq. */
+int rac_attention_probs_rows_dev(const float *q, const float *k, const float *mask, int is_causal,
+                                 float *P, int batch, int n_heads, int seq, int head_dim, int row0,
+                                 int rows, int iters, int mode, void *stream);
+
 /* ── reference launcher ABI (rac_kernels.hip:822-909; bound by
  *    rac_torch_bind.cpp:16-45 with the stream as void*) ──────────────────── */
 

@@ -90,6 +90,7 @@ _SIGNATURES = {
     "rac_attention_noalloc_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "rac_attention_ws_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _l, _i, _i, _vp]),
     "rac_attention_probs_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
+    "rac_attention_probs_rows_dev": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "rac_q8_0_gemv_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rac_q8_0_quantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_q8_0_dequantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),

@@ -638,12 +638,43 @@ RAC_EXPORT long rac_attention_probs_workspace_bytes(int batch, int n_heads, int 
 // scores = (Q K^T) / sqrt(D) by the RAC matmul (batched over b*h), masked
 // row softmax with CORDIC exp in place, out = P V by the RAC matmul; over
 // query chunks of `chunk` rows (see above).
+// Probabilities of query rows t0 .. t0+c-1 of every head into P [bh, c, t]
+// (scores, then the masked softmax in place).  Each score is one
+// accumulator over d in order and each softmax row the full row, so P does
+// not depend on the chunk: these are rows t0.. of the one-chunk P, bit for
+// bit.
+static int attention_probs_chunk(const float* q, const float* k, const float* mask, int causal, float* P,
+                                 int bh, int t, int d, long t0, int c, int iters, int mode, hipStream_t s) {
+    const long td = (long)t * d;
+    const float scale = 1.0f / sqrtf((float)d);
+    // causal: score tiles wholly above the diagonal are masked by the
+    // softmax regardless of their contents, so the scores GEMM schedules
+    // only the tiles on or below it (the whole sequence: the square
+    // triangular schedule; a chunk: its trapezoid).  The product keeps the
+    // strength-reduced rotation chain for every input (exact_specials off):
+    // the attention's parity bar is the row-sum bound, and peaked softmax
+    // rows are full of probabilities below 2^-105, which would otherwise
+    // send most P V tiles through the literal-chain recompute.
+    const int ssched = !causal ? 0 : ((c == t && t0 == 0) ? 1 : 3);
+    int rc = check_hip(gemm_launch(0, 1, q + t0 * d, k, P, c, t, d, scale, 0.0f, iters, mode, s, bh, td, td,
+                                   (long)c * t, ssched, nullptr, false, (int)t0),
+                       "rac_attention scores launch");
+    if (rc) return rc;
+    SoftmaxMask mk;
+    mk.mask = mask;
+    mk.causal = causal != 0;
+    mk.seq = c;
+    mk.row0 = t0;
+    mk.mask_ld = t;
+    mk.zero_guard = 1;
+    return check_hip(softmax_launch(P, P, (long)bh * c, t, iters, s, mk), "rac_attention softmax launch");
+}
+
 static int attention_launch(const float* q, const float* k, const float* v, const float* mask, int causal,
                             float* out, int b, int h, int t, int d, float* ws, long chunk, int iters, int mode,
                             hipStream_t s) {
     const int bh = b * h;
     const long td = (long)t * d;
-    const float scale = 1.0f / sqrtf((float)d);
     // causal: P is exactly 0 above the diagonal, so P V may stop each row
     // tile's K loop at its last query position -- when V is finite (0 * inf
     // is NaN); the flag lives in the workspace tail, evaluated on the device
@@ -657,27 +688,7 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
     for (long t0 = 0; t0 < t; t0 += chunk) {
         const int c = (int)(chunk < t - t0 ? chunk : t - t0);
         const long ct = (long)c * t;
-        // causal: score tiles wholly above the diagonal are masked by the
-        // softmax regardless of their contents, so the scores GEMM schedules
-        // only the tiles on or below it (one chunk: the square triangular
-        // schedule; several: each chunk's trapezoid).  Both products keep
-        // the strength-reduced rotation chain for every input (exact_specials
-        // off): the attention's parity bar is the row-sum bound, and peaked
-        // softmax rows are full of probabilities below 2^-105, which would
-        // otherwise send most P V tiles through the literal-chain recompute.
-        const int ssched = !causal ? 0 : (c == t ? 1 : 3);
-        rc = check_hip(gemm_launch(0, 1, q + t0 * d, k, ws, c, t, d, scale, 0.0f, iters, mode, s, bh, td, td, ct,
-                                   ssched, nullptr, false, (int)t0),
-                       "rac_attention scores launch");
-        if (rc) return rc;
-        SoftmaxMask mk;
-        mk.mask = mask;
-        mk.causal = causal != 0;
-        mk.seq = c;
-        mk.row0 = t0;
-        mk.mask_ld = t;
-        mk.zero_guard = 1;
-        rc = check_hip(softmax_launch(ws, ws, (long)bh * c, t, iters, s, mk), "rac_attention softmax launch");
+        rc = attention_probs_chunk(q, k, mask, causal, ws, bh, t, d, t0, c, iters, mode, s);
         if (rc) return rc;
         const int psched = (causal && c == t) ? 2 : 0;
         rc = check_hip(gemm_launch(0, 0, ws, v, out + t0 * d, c, d, t, 1.0f, 0.0f, iters, mode, s, bh, ct, td, td,
@@ -801,6 +812,23 @@ RAC_EXPORT int rac_attention_probs_dev(const float* q, const float* k, const flo
     if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_probs_dev: mode must be 0, 1 or 2");
     return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, workspace, seq,
                             clamp_iters(iters), mode, (hipStream_t)stream);
+}
+
+// The probabilities of query rows row0 .. row0+rows-1 of every head,
+// P [batch*n_heads, rows, seq], equal to those rows of rac_attention_probs_dev's
+// P: for a backward pass that recomputes P a chunk at a time instead of
+// keeping the [batch*n_heads, seq, seq] matrix.
+RAC_EXPORT int rac_attention_probs_rows_dev(const float* q, const float* k, const float* mask, int is_causal,
+                                            float* P, int batch, int n_heads, int seq, int head_dim, int row0,
+                                            int rows, int iters, int mode, void* stream) {
+    int rc = check_attention(q, k, k, P, batch, n_heads, seq, head_dim);
+    if (rc) return rc;
+    if (mode < 0 || mode > 2) return fail(RAC_ERR_INVALID_DIM, "rac_attention_probs_rows_dev: mode must be 0, 1 or 2");
+    if (row0 < 0 || rows <= 0 || (long)row0 + rows > seq)
+        return fail(RAC_ERR_INVALID_DIM, "rac_attention_probs_rows_dev: rows %d .. %ld outside 0 .. %d", row0,
+                    (long)row0 + rows - 1, seq - 1);
+    return attention_probs_chunk(q, k, mask, is_causal, P, batch * n_heads, seq, head_dim, row0, rows,
+                                 clamp_iters(iters), mode, (hipStream_t)stream);
 }
 
 // ── Q8_0 weights and decode GEMV (lib/c/rac_q8_0.h) ─────────────────────

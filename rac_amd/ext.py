@@ -519,11 +519,14 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 # ── batched products and attention ───────────────────────────────────────
 
 def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool = False,
-        alpha: float = 1.0, iters: int = 0, mode: int = -1) -> torch.Tensor:
-    """C[z] = alpha * op(A[z]) @ op(B[z]) for 3-D contiguous fp32 tensors, one
-    launch over the batch (grid z).  op(A[z]) = A[z] [M, K], or A[z]^T with
-    A stored [Z, K, M] when trans_a; op(B[z]) = B[z] [K, N], or B[z]^T with B
-    stored [Z, N, K] when trans_b."""
+        alpha: float = 1.0, iters: int = 0, mode: int = -1, out: Optional[torch.Tensor] = None,
+        beta: float = 0.0) -> torch.Tensor:
+    """C[z] = alpha * op(A[z]) @ op(B[z]) (+ beta * C[z]) for 3-D contiguous
+    fp32 tensors, one launch over the batch (grid z).  op(A[z]) = A[z]
+    [M, K], or A[z]^T with A stored [Z, K, M] when trans_a; op(B[z]) = B[z]
+    [K, N], or B[z]^T with B stored [Z, N, K] when trans_b.  With `out`
+    (a contiguous fp32 [Z, M, N] tensor) the result is written there, and
+    beta != 0 accumulates into its contents: fma(alpha, acc, beta * C)."""
     _require_f32(A, "A")
     _require_f32(B, "B")
     if A.dim() != 3 or B.dim() != 3 or A.size(0) != B.size(0):
@@ -535,17 +538,25 @@ def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool =
     Kb, N = (B.size(2), B.size(1)) if trans_b else (B.size(1), B.size(2))
     if K != Kb:
         raise RuntimeError("RAC: dimension mismatch")
-    C = torch.empty((Z, M, N), device=A.device, dtype=torch.float32)
+    if out is not None:
+        _require_f32(out, "out")
+        if tuple(out.shape) != (Z, M, N) or not out.is_contiguous():
+            raise RuntimeError("RAC: bmm out must be a contiguous [Z, M, N] tensor")
+        C = out
+    else:
+        if beta != 0.0:
+            raise RuntimeError("RAC: bmm beta needs an out tensor to accumulate into")
+        C = torch.empty((Z, M, N), device=A.device, dtype=torch.float32)
     if C.numel() == 0:
         return C
     if K == 0:
-        return C.zero_()
+        return C.mul_(beta) if beta != 0.0 else C.zero_()
     iters, mode = _resolve(iters, mode)
     lib = _lib.load()
     for z0 in range(0, Z, 65535):
         zb = min(65535, Z - z0)
         check(lib.rac_gemm_batched_dev(A[z0].data_ptr(), B[z0].data_ptr(), C[z0].data_ptr(), M, N, K,
-                                       int(trans_a), int(trans_b), float(alpha), 0.0, iters, mode, zb,
+                                       int(trans_a), int(trans_b), float(alpha), float(beta), iters, mode, zb,
                                        A.stride(0), B.stride(0), C.stride(0), _stream(C)),
               "rac_gemm_batched_dev")
     return C
@@ -619,6 +630,35 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
                                 out.data_ptr(), B, H, T, D, ws.data_ptr(), iters, mode, _stream(out)),
           "rac_attention_dev")
     return out
+
+
+def attention_probs_rows(q: torch.Tensor, k: torch.Tensor, mask: Optional[torch.Tensor], is_causal: bool,
+                         row0: int, rows: int, iters: int = 0, mode: int = -1) -> torch.Tensor:
+    """The attention probabilities of query rows row0 .. row0+rows-1 of every
+    head, [B, H, rows, T], through rac_attention_probs_rows_dev: bit for bit
+    those rows of the P that attention(..., return_probs=True) returns."""
+    for t, n in ((q, "q"), (k, "k")):
+        _require_f32(t, n)
+        if t.dim() != 4:
+            raise RuntimeError("RAC: attention expects [batch, heads, seq, head_dim]")
+    if q.shape != k.shape:
+        raise RuntimeError("RAC: q and k must have the same shape")
+    B, H, T, D = q.shape
+    q, k = q.contiguous(), k.contiguous()
+    iters, mode = _resolve(iters, mode)
+    mptr = None
+    if mask is not None:
+        _require_f32(mask, "mask")
+        if tuple(mask.shape) != (T, T):
+            raise RuntimeError("RAC: attention mask must be [T, T]")
+        mask = mask.contiguous()
+        mptr = mask.data_ptr()
+    P = torch.empty((B, H, rows, T), device=q.device, dtype=torch.float32)
+    check(_lib.load().rac_attention_probs_rows_dev(q.data_ptr(), k.data_ptr(), mptr, int(bool(is_causal)),
+                                                   P.data_ptr(), B, H, T, D, int(row0), int(rows), iters, mode,
+                                                   _stream(P)),
+          "rac_attention_probs_rows_dev")
+    return P
 
 
 # ── vector primitives (rac.h:101-250) ───────────────────────────────────────
@@ -892,7 +932,7 @@ __all__ = [
     "matmul_forward", "matmul_backward", "linear_forward", "linear_backward",
     "softmax", "rmsnorm", "layernorm", "exp", "silu", "sigmoid", "tanh", "gelu", "relu",
     "rsqrt", "sincos", "rope_inv_freq", "rope_cache", "rope_apply_", "rope_apply",
-    "bmm", "softmax_masked_", "attention", "vec2", "inner", "outer", "dct", "VEC2_OPS",
+    "bmm", "softmax_masked_", "attention", "attention_probs_rows", "vec2", "inner", "outer", "dct", "VEC2_OPS",
     "fused_linear_forward", "fused_linear_backward", "act_grad", "attention_scale",
     "q8_quantize", "q8_dequantize", "q8_gemv", "Q8_BLOCK_BYTES",
     "dsp_eval", "dsp_systolic", "DSP_OPS", "SafeTensors",

@@ -728,12 +728,24 @@ def rac_bmm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     return out.view(*lead, A.shape[-2], B.shape[-1])
 
 
+# Above this many bytes of probabilities ([B, H, T, T] fp32) the attention
+# backward recomputes P one chunk of query rows at a time instead of keeping
+# it from the forward pass (RAC_ATTN_KEEP_PROBS_BYTES overrides).
+_ATTN_KEEP_PROBS_BYTES = int(os.environ.get('RAC_ATTN_KEEP_PROBS_BYTES', str(1 << 30)))
+# Bytes of one [B*H, chunk, T] buffer in that recomputing backward.
+_ATTN_BWD_CHUNK_BYTES = 128 << 20
+
+
 class RACAttentionFunction(Function):
     """Scaled dot-product attention through RAC (rac.h:323-335): Q K^T and
     P V on the CORDIC matmul, causal / [T, T] additive mask and softmax on
     the CORDIC-exp kernel.  Backward (standard softmax-attention gradients,
     every product on the RAC matmul): dV = P^T dO, dP = dO V^T,
-    dS = P (dP - rowsum(dP P)), dQ = s dS K, dK = s dS^T Q."""
+    dS = P (dP - rowsum(dP P)), dQ = s dS K, dK = s dS^T Q.  Up to
+    _ATTN_KEEP_PROBS_BYTES of P are kept from the forward pass; beyond that
+    the forward keeps none and the backward recomputes P a chunk of query
+    rows at a time (the same probabilities, bit for bit), accumulating dV
+    and dK over the chunks: memory O(B H chunk T) instead of O(B H T^2)."""
 
     @staticmethod
     def forward(ctx, q, k, v, mask, is_causal):
@@ -744,23 +756,51 @@ class RACAttentionFunction(Function):
             # no backward: the core runs over query-row chunks and keeps no
             # [B, H, T, T] probabilities (same output bits)
             return _rac.attention(q32, k32, v32, m32, bool(is_causal), **_kw()).to(q.dtype)
-        out, P = _rac.attention(q32, k32, v32, m32, bool(is_causal), return_probs=True, **_kw())
-        ctx.save_for_backward(q32, k32, v32, P)
+        B, H, T, _ = q32.shape
+        ctx.is_causal = bool(is_causal)
+        if 4 * B * H * T * T <= _ATTN_KEEP_PROBS_BYTES:
+            out, P = _rac.attention(q32, k32, v32, m32, bool(is_causal), return_probs=True, **_kw())
+            ctx.save_for_backward(q32, k32, v32, m32, P)
+        else:
+            out = _rac.attention(q32, k32, v32, m32, bool(is_causal), **_kw())
+            ctx.save_for_backward(q32, k32, v32, m32, None)
         return out.to(q.dtype)
 
     @staticmethod
     def backward(ctx, g):
-        q, k, v, P = ctx.saved_tensors
+        q, k, v, m, P = ctx.saved_tensors
         B, H, T, D = q.shape
         Z = B * H
         scale = _rac.attention_scale(D)
+        need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         g3 = g.float().contiguous().view(Z, T, D)
-        q3, k3, v3, P3 = q.view(Z, T, D), k.view(Z, T, D), v.view(Z, T, D), P.view(Z, T, T)
-        dV = _rac.bmm(P3, g3, trans_a=True, **_kw())
-        dP = _rac.bmm(g3, v3, trans_b=True, **_kw())
-        dS = P3 * (dP - (dP * P3).sum(-1, keepdim=True))
-        dQ = _rac.bmm(dS, k3, alpha=scale, **_kw()) if ctx.needs_input_grad[0] else None
-        dK = _rac.bmm(dS, q3, trans_a=True, alpha=scale, **_kw()) if ctx.needs_input_grad[1] else None
+        q3, k3, v3 = q.view(Z, T, D), k.view(Z, T, D), v.view(Z, T, D)
+        if P is not None:
+            P3 = P.view(Z, T, T)
+            dV = _rac.bmm(P3, g3, trans_a=True, **_kw())
+            dP = _rac.bmm(g3, v3, trans_b=True, **_kw())
+            dS = P3 * (dP - (dP * P3).sum(-1, keepdim=True))
+            dQ = _rac.bmm(dS, k3, alpha=scale, **_kw()) if need_q else None
+            dK = _rac.bmm(dS, q3, trans_a=True, alpha=scale, **_kw()) if need_k else None
+        else:
+            rows = _ATTN_BWD_CHUNK_BYTES // (4 * Z * T)
+            rows = T if rows >= T else max(64, rows // 64 * 64)
+            dV = torch.zeros((Z, T, D), device=q.device, dtype=torch.float32)
+            dQ = torch.empty((Z, T, D), device=q.device, dtype=torch.float32) if need_q else None
+            dK = torch.zeros((Z, T, D), device=q.device, dtype=torch.float32) if need_k else None
+            for t0 in range(0, T, rows):
+                r = min(rows, T - t0)
+                Pc = _rac.attention_probs_rows(q, k, m, ctx.is_causal, t0, r, **_kw()).view(Z, r, T)
+                gc = g3[:, t0:t0 + r].contiguous()
+                _rac.bmm(Pc, gc, trans_a=True, out=dV, beta=1.0, **_kw())
+                dP = _rac.bmm(gc, v3, trans_b=True, **_kw())
+                dS = Pc * (dP - (dP * Pc).sum(-1, keepdim=True))
+                del dP, Pc
+                if need_q:
+                    dQ[:, t0:t0 + r] = _rac.bmm(dS, k3, alpha=scale, **_kw())
+                if need_k:
+                    _rac.bmm(dS, q3[:, t0:t0 + r].contiguous(), trans_a=True, alpha=scale, out=dK, beta=1.0,
+                             **_kw())
         shape = (B, H, T, D)
         return (dQ.view(shape) if dQ is not None else None, dK.view(shape) if dK is not None else None,
                 dV.view(shape), None, None)

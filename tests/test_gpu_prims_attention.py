@@ -454,3 +454,62 @@ def test_attention_config5_default_chunks_equal_one_chunk():
     for h in (0, 31):
         sl = (slice(0, 1), slice(h, h + 1))
         assert np.array_equal(got[sl], rl.orc_attention_lanes(q[sl], k[sl], v[sl], None, True, 16, 1)), h
+
+
+@pytest.mark.parametrize("causal,masked", [(True, False), (False, True), (True, True), (False, False)])
+def test_attention_probs_rows_equal_one_chunk_rows(causal, masked):
+    """rac_attention_probs_rows_dev: any block of query rows equals those rows
+    of the one-chunk probabilities bit for bit (the rows the recomputing
+    backward uses); out-of-range rows are refused."""
+    e = ext()
+    shape = (2, 3, 200, 32)
+    q, k, v = _qkv(shape, seed=1200)
+    mask = (rl.gen_normal((200, 200), seed=1201) * np.float32(0.5)).astype(np.float32) if masked else None
+    mt = T(mask) if masked else None
+    _, P = e.attention(T(q), T(k), T(v), mt, causal, iters=16, mode=1, return_probs=True)
+    P = H(P)
+    for row0, rows in ((0, 200), (0, 1), (7, 64), (64, 130), (199, 1), (150, 50)):
+        print(f"probs rows causal={causal} masked={masked} rows {row0}+{rows}", flush=True)
+        got = H(e.attention_probs_rows(T(q), T(k), mt, causal, row0, rows, iters=16, mode=1))
+        assert np.array_equal(got, P[:, :, row0:row0 + rows], equal_nan=True), (row0, rows)
+    with pytest.raises(Exception):
+        e.attention_probs_rows(T(q), T(k), mt, causal, 150, 51, iters=16, mode=1)
+
+
+@pytest.mark.parametrize("keep_bytes_all_rows", [False, True])
+def test_attention_backward_recomputing_probs(keep_bytes_all_rows):
+    """The backward that keeps no [B, H, T, T] probabilities (recomputed one
+    chunk of query rows at a time): dQ bit-identical to the backward that
+    keeps P; dK and dV accumulate over the chunks, so within the fp32
+    summation bound of it (identical when one chunk holds every row)."""
+    from rac_amd import rac_torch as rt
+    old = (rt.rac_get_precision(), rt.rac_get_mode(), rt._ATTN_KEEP_PROBS_BYTES, rt._ATTN_BWD_CHUNK_BYTES)
+    try:
+        rt.rac_set_precision(16)
+        rt.rac_set_mode("cordic")
+        shape = (2, 3, 200, 32)
+        q, k, v = _qkv(shape, seed=1300)
+        mask = (rl.gen_normal((200, 200), seed=1301) * np.float32(0.3)).astype(np.float32)
+        g = rl.gen_normal(shape, seed=1302)
+        grads = {}
+        for keep in (True, False):
+            rt._ATTN_KEEP_PROBS_BYTES = 1 << 40 if keep else 0
+            # chunks of 64 query rows (4 chunks of 200), or one chunk of all
+            rt._ATTN_BWD_CHUNK_BYTES = (1 << 40) if keep_bytes_all_rows else 4 * 6 * 64 * 200
+            qt, kt, vt = (T(x).requires_grad_(True) for x in (q, k, v))
+            out = rt.rac_attention(qt, kt, vt, T(mask), True)
+            out.backward(T(g))
+            grads[keep] = (H(out), H(qt.grad), H(kt.grad), H(vt.grad))
+        assert np.array_equal(grads[True][0], grads[False][0])
+        assert np.array_equal(grads[True][1], grads[False][1])          # dQ: rows complete per chunk
+        for i in (2, 3):
+            a, b = grads[True][i], grads[False][i]
+            if keep_bytes_all_rows:
+                assert np.array_equal(a, b)
+            else:
+                bound = 200 * 2.0 ** -23 * float(np.abs(a).max())      # summation split over 4 chunks
+                assert float(np.abs(a - b).max()) <= bound, i
+    finally:
+        rt.rac_set_precision(old[0])
+        rt.rac_set_mode(old[1])
+        rt._ATTN_KEEP_PROBS_BYTES, rt._ATTN_BWD_CHUNK_BYTES = old[2], old[3]
