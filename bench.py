@@ -493,6 +493,51 @@ def bench_row_ops(torch, ext, dev, g):
     return out
 
 
+def bench_q8_ops(torch, ext, dev, g):
+    """Q8_0 decode GEMV (M = 1) at 11008x4096, 32000x4096 and 65536x8192."""
+    lib = ext._lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    reps = 20
+
+    def chk(rc):
+        if rc:
+            raise RuntimeError(lib.rac_last_error())
+
+    def record(name, nbytes, t):
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / PEAK_HBM_GBPS, 4),
+                     **_dist_fields(t, 1e6, "us")}
+        print(f"# {name}: {t * 1e6:.1f} us, {nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+
+    # Q8_0 decode GEMV (M = 1): weight bytes N*K/32*34 streamed once; buffer
+    # sets rotate past the MALL
+    for (Nq, Kq) in ((11008, 4096), (32000, 4096), (65536, 8192)):
+        wbytes = Nq * (Kq // 32) * 34
+        nsets = max(2, -(-600_000_000 // wbytes))
+        wsets = []
+        for _ in range(nsets):
+            wq = torch.randint(0, 256, (Nq, Kq // 32, 34), device=dev, dtype=torch.uint8, generator=g)
+            wq[:, :, 0] = 0x00
+            wq[:, :, 1] = 0x20          # block scale 2^-7 (fp16 0x2000)
+            wsets.append(wq)
+        xq = torch.randn((1, Kq), device=dev, generator=g)
+        yq = torch.empty((1, Nq), device=dev)
+        stq = {"i": 0}
+
+        def q8():
+            i = stq["i"] = (stq["i"] + 1) % nsets
+            chk(lib.rac_q8_0_gemv_dev(xq.data_ptr(), wsets[i].data_ptr(), None, yq.data_ptr(), 1, Nq, Kq, 0,
+                                      stream))
+
+        q8()
+        torch.cuda.synchronize()
+        record(f"q8_0_gemv_{Nq}x{Kq}", wbytes + 4 * (Kq + Nq), _events_time(q8, reps, torch))
+        del wsets
+
+    return out
+
+
 def bench_block_ops(torch, ext, dev, g):
     """Llama block, attention core, Q8_0 GEMV, RAC-DSP and the safetensors loader."""
     lib = ext._lib.load()
@@ -588,30 +633,7 @@ def bench_block_ops(torch, ext, dev, g):
         print(f"# {name}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
     del qa, ka, va, oa, wsp
 
-    # Q8_0 decode GEMV (M = 1): weight bytes N*K/32*34 streamed once; buffer
-    # sets rotate past the MALL
-    for (Nq, Kq) in ((11008, 4096), (32000, 4096), (65536, 8192)):
-        wbytes = Nq * (Kq // 32) * 34
-        nsets = max(2, -(-600_000_000 // wbytes))
-        wsets = []
-        for _ in range(nsets):
-            wq = torch.randint(0, 256, (Nq, Kq // 32, 34), device=dev, dtype=torch.uint8, generator=g)
-            wq[:, :, 0] = 0x00
-            wq[:, :, 1] = 0x20          # block scale 2^-7 (fp16 0x2000)
-            wsets.append(wq)
-        xq = torch.randn((1, Kq), device=dev, generator=g)
-        yq = torch.empty((1, Nq), device=dev)
-        stq = {"i": 0}
-
-        def q8():
-            i = stq["i"] = (stq["i"] + 1) % nsets
-            chk(lib.rac_q8_0_gemv_dev(xq.data_ptr(), wsets[i].data_ptr(), None, yq.data_ptr(), 1, Nq, Kq, 0,
-                                      stream))
-
-        q8()
-        torch.cuda.synchronize()
-        record(f"q8_0_gemv_{Nq}x{Kq}", wbytes + 4 * (Kq + Nq), _events_time(q8, reps, torch))
-        del wsets
+    out.update(bench_q8_ops(torch, ext, dev, g))
 
     # RAC-DSP fixed-point engine (Q32.32 / Q0.63 int64): 2^24 evaluations of
     # rotate (x, y, z in and out: 48 B each) and of project (x, z in, x out:
@@ -908,6 +930,8 @@ def main():
     ap.add_argument("--rowops-only", action="store_true",
                     help="only time softmax, RoPE, RMSNorm and SiLU and print their figures "
                          "(a short run for rocprofv3 --pmc passes; not the benchmark line)")
+    ap.add_argument("--q8-only", action="store_true",
+                    help="only time the Q8_0 decode GEMV shapes (a short run for rocprofv3 --pmc passes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device-to-device tensor copy 3 times (scales the "
                          "FETCH_SIZE/WRITE_SIZE counters of rocprofv3 --pmc runs)")
@@ -932,6 +956,16 @@ def main():
               "build's hot path is single-GPU (every op would shard by rows or output columns with at most one all-reduce per block).", file=sys.stderr)
         sys.exit(2)
 
+    if args.q8_only:
+        import torch
+        sys.path.insert(0, ROOT)
+        from rac_amd import ext
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        print(json.dumps({"ops": bench_q8_ops(torch, ext, dev, g)}), flush=True)
+        return
     if args.rowops_only:
         import torch
         sys.path.insert(0, ROOT)
