@@ -240,13 +240,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             __syncthreads();
             if (k0 + BK < kend) load_tile(k0 + BK);   // prefetch overlaps the MACs
             // CORDIC steps are long VALU chains and stay rolled in the plain
-            // 4x4 schedule; the 2x2 register tile (4 rotations per k-step,
+            // 4x4 schedules; the 2x2 register tile (4 rotations per k-step,
             // too few independent chains to cover each step's LDS reads)
-            // and the causal attention schedules take two k-steps per trip
-            // (measured: 1024^3 0.616 -> 0.542 ms, the attention core with P
-            // kept 9.75 -> 9.36 ms; the 4096^3 NN launch 1% slower, so it
-            // keeps one).  The accumulation order is unchanged.
-            constexpr int KU = (MODE == kModeFast) ? kFastKUnroll : ((TM * TN <= 4 || SCHED != 0) ? 2 : 1);
+            // and the square causal attention schedules take two k-steps
+            // per trip (measured: 1024^3 0.616 -> 0.542 ms, the attention
+            // core with P kept 9.75 -> 9.36 ms; the 4096^3 NN launch 1%
+            // slower, so it keeps one).  The accumulation order is unchanged.
+            constexpr int KU = (MODE == kModeFast) ? kFastKUnroll : ((TM * TN <= 4 || SCHED == 1 || SCHED == 2) ? 2 : 1);
 #pragma unroll 1
             for (int kb = 0; kb < BK; kb += KU)
 #pragma unroll
