@@ -218,7 +218,8 @@ def bench_gpu(args):
         print(f"# matmul n={nn}: {t * 1e3:.2f} ms", file=sys.stderr, flush=True)
 
     # FAST mode (the rac_torch default, rac_kernels.hip:55-62): the plain
-    # fmaf(a, b, acc) MAC, 2 FLOP per MAC against the same FP32 VALU peak
+    # fmaf(a, b, acc) MAC, 2 FLOP per MAC; at this size it runs on the FP32
+    # matrix cores (one fused MAC per k), whose dense peak equals the VALU's
     def mmf():
         rc = lib.rac_gemm_dev(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 0, 0, 1.0, 0.0,
                               24, ext.MODE_FAST, stream)

@@ -1,4 +1,5 @@
-// rac_gemm.hip — rotate-project-accumulate GEMM for gfx950 (VALU, no MFMA).
+// rac_gemm.hip — rotate-project-accumulate GEMM for gfx950 (VALU; FAST mode
+// on the FP32 matrix cores where the launch is large enough).
 //
 // C[M,N] = alpha * op(A) @ op(B) (+ beta * C), row-major, with the MAC of
 // rac_fma_iters (rac_kernels.hip:204-219):
@@ -18,13 +19,14 @@
 // with BK = 16 keeps 16 independent MAC chains per lane for latency hiding
 // and reads only 2 ds_read_b128 per 16 MACs; the rotations of those MACs
 // advance step-major, so independent FMA chains interleave in each wave's
-// instruction stream.  FAST mode (1 FMA per MAC) uses a 128x128 tile with
-// 8x8 per lane (split in 4x4 groups 64 apart, conflict-free LDS reads), the
-// k loop unrolled by 2; at 16 LDS floats per 64 FMAs it is bound by LDS
-// bandwidth (128 B/clk/CU) as much as by the FMA rate.  Launches with
-// fewer than 1024 block tiles step down to 64x64, then 32x32 (2x2 per lane)
-// so every SIMD holds several waves.  The next K-tile is prefetched into
-// registers while the current one is computed.
+// instruction stream.  FAST mode (1 FMA per MAC) runs on the matrix cores
+// (gemm_mfma_fast_kernel, below) when its 128x128 tiles fill the CUs and
+// K >= 128; otherwise on VALU tiles of 8x8 or 16x8 per lane (8x8 split in
+// 4x4 groups 64 apart, conflict-free LDS reads), the k loop unrolled by 2,
+// bound by LDS bandwidth (128 B/clk/CU) as much as by the FMA rate.
+// Launches with fewer than 1024 block tiles step down to 64x64, then 32x32
+// (2x2 per lane) so every SIMD holds several waves.  The next K-tile is
+// prefetched into registers while the current one is computed.
 #include <hip/hip_runtime.h>
 #include <atomic>
 #include "rac_act.hpp"
@@ -377,6 +379,179 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     }   // pass
 }
 
+// ── FAST mode on the matrix cores ───────────────────────────────────────
+//
+// v_mfma_f32_32x32x1_2b_f32 adds one product to each of its 2 x 32 x 32
+// accumulators: D = A_i * B_j + C_ij with a single IEEE rounding, denormals
+// kept — the same value as fmaf(a, b, acc) (checked on gfx950 over 8.4 M
+// random, subnormal, special and exactly cancelling operands, 0 differences,
+// where a separately rounded multiply and add differ in 37%).  Issued once
+// per k in k order, it therefore gives every output the FAST MAC's
+// accumulation chain bit for bit, at 2048 MACs per instruction for 3 LDS
+// floats per lane and k, where the VALU form is bound by LDS bandwidth
+// (4096^3: 1.09-1.15 ms against 1.48-1.53 ms on the 16x8 VALU tile).
+//
+// Block tile 128 x 128, BK = 32, staged global -> registers -> LDS with the
+// next K-tile's loads in flight during the current one's MFMAs; 4
+// waves in 2 x 2, each owning 64 x 64 outputs as two instructions per k:
+// lane l supplies A row l of the wave tile (lanes 0-31 feed the instruction's
+// block 0, lanes 32-63 its block 1) and B column l % 32 of the half (both
+// blocks read the same 32 columns), so block b covers rows 32 b .. 32 b + 31.
+// Accumulator register r of lane l holds block r / 16, row
+// ((r % 16) / 4) * 8 + (l / 32) * 4 + r % 4 of that block, column l % 32.
+typedef float v32f __attribute__((ext_vector_type(32)));
+constexpr int kMfBM = 128, kMfBN = 128, kMfBK = 32, kMfMinK = 128;
+
+// One operand's K-tile (32 k x 128 rows) in LDS.  An operand stored with k
+// contiguous in memory (A, or B^T of the NT layout) is kept as [row][k]
+// rows of 36 floats, so a lane reads 4 consecutive k of its row in one
+// ds_read_b128 (rows 144 B apart: 16 lanes cover all 64 banks); the other
+// layout stays [k][row] (rows of 132 floats) and is read one k at a time.
+template <bool KC>
+struct MfTile {
+    static constexpr int kRows = KC ? 128 : kMfBK;
+    static constexpr int kCols = KC ? kMfBK + 4 : 128 + 4;
+};
+
+// Global -> registers: 4 float4 per lane covering the 32 x 128 tile at k0
+// (rows r0..r0+127 of an operand with `rows` rows, leading dimension ld),
+// zero outside the matrix.  k-contiguous: lanes 8 apart share a row, 8
+// consecutive lanes read its 128 contiguous bytes; otherwise 32 consecutive
+// lanes read 512 contiguous bytes of one k.  `vec`: 16-byte loads are
+// aligned (base and ld multiples of 4 floats); otherwise every element is
+// loaded on its own.
+template <bool KC>
+__device__ __forceinline__ void mf_load(const float* __restrict__ P, long ld, long rows, long K, long r0, int k0,
+                                        bool vec, float4 (&v)[4]) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int idx = tid + r * 256;
+        float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (KC) {
+            const long gr = r0 + (idx >> 3), gk = (long)k0 + (idx & 7) * 4;
+            const float* q = P + gr * ld + gk;
+            if (vec && gr < rows && gk + 3 < K) {
+                v[r] = *reinterpret_cast<const float4*>(q);
+                continue;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (gr < rows && gk + j < K) e[j] = q[j];
+        } else {
+            const long gk = (long)k0 + (idx >> 5), gr = r0 + (idx & 31) * 4;
+            const float* q = P + gk * ld + gr;
+            if (vec && gk < K && gr + 3 < rows) {
+                v[r] = *reinterpret_cast<const float4*>(q);
+                continue;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (gk < K && gr + j < rows) e[j] = q[j];
+        }
+        v[r] = make_float4(e[0], e[1], e[2], e[3]);
+    }
+}
+
+template <bool KC>
+__device__ __forceinline__ void mf_store(float (*S)[MfTile<KC>::kCols], const float4 (&v)[4]) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int idx = tid + r * 256;
+        if constexpr (KC) *reinterpret_cast<float4*>(&S[idx >> 3][(idx & 7) * 4]) = v[r];
+        else *reinterpret_cast<float4*>(&S[idx >> 5][(idx & 31) * 4]) = v[r];
+    }
+}
+
+// k = 4q .. 4q+3 of tile row `row`
+template <bool KC>
+__device__ __forceinline__ float4 mf_read4(const float (*S)[MfTile<KC>::kCols], int row, int q) {
+    if constexpr (KC) return *reinterpret_cast<const float4*>(&S[row][4 * q]);
+    else return make_float4(S[4 * q][row], S[4 * q + 1][row], S[4 * q + 2][row], S[4 * q + 3][row]);
+}
+
+template <bool TA, bool TB, bool FUSED>
+__global__ __launch_bounds__(256) void gemm_mfma_fast_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+    int M, int N, int K, float alpha, float beta, int iters, long sa, long sb, long sc, GemmEpilogue ep,
+    int vec_a, int vec_b, const int* k_causal, int row0)
+{
+    constexpr bool KA = !TA, KB = TB;     // operand stored with k contiguous
+    const long m0 = (long)blockIdx.y * kMfBM, n0 = (long)blockIdx.x * kMfBN;
+    A += (long)blockIdx.z * sa;
+    B += (long)blockIdx.z * sb;
+    C += (long)blockIdx.z * sc;
+    __shared__ __attribute__((aligned(16))) float sA[MfTile<KA>::kRows][MfTile<KA>::kCols];
+    __shared__ __attribute__((aligned(16))) float sB[MfTile<KB>::kRows][MfTile<KB>::kCols];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const long lda = TA ? M : K, ldb = TB ? K : N;
+
+    v32f acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        acc0[r] = 0.0f;
+        acc1[r] = 0.0f;
+    }
+    float4 va[4], vb[4];
+    // Zero operands past K leave an accumulator unchanged: fma(0, 0, acc)
+    // == acc because acc starts at +0 and never becomes -0.  Causal P V
+    // (*k_causal == 1: every v finite) stops after the tile's last query
+    // position, as gemm_kernel does.
+    int kend = K;
+    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + m0 + kMfBM);
+    mf_load<KA>(A, lda, M, K, m0, 0, vec_a, va);
+    mf_load<KB>(B, ldb, N, K, n0, 0, vec_b, vb);
+    for (int k0 = 0; k0 < kend; k0 += kMfBK) {
+        __syncthreads();
+        mf_store<KA>(sA, va);
+        mf_store<KB>(sB, vb);
+        __syncthreads();
+        if (k0 + kMfBK < kend) {
+            mf_load<KA>(A, lda, M, K, m0, k0 + kMfBK, vec_a, va);
+            mf_load<KB>(B, ldb, N, K, n0, k0 + kMfBK, vec_b, vb);
+        }
+#pragma unroll
+        for (int q = 0; q < kMfBK / 4; q++) {
+            const float4 a = mf_read4<KA>(sA, wr + lane, q);
+            const float4 b0 = mf_read4<KB>(sB, wc + (lane & 31), q);
+            const float4 b1 = mf_read4<KB>(sB, wc + 32 + (lane & 31), q);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b0.x, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b1.x, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b0.y, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b1.y, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b0.z, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b1.z, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b0.w, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b1.w, acc1, 0, 0, 0);
+        }
+    }
+
+    const long col0 = n0 + wc + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        const long gm = m0 + wr + (r / 16) * 32 + ((r % 16) / 4) * 8 + (lane / 32) * 4 + (r % 4);
+        if (gm >= M) continue;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const long gn = col0 + 32 * h;
+            if (gn >= N) continue;
+            float* cp = C + gm * N + gn;
+            const float x = h ? acc1[r] : acc0[r];
+            // rac_kernels.hip:267-272
+            float v = (beta != 0.0f) ? __builtin_fmaf(alpha, x, beta * *cp) : alpha * x;
+            if constexpr (FUSED) {
+                // rac_torch.cu:770-775
+                if (ep.bias) v = v + ep.bias[gn];
+                if (ep.pre) ep.pre[gm * N + gn] = v;
+                v = act_rt(v, ep.act, iters, ep.khinv);
+            }
+            *cp = v;
+        }
+    }
+}
+
 // flag = 1 unless some x[i] is inf or NaN (flag must be 1 on entry; lanes
 // only ever store 0, so concurrent stores agree).
 __global__ __launch_bounds__(256) void all_finite_kernel(const float* __restrict__ x, long n,
@@ -435,6 +610,20 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <bool TA, bool TB, bool FUSED>
+static hipError_t launch_mfma_fast(const GemmArgs& g, hipStream_t stream) {
+    const dim3 grid((unsigned)((g.N + kMfBN - 1) / kMfBN), (unsigned)((g.M + kMfBM - 1) / kMfBM), (unsigned)g.batch);
+    // 16-byte loads need 16-byte aligned rows in every batch item
+    auto aligned = [](const float* p, long ld, long stride) {
+        return ((uintptr_t)p % 16 == 0) && ld % 4 == 0 && stride % 4 == 0;
+    };
+    const int vec_a = aligned(g.A, TA ? g.M : g.K, g.batch > 1 ? g.sa : 0);
+    const int vec_b = aligned(g.B, TB ? g.K : g.N, g.batch > 1 ? g.sb : 0);
+    hipLaunchKernelGGL((gemm_mfma_fast_kernel<TA, TB, FUSED>), grid, dim3(256), 0, stream, g.A, g.B, g.C, g.M, g.N,
+                       g.K, g.alpha, g.beta, g.iters, g.sa, g.sb, g.sc, g.ep, vec_a, vec_b, g.k_causal, g.row0);
+    return hipGetLastError();
+}
+
 // Compute units of the current device (256 on MI355X), cached per device.
 static long device_cus() {
     static std::atomic<long> cached[64];
@@ -477,6 +666,12 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
             return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch;
         };
         if constexpr (MODE == kModeFast && SCHED == 0) {
+            // the matrix cores once the 128x128 tiles fill every CU and K
+            // spans a few K-tiles: one MFMA tile costs K x 128 cycles
+            // whatever its fill, so skinny products (decode-sized M) stay
+            // on the VALU tiles below, and so do short K (measured at
+            // 2050 x 2049 x 37: 16 us on VALU 4x4, 20 us on MFMA)
+            if (tiles(kMfBM, kMfBN) >= device_cus() && g.K >= kMfMinK) return launch_mfma_fast<TA, TB, FUSED>(g, s);
             // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
             // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per
             // CU); it is taken when it fills its rounds of resident blocks

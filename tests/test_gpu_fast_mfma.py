@@ -1,0 +1,183 @@
+"""GPU parity of the FAST-mode GEMM on the matrix cores.
+
+FAST launches whose 128x128 tiles fill every CU and whose K is at least 128
+run on v_mfma_f32_32x32x1_2b_f32, one instruction per k in k order; each
+output must equal the reference's fmaf chain (rac_kernels.hip:204-219, mode
+FAST) bit for bit, like the VALU tiles do.  Shapes below are chosen to take
+that path: ragged on every edge, K not a multiple of 4 (element loads), all
+dimensions multiples of 4 (16-byte loads), exact tiles, a base address off
+the 16-byte grid, batched launches with alpha / beta, the fused bias +
+activation epilogue, and special operands (subnormal, infinite, NaN).
+"""
+import numpy as np
+import pytest
+
+import raclib as rl
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    import rac_amd
+    rac_amd.load()
+    yield
+    torch.cuda.synchronize()
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def H(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def lib():
+    import rac_amd
+    return rac_amd.load()
+
+
+def ext():
+    from rac_amd import ext as e
+    return e
+
+
+def gemm(A, B, M, N, K, ta, tb, alpha=1.0, beta=0.0, C0=None, offset=0):
+    """rac_gemm_dev in FAST mode; `offset` floats of padding in front of A
+    and B move their base addresses off the 16-byte grid."""
+    Ad = torch.zeros(A.size + offset, device=DEV)
+    Bd = torch.zeros(B.size + offset, device=DEV)
+    Ad[offset:] = T(A.ravel())
+    Bd[offset:] = T(B.ravel())
+    Cd = T(C0) if C0 is not None else torch.zeros((M, N), device=DEV)
+    rc = lib().rac_gemm_dev(Ad.data_ptr() + 4 * offset, Bd.data_ptr() + 4 * offset, Cd.data_ptr(), M, N, K,
+                            ta, tb, alpha, beta, 24, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    return H(Cd)
+
+
+def operands(M, N, K, ta, tb, seed):
+    A = rl.gen_normal((M, K), seed=seed)
+    B = rl.gen_normal((K, N), seed=seed + 1)
+    As = np.ascontiguousarray(A.T) if ta else A
+    Bs = np.ascontiguousarray(B.T) if tb else B
+    return As, Bs
+
+
+# (2100, 2100, 129): ragged tiles, K % 4 != 0 and N % 4 != 0 (element
+# loads); (2052, 2100, 260): every dimension a multiple of 4 (16-byte loads),
+# ragged tiles; (2048, 2176, 512): exact tiles.  All have >= 256 tiles.
+MF_SHAPES = [(2100, 2100, 129), (2052, 2100, 260), (2048, 2176, 512)]
+
+
+@pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("shape", MF_SHAPES)
+def test_fast_mfma_bit_exact(shape, layout):
+    M, N, K = shape
+    ta, tb = layout
+    print(f"fast mfma shape={shape} layout={layout}", flush=True)
+    As, Bs = operands(M, N, K, ta, tb, seed=M + K + 2 * ta + tb)
+    got = gemm(As, Bs, M, N, K, ta, tb)
+    ref = rl.orc_matmul(As, Bs, M, N, K, 24, 0, ta=ta, tb=tb)
+    assert np.array_equal(got, ref), float(np.max(np.abs(got - ref)))
+
+
+@pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0)])
+def test_fast_mfma_unaligned_base(layout):
+    """Dimensions that allow 16-byte loads, base addresses that do not."""
+    M, N, K = 2052, 2100, 260
+    ta, tb = layout
+    print(f"fast mfma unaligned layout={layout}", flush=True)
+    As, Bs = operands(M, N, K, ta, tb, seed=11)
+    got = gemm(As, Bs, M, N, K, ta, tb, offset=1)
+    assert np.array_equal(got, rl.orc_matmul(As, Bs, M, N, K, 24, 0, ta=ta, tb=tb))
+    assert np.array_equal(got, gemm(As, Bs, M, N, K, ta, tb))
+
+
+SPECIALS = np.array([0.0, -0.0, 1e-45, -3e-39, 2.0 ** -126, -(2.0 ** -110), 3e38, -(2.0 ** 127),
+                     np.inf, -np.inf, np.nan, 1.0, -0.75], np.float32)
+
+
+@pytest.mark.parametrize("layout", [(0, 0), (1, 1)])
+def test_fast_mfma_special_values(layout):
+    """Subnormal, huge, infinite and NaN operands through the matrix cores:
+    every finite output bit-exact, NaN exactly where the checker has NaN."""
+    M, N, K = 2100, 2100, 130
+    ta, tb = layout
+    rng = np.random.default_rng(5)
+    A = rl.gen_uniform((M, K), seed=3)
+    B = rl.gen_uniform((K, N), seed=4)
+    for r in rng.integers(16, M, 8):
+        A[r, rng.integers(0, K, 5)] = rng.choice(SPECIALS, 5)
+    B[rng.integers(0, K, 6), rng.integers(16, N, 6)] = rng.choice(SPECIALS, 6)
+    # subnormal products and a subnormal sum: row 7 of A and column 9 of B
+    # scaled by 2^-70 (no special operand lands in either)
+    A[7, :] *= np.float32(2.0 ** -70)
+    B[:, 9] *= np.float32(2.0 ** -70)
+    As = np.ascontiguousarray(A.T) if ta else A
+    Bs = np.ascontiguousarray(B.T) if tb else B
+    got = gemm(As, Bs, M, N, K, ta, tb)
+    ref = rl.orc_matmul(As, Bs, M, N, K, 24, 0, ta=ta, tb=tb, literal=1)
+    assert np.array_equal(got, ref, equal_nan=True)
+    assert np.isnan(ref).any() and np.isinf(ref).any()
+    assert 0 < abs(ref[7, 9]) < 2.0 ** -126
+
+
+def test_fast_mfma_alpha_beta():
+    M, N, K = 2100, 2052, 300
+    A = rl.gen_normal((M, K), 3)
+    B = rl.gen_normal((K, N), 4)
+    C0 = rl.gen_normal((M, N), 5)
+    got = gemm(A, B, M, N, K, 0, 0, alpha=0.5, beta=-2.0, C0=C0)
+    assert np.array_equal(got, rl.orc_matmul(A, B, M, N, K, 24, 0, alpha=0.5, beta=-2.0, C0=C0))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_fast_mfma_batched(ta, tb):
+    """4 batch items of 1100 x 1100 (324 tiles): bmm with alpha, then
+    accumulating into the result with beta."""
+    e = ext()
+    Z, M, N, K = 4, 1100, 1100, 200
+    A = rl.gen_uniform((Z, K, M) if ta else (Z, M, K), seed=5 + ta)
+    B = rl.gen_uniform((Z, N, K) if tb else (Z, K, N), seed=9 + tb)
+    C = e.bmm(T(A), T(B), trans_a=bool(ta), trans_b=bool(tb), alpha=0.75, iters=24, mode=0)
+    first = H(C).copy()
+    e.bmm(T(A), T(B), trans_a=bool(ta), trans_b=bool(tb), alpha=1.0, iters=24, mode=0, out=C, beta=0.5)
+    second = H(C)
+    for z in range(Z):
+        Az, Bz = np.ascontiguousarray(A[z]), np.ascontiguousarray(B[z])
+        ref = rl.orc_matmul(Az, Bz, M, N, K, 24, 0, ta=ta, tb=tb, alpha=0.75)
+        assert np.array_equal(first[z], ref), z
+        ref2 = rl.orc_matmul(Az, Bz, M, N, K, 24, 0, ta=ta, tb=tb, alpha=1.0, beta=0.5, C0=ref)
+        assert np.array_equal(second[z], ref2), z
+
+
+@pytest.mark.parametrize("act", [0, 1, 3])
+def test_fast_mfma_fused_linear(act):
+    """linear_forward and fused_linear_forward (bias + activation in the
+    epilogue) at an MFMA shape: pre-activations equal the unfused product
+    plus bias, bit-exact vs the checker; outputs equal the activation kernel
+    applied to them."""
+    e = ext()
+    M, N, K = 2050, 2049, 300
+    x = rl.gen_normal((M, K), seed=3)
+    w = rl.gen_normal((N, K), seed=4, std=0.2)
+    b = rl.gen_normal(N, seed=5)
+    out, pre = e.fused_linear_forward(T(x), T(w), T(b), act, iters=24, mode=0, return_pre=True)
+    lin = e.linear_forward(T(x), T(w), T(b), iters=24, mode=0)
+    assert torch.equal(pre, lin)
+    if act == 3:
+        assert torch.equal(out, e.silu(lin, 24))
+    elif act == 1:
+        assert torch.equal(out, e.relu(lin))
+    else:
+        assert torch.equal(out, lin)
+    ref = rl.orc_matmul(x, w, M, N, K, 24, 0, tb=1) + b[None, :]
+    assert np.array_equal(H(pre), ref.astype(np.float32))
