@@ -579,6 +579,19 @@ def bench_block_ops(torch, ext, dev, g):
                                               "linear_equiv_TFLOPs": round(644.2e9 / t / 1e12, 3),
                                               "per_op_ms": parts, **_dist_fields(t, 1e3, "ms")}
             print(f"# llama block n={n}: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
+        # the same block in rac_torch's default configuration (FAST MAC,
+        # precision 24 for the CORDIC activations and softmax exp)
+        rt.rac_set_mode("fast")
+        rt.rac_set_precision(24)
+        with torch.no_grad():
+            blk(xb, is_causal=True)
+            torch.cuda.synchronize()
+            t = _events_time(lambda: blk(xb, is_causal=True), 3, torch, dist_calls=5)
+            parts = _llama_breakdown(torch, blk, xb)
+        out["llama_block_T2048_fast"] = {"ms": round(t * 1e3, 2),
+                                         "linear_TFLOPs": round(644.2e9 / t / 1e12, 3),
+                                         "per_op_ms": parts, **_dist_fields(t, 1e3, "ms")}
+        print(f"# llama block FAST: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
     finally:
         rt.rac_set_mode(prev_mode)
         rt.rac_set_precision(prev_iters)
