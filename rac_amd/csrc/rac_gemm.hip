@@ -389,43 +389,47 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 // per k in k order, it therefore gives every output the FAST MAC's
 // accumulation chain bit for bit, at 2048 MACs per instruction for 3 LDS
 // floats per lane and k, where the VALU form is bound by LDS bandwidth
-// (4096^3: 1.09-1.15 ms against 1.48-1.53 ms on the 16x8 VALU tile).
+// (4096^3: 1.06-1.15 ms against 1.48-1.53 ms on the 16x8 VALU tile).
 //
-// Block tile 128 x 128, BK = 32, staged global -> registers -> LDS with the
-// next K-tile's loads in flight during the current one's MFMAs; 4
-// waves in 2 x 2, each owning 64 x 64 outputs as two instructions per k:
-// lane l supplies A row l of the wave tile (lanes 0-31 feed the instruction's
-// block 0, lanes 32-63 its block 1) and B column l % 32 of the half (both
+// Block tile 2 WR x 128, BK = 32, staged global -> registers -> LDS with
+// the next K-tile's loads in flight during the current one's MFMAs; 4
+// waves in 2 x 2, each owning WR x 64 outputs (WR = 64 or 128) as 2 WR / 32
+// instructions per k on independent accumulators (a dependent MFMA waits
+// ~100 cycles for its predecessor, ~65 cycles of issue, so more chains per
+// wave keep the matrix core busier).  For each 64-row group of the wave
+// tile, lane l supplies A row l (lanes 0-31 feed the instruction's block 0,
+// lanes 32-63 its block 1) and B column l % 32 of a 32-column half (both
 // blocks read the same 32 columns), so block b covers rows 32 b .. 32 b + 31.
 // Accumulator register r of lane l holds block r / 16, row
 // ((r % 16) / 4) * 8 + (l / 32) * 4 + r % 4 of that block, column l % 32.
 typedef float v32f __attribute__((ext_vector_type(32)));
-constexpr int kMfBM = 128, kMfBN = 128, kMfBK = 32, kMfMinK = 128;
+constexpr int kMfBN = 128, kMfBK = 32, kMfMinK = 128;
 
-// One operand's K-tile (32 k x 128 rows) in LDS.  An operand stored with k
+// One operand's K-tile (32 k x ROWS rows) in LDS.  An operand stored with k
 // contiguous in memory (A, or B^T of the NT layout) is kept as [row][k]
 // rows of 36 floats, so a lane reads 4 consecutive k of its row in one
 // ds_read_b128 (rows 144 B apart: 16 lanes cover all 64 banks); the other
-// layout stays [k][row] (rows of 132 floats) and is read one k at a time.
-template <bool KC>
+// layout stays [k][row] (rows of ROWS + 4 floats) and is read one k at a time.
+template <bool KC, int ROWS>
 struct MfTile {
-    static constexpr int kRows = KC ? 128 : kMfBK;
-    static constexpr int kCols = KC ? kMfBK + 4 : 128 + 4;
+    static constexpr int kRows = KC ? ROWS : kMfBK;
+    static constexpr int kCols = KC ? kMfBK + 4 : ROWS + 4;
+    static constexpr int kVecs = ROWS * kMfBK / 4 / 256;      // float4 per lane
 };
 
-// Global -> registers: 4 float4 per lane covering the 32 x 128 tile at k0
-// (rows r0..r0+127 of an operand with `rows` rows, leading dimension ld),
-// zero outside the matrix.  k-contiguous: lanes 8 apart share a row, 8
-// consecutive lanes read its 128 contiguous bytes; otherwise 32 consecutive
-// lanes read 512 contiguous bytes of one k.  `vec`: 16-byte loads are
-// aligned (base and ld multiples of 4 floats); otherwise every element is
-// loaded on its own.
-template <bool KC>
+// Global -> registers: the 32 x ROWS tile at k0 (rows r0.. of an operand
+// with `rows` rows, leading dimension ld) as float4 per lane, zero outside
+// the matrix.  k-contiguous: 8 consecutive lanes read a row's 128
+// contiguous bytes; otherwise ROWS / 4 consecutive lanes read one k's
+// 4 ROWS contiguous bytes.  `vec`: 16-byte loads are aligned (base and ld
+// multiples of 4 floats); otherwise every element is loaded on its own.
+template <bool KC, int ROWS>
 __device__ __forceinline__ void mf_load(const float* __restrict__ P, long ld, long rows, long K, long r0, int k0,
-                                        bool vec, float4 (&v)[4]) {
+                                        bool vec, float4 (&v)[MfTile<KC, ROWS>::kVecs]) {
+    constexpr int kPerK = ROWS / 4;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < MfTile<KC, ROWS>::kVecs; r++) {
         const int idx = tid + r * 256;
         float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (KC) {
@@ -439,7 +443,7 @@ __device__ __forceinline__ void mf_load(const float* __restrict__ P, long ld, lo
             for (int j = 0; j < 4; j++)
                 if (gr < rows && gk + j < K) e[j] = q[j];
         } else {
-            const long gk = (long)k0 + (idx >> 5), gr = r0 + (idx & 31) * 4;
+            const long gk = (long)k0 + idx / kPerK, gr = r0 + (idx % kPerK) * 4;
             const float* q = P + gk * ld + gr;
             if (vec && gk < K && gr + 3 < rows) {
                 v[r] = *reinterpret_cast<const float4*>(q);
@@ -453,92 +457,109 @@ __device__ __forceinline__ void mf_load(const float* __restrict__ P, long ld, lo
     }
 }
 
-template <bool KC>
-__device__ __forceinline__ void mf_store(float (*S)[MfTile<KC>::kCols], const float4 (&v)[4]) {
+// S: the tile's LDS array (kRows x kCols floats, row-major)
+template <bool KC, int ROWS>
+__device__ __forceinline__ void mf_store(float* S, const float4 (&v)[MfTile<KC, ROWS>::kVecs]) {
+    constexpr int kPerK = ROWS / 4, kC = MfTile<KC, ROWS>::kCols;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < MfTile<KC, ROWS>::kVecs; r++) {
         const int idx = tid + r * 256;
-        if constexpr (KC) *reinterpret_cast<float4*>(&S[idx >> 3][(idx & 7) * 4]) = v[r];
-        else *reinterpret_cast<float4*>(&S[idx >> 5][(idx & 31) * 4]) = v[r];
+        if constexpr (KC) *reinterpret_cast<float4*>(&S[(idx >> 3) * kC + (idx & 7) * 4]) = v[r];
+        else *reinterpret_cast<float4*>(&S[(idx / kPerK) * kC + (idx % kPerK) * 4]) = v[r];
     }
 }
 
 // k = 4q .. 4q+3 of tile row `row`
-template <bool KC>
-__device__ __forceinline__ float4 mf_read4(const float (*S)[MfTile<KC>::kCols], int row, int q) {
-    if constexpr (KC) return *reinterpret_cast<const float4*>(&S[row][4 * q]);
-    else return make_float4(S[4 * q][row], S[4 * q + 1][row], S[4 * q + 2][row], S[4 * q + 3][row]);
+template <bool KC, int ROWS>
+__device__ __forceinline__ float4 mf_read4(const float* S, int row, int q) {
+    constexpr int kC = MfTile<KC, ROWS>::kCols;
+    if constexpr (KC) return *reinterpret_cast<const float4*>(&S[row * kC + 4 * q]);
+    else return make_float4(S[4 * q * kC + row], S[(4 * q + 1) * kC + row], S[(4 * q + 2) * kC + row],
+                            S[(4 * q + 3) * kC + row]);
 }
 
-template <bool TA, bool TB, bool FUSED>
-__global__ __launch_bounds__(256) void gemm_mfma_fast_kernel(
+// WR: rows of a wave's tile (64: 2 accumulator chains per wave, 128: 4);
+// the block tile is 2 WR x 128.
+template <bool TA, bool TB, bool FUSED, int WR>
+__global__ __launch_bounds__(256, WR == 128 ? 2 : 1) void gemm_mfma_fast_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, long sa, long sb, long sc, GemmEpilogue ep,
     int vec_a, int vec_b, const int* k_causal, int row0)
 {
     constexpr bool KA = !TA, KB = TB;     // operand stored with k contiguous
-    const long m0 = (long)blockIdx.y * kMfBM, n0 = (long)blockIdx.x * kMfBN;
+    constexpr int BM = 2 * WR, BN = kMfBN, WI = WR / 64;
+    using TAt = MfTile<KA, BM>;
+    using TBt = MfTile<KB, BN>;
+    const long m0 = (long)blockIdx.y * BM, n0 = (long)blockIdx.x * BN;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
-    __shared__ __attribute__((aligned(16))) float sA[MfTile<KA>::kRows][MfTile<KA>::kCols];
-    __shared__ __attribute__((aligned(16))) float sB[MfTile<KB>::kRows][MfTile<KB>::kCols];
+    __shared__ __attribute__((aligned(16))) float sA[TAt::kRows][TAt::kCols];
+    __shared__ __attribute__((aligned(16))) float sB[TBt::kRows][TBt::kCols];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int wr = (wave >> 1) * WR, wc = (wave & 1) * 64;
     const long lda = TA ? M : K, ldb = TB ? K : N;
 
-    v32f acc0, acc1;
+    v32f acc[WI][2];
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-        acc0[r] = 0.0f;
-        acc1[r] = 0.0f;
-    }
-    float4 va[4], vb[4];
+    for (int i = 0; i < WI; i++)
+#pragma unroll
+        for (int r = 0; r < 32; r++) {
+            acc[i][0][r] = 0.0f;
+            acc[i][1][r] = 0.0f;
+        }
+    float4 va[TAt::kVecs], vb[TBt::kVecs];
     // Zero operands past K leave an accumulator unchanged: fma(0, 0, acc)
     // == acc because acc starts at +0 and never becomes -0.  Causal P V
     // (*k_causal == 1: every v finite) stops after the tile's last query
     // position, as gemm_kernel does.
     int kend = K;
-    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + m0 + kMfBM);
-    mf_load<KA>(A, lda, M, K, m0, 0, vec_a, va);
-    mf_load<KB>(B, ldb, N, K, n0, 0, vec_b, vb);
+    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + m0 + BM);
+    mf_load<KA, BM>(A, lda, M, K, m0, 0, vec_a, va);
+    mf_load<KB, BN>(B, ldb, N, K, n0, 0, vec_b, vb);
     for (int k0 = 0; k0 < kend; k0 += kMfBK) {
         __syncthreads();
-        mf_store<KA>(sA, va);
-        mf_store<KB>(sB, vb);
+        mf_store<KA, BM>(&sA[0][0], va);
+        mf_store<KB, BN>(&sB[0][0], vb);
         __syncthreads();
         if (k0 + kMfBK < kend) {
-            mf_load<KA>(A, lda, M, K, m0, k0 + kMfBK, vec_a, va);
-            mf_load<KB>(B, ldb, N, K, n0, k0 + kMfBK, vec_b, vb);
+            mf_load<KA, BM>(A, lda, M, K, m0, k0 + kMfBK, vec_a, va);
+            mf_load<KB, BN>(B, ldb, N, K, n0, k0 + kMfBK, vec_b, vb);
         }
 #pragma unroll
         for (int q = 0; q < kMfBK / 4; q++) {
-            const float4 a = mf_read4<KA>(sA, wr + lane, q);
-            const float4 b0 = mf_read4<KB>(sB, wc + (lane & 31), q);
-            const float4 b1 = mf_read4<KB>(sB, wc + 32 + (lane & 31), q);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b0.x, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b1.x, acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b0.y, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b1.y, acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b0.z, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b1.z, acc1, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b0.w, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b1.w, acc1, 0, 0, 0);
+            float4 a[WI];
+#pragma unroll
+            for (int i = 0; i < WI; i++) a[i] = mf_read4<KA, BM>(&sA[0][0], wr + 64 * i + lane, q);
+            const float4 b0 = mf_read4<KB, BN>(&sB[0][0], wc + (lane & 31), q);
+            const float4 b1 = mf_read4<KB, BN>(&sB[0][0], wc + 32 + (lane & 31), q);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int i = 0; i < WI; i++) {
+                    const float aj = j == 0 ? a[i].x : j == 1 ? a[i].y : j == 2 ? a[i].z : a[i].w;
+                    const float b0j = j == 0 ? b0.x : j == 1 ? b0.y : j == 2 ? b0.z : b0.w;
+                    const float b1j = j == 0 ? b1.x : j == 1 ? b1.y : j == 2 ? b1.z : b1.w;
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x1f32(aj, b0j, acc[i][0], 0, 0, 0);
+                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x1f32(aj, b1j, acc[i][1], 0, 0, 0);
+                }
         }
     }
 
     const long col0 = n0 + wc + (lane & 31);
 #pragma unroll
+    for (int i = 0; i < WI; i++)
+#pragma unroll
     for (int r = 0; r < 32; r++) {
-        const long gm = m0 + wr + (r / 16) * 32 + ((r % 16) / 4) * 8 + (lane / 32) * 4 + (r % 4);
+        const long gm = m0 + wr + 64 * i + (r / 16) * 32 + ((r % 16) / 4) * 8 + (lane / 32) * 4 + (r % 4);
         if (gm >= M) continue;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const long gn = col0 + 32 * h;
             if (gn >= N) continue;
             float* cp = C + gm * N + gn;
-            const float x = h ? acc1[r] : acc0[r];
+            const float x = acc[i][h][r];
             // rac_kernels.hip:267-272
             float v = (beta != 0.0f) ? __builtin_fmaf(alpha, x, beta * *cp) : alpha * x;
             if constexpr (FUSED) {
@@ -610,17 +631,18 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <bool TA, bool TB, bool FUSED>
+template <bool TA, bool TB, bool FUSED, int WR>
 static hipError_t launch_mfma_fast(const GemmArgs& g, hipStream_t stream) {
-    const dim3 grid((unsigned)((g.N + kMfBN - 1) / kMfBN), (unsigned)((g.M + kMfBM - 1) / kMfBM), (unsigned)g.batch);
+    constexpr int BM = 2 * WR;
+    const dim3 grid((unsigned)((g.N + kMfBN - 1) / kMfBN), (unsigned)((g.M + BM - 1) / BM), (unsigned)g.batch);
     // 16-byte loads need 16-byte aligned rows in every batch item
     auto aligned = [](const float* p, long ld, long stride) {
         return ((uintptr_t)p % 16 == 0) && ld % 4 == 0 && stride % 4 == 0;
     };
     const int vec_a = aligned(g.A, TA ? g.M : g.K, g.batch > 1 ? g.sa : 0);
     const int vec_b = aligned(g.B, TB ? g.K : g.N, g.batch > 1 ? g.sb : 0);
-    hipLaunchKernelGGL((gemm_mfma_fast_kernel<TA, TB, FUSED>), grid, dim3(256), 0, stream, g.A, g.B, g.C, g.M, g.N,
-                       g.K, g.alpha, g.beta, g.iters, g.sa, g.sb, g.sc, g.ep, vec_a, vec_b, g.k_causal, g.row0);
+    hipLaunchKernelGGL((gemm_mfma_fast_kernel<TA, TB, FUSED, WR>), grid, dim3(256), 0, stream, g.A, g.B, g.C, g.M,
+                       g.N, g.K, g.alpha, g.beta, g.iters, g.sa, g.sb, g.sc, g.ep, vec_a, vec_b, g.k_causal, g.row0);
     return hipGetLastError();
 }
 
@@ -670,19 +692,32 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
             // spans a few K-tiles: one MFMA tile costs K x 128 cycles
             // whatever its fill, so skinny products (decode-sized M) stay
             // on the VALU tiles below, and so do short K (measured at
-            // 2050 x 2049 x 37: 16 us on VALU 4x4, 20 us on MFMA)
-            if (tiles(kMfBM, kMfBN) >= device_cus() && g.K >= kMfMinK) return launch_mfma_fast<TA, TB, FUSED>(g, s);
-            // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
-            // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per
-            // CU); it is taken when it fills its rounds of resident blocks
-            // at least as completely as 8x8 does
+            // 2050 x 2049 x 37: 16 us on VALU 4x4, 20 us on MFMA).
+            // Wave tiles of 128 x 64 (4 accumulator chains per wave, 2
+            // blocks of 256 x 128 per CU) beat 64 x 64 (2 chains, 3 blocks
+            // of 128 x 128 per CU) by 5-7% when their rounds of resident
+            // blocks are as full (4096^3, 8192^3) and lose up to 19% when a
+            // partial last round remains (2048 x 12288: 1.5 rounds against
+            // 2), so the fuller one is taken, 64 x 64 on a tie.  The fused
+            // epilogue keeps 64 x 64 (with 4 chains it no longer fits the
+            // registers).
             const long cus = device_cus();
             auto fill = [&](long t, long per_cu) {
                 const long slots = per_cu * cus, rounds = (t + slots - 1) / slots;
                 return (double)t / (double)(rounds * slots);
             };
-            const long t16 = tiles(256, 128), t8 = tiles(128, 128);
-            if (t16 >= 2 * cus && fill(t16, 2) >= fill(t8, 3))
+            const long t128 = tiles(128, kMfBN), t256 = tiles(256, kMfBN);
+            if (g.K >= kMfMinK && t128 >= cus) {
+                if constexpr (!FUSED) {
+                    if (fill(t256, 2) > fill(t128, 3)) return launch_mfma_fast<TA, TB, FUSED, 128>(g, s);
+                }
+                return launch_mfma_fast<TA, TB, FUSED, 64>(g, s);
+            }
+            // 16x8 per lane (256x128 blocks, 2 per CU at its register count)
+            // reads 25% fewer LDS bytes per FMA than 8x8 (128x128, 3 per
+            // CU); it is taken when it fills its rounds of resident blocks
+            // at least as completely as 8x8 does
+            if (t256 >= 2 * cus && fill(t256, 2) >= fill(t128, 3))
                 return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 16, 8>(g, s);
         }
         if (tiles(16 * kBig, 16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, kBig>(g, s);

@@ -73,8 +73,10 @@ def operands(M, N, K, ta, tb, seed):
 
 # (2100, 2100, 129): ragged tiles, K % 4 != 0 and N % 4 != 0 (element
 # loads); (2052, 2100, 260): every dimension a multiple of 4 (16-byte loads),
-# ragged tiles; (2048, 2176, 512): exact tiles.  All have >= 256 tiles.
-MF_SHAPES = [(2100, 2100, 129), (2052, 2100, 260), (2048, 2176, 512)]
+# ragged tiles; (2048, 2176, 512): exact tiles.  These take wave tiles of
+# 64 x 64 (128 x 128 blocks); the 4000 x 4000 shapes fill one round of
+# 256 x 128 blocks and take 128 x 64 wave tiles (ragged on both edges).
+MF_SHAPES = [(2100, 2100, 129), (2052, 2100, 260), (2048, 2176, 512), (4000, 4000, 129), (4000, 4000, 260)]
 
 
 @pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0), (1, 1)])
@@ -89,10 +91,11 @@ def test_fast_mfma_bit_exact(shape, layout):
     assert np.array_equal(got, ref), float(np.max(np.abs(got - ref)))
 
 
+@pytest.mark.parametrize("shape", [(2052, 2100, 260), (4000, 4000, 260)])
 @pytest.mark.parametrize("layout", [(0, 0), (0, 1), (1, 0)])
-def test_fast_mfma_unaligned_base(layout):
+def test_fast_mfma_unaligned_base(layout, shape):
     """Dimensions that allow 16-byte loads, base addresses that do not."""
-    M, N, K = 2052, 2100, 260
+    M, N, K = shape
     ta, tb = layout
     print(f"fast mfma unaligned layout={layout}", flush=True)
     As, Bs = operands(M, N, K, ta, tb, seed=11)
@@ -105,11 +108,12 @@ SPECIALS = np.array([0.0, -0.0, 1e-45, -3e-39, 2.0 ** -126, -(2.0 ** -110), 3e38
                      np.inf, -np.inf, np.nan, 1.0, -0.75], np.float32)
 
 
+@pytest.mark.parametrize("shape", [(2100, 2100, 130), (4000, 4000, 130)])
 @pytest.mark.parametrize("layout", [(0, 0), (1, 1)])
-def test_fast_mfma_special_values(layout):
+def test_fast_mfma_special_values(layout, shape):
     """Subnormal, huge, infinite and NaN operands through the matrix cores:
     every finite output bit-exact, NaN exactly where the checker has NaN."""
-    M, N, K = 2100, 2100, 130
+    M, N, K = shape
     ta, tb = layout
     rng = np.random.default_rng(5)
     A = rl.gen_uniform((M, K), seed=3)
