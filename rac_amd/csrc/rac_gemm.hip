@@ -480,8 +480,12 @@ __device__ __forceinline__ float4 mf_read4(const float* S, int row, int q) {
 }
 
 // WR: rows of a wave's tile (64: 2 accumulator chains per wave, 128: 4);
-// the block tile is 2 WR x 128.
-template <bool TA, bool TB, bool FUSED, int WR>
+// the block tile is 2 WR x 128.  TRAP: causal attention scores of query
+// rows row0 .. row0 + M - 1 against keys 0 .. N - 1, only the tiles on or
+// below the diagonal (trap_cols per row tile, numbered row by row along
+// grid x, as gemm_kernel's schedule 3); the masked softmax overwrites the
+// scores above the diagonal, so the others are never read.
+template <bool TA, bool TB, bool FUSED, int WR, bool TRAP = false>
 __global__ __launch_bounds__(256, WR == 128 ? 2 : 1) void gemm_mfma_fast_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     int M, int N, int K, float alpha, float beta, int iters, long sa, long sb, long sc, GemmEpilogue ep,
@@ -491,7 +495,19 @@ __global__ __launch_bounds__(256, WR == 128 ? 2 : 1) void gemm_mfma_fast_kernel(
     constexpr int BM = 2 * WR, BN = kMfBN, WI = WR / 64;
     using TAt = MfTile<KA, BM>;
     using TBt = MfTile<KB, BN>;
-    const long m0 = (long)blockIdx.y * BM, n0 = (long)blockIdx.x * BN;
+    int tm = blockIdx.y, tn = blockIdx.x;
+    if constexpr (TRAP) {
+        int l = blockIdx.x;
+        tm = 0;
+        for (;;) {
+            const int c = trap_cols(row0, tm, BM, BN, N);
+            if (l < c) break;
+            l -= c;
+            tm++;
+        }
+        tn = l;
+    }
+    const long m0 = (long)tm * BM, n0 = (long)tn * BN;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
@@ -631,18 +647,24 @@ static hipError_t launch_cfg(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <bool TA, bool TB, bool FUSED, int WR>
+template <bool TA, bool TB, bool FUSED, int WR, bool TRAP = false>
 static hipError_t launch_mfma_fast(const GemmArgs& g, hipStream_t stream) {
     constexpr int BM = 2 * WR;
-    const dim3 grid((unsigned)((g.N + kMfBN - 1) / kMfBN), (unsigned)((g.M + BM - 1) / BM), (unsigned)g.batch);
+    dim3 grid((unsigned)((g.N + kMfBN - 1) / kMfBN), (unsigned)((g.M + BM - 1) / BM), (unsigned)g.batch);
+    if constexpr (TRAP) {
+        long t = 0;
+        for (int r = 0; r < (int)grid.y; r++) t += trap_cols(g.row0, r, BM, kMfBN, g.N);
+        grid = dim3((unsigned)t, 1, (unsigned)g.batch);
+    }
     // 16-byte loads need 16-byte aligned rows in every batch item
     auto aligned = [](const float* p, long ld, long stride) {
         return ((uintptr_t)p % 16 == 0) && ld % 4 == 0 && stride % 4 == 0;
     };
     const int vec_a = aligned(g.A, TA ? g.M : g.K, g.batch > 1 ? g.sa : 0);
     const int vec_b = aligned(g.B, TB ? g.K : g.N, g.batch > 1 ? g.sb : 0);
-    hipLaunchKernelGGL((gemm_mfma_fast_kernel<TA, TB, FUSED, WR>), grid, dim3(256), 0, stream, g.A, g.B, g.C, g.M,
-                       g.N, g.K, g.alpha, g.beta, g.iters, g.sa, g.sb, g.sc, g.ep, vec_a, vec_b, g.k_causal, g.row0);
+    hipLaunchKernelGGL((gemm_mfma_fast_kernel<TA, TB, FUSED, WR, TRAP>), grid, dim3(256), 0, stream, g.A, g.B, g.C,
+                       g.M, g.N, g.K, g.alpha, g.beta, g.iters, g.sa, g.sb, g.sc, g.ep, vec_a, vec_b, g.k_causal,
+                       g.row0);
     return hipGetLastError();
 }
 
@@ -676,6 +698,28 @@ static long device_cus() {
 template <int MODE, int NITER, bool TA, bool TB, bool FUSED, int SCHED = 0>
 static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
     constexpr int kBig = (MODE == kModeFast) ? 8 : 4;
+    if constexpr (MODE == kModeFast && SCHED != 0) {
+        // Causal attention products on the matrix cores under the rule of
+        // the plain schedule below: the scores (1: square, row0 = 0; 3: a
+        // chunk of query rows) over the tiles on or below the diagonal,
+        // P V (2) as a plain launch whose row tiles stop at their causal
+        // K limit (pairing row tiles for balance is not needed at MFMA
+        // block counts).
+        const long cus = device_cus();
+        if (g.K >= kMfMinK) {
+            if constexpr (SCHED == 2) {
+                const long t = ((g.M + 127) / 128) * ((g.N + kMfBN - 1) / kMfBN) * (long)g.batch;
+                if (4 * t >= cus && (double)g.M * g.N * g.batch >= 0.5 * (double)t * 128.0 * kMfBN)
+                    return launch_mfma_fast<TA, TB, FUSED, 64>(g, s);
+            } else {
+                GemmArgs h = g;
+                if constexpr (SCHED == 1) h.row0 = 0;
+                long t = 0;
+                for (int r = 0; r < (int)((g.M + 127) / 128); r++) t += trap_cols(h.row0, r, 128, kMfBN, g.N);
+                if (g.M >= 64 && 4 * t * (long)g.batch >= cus) return launch_mfma_fast<TA, TB, FUSED, 64, true>(h, s);
+            }
+        }
+    }
     if constexpr (SCHED == 1 || SCHED == 2) {
         return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
     } else {
@@ -688,28 +732,33 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
             return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * (long)g.batch;
         };
         if constexpr (MODE == kModeFast && SCHED == 0) {
-            // the matrix cores once the 128x128 tiles fill every CU and K
-            // spans a few K-tiles: one MFMA tile costs K x 128 cycles
-            // whatever its fill, so skinny products (decode-sized M) stay
-            // on the VALU tiles below, and so do short K (measured at
-            // 2050 x 2049 x 37: 16 us on VALU 4x4, 20 us on MFMA).
+            // The matrix cores, once there are cus / 4 blocks of 128 x 128,
+            // at least half of their outputs real and K >= 128.  An MFMA
+            // block costs K x 128 cycles of its SIMDs whatever its fill:
+            // measured against the VALU tiles (bit-identical), 64 blocks
+            // (1024^2 x 1024, 32 x 256 x 128 x 2048) are 5-8% faster, 128
+            // blocks (the attention P V chunks 32 x 512 x 128 x K, 512 x
+            // 4096 x 4096 NT) 65-84% faster, while 32 blocks of a short M
+            // (128 x 4096 x 4096) are 3x slower, and K = 37 (2050 x 2049)
+            // 20 us against 16.
             // Wave tiles of 128 x 64 (4 accumulator chains per wave, 2
             // blocks of 256 x 128 per CU) beat 64 x 64 (2 chains, 3 blocks
-            // of 128 x 128 per CU) by 5-7% when their rounds of resident
-            // blocks are as full (4096^3, 8192^3) and lose up to 19% when a
-            // partial last round remains (2048 x 12288: 1.5 rounds against
-            // 2), so the fuller one is taken, 64 x 64 on a tie.  The fused
-            // epilogue keeps 64 x 64 (with 4 chains it no longer fits the
-            // registers).
+            // of 128 x 128 per CU) by 5-7% when they fill a round of the CUs
+            // and their rounds of resident blocks are fuller (4096^3,
+            // 8192^3), and lose up to 19% when a partial last round remains
+            // (2048 x 12288: 1.5 rounds against 2), so the fuller one is
+            // taken, 64 x 64 on a tie.  The fused epilogue keeps 64 x 64
+            // (with 4 chains it no longer fits the registers).
             const long cus = device_cus();
             auto fill = [&](long t, long per_cu) {
                 const long slots = per_cu * cus, rounds = (t + slots - 1) / slots;
                 return (double)t / (double)(rounds * slots);
             };
             const long t128 = tiles(128, kMfBN), t256 = tiles(256, kMfBN);
-            if (g.K >= kMfMinK && t128 >= cus) {
+            const double used = (double)g.M * (double)g.N * (double)g.batch / ((double)t128 * kMfBN * 128.0);
+            if (g.K >= kMfMinK && 4 * t128 >= cus && used >= 0.5) {
                 if constexpr (!FUSED) {
-                    if (fill(t256, 2) > fill(t128, 3)) return launch_mfma_fast<TA, TB, FUSED, 128>(g, s);
+                    if (t256 >= cus && fill(t256, 2) > fill(t128, 3)) return launch_mfma_fast<TA, TB, FUSED, 128>(g, s);
                 }
                 return launch_mfma_fast<TA, TB, FUSED, 64>(g, s);
             }

@@ -1,13 +1,15 @@
 """GPU parity of the FAST-mode GEMM on the matrix cores.
 
-FAST launches whose 128x128 tiles fill every CU and whose K is at least 128
-run on v_mfma_f32_32x32x1_2b_f32, one instruction per k in k order; each
+FAST launches with at least a quarter as many 128x128 blocks as CUs, at
+least half of their outputs real, and K >= 128 run on
+v_mfma_f32_32x32x1_2b_f32, one instruction per k in k order; each
 output must equal the reference's fmaf chain (rac_kernels.hip:204-219, mode
 FAST) bit for bit, like the VALU tiles do.  Shapes below are chosen to take
 that path: ragged on every edge, K not a multiple of 4 (element loads), all
 dimensions multiples of 4 (16-byte loads), exact tiles, a base address off
 the 16-byte grid, batched launches with alpha / beta, the fused bias +
-activation epilogue, and special operands (subnormal, infinite, NaN).
+activation epilogue, special operands (subnormal, infinite, NaN), launches
+of fewer blocks than CUs, and the config-5 attention core's P V chunks.
 """
 import numpy as np
 import pytest
@@ -185,3 +187,78 @@ def test_fast_mfma_fused_linear(act):
         assert torch.equal(out, lin)
     ref = rl.orc_matmul(x, w, M, N, K, 24, 0, tb=1) + b[None, :]
     assert np.array_equal(H(pre), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_fast_attention_config5_mfma_products(causal):
+    """The config-5 attention core in FAST mode: each 512-row chunk's P V
+    (32 heads of 512 x 128, 128 blocks, the causal K limit per row tile)
+    runs on the matrix cores; the output equals the one-chunk form (P V on
+    the VALU tiles) and the checker's composition on sampled heads, bit for
+    bit."""
+    e = ext()
+    shape = (1, 32, 2048, 128)
+    q = rl.gen_normal(shape, seed=700)
+    k = rl.gen_normal(shape, seed=701)
+    v = rl.gen_normal(shape, seed=702)
+    got = H(e.attention(T(q), T(k), T(v), None, causal, iters=24, mode=0))
+    one, _ = e.attention(T(q), T(k), T(v), None, causal, iters=24, mode=0, return_probs=True)
+    assert np.array_equal(got, H(one))
+    for h in (0, 17):
+        sl = (slice(0, 1), slice(h, h + 1))
+        assert np.array_equal(got[sl], rl.orc_attention_lanes(q[sl], k[sl], v[sl], None, causal, 24, 0)), h
+
+
+@pytest.mark.parametrize("Z,M,N,K", [(32, 512, 128, 600), (1, 1024, 1024, 1030), (8, 512, 512, 512)])
+def test_fast_mfma_few_blocks(Z, M, N, K):
+    """Launches of 64-128 blocks of 128 x 128 (fewer than the CUs) on the
+    matrix cores: bit-exact vs the checker."""
+    e = ext()
+    A = rl.gen_uniform((Z, M, K), seed=Z + M)
+    B = rl.gen_uniform((Z, K, N), seed=N + K)
+    got = H(e.bmm(T(A), T(B), iters=24, mode=0))
+    for z in range(Z):
+        ref = rl.orc_matmul(np.ascontiguousarray(A[z]), np.ascontiguousarray(B[z]), M, N, K, 24, 0)
+        assert np.array_equal(got[z], ref), z
+
+
+def _attention_ws(q, k, v, mask, causal, chunk_rows):
+    """rac_attention_ws_dev in FAST mode (iters 24) with a NaN-filled
+    workspace of `chunk_rows` query rows per chunk: a chunk that read scores
+    it had not written would show."""
+    L = lib()
+    B, Hh, Tn, D = q.shape
+    qt, kt, vt = T(q), T(k), T(v)
+    mt = T(mask) if mask is not None else None
+    out = torch.empty_like(qt)
+    nbytes = 4 * B * Hh * chunk_rows * Tn + 256
+    ws = torch.full((nbytes // 4,), float("nan"), device=DEV)
+    rc = L.rac_attention_ws_dev(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), mt.data_ptr() if mt is not None else None,
+                                int(causal), out.data_ptr(), B, Hh, Tn, D, ws.data_ptr(), nbytes, 24, 0,
+                                torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, L.rac_last_error()
+    return H(out)
+
+
+def test_fast_attention_chunks_mfma():
+    """[1, 16, 512, 128] in FAST mode: the causal scores of each chunk of
+    query rows (the trapezoid of 128 x 128 tiles on or below the diagonal)
+    and P V run on the matrix cores for chunks of 64 rows and more; every
+    chunk size gives the one-chunk bits, which equal the checker's."""
+    e = ext()
+    shape = (1, 16, 512, 128)
+    q = rl.gen_normal(shape, seed=720)
+    k = rl.gen_normal(shape, seed=721)
+    v = rl.gen_normal(shape, seed=722)
+    mask = (rl.gen_normal((512, 512), seed=723) * np.float32(0.5)).astype(np.float32)
+    for mk, causal in ((None, True), (mask, True), (mask, False)):
+        print(f"fast attention chunks mask={mk is not None} causal={causal}", flush=True)
+        ref, _ = e.attention(T(q), T(k), T(v), T(mk) if mk is not None else None, causal, iters=24, mode=0,
+                             return_probs=True)
+        ref = H(ref)
+        for rows in (7, 64, 130, 256, 512):
+            got = _attention_ws(q, k, v, mk, causal, rows)
+            assert np.array_equal(got, ref, equal_nan=True), (rows, mk is not None, causal)
+        for h in (0, 15):
+            sl = (slice(0, 1), slice(h, h + 1))
+            assert np.array_equal(ref[sl], rl.orc_attention_lanes(q[sl], k[sl], v[sl], mk, causal, 24, 0)), h
