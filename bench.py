@@ -592,6 +592,22 @@ def bench_block_ops(torch, ext, dev, g):
                                          "linear_TFLOPs": round(644.2e9 / t / 1e12, 3),
                                          "per_op_ms": parts, **_dist_fields(t, 1e3, "ms")}
         print(f"# llama block FAST: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
+        # one training step of it: forward, then backward of a fixed output
+        # gradient through every autograd function (weight, input and
+        # attention gradients)
+        xg = xb.clone().requires_grad_(True)
+        gy = dev_normal((1, 2048, 4096), 1, dev)
+
+        def train_step():
+            blk(xg, is_causal=True).backward(gy)
+
+        train_step()
+        torch.cuda.synchronize()
+        t = _events_time(train_step, 3, torch, dist_calls=5)
+        blk.zero_grad(set_to_none=True)
+        out["llama_block_T2048_fast_train_step"] = {"ms": round(t * 1e3, 2), **_dist_fields(t, 1e3, "ms")}
+        print(f"# llama block FAST forward + backward: {t * 1e3:.1f} ms", file=sys.stderr, flush=True)
+        del xg, gy
     finally:
         rt.rac_set_mode(prev_mode)
         rt.rac_set_precision(prev_iters)
