@@ -614,7 +614,7 @@ def bench_block_ops(torch, ext, dev, g):
     del blk, xb
 
     # attention core of config 5 through RAC (rac_attention_dev): [1, 32, 2048,
-    # 128], causal, CORDIC mode n = 16; Q K^T and P V each 17.2 G causal MACs
+    # 128], causal, CORDIC mode n = 16; Q K^T and P V 8.6 G causal MACs each
     Ba, Ha, Ta, Da = 1, 32, 2048, 128
     qa, ka, va = (dev_normal((Ba, Ha, Ta, Da), i, dev) for i in range(3))
     oa = torch.empty_like(qa)
