@@ -8,8 +8,11 @@ over synthetic U[-1,1] operands resident in HBM.  value = 2*4096^3 / t.
 
 Also measured in the same run (fields "ops" and "cpu_baseline"):
   * the matmul at n = 8 and 24, and config 1 (1024^3, n = 16) both
-    device-resident and through the synchronous rac.h call on host buffers;
-  * the Llama block (config 5) at n = 8/16/24 with a per-op breakdown;
+    device-resident and through the synchronous rac.h call on host buffers,
+    and in FAST mode (the rac_torch default MAC, on the matrix cores);
+  * the Llama block (config 5) at n = 8/16/24 with a per-op breakdown, and
+    in rac_torch's default configuration (FAST): forward, per-op breakdown
+    and one training step (forward + backward);
   * the config-5 attention core through RAC ([1,32,2048,128], causal, n=16)
     and the Q8_0 decode GEMV (11008x4096, 32000x4096, 65536x8192; HBM GB/s);
   * softmax 4096x4096 N(0, std 2) at n = 8/16/24, RoPE on Q and K
