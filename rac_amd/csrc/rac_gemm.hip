@@ -37,7 +37,8 @@ namespace rac {
 // step-major (8 interleaved chains in the 4x4 register tile).
 constexpr int kGroupRows = 2;
 // Fewer block tiles than this (4 per CU) leave SIMDs with one wave or none;
-// such launches step down to a smaller tile (64x64, then 32x32).
+// such launches step down to a smaller tile (64x64, then 32x32; the CORDIC
+// and SHIFTADD 64x64 tile down to 2 blocks per CU).
 constexpr long kMinTiles = 1024;
 
 // Offset of a lane's i-th row (or column) inside the block tile, for the
@@ -770,6 +771,13 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
                 return launch_cfg<MODE, NITER, TA, TB, FUSED, 0, 16, 8>(g, s);
         }
         if (tiles(16 * kBig, 16 * kBig) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, kBig>(g, s);
+        if constexpr (kBig == 4) {
+            // CORDIC / SHIFTADD: two 64x64 blocks per CU (2 waves per SIMD,
+            // 16 MAC chains each) still beat 32x32 blocks (measured, same
+            // bits: 512-1023 blocks 5-6% faster, e.g. the attention core's
+            // P V chunks 32 x 512 x 128 x K; at one block per CU 43% slower)
+            if (tiles(64, 64) >= 2 * device_cus()) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
+        }
         if constexpr (kBig == 8) {
             if (tiles(64, 64) >= kMinTiles) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
         }

@@ -202,9 +202,11 @@ def test_cordic_matmul_4096_sampled(iters):
 # Launches pick their register tile from the block count: (3996, 4000) fills
 # whole rounds of 256x128 blocks on 256 CUs (FAST 16x8 per lane), (4100,
 # 4097) has >= 1024 128x128 blocks (FAST 8x8, CORDIC / SHIFTADD 4x4), (2050,
-# 2049) >= 1024 64x64 blocks but fewer 128x128 ones (4x4 for every mode), and
-# small shapes take 2x2.  Each is ragged on both edges.
-TILE_SHAPES = [(3996, 4000, 19), (4100, 4097, 21), (2050, 2049, 37), (90, 70, 50)]
+# 2049) >= 1024 64x64 blocks but fewer 128x128 ones (4x4 for every mode),
+# (1500, 1400) 528 64x64 blocks (CORDIC / SHIFTADD 4x4, FAST 2x2), and
+# small shapes take 2x2.  Each is ragged on both edges; K < 128 keeps FAST
+# on the VALU tiles.
+TILE_SHAPES = [(3996, 4000, 19), (4100, 4097, 21), (2050, 2049, 37), (1500, 1400, 45), (90, 70, 50)]
 
 
 @pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24), (2, 8), (1, 5)])
