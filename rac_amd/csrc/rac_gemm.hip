@@ -20,12 +20,13 @@
 // and reads only 2 ds_read_b128 per 16 MACs; the rotations of those MACs
 // advance step-major, so independent FMA chains interleave in each wave's
 // instruction stream.  FAST mode (1 FMA per MAC) runs on the matrix cores
-// (gemm_mfma_fast_kernel, below) when its 128x128 tiles fill the CUs and
+// (gemm_mfma_fast_kernel, below) when it has enough 128x128 blocks and
 // K >= 128; otherwise on VALU tiles of 8x8 or 16x8 per lane (8x8 split in
 // 4x4 groups 64 apart, conflict-free LDS reads), the k loop unrolled by 2,
 // bound by LDS bandwidth (128 B/clk/CU) as much as by the FMA rate.
 // Launches with fewer than 1024 block tiles step down to 64x64, then 32x32
-// (2x2 per lane) so every SIMD holds several waves.  The next K-tile is
+// (2x2 per lane; CORDIC and SHIFTADD below 2 blocks of 64x64 per CU) so
+// every SIMD holds several waves.  The next K-tile is
 // prefetched into registers while the current one is computed.
 #include <hip/hip_runtime.h>
 #include <atomic>
