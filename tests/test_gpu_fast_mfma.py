@@ -262,3 +262,22 @@ def test_fast_attention_chunks_mfma():
         for h in (0, 15):
             sl = (slice(0, 1), slice(h, h + 1))
             assert np.array_equal(ref[sl], rl.orc_attention_lanes(q[sl], k[sl], v[sl], mk, causal, 24, 0)), h
+
+
+@pytest.mark.parametrize("act", [0, 3])
+def test_fast_mfma_linear_backward(act):
+    """The FAST training products at MFMA sizes: fused_linear_backward's
+    grad_input (d W, NN) and grad_weight (d^T x, TN) bit-exact vs the
+    checker, d = the activation gradient of the saved pre-activations."""
+    e = ext()
+    M, N, K = 1024, 2304, 1030         # 144 / 72 / 162 blocks of 128 x 128
+    x = rl.gen_normal((M, K), seed=31)
+    w = rl.gen_normal((N, K), seed=32, std=0.05)
+    b = rl.gen_normal(N, seed=33)
+    g = rl.gen_normal((M, N), seed=34)
+    _, pre = e.fused_linear_forward(T(x), T(w), T(b), act, iters=24, mode=0, return_pre=True)
+    d = H(e.act_grad(T(g), pre, act, iters=24)) if act else g
+    gi, gw, gb = e.fused_linear_backward(T(g), T(x), T(w), T(b), pre, act, True, iters=24, mode=0)
+    assert np.array_equal(H(gi), rl.orc_matmul(d, w, M, K, N, 24, 0))
+    assert np.array_equal(H(gw), rl.orc_matmul(d, x, N, K, M, 24, 0, ta=1))
+    assert np.allclose(H(gb), d.astype(np.float64).sum(0), rtol=1e-5, atol=1e-5)
