@@ -279,6 +279,26 @@ def bench_gpu(args):
           file=sys.stderr, flush=True)
     del A1, B1, C1
 
+    # Decode-time linears (one token): x[1, K] @ W[N, K]^T, the few-row GEMM
+    # path, FAST and CORDIC n = 16; the weights are read once (N*K*4 bytes)
+    for (Nd, Kd) in ((4096, 4096), (11008, 4096)):
+        xd = dev_uniform((1, Kd), 2, dev)
+        wd = dev_uniform((Nd, Kd), 3, dev)
+        yd = torch.empty((1, Nd), device=dev)
+        for mode_name, mode, nit in (("fast", ext.MODE_FAST, 24), ("cordic_n16", ext.MODE_CORDIC, 16)):
+            def dec():
+                rc = lib.rac_gemm_dev(xd.data_ptr(), wd.data_ptr(), yd.data_ptr(), 1, Nd, Kd, 0, 1, 1.0, 0.0,
+                                      nit, mode, stream)
+                if rc:
+                    raise RuntimeError(lib.rac_last_error())
+            dec()
+            torch.cuda.synchronize()
+            t = _events_time(dec, 10, torch)
+            ops[f"decode_linear_1x{Nd}x{Kd}_{mode_name}"] = {
+                "us": round(t * 1e6, 2), "weights_GBps": round(Nd * Kd * 4 / t / 1e9, 1), **_dist_fields(t, 1e6, "us")}
+            print(f"# decode linear 1x{Nd}x{Kd} {mode_name}: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
+        del xd, wd, yd
+
     if not args.matmul_only:
         ops.update(bench_row_ops(torch, ext, dev, g))
         ops.update(bench_block_ops(torch, ext, dev, g))

@@ -803,6 +803,11 @@ static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s
 }
 
 static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStream_t s) {
+    if (g.sched == 0 && !ta && g.M <= kSkinnyMaxRows) {
+        const SkinnyArgs k{g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, g.batch, g.sa, g.sb, g.sc,
+                           g.ep, g.fused, tb != 0, g.k_causal, g.exact_specials, g.row0};
+        return gemm_skinny_launch(k, mode, s);
+    }
     if (mode == kModeFast) return launch_layout<kModeFast, 0>(ta, tb, g, s);
     if (mode == kModeShiftAdd) return launch_layout<kModeShiftAdd, 0>(ta, tb, g, s);
     switch (g.iters) {

@@ -1,0 +1,262 @@
+// rac_gemm_skinny.hip — the RAC GEMM for products with few rows of op(A)
+// (M <= 16: decode-time linears, one token or a few), all three MACs.
+//
+// Each output is ONE accumulator over k = 0..K-1 in order (rac_fma_iters,
+// rac_kernels.hip:204-219), so a product of M rows has only M * N serial
+// chains.  The block tiles of gemm_kernel give such a product few
+// workgroups with most of their rows empty (1 x 4096 x 4096 NT ran ~200 us
+// in FAST mode and ~1 ms in CORDIC mode n = 16).  Here the per-MAC work and
+// the serial fold are separated:
+//   * a workgroup owns 16 output columns and every row (grid x = N / 16, so
+//     N = 4096 already fills the 256 CUs) and walks K in tiles of KT;
+//   * A's M x KT and B's KT x 16 slices go global -> registers -> LDS (the
+//     next tile's loads in flight during the current tile's work);
+//   * all 256 lanes then compute the per-MAC terms of the tile, 4
+//     consecutive k at a time: CORDIC the rotation of (a ^ sign(b), 0)
+//     and its gain correction p = R_n(.) * (1/K-hat(n)) (rac_kernels.hip:
+//     140-185; the literal chain for inputs outside the strength-reduced
+//     one's range, as gemm_kernel), SHIFTADD the shift-add product
+//     (rac_kernels.hip:85-122); FAST has no term to prepare;
+//   * lane m * 16 + n folds output (m, n) over the tile's k in order:
+//     fma(p, |b|, acc), acc + prod or fma(a, b, acc), exactly the MAC of
+//     gemm_kernel, so every result has the same bits as there and in the
+//     reference.
+// Every MAC's rotation or shift-add product is still computed, per MAC.
+#include <hip/hip_runtime.h>
+#include "rac_act.hpp"
+
+namespace rac {
+
+constexpr int kSkCols = 16;                     // output columns per workgroup
+
+// Where the per-MAC terms are computed.  FAST has none.  With 16 rows
+// (256 outputs, one per lane) each lane computes its own MACs' terms and
+// folds them at once ("own"); with fewer rows every lane computes terms
+// for the tile into LDS and the lanes owning outputs fold them ("shared").
+// k per tile keeps the workgroup's LDS under 64 KB.
+template <int MODE, int MT>
+struct SkCfg {
+    static constexpr bool kShared = MODE != kModeFast && MT * kSkCols < 256;
+    static constexpr bool kOwn = MODE != kModeFast && MT * kSkCols == 256;
+    static constexpr int kKT = !kShared ? (kOwn ? 128 : 256) : (MT == 1 ? 256 : (MT <= 4 ? 128 : 64));
+    static constexpr int kRow = kKT + 4;        // LDS row stride (16 rows cover all banks)
+    static constexpr int kALoads = (MT * kKT + 255) / 256;
+    static constexpr int kBLoads = kSkCols * kKT / 256;
+};
+
+// The CORDIC term of one MAC: the rotation of (a ^ sign(b), 0) times the
+// gain correction, for 4 consecutive k; inputs outside the strength-reduced
+// chain's range take the literal chain when `lit` (rac_kernels.hip:152-163).
+template <int NITER>
+__device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, float* p, int iters, float kinv,
+                                                bool lit) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) p[e] = as_f(as_u(a[e]) ^ (as_u(b[e]) & 0x80000000u));
+    if constexpr (NITER > 0) {
+        cordic_rot_x_vec<NITER, 4>(p);
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = p[e] * cordic_kinv(NITER);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = cordic_rot_x_rt(p[e], iters) * kinv;
+    }
+    if (lit) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (cordic_needs_literal(a[e]))
+                p[e] = cordic_rot_x_literal_rt(as_f(as_u(a[e]) ^ (as_u(b[e]) & 0x80000000u)),
+                                               NITER > 0 ? NITER : iters) *
+                       (NITER > 0 ? cordic_kinv(NITER > 0 ? NITER : 1) : kinv);
+    }
+}
+
+template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
+    float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
+    const int* k_causal, int exact_specials, int row0)
+{
+    using Cfg = SkCfg<MODE, MT>;
+    constexpr int KT = Cfg::kKT, ROW = Cfg::kRow;
+    constexpr bool kShared = Cfg::kShared;
+    __shared__ __attribute__((aligned(16))) float sA[MT][ROW];
+    __shared__ __attribute__((aligned(16))) float sB[kSkCols][ROW];
+    __shared__ __attribute__((aligned(16))) float sP[kShared ? MT * kSkCols : 1][kShared ? ROW : 4];
+    // CORDIC: lit[t & 1] is set when tile t's A slice holds an input outside
+    // the strength-reduced chain's range; two flags, so the next tile's is
+    // cleared while no lane reads it
+    __shared__ int lit[2];
+
+    const int tid = threadIdx.x;
+    const long n0 = (long)blockIdx.x * kSkCols;
+    A += (long)blockIdx.z * sa;
+    B += (long)blockIdx.z * sb;
+    C += (long)blockIdx.z * sc;
+    if (tid == 0) lit[0] = lit[1] = 0;               // ordered before any set by the loop's first barrier
+
+    // element (m, k) of A (row-major M x K) and (k, n) of op(B), zero outside
+    float ra[Cfg::kALoads], rb[Cfg::kBLoads];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int r = 0; r < Cfg::kALoads; r++) {
+            const int idx = tid + r * 256, m = idx / KT, kk = idx % KT;
+            const long gk = (long)k0 + kk;
+            ra[r] = (m < M && idx < MT * KT && gk < K) ? A[(long)m * K + gk] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < Cfg::kBLoads; r++) {
+            const int idx = tid + r * 256;
+            int nn, kk;
+            if constexpr (TB) { nn = idx / KT; kk = idx % KT; }      // W[n][k]: k contiguous
+            else { kk = idx / kSkCols; nn = idx % kSkCols; }         // B[k][n]: n contiguous
+            const long gn = n0 + nn, gk = (long)k0 + kk;
+            rb[r] = (gn < N && gk < K) ? (TB ? B[gn * K + gk] : B[gk * N + gn]) : 0.0f;
+        }
+    };
+    auto store = [&](int t) {
+        bool special = false;
+#pragma unroll
+        for (int r = 0; r < Cfg::kALoads; r++) {
+            const int idx = tid + r * 256;
+            if (idx < MT * KT) sA[idx / KT][idx % KT] = ra[r];
+            if constexpr (MODE == kModeCordic) special |= cordic_needs_literal(ra[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < Cfg::kBLoads; r++) {
+            const int idx = tid + r * 256;
+            if constexpr (TB) sB[idx / KT][idx % KT] = rb[r];
+            else sB[idx % kSkCols][idx / kSkCols] = rb[r];
+        }
+        if constexpr (MODE == kModeCordic) {
+            if (special && exact_specials) lit[t & 1] = 1;
+        }
+    };
+
+    // Causal P V: rows past a query position's key range are exactly 0 in P
+    // and, with every v finite, fma(0, v, acc) == acc (acc starts at +0 and
+    // never becomes -0), so the k loop may stop after the last row's range.
+    int kend = K;
+    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + M);
+
+    const int om = tid / kSkCols, on = tid % kSkCols;   // output owned by lanes tid < MT * 16
+    float acc = 0.0f;
+    load(0);
+    for (int k0 = 0, t = 0; k0 < kend; k0 += KT, t++) {
+        __syncthreads();                                // previous tile's fold done with LDS
+        store(t);
+        __syncthreads();
+        if (k0 + KT < kend) load(k0 + KT);
+        const bool lit_tile = MODE == kModeCordic && lit[t & 1] != 0;
+        if constexpr (kShared) {
+            // per-MAC terms, 4 consecutive k of one (m, n) per step
+            constexpr int kQuads = MT * kSkCols * KT / 4;
+#pragma unroll 2
+            for (int q = tid; q < kQuads; q += 256) {
+                const int kk = (q % (KT / 4)) * 4, mn = q / (KT / 4), m = mn / kSkCols, n = mn % kSkCols;
+                if (m >= M) continue;
+                const float4 a4 = *reinterpret_cast<const float4*>(&sA[m][kk]);
+                const float4 b4 = *reinterpret_cast<const float4*>(&sB[n][kk]);
+                const float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+                float p[4];
+                if constexpr (MODE == kModeCordic) {
+                    sk_cordic_terms<NITER>(a, b, p, iters, kinv, lit_tile);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) p[e] = shiftadd_mul(a[e], b[e], iters);
+                }
+                *reinterpret_cast<float4*>(&sP[mn][kk]) = make_float4(p[0], p[1], p[2], p[3]);
+            }
+            __syncthreads();
+        }
+        if (tid == 0) lit[(t + 1) & 1] = 0;            // tile t+1's flag: set after the loop-top barrier
+        // the serial fold of each output over this tile's k, in order
+        if (tid < MT * kSkCols && om < M) {
+            const int kn = min(KT, kend - k0);
+            // unrolled so the LDS reads of 32 k run ahead of the dependent
+            // chain of FMAs (rolled, each 4-k step waited for its reads;
+            // 64 k ran no faster)
+#pragma unroll 8
+            for (int kk = 0; kk < kn; kk += 4) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&sB[on][kk]);
+                const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+                float t4[4];
+                if constexpr (kShared) {
+                    const float4 p4 = *reinterpret_cast<const float4*>(&sP[tid][kk]);
+                    t4[0] = p4.x; t4[1] = p4.y; t4[2] = p4.z; t4[3] = p4.w;
+                } else {
+                    const float4 a4 = *reinterpret_cast<const float4*>(&sA[om][kk]);
+                    const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+                    if constexpr (MODE == kModeCordic) {
+                        sk_cordic_terms<NITER>(a, b, t4, iters, kinv, lit_tile);
+                    } else if constexpr (MODE == kModeShiftAdd) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) t4[e] = shiftadd_mul(a[e], b[e], iters);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) t4[e] = a[e];
+                    }
+                }
+                // the k-padding of the last tile holds zeros: it leaves acc as is
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if constexpr (MODE == kModeCordic) acc = __builtin_fmaf(t4[e], __builtin_fabsf(b[e]), acc);
+                    else if constexpr (MODE == kModeShiftAdd) acc = acc + t4[e];
+                    else acc = __builtin_fmaf(t4[e], b[e], acc);
+                }
+            }
+        }
+    }
+
+    if (tid < MT * kSkCols && om < M) {
+        const long gn = n0 + on;
+        if (gn < N) {
+            float* cp = C + (long)om * N + gn;
+            // rac_kernels.hip:267-272
+            float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc, beta * *cp) : alpha * acc;
+            if constexpr (FUSED) {
+                // rac_torch.cu:770-775
+                if (ep.bias) v = v + ep.bias[gn];
+                if (ep.pre) ep.pre[(long)om * N + gn] = v;
+                v = act_rt(v, ep.act, iters, ep.khinv);
+            }
+            *cp = v;
+        }
+    }
+}
+
+template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+static hipError_t skinny_cfg(const SkinnyArgs& g, hipStream_t s) {
+    const dim3 grid((unsigned)((g.N + kSkCols - 1) / kSkCols), 1, (unsigned)g.batch);
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, MT>), grid, dim3(256), 0, s, g.A, g.B, g.C, g.M,
+                       g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb, g.sc, g.ep, g.k_causal,
+                       g.exact_specials, g.row0);
+    return hipGetLastError();
+}
+
+template <int MODE, int NITER, bool TB, bool FUSED>
+static hipError_t skinny_rows(const SkinnyArgs& g, hipStream_t s) {
+    if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
+    if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
+    if (g.M <= 8) return skinny_cfg<MODE, NITER, TB, FUSED, 8>(g, s);
+    return skinny_cfg<MODE, NITER, TB, FUSED, 16>(g, s);
+}
+
+template <int MODE, int NITER>
+static hipError_t skinny_layout(const SkinnyArgs& g, hipStream_t s) {
+    if (g.fused) return skinny_rows<MODE, NITER, true, true>(g, s);
+    if (g.tb) return skinny_rows<MODE, NITER, true, false>(g, s);
+    return skinny_rows<MODE, NITER, false, false>(g, s);
+}
+
+hipError_t gemm_skinny_launch(const SkinnyArgs& g, int mode, hipStream_t s) {
+    if (mode == kModeFast) return skinny_layout<kModeFast, 0>(g, s);
+    if (mode == kModeShiftAdd) return skinny_layout<kModeShiftAdd, 0>(g, s);
+    switch (g.iters) {
+        case 8: return skinny_layout<kModeCordic, 8>(g, s);
+        case 16: return skinny_layout<kModeCordic, 16>(g, s);
+        case 24: return skinny_layout<kModeCordic, 24>(g, s);
+        default: return skinny_layout<kModeCordic, 0>(g, s);
+    }
+}
+
+}  // namespace rac

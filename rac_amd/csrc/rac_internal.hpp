@@ -54,6 +54,27 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 // keeps the strength-reduced chain for every input (callers whose parity
 // bar is a summation bound, where subnormal-rounding differences of tiny
 // products are far below it).
+// The same product for M <= 16 rows of A (row-major, not transposed):
+// gemm_launch hands such launches (schedule 0) to this kernel.
+struct SkinnyArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    float alpha, beta;
+    int iters;                 // clamped
+    int batch;
+    long sa, sb, sc;
+    GemmEpilogue ep;
+    bool fused;
+    bool tb;
+    const int* k_causal;
+    int exact_specials;
+    int row0;
+};
+hipError_t gemm_skinny_launch(const SkinnyArgs& g, int mode, hipStream_t s);
+constexpr int kSkinnyMaxRows = 16;
+
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,
                        hipStream_t s, int batch = 1, long sa = 0, long sb = 0, long sc = 0,
