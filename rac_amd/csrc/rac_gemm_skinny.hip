@@ -34,11 +34,17 @@ constexpr int kSkCols = 16;                     // output columns per workgroup
 // folds them at once ("own"); with fewer rows every lane computes terms
 // for the tile into LDS and the lanes owning outputs fold them ("shared").
 // k per tile keeps the workgroup's LDS under 64 KB.
-template <int MODE, int MT>
+// BIGK (FAST, M <= 4): 512-k tiles, taken when the grid has at most one
+// workgroup per CU, whose loads then need twice the bytes in flight
+// (1x4096x4096: 42 -> 31 us); with several workgroups per CU they overlap
+// each other's loads already and the smaller tile is faster (1x11008x4096:
+// 49 against 63 us).
+template <int MODE, int MT, bool BIGK = false>
 struct SkCfg {
     static constexpr bool kShared = MODE != kModeFast && MT * kSkCols < 256;
     static constexpr bool kOwn = MODE != kModeFast && MT * kSkCols == 256;
-    static constexpr int kKT = !kShared ? (kOwn ? 128 : 256) : (MT == 1 ? 256 : (MT <= 4 ? 128 : 64));
+    static constexpr int kKT = MODE == kModeFast ? (BIGK ? 512 : 256)
+                               : kOwn ? 128 : (MT == 1 ? 256 : (MT <= 4 ? 128 : 64));
     static constexpr int kRow = kKT + 4;        // LDS row stride (16 rows cover all banks)
     static constexpr int kALoads = (MT * kKT + 255) / 256;
     static constexpr int kBLoads = kSkCols * kKT / 256;
@@ -70,13 +76,13 @@ __device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, 
     }
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
-    using Cfg = SkCfg<MODE, MT>;
+    using Cfg = SkCfg<MODE, MT, BIGK>;
     constexpr int KT = Cfg::kKT, ROW = Cfg::kRow;
     constexpr bool kShared = Cfg::kShared;
     __shared__ __attribute__((aligned(16))) float sA[MT][ROW];
@@ -224,10 +230,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     }
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK = false>
 static hipError_t skinny_cfg(const SkinnyArgs& g, hipStream_t s) {
     const dim3 grid((unsigned)((g.N + kSkCols - 1) / kSkCols), 1, (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, MT>), grid, dim3(256), 0, s, g.A, g.B, g.C, g.M,
+    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, MT, BIGK>), grid, dim3(256), 0, s, g.A, g.B, g.C, g.M,
                        g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb, g.sc, g.ep, g.k_causal,
                        g.exact_specials, g.row0);
     return hipGetLastError();
@@ -235,6 +241,19 @@ static hipError_t skinny_cfg(const SkinnyArgs& g, hipStream_t s) {
 
 template <int MODE, int NITER, bool TB, bool FUSED>
 static hipError_t skinny_rows(const SkinnyArgs& g, hipStream_t s) {
+    if constexpr (MODE == kModeFast) {
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            (void)hipGetLastError();
+            cus = 256;
+        }
+        const long wgs = (long)((g.N + kSkCols - 1) / kSkCols) * g.batch;
+        if (g.M <= 4 && wgs <= cus) {
+            if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1, true>(g, s);
+            return skinny_cfg<MODE, NITER, TB, FUSED, 4, true>(g, s);
+        }
+    }
     if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
     if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
     if (g.M <= 8) return skinny_cfg<MODE, NITER, TB, FUSED, 8>(g, s);

@@ -60,10 +60,13 @@ def gemm(A, B, M, N, K, tb, iters, mode, alpha=1.0, beta=0.0, C0=None):
 
 
 MODES = [(0, 24), (1, 16), (1, 8), (1, 24), (1, 5), (2, 16), (2, 24)]
-# (1, 4096, 1030): one row (M-tile 1, KT 256, K ragged); (3, 2100, 777):
-# M-tile 4; (7, 1500, 333): M-tile 8; (16, 1000, 300) and (9, 35, 67):
-# M-tile 16; (1, 5, 3): tiny.
-SHAPES = [(1, 4096, 1030), (3, 2100, 777), (7, 1500, 333), (16, 1000, 300), (9, 35, 67), (1, 5, 3)]
+# (1, 4096, 1030): one row (M-tile 1, K ragged); (3, 2100, 777): M-tile 4
+# (FAST: 512-k tiles on grids of at most one workgroup per CU, both);
+# (2, 5000, 300): M-tile 4 on a wider grid (FAST: 256-k tiles); (7, 1500,
+# 333): M-tile 8; (16, 1000, 300) and (9, 35, 67): M-tile 16 (CORDIC /
+# SHIFTADD: each lane computes its own terms); (1, 5, 3): tiny.
+SHAPES = [(1, 4096, 1030), (3, 2100, 777), (2, 5000, 300), (7, 1500, 333), (16, 1000, 300), (9, 35, 67),
+          (1, 5, 3)]
 
 
 @pytest.mark.parametrize("tb", [0, 1])
