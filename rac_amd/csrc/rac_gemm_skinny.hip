@@ -76,6 +76,130 @@ __device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, 
     }
 }
 
+// Global -> registers: element (m, k) of A (row-major M x K) and (k, n) of
+// op(B) for the K-tile at k0, zero outside the matrices.
+template <int MT, int KT, bool TB>
+__device__ __forceinline__ void sk_load(const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                                        int K, long n0, int k0, float* ra, float* rb) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < (MT * KT + 255) / 256; r++) {
+        const int idx = tid + r * 256, m = idx / KT, kk = idx % KT;
+        const long gk = (long)k0 + kk;
+        ra[r] = (m < M && idx < MT * KT && gk < K) ? A[(long)m * K + gk] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < kSkCols * KT / 256; r++) {
+        const int idx = tid + r * 256;
+        int nn, kk;
+        if constexpr (TB) { nn = idx / KT; kk = idx % KT; }      // W[n][k]: k contiguous
+        else { kk = idx / kSkCols; nn = idx % kSkCols; }         // B[k][n]: n contiguous
+        const long gn = n0 + nn, gk = (long)k0 + kk;
+        rb[r] = (gn < N && gk < K) ? (TB ? B[gn * K + gk] : B[gk * N + gn]) : 0.0f;
+    }
+}
+
+// Registers -> LDS (A as [MT][ROW], B as [16][ROW], k contiguous); true when
+// this lane staged a CORDIC input outside the strength-reduced chain's range.
+template <int MODE, int MT, int KT, int ROW, bool TB>
+__device__ __forceinline__ bool sk_store(float* sA, float* sB, const float* ra, const float* rb) {
+    const int tid = threadIdx.x;
+    bool special = false;
+#pragma unroll
+    for (int r = 0; r < (MT * KT + 255) / 256; r++) {
+        const int idx = tid + r * 256;
+        if (idx < MT * KT) sA[(idx / KT) * ROW + idx % KT] = ra[r];
+        if constexpr (MODE == kModeCordic) special |= cordic_needs_literal(ra[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < kSkCols * KT / 256; r++) {
+        const int idx = tid + r * 256;
+        if constexpr (TB) sB[(idx / KT) * ROW + idx % KT] = rb[r];
+        else sB[(idx % kSkCols) * ROW + idx / kSkCols] = rb[r];
+    }
+    return special;
+}
+
+// The tile's per-MAC terms into sP (row m * 16 + n), 4 consecutive k of one
+// (m, n) per step, spread over lanes L0 .. L0 + NL - 1 (the others return).
+template <int MODE, int NITER, int MT, int KT, int ROW, int L0 = 0, int NL = 256>
+__device__ __forceinline__ void sk_terms(const float* sA, const float* sB, float* sP, int M, int iters, float kinv,
+                                         bool lit) {
+    constexpr int kQuads = MT * kSkCols * KT / 4;
+    if ((int)threadIdx.x < L0) return;
+#pragma unroll 2
+    for (int q = (int)threadIdx.x - L0; q < kQuads; q += NL) {
+        const int kk = (q % (KT / 4)) * 4, mn = q / (KT / 4), m = mn / kSkCols, n = mn % kSkCols;
+        if (m >= M) continue;
+        const float4 a4 = *reinterpret_cast<const float4*>(&sA[m * ROW + kk]);
+        const float4 b4 = *reinterpret_cast<const float4*>(&sB[n * ROW + kk]);
+        const float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+        float p[4];
+        if constexpr (MODE == kModeCordic) {
+            sk_cordic_terms<NITER>(a, b, p, iters, kinv, lit);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) p[e] = shiftadd_mul(a[e], b[e], iters);
+        }
+        *reinterpret_cast<float4*>(&sP[mn * ROW + kk]) = make_float4(p[0], p[1], p[2], p[3]);
+    }
+}
+
+// The serial fold of output (om, on) over kn k of a tile, in order: the
+// terms from sP row `prow` (SHARED), or computed here from sA row om (own
+// terms; FAST: the A element itself).  Zero k-padding leaves acc as is.
+template <int MODE, int NITER, int ROW, bool SHARED>
+__device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const float* sP, int om, int on,
+                                         int prow, int kn, float acc, int iters, float kinv, bool lit) {
+    // unrolled so the LDS reads of 32 k run ahead of the dependent chain of
+    // FMAs (rolled, each 4-k step waited for its reads; 64 k ran no faster)
+#pragma unroll 8
+    for (int kk = 0; kk < kn; kk += 4) {
+        const float4 b4 = *reinterpret_cast<const float4*>(&sB[on * ROW + kk]);
+        const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+        float t4[4];
+        if constexpr (SHARED) {
+            const float4 p4 = *reinterpret_cast<const float4*>(&sP[prow * ROW + kk]);
+            t4[0] = p4.x; t4[1] = p4.y; t4[2] = p4.z; t4[3] = p4.w;
+        } else {
+            const float4 a4 = *reinterpret_cast<const float4*>(&sA[om * ROW + kk]);
+            const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+            if constexpr (MODE == kModeCordic) {
+                sk_cordic_terms<NITER>(a, b, t4, iters, kinv, lit);
+            } else if constexpr (MODE == kModeShiftAdd) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) t4[e] = shiftadd_mul(a[e], b[e], iters);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) t4[e] = a[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if constexpr (MODE == kModeCordic) acc = __builtin_fmaf(t4[e], __builtin_fabsf(b[e]), acc);
+            else if constexpr (MODE == kModeShiftAdd) acc = acc + t4[e];
+            else acc = __builtin_fmaf(t4[e], b[e], acc);
+        }
+    }
+    return acc;
+}
+
+// alpha / beta, bias and activation of output (m, gn), as gemm_kernel's
+template <bool FUSED>
+__device__ __forceinline__ void sk_epilogue(float* C, int N, int m, long gn, float acc, float alpha, float beta,
+                                            const GemmEpilogue& ep, int iters) {
+    float* cp = C + (long)m * N + gn;
+    // rac_kernels.hip:267-272
+    float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc, beta * *cp) : alpha * acc;
+    if constexpr (FUSED) {
+        // rac_torch.cu:770-775
+        if (ep.bias) v = v + ep.bias[gn];
+        if (ep.pre) ep.pre[(long)m * N + gn] = v;
+        v = act_rt(v, ep.act, iters, ep.khinv);
+    }
+    *cp = v;
+}
+
 template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
@@ -85,9 +209,9 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     using Cfg = SkCfg<MODE, MT, BIGK>;
     constexpr int KT = Cfg::kKT, ROW = Cfg::kRow;
     constexpr bool kShared = Cfg::kShared;
-    __shared__ __attribute__((aligned(16))) float sA[MT][ROW];
-    __shared__ __attribute__((aligned(16))) float sB[kSkCols][ROW];
-    __shared__ __attribute__((aligned(16))) float sP[kShared ? MT * kSkCols : 1][kShared ? ROW : 4];
+    __shared__ __attribute__((aligned(16))) float sA[MT * ROW];
+    __shared__ __attribute__((aligned(16))) float sB[kSkCols * ROW];
+    __shared__ __attribute__((aligned(16))) float sP[kShared ? MT * kSkCols * ROW : 4];
     // CORDIC: lit[t & 1] is set when tile t's A slice holds an input outside
     // the strength-reduced chain's range; two flags, so the next tile's is
     // cleared while no lane reads it
@@ -100,44 +224,6 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     C += (long)blockIdx.z * sc;
     if (tid == 0) lit[0] = lit[1] = 0;               // ordered before any set by the loop's first barrier
 
-    // element (m, k) of A (row-major M x K) and (k, n) of op(B), zero outside
-    float ra[Cfg::kALoads], rb[Cfg::kBLoads];
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int r = 0; r < Cfg::kALoads; r++) {
-            const int idx = tid + r * 256, m = idx / KT, kk = idx % KT;
-            const long gk = (long)k0 + kk;
-            ra[r] = (m < M && idx < MT * KT && gk < K) ? A[(long)m * K + gk] : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < Cfg::kBLoads; r++) {
-            const int idx = tid + r * 256;
-            int nn, kk;
-            if constexpr (TB) { nn = idx / KT; kk = idx % KT; }      // W[n][k]: k contiguous
-            else { kk = idx / kSkCols; nn = idx % kSkCols; }         // B[k][n]: n contiguous
-            const long gn = n0 + nn, gk = (long)k0 + kk;
-            rb[r] = (gn < N && gk < K) ? (TB ? B[gn * K + gk] : B[gk * N + gn]) : 0.0f;
-        }
-    };
-    auto store = [&](int t) {
-        bool special = false;
-#pragma unroll
-        for (int r = 0; r < Cfg::kALoads; r++) {
-            const int idx = tid + r * 256;
-            if (idx < MT * KT) sA[idx / KT][idx % KT] = ra[r];
-            if constexpr (MODE == kModeCordic) special |= cordic_needs_literal(ra[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < Cfg::kBLoads; r++) {
-            const int idx = tid + r * 256;
-            if constexpr (TB) sB[idx / KT][idx % KT] = rb[r];
-            else sB[idx % kSkCols][idx / kSkCols] = rb[r];
-        }
-        if constexpr (MODE == kModeCordic) {
-            if (special && exact_specials) lit[t & 1] = 1;
-        }
-    };
-
     // Causal P V: rows past a query position's key range are exactly 0 in P
     // and, with every v finite, fma(0, v, acc) == acc (acc starts at +0 and
     // never becomes -0), so the k loop may stop after the last row's range.
@@ -145,89 +231,101 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + M);
 
     const int om = tid / kSkCols, on = tid % kSkCols;   // output owned by lanes tid < MT * 16
+    float ra[(MT * KT + 255) / 256], rb[kSkCols * KT / 256];
     float acc = 0.0f;
-    load(0);
+    sk_load<MT, KT, TB>(A, B, M, N, K, n0, 0, ra, rb);
     for (int k0 = 0, t = 0; k0 < kend; k0 += KT, t++) {
         __syncthreads();                                // previous tile's fold done with LDS
-        store(t);
+        if (sk_store<MODE, MT, KT, ROW, TB>(sA, sB, ra, rb) && exact_specials) lit[t & 1] = 1;
         __syncthreads();
-        if (k0 + KT < kend) load(k0 + KT);
+        if (k0 + KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, k0 + KT, ra, rb);
         const bool lit_tile = MODE == kModeCordic && lit[t & 1] != 0;
         if constexpr (kShared) {
-            // per-MAC terms, 4 consecutive k of one (m, n) per step
-            constexpr int kQuads = MT * kSkCols * KT / 4;
-#pragma unroll 2
-            for (int q = tid; q < kQuads; q += 256) {
-                const int kk = (q % (KT / 4)) * 4, mn = q / (KT / 4), m = mn / kSkCols, n = mn % kSkCols;
-                if (m >= M) continue;
-                const float4 a4 = *reinterpret_cast<const float4*>(&sA[m][kk]);
-                const float4 b4 = *reinterpret_cast<const float4*>(&sB[n][kk]);
-                const float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
-                float p[4];
-                if constexpr (MODE == kModeCordic) {
-                    sk_cordic_terms<NITER>(a, b, p, iters, kinv, lit_tile);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) p[e] = shiftadd_mul(a[e], b[e], iters);
-                }
-                *reinterpret_cast<float4*>(&sP[mn][kk]) = make_float4(p[0], p[1], p[2], p[3]);
-            }
+            sk_terms<MODE, NITER, MT, KT, ROW>(sA, sB, sP, M, iters, kinv, lit_tile);
             __syncthreads();
         }
         if (tid == 0) lit[(t + 1) & 1] = 0;            // tile t+1's flag: set after the loop-top barrier
-        // the serial fold of each output over this tile's k, in order
-        if (tid < MT * kSkCols && om < M) {
-            const int kn = min(KT, kend - k0);
-            // unrolled so the LDS reads of 32 k run ahead of the dependent
-            // chain of FMAs (rolled, each 4-k step waited for its reads;
-            // 64 k ran no faster)
-#pragma unroll 8
-            for (int kk = 0; kk < kn; kk += 4) {
-                const float4 b4 = *reinterpret_cast<const float4*>(&sB[on][kk]);
-                const float b[4] = {b4.x, b4.y, b4.z, b4.w};
-                float t4[4];
-                if constexpr (kShared) {
-                    const float4 p4 = *reinterpret_cast<const float4*>(&sP[tid][kk]);
-                    t4[0] = p4.x; t4[1] = p4.y; t4[2] = p4.z; t4[3] = p4.w;
-                } else {
-                    const float4 a4 = *reinterpret_cast<const float4*>(&sA[om][kk]);
-                    const float a[4] = {a4.x, a4.y, a4.z, a4.w};
-                    if constexpr (MODE == kModeCordic) {
-                        sk_cordic_terms<NITER>(a, b, t4, iters, kinv, lit_tile);
-                    } else if constexpr (MODE == kModeShiftAdd) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) t4[e] = shiftadd_mul(a[e], b[e], iters);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) t4[e] = a[e];
-                    }
-                }
-                // the k-padding of the last tile holds zeros: it leaves acc as is
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    if constexpr (MODE == kModeCordic) acc = __builtin_fmaf(t4[e], __builtin_fabsf(b[e]), acc);
-                    else if constexpr (MODE == kModeShiftAdd) acc = acc + t4[e];
-                    else acc = __builtin_fmaf(t4[e], b[e], acc);
-                }
-            }
-        }
+        if (tid < MT * kSkCols && om < M)
+            acc = sk_fold<MODE, NITER, ROW, kShared>(sA, sB, sP, om, on, tid, min(KT, kend - k0), acc, iters, kinv,
+                                                     lit_tile);
     }
+    if (tid < MT * kSkCols && om < M && n0 + on < N)
+        sk_epilogue<FUSED>(C, N, om, n0 + on, acc, alpha, beta, ep, iters);
+}
 
-    if (tid < MT * kSkCols && om < M) {
-        const long gn = n0 + on;
-        if (gn < N) {
-            float* cp = C + (long)om * N + gn;
-            // rac_kernels.hip:267-272
-            float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc, beta * *cp) : alpha * acc;
-            if constexpr (FUSED) {
-                // rac_torch.cu:770-775
-                if (ep.bias) v = v + ep.bias[gn];
-                if (ep.pre) ep.pre[(long)om * N + gn] = v;
-                v = act_rt(v, ep.act, iters, ep.khinv);
-            }
-            *cp = v;
-        }
+// The shared terms pipelined (CORDIC, M <= 4): B slices and terms
+// in two LDS buffers, so waves 1-3 compute tile t+1's terms while wave 0's
+// output lanes fold tile t (in the form above the fold, a serial chain of
+// KT dependent operations per output, waited for the terms and the terms
+// for the fold).  Tile t+1's A slice has one buffer: only the terms read it.
+// The prologue's terms of tile 0 use every lane.
+template <int MT>
+struct SkPipeCfg {
+    static constexpr int kKT = MT == 1 ? 128 : 64;
+    static constexpr int kRow = kKT + 4;
+};
+
+template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+__global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
+    float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
+    const int* k_causal, int exact_specials, int row0)
+{
+    constexpr int KT = SkPipeCfg<MT>::kKT, ROW = SkPipeCfg<MT>::kRow;
+    __shared__ __attribute__((aligned(16))) float sA[MT * ROW];
+    __shared__ __attribute__((aligned(16))) float sB[2][kSkCols * ROW];
+    __shared__ __attribute__((aligned(16))) float sP[2][MT * kSkCols * ROW];
+    // lit[t & 1]: tile t's A slice holds an input outside the strength-
+    // reduced chain's range (set when the tile is staged, read by its terms,
+    // cleared two tiles later)
+    __shared__ int lit[2];
+
+    const int tid = threadIdx.x;
+    const long n0 = (long)blockIdx.x * kSkCols;
+    A += (long)blockIdx.z * sa;
+    B += (long)blockIdx.z * sb;
+    C += (long)blockIdx.z * sc;
+    if (tid == 0) lit[0] = lit[1] = 0;
+
+    int kend = K;                                        // causal P V, as gemm_skinny_kernel
+    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + M);
+
+    const int om = tid / kSkCols, on = tid % kSkCols;
+    float ra[(MT * KT + 255) / 256], rb[kSkCols * KT / 256];
+    float acc = 0.0f;
+    // prologue: tile 0 staged and its terms computed, tile 1 in flight
+    sk_load<MT, KT, TB>(A, B, M, N, K, n0, 0, ra, rb);
+    __syncthreads();                                     // flags cleared
+    if (sk_store<MODE, MT, KT, ROW, TB>(sA, sB[0], ra, rb) && exact_specials) lit[0] = 1;
+    __syncthreads();
+    if (KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, KT, ra, rb);
+    sk_terms<MODE, NITER, MT, KT, ROW>(sA, sB[0], sP[0], M, iters, kinv, MODE == kModeCordic && lit[0] != 0);
+    for (int k0 = 0, t = 0; k0 < kend; k0 += KT, t++) {
+        const int cur = t & 1, nxt = cur ^ 1;
+        const bool more = k0 + KT < kend;
+        __syncthreads();                                 // tile t's terms written; tile t-1 folded
+        if (more && sk_store<MODE, MT, KT, ROW, TB>(sA, sB[nxt], ra, rb) && exact_specials) lit[nxt] = 1;
+        __syncthreads();                                 // tile t+1 staged
+        if (k0 + 2 * KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, k0 + 2 * KT, ra, rb);
+        if (more)
+            sk_terms<MODE, NITER, MT, KT, ROW, 64, 192>(sA, sB[nxt], sP[nxt], M, iters, kinv,
+                                                        MODE == kModeCordic && lit[nxt] != 0);
+        if (tid == 0) lit[cur] = 0;                      // tile t+2's flag (tile t's was read a phase ago)
+        if (tid < MT * kSkCols && om < M)
+            acc = sk_fold<MODE, NITER, ROW, true>(sA, sB[cur], sP[cur], om, on, tid, min(KT, kend - k0), acc, iters,
+                                                  kinv, false);
     }
+    if (tid < MT * kSkCols && om < M && n0 + on < N)
+        sk_epilogue<FUSED>(C, N, om, n0 + on, acc, alpha, beta, ep, iters);
+}
+
+template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+static hipError_t skinny_pipe_cfg(const SkinnyArgs& g, hipStream_t s) {
+    const dim3 grid((unsigned)((g.N + kSkCols - 1) / kSkCols), 1, (unsigned)g.batch);
+    hipLaunchKernelGGL((gemm_skinny_pipe_kernel<MODE, NITER, TB, FUSED, MT>), grid, dim3(256), 0, s, g.A, g.B, g.C,
+                       g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb, g.sc, g.ep,
+                       g.k_causal, g.exact_specials, g.row0);
+    return hipGetLastError();
 }
 
 template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK = false>
@@ -253,9 +351,18 @@ static hipError_t skinny_rows(const SkinnyArgs& g, hipStream_t s) {
             if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1, true>(g, s);
             return skinny_cfg<MODE, NITER, TB, FUSED, 4, true>(g, s);
         }
+        if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
+        if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
+    } else if constexpr (MODE == kModeCordic) {
+        if (g.M == 1) return skinny_pipe_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
+        if (g.M <= 4) return skinny_pipe_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
+    } else {
+        // SHIFTADD's terms (a shift-add product each) outweigh the fold:
+        // they keep all four waves (pipelined on three: 1x4096x4096 213 ->
+        // 297 us)
+        if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
+        if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
     }
-    if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
-    if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
     if (g.M <= 8) return skinny_cfg<MODE, NITER, TB, FUSED, 8>(g, s);
     return skinny_cfg<MODE, NITER, TB, FUSED, 16>(g, s);
 }
