@@ -690,7 +690,9 @@ static int attention_launch(const float* q, const float* k, const float* v, cons
         const long ct = (long)c * t;
         rc = attention_probs_chunk(q, k, mask, causal, ws, bh, t, d, t0, c, iters, mode, s);
         if (rc) return rc;
-        const int psched = (causal && c == t) ? 2 : 0;
+        // causal: row tiles paired for balance (the GEMM falls back to the
+        // plain schedule where pairing leaves too few workgroups)
+        const int psched = causal ? 2 : 0;
         rc = check_hip(gemm_launch(0, 0, ws, v, out + t0 * d, c, d, t, 1.0f, 0.0f, iters, mode, s, bh, ct, td, td,
                                    psched, flag, false, (int)t0),
                        "rac_attention output launch");

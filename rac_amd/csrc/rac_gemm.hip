@@ -722,7 +722,20 @@ static hipError_t launch_tiles(const GemmArgs& g, hipStream_t s) {
             }
         }
     }
-    if constexpr (SCHED == 1 || SCHED == 2) {
+    if constexpr (SCHED == 2) {
+        // Causal P V, row tiles p and nt-1-p per workgroup (equal K sums): on
+        // 64x64 tiles while that gives 2 workgroups per CU, else on 32x32
+        // while 4 per CU (the attention core's 512-row chunks: 4-9% faster
+        // than unpaired), else unpaired (256-row chunks: no gain)
+        const long cus = device_cus();
+        const long pairs4 = (((g.M + 63) / 64 + 1) / 2) * ((g.N + 63) / 64) * (long)g.batch;
+        if (pairs4 >= 2 * cus) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
+        const long pairs2 = (((g.M + 31) / 32 + 1) / 2) * ((g.N + 31) / 32) * (long)g.batch;
+        if (pairs2 >= 4 * cus) return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 2>(g, s);
+        GemmArgs h = g;
+        h.sched = 0;
+        return launch_tiles<MODE, NITER, TA, TB, FUSED, 0>(h, s);
+    } else if constexpr (SCHED == 1) {
         return launch_cfg<MODE, NITER, TA, TB, FUSED, SCHED, 4>(g, s);
     } else {
         auto tiles = [&](long bm, long bn) {
@@ -803,7 +816,9 @@ static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s
 }
 
 static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStream_t s) {
-    if (g.sched == 0 && !ta && g.M <= kSkinnyMaxRows) {
+    // few rows (schedule 2, the causal P V, is then the plain product with
+    // its causal K limit, which the few-row kernel applies)
+    if ((g.sched == 0 || g.sched == 2) && !ta && g.M <= kSkinnyMaxRows) {
         const SkinnyArgs k{g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, g.batch, g.sa, g.sb, g.sc,
                            g.ep, g.fused, tb != 0, g.k_causal, g.exact_specials, g.row0};
         return gemm_skinny_launch(k, mode, s);

@@ -55,7 +55,7 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 // bar is a summation bound, where subnormal-rounding differences of tiny
 // products are far below it).
 // The same product for M <= 16 rows of A (row-major, not transposed):
-// gemm_launch hands such launches (schedule 0) to this kernel.
+// gemm_launch hands such launches (schedules 0 and 2) to this kernel.
 struct SkinnyArgs {
     const float* A;
     const float* B;
