@@ -298,6 +298,24 @@ def bench_gpu(args):
                 "us": round(t * 1e6, 2), "weights_GBps": round(Nd * Kd * 4 / t / 1e9, 1), **_dist_fields(t, 1e6, "us")}
             print(f"# decode linear 1x{Nd}x{Kd} {mode_name}: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
         del xd, wd, yd
+    # a matrix-vector product through rac_matmul: A[4096, 4096] @ x[4096, 1]
+    # (the few-column path)
+    Am = dev_uniform((4096, 4096), 4, dev)
+    xm = dev_uniform((4096, 1), 5, dev)
+    ym = torch.empty((4096, 1), device=dev)
+    for mode_name, mode, nit in (("fast", ext.MODE_FAST, 24), ("cordic_n16", ext.MODE_CORDIC, 16)):
+        def mv():
+            rc = lib.rac_gemm_dev(Am.data_ptr(), xm.data_ptr(), ym.data_ptr(), 4096, 1, 4096, 0, 0, 1.0, 0.0, nit,
+                                  mode, stream)
+            if rc:
+                raise RuntimeError(lib.rac_last_error())
+        mv()
+        torch.cuda.synchronize()
+        t = _events_time(mv, 10, torch)
+        ops[f"matvec_4096x4096_{mode_name}"] = {"us": round(t * 1e6, 2), "A_GBps": round(4096 * 4096 * 4 / t / 1e9, 1),
+                                                **_dist_fields(t, 1e6, "us")}
+        print(f"# matvec 4096x4096 {mode_name}: {t * 1e6:.1f} us", file=sys.stderr, flush=True)
+    del Am, xm, ym
 
     if not args.matmul_only:
         ops.update(bench_row_ops(torch, ext, dev, g))

@@ -816,9 +816,9 @@ static hipError_t launch_layout(int ta, int tb, const GemmArgs& g, hipStream_t s
 }
 
 static hipError_t dispatch(int ta, int tb, int mode, const GemmArgs& g, hipStream_t s) {
-    // few rows (schedule 2, the causal P V, is then the plain product with
-    // its causal K limit, which the few-row kernel applies)
-    if ((g.sched == 0 || g.sched == 2) && !ta && g.M <= kSkinnyMaxRows) {
+    // few rows or columns (schedule 2, the causal P V, is then the plain
+    // product with its causal K limit, which those kernels apply)
+    if ((g.sched == 0 || g.sched == 2) && !ta && (g.M <= kSkinnyMaxRows || g.N <= kSkinnyMaxRows)) {
         const SkinnyArgs k{g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, g.batch, g.sa, g.sb, g.sc,
                            g.ep, g.fused, tb != 0, g.k_causal, g.exact_specials, g.row0};
         return gemm_skinny_launch(k, mode, s);

@@ -1,23 +1,25 @@
 // rac_gemm_skinny.hip — the RAC GEMM for products with few rows of op(A)
-// (M <= 16: decode-time linears, one token or a few), all three MACs.
+// (M <= 16: decode-time linears, one token or a few) or few columns
+// (N <= 16: a matrix-vector product, a classifier head), all three MACs.
 //
 // Each output is ONE accumulator over k = 0..K-1 in order (rac_fma_iters,
-// rac_kernels.hip:204-219), so a product of M rows has only M * N serial
-// chains.  The block tiles of gemm_kernel give such a product few
-// workgroups with most of their rows empty (1 x 4096 x 4096 NT ran ~200 us
-// in FAST mode and ~1 ms in CORDIC mode n = 16).  Here the per-MAC work and
-// the serial fold are separated:
-//   * a workgroup owns 16 output columns and every row (grid x = N / 16, so
-//     N = 4096 already fills the 256 CUs) and walks K in tiles of KT;
-//   * A's M x KT and B's KT x 16 slices go global -> registers -> LDS (the
+// rac_kernels.hip:204-219), so such a product has only M * N serial chains.
+// The block tiles of gemm_kernel give it few workgroups with most of their
+// rows or columns empty (1 x 4096 x 4096 NT ran ~200 us in FAST mode and ~1
+// ms in CORDIC mode n = 16; 4096 x 1 x 4096 alike).  Here the per-MAC work
+// and the serial fold are separated:
+//   * a workgroup owns an RB x CB block of outputs: RB = M (<= 16) rows by
+//     16 columns, the grid over N (few rows), or 16 rows by CB = N (<= 16)
+//     columns, the grid over M (few columns); it walks K in tiles of KT;
+//   * A's RB x KT and B's KT x CB slices go global -> registers -> LDS (the
 //     next tile's loads in flight during the current tile's work);
-//   * all 256 lanes then compute the per-MAC terms of the tile, 4
-//     consecutive k at a time: CORDIC the rotation of (a ^ sign(b), 0)
-//     and its gain correction p = R_n(.) * (1/K-hat(n)) (rac_kernels.hip:
-//     140-185; the literal chain for inputs outside the strength-reduced
-//     one's range, as gemm_kernel), SHIFTADD the shift-add product
-//     (rac_kernels.hip:85-122); FAST has no term to prepare;
-//   * lane m * 16 + n folds output (m, n) over the tile's k in order:
+//   * the lanes compute the per-MAC terms of the tile, 4 consecutive k at a
+//     time: CORDIC the rotation of (a ^ sign(b), 0) and its gain correction
+//     p = R_n(.) * (1/K-hat(n)) (rac_kernels.hip:140-185; the literal chain
+//     for inputs outside the strength-reduced one's range, as gemm_kernel),
+//     SHIFTADD the shift-add product (rac_kernels.hip:85-122); FAST has no
+//     term to prepare;
+//   * lane m * CB + n folds output (m, n) over the tile's k in order:
 //     fma(p, |b|, acc), acc + prod or fma(a, b, acc), exactly the MAC of
 //     gemm_kernel, so every result has the same bits as there and in the
 //     reference.
@@ -27,27 +29,23 @@
 
 namespace rac {
 
-constexpr int kSkCols = 16;                     // output columns per workgroup
-
-// Where the per-MAC terms are computed.  FAST has none.  With 16 rows
-// (256 outputs, one per lane) each lane computes its own MACs' terms and
-// folds them at once ("own"); with fewer rows every lane computes terms
-// for the tile into LDS and the lanes owning outputs fold them ("shared").
-// k per tile keeps the workgroup's LDS under 64 KB.
-// BIGK (FAST, M <= 4): 512-k tiles, taken when the grid has at most one
-// workgroup per CU, whose loads then need twice the bytes in flight
+// Where the per-MAC terms are computed.  FAST has none.  With 256 outputs
+// per workgroup (one per lane) each lane computes its own MACs' terms and
+// folds them at once ("own"); with fewer, every lane computes terms for the
+// tile into LDS and the lanes owning outputs fold them ("shared").  k per
+// tile keeps the workgroup's LDS under 64 KB.
+// BIGK (FAST, <= 64 outputs): 512-k tiles, taken when the grid has at most
+// one workgroup per CU, whose loads then need twice the bytes in flight
 // (1x4096x4096: 42 -> 31 us); with several workgroups per CU they overlap
 // each other's loads already and the smaller tile is faster (1x11008x4096:
 // 49 against 63 us).
-template <int MODE, int MT, bool BIGK = false>
+template <int MODE, int OUTS, bool BIGK = false>
 struct SkCfg {
-    static constexpr bool kShared = MODE != kModeFast && MT * kSkCols < 256;
-    static constexpr bool kOwn = MODE != kModeFast && MT * kSkCols == 256;
+    static constexpr bool kShared = MODE != kModeFast && OUTS < 256;
+    static constexpr bool kOwn = MODE != kModeFast && OUTS == 256;
     static constexpr int kKT = MODE == kModeFast ? (BIGK ? 512 : 256)
-                               : kOwn ? 128 : (MT == 1 ? 256 : (MT <= 4 ? 128 : 64));
+                               : kOwn ? 128 : (OUTS == 16 ? 256 : (OUTS <= 64 ? 128 : 64));
     static constexpr int kRow = kKT + 4;        // LDS row stride (16 rows cover all banks)
-    static constexpr int kALoads = (MT * kKT + 255) / 256;
-    static constexpr int kBLoads = kSkCols * kKT / 256;
 };
 
 // The CORDIC term of one MAC: the rotation of (a ^ sign(b), 0) times the
@@ -76,61 +74,64 @@ __device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, 
     }
 }
 
-// Global -> registers: element (m, k) of A (row-major M x K) and (k, n) of
-// op(B) for the K-tile at k0, zero outside the matrices.
-template <int MT, int KT, bool TB>
+// Global -> registers: element (m0 + m, k) of A (row-major M x K) and
+// (k, n0 + n) of op(B) for the K-tile at k0, zero outside the matrices.
+template <int RB, int CB, int KT, bool TB>
 __device__ __forceinline__ void sk_load(const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                                        int K, long n0, int k0, float* ra, float* rb) {
+                                        int K, long m0, long n0, int k0, float* ra, float* rb) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < (MT * KT + 255) / 256; r++) {
-        const int idx = tid + r * 256, m = idx / KT, kk = idx % KT;
-        const long gk = (long)k0 + kk;
-        ra[r] = (m < M && idx < MT * KT && gk < K) ? A[(long)m * K + gk] : 0.0f;
+    for (int r = 0; r < (RB * KT + 255) / 256; r++) {
+        const int idx = tid + r * 256, kk = idx % KT;
+        const long gm = m0 + idx / KT, gk = (long)k0 + kk;
+        ra[r] = (idx < RB * KT && gm < M && gk < K) ? A[gm * K + gk] : 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < kSkCols * KT / 256; r++) {
+    for (int r = 0; r < (CB * KT + 255) / 256; r++) {
         const int idx = tid + r * 256;
         int nn, kk;
         if constexpr (TB) { nn = idx / KT; kk = idx % KT; }      // W[n][k]: k contiguous
-        else { kk = idx / kSkCols; nn = idx % kSkCols; }         // B[k][n]: n contiguous
+        else { kk = idx / CB; nn = idx % CB; }                   // B[k][n]: n contiguous
         const long gn = n0 + nn, gk = (long)k0 + kk;
-        rb[r] = (gn < N && gk < K) ? (TB ? B[gn * K + gk] : B[gk * N + gn]) : 0.0f;
+        rb[r] = (idx < CB * KT && gn < N && gk < K) ? (TB ? B[gn * K + gk] : B[gk * N + gn]) : 0.0f;
     }
 }
 
-// Registers -> LDS (A as [MT][ROW], B as [16][ROW], k contiguous); true when
+// Registers -> LDS (A as [RB][ROW], B as [CB][ROW], k contiguous); true when
 // this lane staged a CORDIC input outside the strength-reduced chain's range.
-template <int MODE, int MT, int KT, int ROW, bool TB>
+template <int MODE, int RB, int CB, int KT, int ROW, bool TB>
 __device__ __forceinline__ bool sk_store(float* sA, float* sB, const float* ra, const float* rb) {
     const int tid = threadIdx.x;
     bool special = false;
 #pragma unroll
-    for (int r = 0; r < (MT * KT + 255) / 256; r++) {
+    for (int r = 0; r < (RB * KT + 255) / 256; r++) {
         const int idx = tid + r * 256;
-        if (idx < MT * KT) sA[(idx / KT) * ROW + idx % KT] = ra[r];
+        if (idx < RB * KT) sA[(idx / KT) * ROW + idx % KT] = ra[r];
         if constexpr (MODE == kModeCordic) special |= cordic_needs_literal(ra[r]);
     }
 #pragma unroll
-    for (int r = 0; r < kSkCols * KT / 256; r++) {
+    for (int r = 0; r < (CB * KT + 255) / 256; r++) {
         const int idx = tid + r * 256;
-        if constexpr (TB) sB[(idx / KT) * ROW + idx % KT] = rb[r];
-        else sB[(idx % kSkCols) * ROW + idx / kSkCols] = rb[r];
+        if (idx < CB * KT) {
+            if constexpr (TB) sB[(idx / KT) * ROW + idx % KT] = rb[r];
+            else sB[(idx % CB) * ROW + idx / CB] = rb[r];
+        }
     }
     return special;
 }
 
-// The tile's per-MAC terms into sP (row m * 16 + n), 4 consecutive k of one
-// (m, n) per step, spread over lanes L0 .. L0 + NL - 1 (the others return).
-template <int MODE, int NITER, int MT, int KT, int ROW, int L0 = 0, int NL = 256>
-__device__ __forceinline__ void sk_terms(const float* sA, const float* sB, float* sP, int M, int iters, float kinv,
-                                         bool lit) {
-    constexpr int kQuads = MT * kSkCols * KT / 4;
+// The tile's per-MAC terms into sP (row m * CB + n) for the outputs inside
+// the matrix (m < mv, n < nv), 4 consecutive k of one (m, n) per step,
+// spread over lanes L0 .. L0 + NL - 1 (the others return).
+template <int MODE, int NITER, int RB, int CB, int KT, int ROW, int L0 = 0, int NL = 256>
+__device__ __forceinline__ void sk_terms(const float* sA, const float* sB, float* sP, int mv, int nv, int iters,
+                                         float kinv, bool lit) {
+    constexpr int kQuads = RB * CB * KT / 4;
     if ((int)threadIdx.x < L0) return;
 #pragma unroll 2
     for (int q = (int)threadIdx.x - L0; q < kQuads; q += NL) {
-        const int kk = (q % (KT / 4)) * 4, mn = q / (KT / 4), m = mn / kSkCols, n = mn % kSkCols;
-        if (m >= M) continue;
+        const int kk = (q % (KT / 4)) * 4, mn = q / (KT / 4), m = mn / CB, n = mn % CB;
+        if (m >= mv || n >= nv) continue;
         const float4 a4 = *reinterpret_cast<const float4*>(&sA[m * ROW + kk]);
         const float4 b4 = *reinterpret_cast<const float4*>(&sB[n * ROW + kk]);
         const float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -184,204 +185,215 @@ __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const
     return acc;
 }
 
-// alpha / beta, bias and activation of output (m, gn), as gemm_kernel's
+// alpha / beta, bias and activation of output (gm, gn), as gemm_kernel's
 template <bool FUSED>
-__device__ __forceinline__ void sk_epilogue(float* C, int N, int m, long gn, float acc, float alpha, float beta,
+__device__ __forceinline__ void sk_epilogue(float* C, int N, long gm, long gn, float acc, float alpha, float beta,
                                             const GemmEpilogue& ep, int iters) {
-    float* cp = C + (long)m * N + gn;
+    float* cp = C + gm * N + gn;
     // rac_kernels.hip:267-272
     float v = (beta != 0.0f) ? __builtin_fmaf(alpha, acc, beta * *cp) : alpha * acc;
     if constexpr (FUSED) {
         // rac_torch.cu:770-775
         if (ep.bias) v = v + ep.bias[gn];
-        if (ep.pre) ep.pre[(long)m * N + gn] = v;
+        if (ep.pre) ep.pre[gm * N + gn] = v;
         v = act_rt(v, ep.act, iters, ep.khinv);
     }
     *cp = v;
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK>
+// The block of outputs a workgroup owns: rows m0 .. m0 + mv - 1, columns
+// n0 .. n0 + nv - 1; the causal P V limit of those rows (rows past a query
+// position's key range are exactly 0 in P and, with every v finite,
+// fma(0, v, acc) == acc: acc starts at +0 and never becomes -0).
+template <int RB, int CB, bool FEWCOL>
+struct SkBlock {
+    long m0, n0;
+    int mv, nv, kend;
+    __device__ SkBlock(int M, int N, int K, const int* k_causal, int row0) {
+        m0 = FEWCOL ? (long)blockIdx.x * RB : 0;
+        n0 = FEWCOL ? 0 : (long)blockIdx.x * CB;
+        mv = (int)min((long)RB, (long)M - m0);
+        nv = (int)min((long)CB, (long)N - n0);
+        kend = K;
+        if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + m0 + mv);
+    }
+};
+
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool BIGK>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
-    using Cfg = SkCfg<MODE, MT, BIGK>;
+    using Cfg = SkCfg<MODE, RB * CB, BIGK>;
     constexpr int KT = Cfg::kKT, ROW = Cfg::kRow;
     constexpr bool kShared = Cfg::kShared;
-    __shared__ __attribute__((aligned(16))) float sA[MT * ROW];
-    __shared__ __attribute__((aligned(16))) float sB[kSkCols * ROW];
-    __shared__ __attribute__((aligned(16))) float sP[kShared ? MT * kSkCols * ROW : 4];
+    __shared__ __attribute__((aligned(16))) float sA[RB * ROW];
+    __shared__ __attribute__((aligned(16))) float sB[CB * ROW];
+    __shared__ __attribute__((aligned(16))) float sP[kShared ? RB * CB * ROW : 4];
     // CORDIC: lit[t & 1] is set when tile t's A slice holds an input outside
     // the strength-reduced chain's range; two flags, so the next tile's is
     // cleared while no lane reads it
     __shared__ int lit[2];
 
     const int tid = threadIdx.x;
-    const long n0 = (long)blockIdx.x * kSkCols;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
+    const SkBlock<RB, CB, FEWCOL> blk(M, N, K, k_causal, row0);
     if (tid == 0) lit[0] = lit[1] = 0;               // ordered before any set by the loop's first barrier
 
-    // Causal P V: rows past a query position's key range are exactly 0 in P
-    // and, with every v finite, fma(0, v, acc) == acc (acc starts at +0 and
-    // never becomes -0), so the k loop may stop after the last row's range.
-    int kend = K;
-    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + M);
-
-    const int om = tid / kSkCols, on = tid % kSkCols;   // output owned by lanes tid < MT * 16
-    float ra[(MT * KT + 255) / 256], rb[kSkCols * KT / 256];
+    const int om = tid / CB, on = tid % CB;           // output owned by lanes tid < RB * CB
+    const bool owner = tid < RB * CB && om < blk.mv && on < blk.nv;
+    float ra[(RB * KT + 255) / 256], rb[(CB * KT + 255) / 256];
     float acc = 0.0f;
-    sk_load<MT, KT, TB>(A, B, M, N, K, n0, 0, ra, rb);
-    for (int k0 = 0, t = 0; k0 < kend; k0 += KT, t++) {
+    sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
+    for (int k0 = 0, t = 0; k0 < blk.kend; k0 += KT, t++) {
         __syncthreads();                                // previous tile's fold done with LDS
-        if (sk_store<MODE, MT, KT, ROW, TB>(sA, sB, ra, rb) && exact_specials) lit[t & 1] = 1;
+        if (sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB, ra, rb) && exact_specials) lit[t & 1] = 1;
         __syncthreads();
-        if (k0 + KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, k0 + KT, ra, rb);
+        if (k0 + KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, k0 + KT, ra, rb);
         const bool lit_tile = MODE == kModeCordic && lit[t & 1] != 0;
         if constexpr (kShared) {
-            sk_terms<MODE, NITER, MT, KT, ROW>(sA, sB, sP, M, iters, kinv, lit_tile);
+            sk_terms<MODE, NITER, RB, CB, KT, ROW>(sA, sB, sP, blk.mv, blk.nv, iters, kinv, lit_tile);
             __syncthreads();
         }
         if (tid == 0) lit[(t + 1) & 1] = 0;            // tile t+1's flag: set after the loop-top barrier
-        if (tid < MT * kSkCols && om < M)
-            acc = sk_fold<MODE, NITER, ROW, kShared>(sA, sB, sP, om, on, tid, min(KT, kend - k0), acc, iters, kinv,
-                                                     lit_tile);
+        if (owner)
+            acc = sk_fold<MODE, NITER, ROW, kShared>(sA, sB, sP, om, on, tid, min(KT, blk.kend - k0), acc, iters,
+                                                     kinv, lit_tile);
     }
-    if (tid < MT * kSkCols && om < M && n0 + on < N)
-        sk_epilogue<FUSED>(C, N, om, n0 + on, acc, alpha, beta, ep, iters);
+    if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
 }
 
-// The shared terms pipelined (CORDIC, M <= 4): B slices and terms
+// The shared terms pipelined (CORDIC, <= 64 outputs): B slices and terms
 // in two LDS buffers, so waves 1-3 compute tile t+1's terms while wave 0's
 // output lanes fold tile t (in the form above the fold, a serial chain of
 // KT dependent operations per output, waited for the terms and the terms
 // for the fold).  Tile t+1's A slice has one buffer: only the terms read it.
 // The prologue's terms of tile 0 use every lane.
-template <int MT>
-struct SkPipeCfg {
-    static constexpr int kKT = MT == 1 ? 128 : 64;
-    static constexpr int kRow = kKT + 4;
-};
-
-template <int MODE, int NITER, bool TB, bool FUSED, int MT>
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 __global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
-    constexpr int KT = SkPipeCfg<MT>::kKT, ROW = SkPipeCfg<MT>::kRow;
-    __shared__ __attribute__((aligned(16))) float sA[MT * ROW];
-    __shared__ __attribute__((aligned(16))) float sB[2][kSkCols * ROW];
-    __shared__ __attribute__((aligned(16))) float sP[2][MT * kSkCols * ROW];
+    static_assert(RB * CB <= 64, "the fold lanes are wave 0");
+    constexpr int KT = RB * CB == 16 ? 128 : 64, ROW = KT + 4;
+    __shared__ __attribute__((aligned(16))) float sA[RB * ROW];
+    __shared__ __attribute__((aligned(16))) float sB[2][CB * ROW];
+    __shared__ __attribute__((aligned(16))) float sP[2][RB * CB * ROW];
     // lit[t & 1]: tile t's A slice holds an input outside the strength-
     // reduced chain's range (set when the tile is staged, read by its terms,
     // cleared two tiles later)
     __shared__ int lit[2];
 
     const int tid = threadIdx.x;
-    const long n0 = (long)blockIdx.x * kSkCols;
     A += (long)blockIdx.z * sa;
     B += (long)blockIdx.z * sb;
     C += (long)blockIdx.z * sc;
+    const SkBlock<RB, CB, FEWCOL> blk(M, N, K, k_causal, row0);
     if (tid == 0) lit[0] = lit[1] = 0;
 
-    int kend = K;                                        // causal P V, as gemm_skinny_kernel
-    if (k_causal && *k_causal == 1) kend = (int)min((long)K, (long)row0 + M);
-
-    const int om = tid / kSkCols, on = tid % kSkCols;
-    float ra[(MT * KT + 255) / 256], rb[kSkCols * KT / 256];
+    const int om = tid / CB, on = tid % CB;
+    const bool owner = tid < RB * CB && om < blk.mv && on < blk.nv;
+    float ra[(RB * KT + 255) / 256], rb[(CB * KT + 255) / 256];
     float acc = 0.0f;
     // prologue: tile 0 staged and its terms computed, tile 1 in flight
-    sk_load<MT, KT, TB>(A, B, M, N, K, n0, 0, ra, rb);
+    sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
     __syncthreads();                                     // flags cleared
-    if (sk_store<MODE, MT, KT, ROW, TB>(sA, sB[0], ra, rb) && exact_specials) lit[0] = 1;
+    if (sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB[0], ra, rb) && exact_specials) lit[0] = 1;
     __syncthreads();
-    if (KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, KT, ra, rb);
-    sk_terms<MODE, NITER, MT, KT, ROW>(sA, sB[0], sP[0], M, iters, kinv, MODE == kModeCordic && lit[0] != 0);
-    for (int k0 = 0, t = 0; k0 < kend; k0 += KT, t++) {
+    if (KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, KT, ra, rb);
+    sk_terms<MODE, NITER, RB, CB, KT, ROW>(sA, sB[0], sP[0], blk.mv, blk.nv, iters, kinv,
+                                           MODE == kModeCordic && lit[0] != 0);
+    for (int k0 = 0, t = 0; k0 < blk.kend; k0 += KT, t++) {
         const int cur = t & 1, nxt = cur ^ 1;
-        const bool more = k0 + KT < kend;
+        const bool more = k0 + KT < blk.kend;
         __syncthreads();                                 // tile t's terms written; tile t-1 folded
-        if (more && sk_store<MODE, MT, KT, ROW, TB>(sA, sB[nxt], ra, rb) && exact_specials) lit[nxt] = 1;
+        if (more && sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB[nxt], ra, rb) && exact_specials) lit[nxt] = 1;
         __syncthreads();                                 // tile t+1 staged
-        if (k0 + 2 * KT < kend) sk_load<MT, KT, TB>(A, B, M, N, K, n0, k0 + 2 * KT, ra, rb);
+        if (k0 + 2 * KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, k0 + 2 * KT, ra, rb);
         if (more)
-            sk_terms<MODE, NITER, MT, KT, ROW, 64, 192>(sA, sB[nxt], sP[nxt], M, iters, kinv,
-                                                        MODE == kModeCordic && lit[nxt] != 0);
+            sk_terms<MODE, NITER, RB, CB, KT, ROW, 64, 192>(sA, sB[nxt], sP[nxt], blk.mv, blk.nv, iters, kinv,
+                                                            MODE == kModeCordic && lit[nxt] != 0);
         if (tid == 0) lit[cur] = 0;                      // tile t+2's flag (tile t's was read a phase ago)
-        if (tid < MT * kSkCols && om < M)
-            acc = sk_fold<MODE, NITER, ROW, true>(sA, sB[cur], sP[cur], om, on, tid, min(KT, kend - k0), acc, iters,
-                                                  kinv, false);
+        if (owner)
+            acc = sk_fold<MODE, NITER, ROW, true>(sA, sB[cur], sP[cur], om, on, tid, min(KT, blk.kend - k0), acc,
+                                                  iters, kinv, false);
     }
-    if (tid < MT * kSkCols && om < M && n0 + on < N)
-        sk_epilogue<FUSED>(C, N, om, n0 + on, acc, alpha, beta, ep, iters);
+    if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int MT>
-static hipError_t skinny_pipe_cfg(const SkinnyArgs& g, hipStream_t s) {
-    const dim3 grid((unsigned)((g.N + kSkCols - 1) / kSkCols), 1, (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_skinny_pipe_kernel<MODE, NITER, TB, FUSED, MT>), grid, dim3(256), 0, s, g.A, g.B, g.C,
-                       g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb, g.sc, g.ep,
-                       g.k_causal, g.exact_specials, g.row0);
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE, bool BIGK = false>
+static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
+    const unsigned wgs = FEWCOL ? (unsigned)((g.M + RB - 1) / RB) : (unsigned)((g.N + CB - 1) / CB);
+    const dim3 grid(wgs, 1, (unsigned)g.batch);
+    if constexpr (PIPE) {
+        hipLaunchKernelGGL((gemm_skinny_pipe_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL>), grid, dim3(256), 0, s,
+                           g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
+                           g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
+    } else {
+        hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, BIGK>), grid, dim3(256), 0, s,
+                           g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
+                           g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
+    }
     return hipGetLastError();
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int MT, bool BIGK = false>
-static hipError_t skinny_cfg(const SkinnyArgs& g, hipStream_t s) {
-    const dim3 grid((unsigned)((g.N + kSkCols - 1) / kSkCols), 1, (unsigned)g.batch);
-    hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, MT, BIGK>), grid, dim3(256), 0, s, g.A, g.B, g.C, g.M,
-                       g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb, g.sc, g.ep, g.k_causal,
-                       g.exact_specials, g.row0);
-    return hipGetLastError();
+// One output block shape (RB x CB): FAST takes 512-k tiles on small grids
+// (<= 64 outputs), CORDIC the pipelined terms (<= 64 outputs); SHIFTADD's
+// terms (a shift-add product each) outweigh its fold and keep all four
+// waves (pipelined on three: 1x4096x4096 213 -> 297 us).
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
+static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
+    if constexpr (RB * CB <= 64) {
+        if constexpr (MODE == kModeFast) {
+            int dev = 0, cus = 256;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+                (void)hipGetLastError();
+                cus = 256;
+            }
+            const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
+            if (wgs <= cus) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
+        } else if constexpr (MODE == kModeCordic) {
+            return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
+        }
+    }
+    return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false>(g, s);
 }
 
 template <int MODE, int NITER, bool TB, bool FUSED>
-static hipError_t skinny_rows(const SkinnyArgs& g, hipStream_t s) {
-    if constexpr (MODE == kModeFast) {
-        int dev = 0, cus = 256;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-            (void)hipGetLastError();
-            cus = 256;
-        }
-        const long wgs = (long)((g.N + kSkCols - 1) / kSkCols) * g.batch;
-        if (g.M <= 4 && wgs <= cus) {
-            if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1, true>(g, s);
-            return skinny_cfg<MODE, NITER, TB, FUSED, 4, true>(g, s);
-        }
-        if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
-        if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
-    } else if constexpr (MODE == kModeCordic) {
-        if (g.M == 1) return skinny_pipe_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
-        if (g.M <= 4) return skinny_pipe_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
-    } else {
-        // SHIFTADD's terms (a shift-add product each) outweigh the fold:
-        // they keep all four waves (pipelined on three: 1x4096x4096 213 ->
-        // 297 us)
-        if (g.M == 1) return skinny_cfg<MODE, NITER, TB, FUSED, 1>(g, s);
-        if (g.M <= 4) return skinny_cfg<MODE, NITER, TB, FUSED, 4>(g, s);
+static hipError_t sk_shape(const SkinnyArgs& g, hipStream_t s) {
+    if (g.M <= kSkinnyMaxRows) {                         // few rows: RB = M rounded up, 16 columns
+        if (g.M == 1) return sk_block<MODE, NITER, TB, FUSED, 1, 16, false>(g, s);
+        if (g.M <= 4) return sk_block<MODE, NITER, TB, FUSED, 4, 16, false>(g, s);
+        if (g.M <= 8) return sk_block<MODE, NITER, TB, FUSED, 8, 16, false>(g, s);
+        return sk_block<MODE, NITER, TB, FUSED, 16, 16, false>(g, s);
     }
-    if (g.M <= 8) return skinny_cfg<MODE, NITER, TB, FUSED, 8>(g, s);
-    return skinny_cfg<MODE, NITER, TB, FUSED, 16>(g, s);
+    // few columns: 16 rows, CB = N rounded up
+    if (g.N == 1) return sk_block<MODE, NITER, TB, FUSED, 16, 1, true>(g, s);
+    if (g.N <= 4) return sk_block<MODE, NITER, TB, FUSED, 16, 4, true>(g, s);
+    if (g.N <= 8) return sk_block<MODE, NITER, TB, FUSED, 16, 8, true>(g, s);
+    return sk_block<MODE, NITER, TB, FUSED, 16, 16, true>(g, s);
 }
 
 template <int MODE, int NITER>
-static hipError_t skinny_layout(const SkinnyArgs& g, hipStream_t s) {
-    if (g.fused) return skinny_rows<MODE, NITER, true, true>(g, s);
-    if (g.tb) return skinny_rows<MODE, NITER, true, false>(g, s);
-    return skinny_rows<MODE, NITER, false, false>(g, s);
+static hipError_t sk_layout(const SkinnyArgs& g, hipStream_t s) {
+    if (g.fused) return sk_shape<MODE, NITER, true, true>(g, s);
+    if (g.tb) return sk_shape<MODE, NITER, true, false>(g, s);
+    return sk_shape<MODE, NITER, false, false>(g, s);
 }
 
 hipError_t gemm_skinny_launch(const SkinnyArgs& g, int mode, hipStream_t s) {
-    if (mode == kModeFast) return skinny_layout<kModeFast, 0>(g, s);
-    if (mode == kModeShiftAdd) return skinny_layout<kModeShiftAdd, 0>(g, s);
+    if (mode == kModeFast) return sk_layout<kModeFast, 0>(g, s);
+    if (mode == kModeShiftAdd) return sk_layout<kModeShiftAdd, 0>(g, s);
     switch (g.iters) {
-        case 8: return skinny_layout<kModeCordic, 8>(g, s);
-        case 16: return skinny_layout<kModeCordic, 16>(g, s);
-        case 24: return skinny_layout<kModeCordic, 24>(g, s);
-        default: return skinny_layout<kModeCordic, 0>(g, s);
+        case 8: return sk_layout<kModeCordic, 8>(g, s);
+        case 16: return sk_layout<kModeCordic, 16>(g, s);
+        case 24: return sk_layout<kModeCordic, 24>(g, s);
+        default: return sk_layout<kModeCordic, 0>(g, s);
     }
 }
 

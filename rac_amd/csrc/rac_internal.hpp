@@ -54,8 +54,9 @@ hipError_t act_grad_launch(const float* g, const float* pre, float* d, long coun
 // keeps the strength-reduced chain for every input (callers whose parity
 // bar is a summation bound, where subnormal-rounding differences of tiny
 // products are far below it).
-// The same product for M <= 16 rows of A (row-major, not transposed):
-// gemm_launch hands such launches (schedules 0 and 2) to this kernel.
+// The same product for M <= 16 rows or N <= 16 columns, A row-major (not
+// transposed): gemm_launch hands such launches (schedules 0 and 2) to the
+// few-row / few-column kernels.
 struct SkinnyArgs {
     const float* A;
     const float* B;
@@ -73,7 +74,7 @@ struct SkinnyArgs {
     int row0;
 };
 hipError_t gemm_skinny_launch(const SkinnyArgs& g, int mode, hipStream_t s);
-constexpr int kSkinnyMaxRows = 16;
+constexpr int kSkinnyMaxRows = 16;      // and columns
 
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
                        int M, int N, int K, float alpha, float beta, int iters, int mode,

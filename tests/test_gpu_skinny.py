@@ -1,14 +1,17 @@
-"""GPU parity of the RAC GEMM for few rows (M <= 16, A not transposed).
+"""GPU parity of the RAC GEMM for few rows (M <= 16) or few columns
+(N <= 16), A not transposed.
 
-Such launches run gemm_skinny_kernel: the per-MAC terms of a K-tile (the
-CORDIC rotation with its gain correction, the shift-add product) are
-computed by every lane, then one lane per output folds them in k order.
+Such launches run gemm_skinny_kernel / gemm_skinny_pipe_kernel: the per-MAC
+terms of a K-tile (the CORDIC rotation with its gain correction, the
+shift-add product) are computed by the lanes, then one lane per output
+folds them in k order.
 Each output must equal the reference's rac_fma_iters chain
 (rac_kernels.hip:204-219) bit for bit, as the block-tiled kernel does, in
-all three MAC modes: one row and several, NN and NT, ragged N and K, the
-iteration counts with compile-time chains (8, 16, 24) and a run-time one
-(5), special operands (the literal rotation chain), alpha / beta, batches,
-and the fused bias + activation epilogue of a decode-time linear.
+all three MAC modes: one row or column and several, NN and NT, ragged
+dimensions, the iteration counts with compile-time chains (8, 16, 24) and
+a run-time one (5), special operands (the literal rotation chain), alpha /
+beta, batches, and the fused bias + activation epilogue of a decode-time
+linear and of a classifier head.
 """
 import numpy as np
 import pytest
@@ -142,5 +145,79 @@ def test_skinny_decode_linear(mode, iters):
     lin = e.linear_forward(T(x), T(w), T(b), iters=iters, mode=mode)
     assert torch.equal(pre, lin)
     assert torch.equal(out, e.silu(lin, iters))
+    ref = rl.orc_matmul(x, w, M, N, K, iters, mode, tb=1) + b[None, :]
+    assert np.array_equal(H(pre), ref.astype(np.float32))
+
+
+# Few columns: (4096, 1, 1030) a matrix-vector product; (2100, 3, 777)
+# 4-column blocks; (1500, 7, 333) 8; (1000, 16, 300) and (35, 9, 67) 16
+# (CORDIC / SHIFTADD: each lane computes its own terms); (2048, 10, 4096) a
+# classifier head.
+COL_SHAPES = [(4096, 1, 1030), (2100, 3, 777), (1500, 7, 333), (1000, 16, 300), (35, 9, 67), (2048, 10, 4096)]
+
+
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("mode,iters", MODES)
+def test_fewcol_bit_exact(mode, iters, tb):
+    for (M, N, K) in COL_SHAPES:
+        if mode == 2 and M * N * K > 2 ** 26:
+            continue                                    # the checker's SHIFTADD loop: keep it short
+        print(f"fewcol mode={mode} iters={iters} tb={tb} shape={(M, N, K)}", flush=True)
+        A = rl.gen_normal((M, K), seed=M + K + 1)
+        B = rl.gen_normal((N, K) if tb else (K, N), seed=N + 2 * K + 1)
+        got = gemm(A, B, M, N, K, tb, iters, mode)
+        ref = rl.orc_matmul(A, B, M, N, K, iters, mode, tb=tb)
+        assert np.array_equal(got, ref), (M, N, K, float(np.max(np.abs(got - ref))))
+
+
+@pytest.mark.parametrize("mode,iters", [(1, 16), (1, 5), (0, 24), (2, 8)])
+def test_fewcol_special_values(mode, iters):
+    rng = np.random.default_rng(mode * 37 + iters)
+    for (M, N, K, tb) in [(700, 4, 300, 1), (1500, 1, 513, 0)]:
+        print(f"fewcol specials mode={mode} iters={iters} shape={(M, N, K)} tb={tb}", flush=True)
+        A = rl.gen_uniform((M, K), seed=M + K)
+        B = rl.gen_uniform((N, K) if tb else (K, N), seed=N)
+        for r in rng.integers(0, M, 40):
+            A[r, rng.integers(0, K, 4)] = rng.choice(SPECIALS, 4)
+        for r in rng.integers(0, M, 40):
+            A[r, rng.integers(0, K, 4)] = rng.choice(SPECIALS[:8], 4)
+        got = gemm(A, B, M, N, K, tb, iters, mode)
+        ref = rl.orc_matmul(A, B, M, N, K, iters, mode, tb=tb, literal=1)
+        assert np.array_equal(got, ref, equal_nan=True), (M, N, K)
+        assert np.isfinite(ref).any() and (mode == 2 or np.isnan(ref).any())
+
+
+@pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24), (2, 16)])
+def test_fewcol_alpha_beta_and_batch(mode, iters):
+    M, N, K = 1300, 5, 400
+    A = rl.gen_normal((M, K), 3)
+    B = rl.gen_normal((K, N), 4)
+    C0 = rl.gen_normal((M, N), 5)
+    got = gemm(A, B, M, N, K, 0, iters, mode, alpha=0.5, beta=-2.0, C0=C0)
+    assert np.array_equal(got, rl.orc_matmul(A, B, M, N, K, iters, mode, alpha=0.5, beta=-2.0, C0=C0))
+    e = ext()
+    Z = 3
+    Ab = rl.gen_uniform((Z, 900, 600), seed=7)
+    Bb = rl.gen_uniform((Z, 2, 600), seed=8)
+    out = H(e.bmm(T(Ab), T(Bb), trans_b=True, alpha=0.75, iters=iters, mode=mode))
+    for z in range(Z):
+        ref = rl.orc_matmul(np.ascontiguousarray(Ab[z]), np.ascontiguousarray(Bb[z]), 900, 2, 600, iters, mode,
+                            tb=1, alpha=0.75)
+        assert np.array_equal(out[z], ref), z
+
+
+@pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24)])
+def test_fewcol_classifier_head(mode, iters):
+    """x [512, 4096] @ W[10, 4096]^T + b with GELU and without, fused and
+    unfused: pre-activations bit-exact vs the checker."""
+    e = ext()
+    M, N, K = 512, 10, 4096
+    x = rl.gen_normal((M, K), seed=51)
+    w = rl.gen_normal((N, K), seed=52, std=0.02)
+    b = rl.gen_normal(N, seed=53)
+    out, pre = e.fused_linear_forward(T(x), T(w), T(b), 2, iters=iters, mode=mode, return_pre=True)
+    lin = e.linear_forward(T(x), T(w), T(b), iters=iters, mode=mode)
+    assert torch.equal(pre, lin)
+    assert torch.equal(out, e.gelu(lin))
     ref = rl.orc_matmul(x, w, M, N, K, iters, mode, tb=1) + b[None, :]
     assert np.array_equal(H(pre), ref.astype(np.float32))
