@@ -10,6 +10,8 @@ Also measured in the same run (fields "ops" and "cpu_baseline"):
   * the matmul at n = 8 and 24, and config 1 (1024^3, n = 16) both
     device-resident and through the synchronous rac.h call on host buffers,
     and in FAST mode (the rac_torch default MAC, on the matrix cores);
+  * decode-time linears (one token: 1x4096x4096, 1x11008x4096) and a
+    matrix-vector product (4096x4096 by a vector), FAST and CORDIC n = 16;
   * the Llama block (config 5) at n = 8/16/24 with a per-op breakdown, and
     in rac_torch's default configuration (FAST): forward, per-op breakdown
     and one training step (forward + backward);
