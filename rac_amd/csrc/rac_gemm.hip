@@ -671,7 +671,7 @@ static hipError_t launch_mfma_fast(const GemmArgs& g, hipStream_t stream) {
 }
 
 // Compute units of the current device (256 on MI355X), cached per device.
-static long device_cus() {
+long device_cus() {
     static std::atomic<long> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {

@@ -349,12 +349,7 @@ template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
     if constexpr (RB * CB <= 64) {
         if constexpr (MODE == kModeFast) {
-            int dev = 0, cus = 256;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-                (void)hipGetLastError();
-                cus = 256;
-            }
+            const long cus = device_cus();
             const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
             if (wgs <= cus) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
         } else if constexpr (MODE == kModeCordic) {

@@ -74,6 +74,8 @@ struct SkinnyArgs {
     int row0;
 };
 hipError_t gemm_skinny_launch(const SkinnyArgs& g, int mode, hipStream_t s);
+// Compute units of the current device (256 on MI355X), cached per device.
+long device_cus();
 constexpr int kSkinnyMaxRows = 16;      // and columns
 
 hipError_t gemm_launch(int ta, int tb, const float* A, const float* B, float* C,
