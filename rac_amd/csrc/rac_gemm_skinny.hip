@@ -49,24 +49,24 @@ struct SkCfg {
 };
 
 // The CORDIC term of one MAC: the rotation of (a ^ sign(b), 0) times the
-// gain correction, for 4 consecutive k; inputs outside the strength-reduced
+// gain correction, for E consecutive k; inputs outside the strength-reduced
 // chain's range take the literal chain when `lit` (rac_kernels.hip:152-163).
-template <int NITER>
+template <int NITER, int E = 4>
 __device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, float* p, int iters, float kinv,
                                                 bool lit) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) p[e] = as_f(as_u(a[e]) ^ (as_u(b[e]) & 0x80000000u));
+    for (int e = 0; e < E; e++) p[e] = as_f(as_u(a[e]) ^ (as_u(b[e]) & 0x80000000u));
     if constexpr (NITER > 0) {
-        cordic_rot_x_vec<NITER, 4>(p);
+        cordic_rot_x_vec<NITER, E>(p);
 #pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = p[e] * cordic_kinv(NITER);
+        for (int e = 0; e < E; e++) p[e] = p[e] * cordic_kinv(NITER);
     } else {
 #pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = cordic_rot_x_rt(p[e], iters) * kinv;
+        for (int e = 0; e < E; e++) p[e] = cordic_rot_x_rt(p[e], iters) * kinv;
     }
     if (lit) {
 #pragma unroll
-        for (int e = 0; e < 4; e++)
+        for (int e = 0; e < E; e++)
             if (cordic_needs_literal(a[e]))
                 p[e] = cordic_rot_x_literal_rt(as_f(as_u(a[e]) ^ (as_u(b[e]) & 0x80000000u)),
                                                NITER > 0 ? NITER : iters) *
@@ -152,6 +152,23 @@ __device__ __forceinline__ void sk_terms(const float* sA, const float* sB, float
 template <int MODE, int NITER, int ROW, bool SHARED>
 __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const float* sP, int om, int on,
                                          int prow, int kn, float acc, int iters, float kinv, bool lit) {
+    if constexpr (!SHARED && MODE == kModeCordic) {
+        // own terms: 8 k per step, so 8 rotation chains interleave (the k
+        // past kn are zero padding or, in a causal P V, zeros of P)
+        for (int kk = 0; kk < kn; kk += 8) {
+            const float4 a0 = *reinterpret_cast<const float4*>(&sA[om * ROW + kk]);
+            const float4 a1 = *reinterpret_cast<const float4*>(&sA[om * ROW + kk + 4]);
+            const float4 b0 = *reinterpret_cast<const float4*>(&sB[on * ROW + kk]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&sB[on * ROW + kk + 4]);
+            const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            float t8[8];
+            sk_cordic_terms<NITER, 8>(a, b, t8, iters, kinv, lit);
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc = __builtin_fmaf(t8[e], __builtin_fabsf(b[e]), acc);
+        }
+        return acc;
+    }
     // unrolled so the LDS reads of 32 k run ahead of the dependent chain of
     // FMAs (rolled, each 4-k step waited for its reads; 64 k ran no faster)
 #pragma unroll 8
