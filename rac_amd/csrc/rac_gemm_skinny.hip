@@ -376,18 +376,38 @@ static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
     return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false>(g, s);
 }
 
+// The output block.  Few rows: RB = M rounded up (1, 4, 8, 16) by 16
+// columns; few columns: 16 rows by CB = N rounded up.  With 5-16 rows (or
+// columns), when the 16-wide grid would leave at most one workgroup per CU,
+// half as wide blocks double the workgroups (two waves per SIMD instead of
+// one): measured, bit-identical, 8x4096x4096 CORDIC n = 16 218 -> 177 us,
+// 16x4096x4096 330 -> 225 us, SHIFTADD 1.54 -> 0.85 ms and 2.97 -> 1.69
+// ms, FAST 16 rows 52 -> 37 us; on wider grids (N = 11008) the narrow
+// blocks lost 6-29% (CORDIC, FAST), and FAST lost with 8 rows everywhere.
+// SHIFTADD, bound by its terms, takes them at 9-16 rows on any grid.
 template <int MODE, int NITER, bool TB, bool FUSED>
 static hipError_t sk_shape(const SkinnyArgs& g, hipStream_t s) {
-    if (g.M <= kSkinnyMaxRows) {                         // few rows: RB = M rounded up, 16 columns
+    const long cus = device_cus();
+    if (g.M <= kSkinnyMaxRows) {                         // few rows, the grid over N
+        const bool one_per_cu = (long)((g.N + 15) / 16) * g.batch <= cus;
         if (g.M == 1) return sk_block<MODE, NITER, TB, FUSED, 1, 16, false>(g, s);
         if (g.M <= 4) return sk_block<MODE, NITER, TB, FUSED, 4, 16, false>(g, s);
-        if (g.M <= 8) return sk_block<MODE, NITER, TB, FUSED, 8, 16, false>(g, s);
+        if (g.M <= 8) {
+            if (MODE != kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, false>(g, s);
+            return sk_block<MODE, NITER, TB, FUSED, 8, 16, false>(g, s);
+        }
+        if (MODE == kModeShiftAdd || one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 16, 8, false>(g, s);
         return sk_block<MODE, NITER, TB, FUSED, 16, 16, false>(g, s);
     }
-    // few columns: 16 rows, CB = N rounded up
+    // few columns, the grid over M
+    const bool one_per_cu = (long)((g.M + 15) / 16) * g.batch <= cus;
     if (g.N == 1) return sk_block<MODE, NITER, TB, FUSED, 16, 1, true>(g, s);
     if (g.N <= 4) return sk_block<MODE, NITER, TB, FUSED, 16, 4, true>(g, s);
-    if (g.N <= 8) return sk_block<MODE, NITER, TB, FUSED, 16, 8, true>(g, s);
+    if (g.N <= 8) {
+        if (MODE != kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, true>(g, s);
+        return sk_block<MODE, NITER, TB, FUSED, 16, 8, true>(g, s);
+    }
+    if (MODE == kModeShiftAdd || one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 16, true>(g, s);
     return sk_block<MODE, NITER, TB, FUSED, 16, 16, true>(g, s);
 }
 

@@ -63,13 +63,14 @@ def gemm(A, B, M, N, K, tb, iters, mode, alpha=1.0, beta=0.0, C0=None):
 
 
 MODES = [(0, 24), (1, 16), (1, 8), (1, 24), (1, 5), (2, 16), (2, 24)]
-# (1, 4096, 1030): one row (M-tile 1, K ragged); (3, 2100, 777): M-tile 4
+# (1, 4096, 1030): one row (1 x 16 blocks, K ragged); (3, 2100, 777): 4 x 16
 # (FAST: 512-k tiles on grids of at most one workgroup per CU, both);
-# (2, 5000, 300): M-tile 4 on a wider grid (FAST: 256-k tiles); (7, 1500,
-# 333): M-tile 8; (16, 1000, 300) and (9, 35, 67): M-tile 16 (CORDIC /
-# SHIFTADD: each lane computes its own terms); (1, 5, 3): tiny.
-SHAPES = [(1, 4096, 1030), (3, 2100, 777), (2, 5000, 300), (7, 1500, 333), (16, 1000, 300), (9, 35, 67),
-          (1, 5, 3)]
+# (2, 5000, 300): 4 x 16 on a wider grid (FAST: 256-k tiles); (7, 1500,
+# 333): 8 x 8 (FAST 8 x 16); (6, 5000, 300): 8 x 16; (16, 1000, 300) and
+# (9, 35, 67): 16 x 8; (16, 5000, 200): 16 x 16 (CORDIC: each lane computes
+# its own terms; SHIFTADD 16 x 8); (1, 5, 3): tiny.
+SHAPES = [(1, 4096, 1030), (3, 2100, 777), (2, 5000, 300), (7, 1500, 333), (6, 5000, 300), (16, 1000, 300),
+          (9, 35, 67), (16, 5000, 200), (1, 5, 3)]
 
 
 @pytest.mark.parametrize("tb", [0, 1])
@@ -149,11 +150,12 @@ def test_skinny_decode_linear(mode, iters):
     assert np.array_equal(H(pre), ref.astype(np.float32))
 
 
-# Few columns: (4096, 1, 1030) a matrix-vector product; (2100, 3, 777)
-# 4-column blocks; (1500, 7, 333) 8; (1000, 16, 300) and (35, 9, 67) 16
-# (CORDIC / SHIFTADD: each lane computes its own terms); (2048, 10, 4096) a
-# classifier head.
-COL_SHAPES = [(4096, 1, 1030), (2100, 3, 777), (1500, 7, 333), (1000, 16, 300), (35, 9, 67), (2048, 10, 4096)]
+# Few columns (the same blocks transposed): (4096, 1, 1030) a matrix-vector
+# product, 16 x 1 blocks; (2100, 3, 777) 16 x 4; (1500, 7, 333) 8 x 8
+# (FAST 16 x 8); (5000, 6, 300) 16 x 8; (1000, 16, 300), (35, 9, 67) and
+# (2048, 10, 4096), a classifier head, 8 x 16; (5000, 16, 200) 16 x 16.
+COL_SHAPES = [(4096, 1, 1030), (2100, 3, 777), (1500, 7, 333), (5000, 6, 300), (1000, 16, 300), (35, 9, 67),
+              (2048, 10, 4096), (5000, 16, 200)]
 
 
 @pytest.mark.parametrize("tb", [0, 1])
