@@ -518,11 +518,22 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 
 # ── batched products and attention ───────────────────────────────────────
 
+def _rows_contiguous(t: torch.Tensor) -> torch.Tensor:
+    """t [Z, R, C] unchanged when every t[z] is a row-major R x C matrix
+    (stride(2) == 1, stride(1) == C) and the batch stride is non-negative;
+    a contiguous copy otherwise."""
+    if ((t.size(2) <= 1 or t.stride(2) == 1) and (t.size(1) <= 1 or t.stride(1) == t.size(2))
+            and t.stride(0) >= 0):
+        return t
+    return t.contiguous()
+
+
 def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool = False,
         alpha: float = 1.0, iters: int = 0, mode: int = -1, out: Optional[torch.Tensor] = None,
         beta: float = 0.0) -> torch.Tensor:
-    """C[z] = alpha * op(A[z]) @ op(B[z]) (+ beta * C[z]) for 3-D contiguous
-    fp32 tensors, one launch over the batch (grid z).  op(A[z]) = A[z]
+    """C[z] = alpha * op(A[z]) @ op(B[z]) (+ beta * C[z]) for 3-D fp32
+    tensors whose items are row-major matrices (items may be strided apart,
+    e.g. a slice of a cache), one launch over the batch (grid z).  op(A[z]) = A[z]
     [M, K], or A[z]^T with A stored [Z, K, M] when trans_a; op(B[z]) = B[z]
     [K, N], or B[z]^T with B stored [Z, N, K] when trans_b.  With `out`
     (a contiguous fp32 [Z, M, N] tensor) the result is written there, and
@@ -531,8 +542,10 @@ def bmm(A: torch.Tensor, B: torch.Tensor, trans_a: bool = False, trans_b: bool =
     _require_f32(B, "B")
     if A.dim() != 3 or B.dim() != 3 or A.size(0) != B.size(0):
         raise RuntimeError("RAC: bmm expects [Z, ., .] tensors with the same Z")
-    A = A.contiguous()
-    B = B.contiguous()
+    # each batch item must be a row-major matrix; items may sit any
+    # (non-negative) distance apart, e.g. a slice of a longer cache
+    A = _rows_contiguous(A)
+    B = _rows_contiguous(B)
     Z = A.size(0)
     M, K = (A.size(2), A.size(1)) if trans_a else (A.size(1), A.size(2))
     Kb, N = (B.size(2), B.size(1)) if trans_b else (B.size(1), B.size(2))
