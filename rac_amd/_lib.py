@@ -91,6 +91,11 @@ _SIGNATURES = {
     "rac_attention_ws_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _l, _i, _i, _vp]),
     "rac_attention_probs_dev": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "rac_attention_probs_rows_dev": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    # rac_decode.h — decode step pieces, cache position in device memory
+    "rac_decode_attention_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _l, _vp, _f, _i, _vp]),
+    "rac_kv_append_dev": (_i, [_vp, _vp, _vp, _i, _i, _l, _vp, _vp]),
+    "rac_position_advance_dev": (_i, [_vp, _i, _vp]),
+    "rac_swiglu_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_q8_0_gemv_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rac_q8_0_quantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_q8_0_dequantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),

@@ -411,6 +411,54 @@ RAC_EXPORT int rac_softmax_dev(const float* x, float* y, long rows, long n, int 
     return check_hip(softmax_launch(x, y, rows, n, iters, (hipStream_t)stream), "rac_softmax_dev launch");
 }
 
+// ── decode step (bench_rac_transformer.c decoder_forward_kv, T_new = 1) ──
+
+// Grouped-query attention of one token over positions 0 .. *pos of the
+// cache (bench_rac_transformer.c:508-548, query head h on key/value head
+// h / (n_heads / n_kv_heads)).
+RAC_EXPORT int rac_decode_attention_dev(const float* q, const float* k_cache, const float* v_cache, float* out,
+                                        int n_heads, int n_kv_heads, int d_head, long t_cap, const int* pos,
+                                        float scale, int iters, void* stream) {
+    if (!q || !k_cache || !v_cache || !out || !pos)
+        return fail(RAC_ERR_NULL_PTR, "rac_decode_attention_dev: null buffer");
+    if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads)
+        return fail(RAC_ERR_INVALID_DIM, "rac_decode_attention_dev: n_heads must be a positive multiple of n_kv_heads");
+    if (n_heads > 65535) return fail(RAC_ERR_INVALID_DIM, "rac_decode_attention_dev: at most 65535 heads");
+    if (d_head <= 0 || d_head > kDecodeMaxHead)
+        return fail(RAC_ERR_INVALID_DIM, "rac_decode_attention_dev: d_head must be in [1, %d]", kDecodeMaxHead);
+    if (t_cap <= 0 || t_cap > kDecodeMaxLen)
+        return fail(RAC_ERR_INVALID_DIM, "rac_decode_attention_dev: t_cap must be in [1, %d]", kDecodeMaxLen);
+    return check_hip(decode_attention_launch(q, k_cache, v_cache, out, n_heads, n_kv_heads, d_head, t_cap, pos,
+                                             scale, iters, (hipStream_t)stream),
+                     "rac_decode_attention_dev launch");
+}
+
+// The new token's keys and values into the cache at *pos
+// (bench_rac_transformer.c:569-574).
+RAC_EXPORT int rac_kv_append_dev(const float* kv, float* k_cache, float* v_cache, int n_kv_heads, int d_head,
+                                 long t_cap, const int* pos, void* stream) {
+    if (!kv || !k_cache || !v_cache || !pos) return fail(RAC_ERR_NULL_PTR, "rac_kv_append_dev: null buffer");
+    if (n_kv_heads <= 0 || d_head <= 0 || t_cap <= 0)
+        return fail(RAC_ERR_INVALID_DIM, "rac_kv_append_dev: sizes must be positive");
+    return check_hip(kv_append_launch(kv, k_cache, v_cache, n_kv_heads, d_head, t_cap, pos, (hipStream_t)stream),
+                     "rac_kv_append_dev launch");
+}
+
+// *pos += by on the stream (full_model_forward's cur_len += T_new, :624).
+RAC_EXPORT int rac_position_advance_dev(int* pos, int by, void* stream) {
+    if (!pos) return fail(RAC_ERR_NULL_PTR, "rac_position_advance_dev: null buffer");
+    return check_hip(position_advance_launch(pos, by, (hipStream_t)stream), "rac_position_advance_dev launch");
+}
+
+// out[i] = silu(gu[i]) * gu[n + i] (bench_rac_transformer.c:607-611, SiLU
+// by the CORDIC exp).
+RAC_EXPORT int rac_swiglu_dev(const float* gu, float* out, long n, int iters, void* stream) {
+    if (!gu || !out) return fail(RAC_ERR_NULL_PTR, "rac_swiglu_dev: null buffer");
+    if (n < 0) return fail(RAC_ERR_INVALID_DIM, "rac_swiglu_dev: negative count");
+    if (n == 0) return RAC_OK;
+    return check_hip(swiglu_launch(gu, out, n, iters, (hipStream_t)stream), "rac_swiglu_dev launch");
+}
+
 static int elt_dev(const char* who, int op, const float* x, float* y, long count, int iters, void* stream) {
     if (!x || !y) return fail(RAC_ERR_NULL_PTR, "%s: null buffer", who);
     if (count < 0) return fail(RAC_ERR_INVALID_DIM, "%s: negative count", who);

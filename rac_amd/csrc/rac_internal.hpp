@@ -136,6 +136,19 @@ hipError_t inner_launch(const float2* a, const float2* b, long n, float* out, hi
 hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, float* out, int M, int N,
                           int K, int act, hipStream_t s);
 hipError_t q8_quantize_launch(const float* src, uint8_t* dst, long nblocks, hipStream_t s);
+// Decode step of a decoder layer (rac_decode.hip): the token's cache
+// position is read from *pos in device memory.  Attention: one workgroup
+// per query head over positions 0 .. *pos of a cache [n_kv_heads, t_cap,
+// d_head]; d_head <= kDecodeMaxHead, positions < kDecodeMaxLen.
+constexpr int kDecodeMaxHead = 256;
+constexpr int kDecodeMaxLen = 8192;
+hipError_t decode_attention_launch(const float* q, const float* kc, const float* vc, float* out, int n_heads,
+                                   int n_kv_heads, int dh, long t_cap, const int* pos, float scale, int iters,
+                                   hipStream_t s);
+hipError_t kv_append_launch(const float* kv, float* kc, float* vc, int n_kv_heads, int dh, long t_cap,
+                            const int* pos, hipStream_t s);
+hipError_t position_advance_launch(int* pos, int by, hipStream_t s);
+hipError_t swiglu_launch(const float* gu, float* out, long n, int iters, hipStream_t s);
 hipError_t q8_dequantize_launch(const uint8_t* src, float* dst, long nblocks, hipStream_t s);
 // Error channel of the C ABI (rac_last_error): set the message, return code.
 int report(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

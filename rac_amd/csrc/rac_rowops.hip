@@ -20,51 +20,9 @@
 #include <hip/hip_runtime.h>
 #include "rac_math.hpp"
 #include "rac_internal.hpp"
+#include "rac_rowred.hpp"
 
 namespace rac {
-
-constexpr int kRowThreads = 256;
-constexpr int kRowWaves = kRowThreads / 64;
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// Block-wide reductions; `red` holds kRowWaves floats.  The result is the
-// same value in every lane (fixed combination order).  TRAIL: end with a
-// barrier, so that `red` may be rewritten at once; callers that give each
-// reduction of a row its own `red` leave it off.
-template <bool TRAIL = true>
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int i = 1; i < kRowWaves; i++) r += red[i];
-    if constexpr (TRAIL) __syncthreads();
-    return r;
-}
-template <bool TRAIL = true>
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    const int w = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int i = 1; i < kRowWaves; i++) r = fmaxf(r, red[i]);
-    if constexpr (TRAIL) __syncthreads();
-    return r;
-}
 
 template <int NITER>
 __device__ __forceinline__ float exp_n(float x, int iters, float khinv) {

@@ -22,14 +22,25 @@ computed on its own, so one launch gives the same bits as three (two).
 
 MI355X form: weights resident in HBM; the cache is [n_kv_heads, T_max,
 d_head] per layer, so each key/value head's keys and values are one
-row-major matrix and the attention of a head group is two few-row RAC
-products (scores = Q_group K^T / sqrt(d_head), out = P V; FAST MAC, the
-reference's fp32 dot products) around the RAC softmax, reading the cache in
-place.  Masked scores are -inf (the reference writes -1e30); either gives
+row-major matrix.  Prefill attention of a head group is two RAC products
+(scores = Q_group K^T / sqrt(d_head), out = P V; FAST MAC, the reference's
+fp32 dot products) around the RAC softmax, reading the cache in place.  Masked scores are -inf (the reference writes -1e30); either gives
 probability 0.  SiLU is the RAC CORDIC SiLU (rac_cpu.c:453-457) at
 `iters` and RMSNorm is rac_rmsnorm (rac_cpu.c:548-574, eps 1e-5); the
 reference's bench computes those two with libm (expf, 1 / sqrtf), which
 differs by float rounding.
+
+Decode (one new token) runs on kernels that read the cache position from
+device memory (rac_decode.h): RMSNorm, the Q|K|V GEMV, the cache append,
+the fused attention of each query head over the cache, the output GEMV with
+the residual as its bias (x + W_o a: the GEMV adds its bias last, and float
+addition commutes), RMSNorm, the gate|up GEMV, SiLU(gate) * up, and the down
+GEMV with the residual as bias; then the position advances on the device.
+Every launch of a decode step then has fixed arguments, so `capture()`
+records the whole step, all layers, as one HIP graph that `step()` replays
+per token, bit-identical to the eager step.  The attention's softmax sums
+the row as the row kernel does on the scores padded with -inf to a
+multiple of 4 (a summation order; the padded probabilities are 0).
 """
 from __future__ import annotations
 
@@ -108,6 +119,9 @@ class RACDecoder:
         self.iters = iters
         self.t_max = t_max
         self.layers = [_Layer(w, keep_f32) for w in layers]
+        if t_max > ext.DECODE_MAX_LEN or cfg.d_head > ext.DECODE_MAX_HEAD:
+            raise ValueError(f"RAC: decode supports t_max <= {ext.DECODE_MAX_LEN} and "
+                             f"d_head <= {ext.DECODE_MAX_HEAD}")
         dev = layers[0]["W_q"].device
         shape = (cfg.n_kv_heads, t_max, cfg.d_head)
         # positions at or beyond the current length are never read: every
@@ -115,63 +129,91 @@ class RACDecoder:
         self.k_cache = [torch.zeros(shape, device=dev) for _ in range(cfg.n_layers)]
         self.v_cache = [torch.zeros(shape, device=dev) for _ in range(cfg.n_layers)]
         self.length = 0
+        self.pos = torch.zeros(1, device=dev, dtype=torch.int32)     # the length, on the device
+        self._graph = None
         # 1.0f / sqrtf((float)d_head), as attention_head_causal (:515)
         self.scale = float(torch.tensor(1.0) / torch.sqrt(torch.tensor(float(cfg.d_head))))
 
     def reset(self):
         """kv_reset (:492): the cache is empty again."""
         self.length = 0
+        self.pos.zero_()
 
-    def _linear(self, x: torch.Tensor, q8: torch.Tensor, f32: torch.Tensor, act: int = 0) -> torch.Tensor:
-        if x.size(0) == 1:
-            return ext.q8_gemv(x, q8)
-        return ext.fused_linear_forward(x, f32, None, act, iters=self.iters, mode=ext.MODE_FAST)
+    def _linear(self, x: torch.Tensor, w: torch.Tensor, act: int = 0) -> torch.Tensor:
+        return ext.fused_linear_forward(x, w, None, act, iters=self.iters, mode=ext.MODE_FAST)
 
-    def _attention(self, L: int, q: torch.Tensor, start: int, T: int) -> torch.Tensor:
+    def _prefill_attention(self, L: int, q: torch.Tensor, start: int, T: int) -> torch.Tensor:
         cfg = self.cfg
         nkv, dh = cfg.n_kv_heads, cfg.d_head
         rep = cfg.n_heads // nkv
         total = start + T
         # query rows of head group g: row r * T + t is head g * rep + r, token t
-        if T == 1:
-            qg = q.view(nkv, rep, dh)
-        else:
-            qg = q.view(T, nkv, rep, dh).permute(1, 2, 0, 3).reshape(nkv, rep * T, dh)
+        qg = q.view(T, nkv, rep, dh).permute(1, 2, 0, 3).reshape(nkv, rep * T, dh)
         kc = self.k_cache[L][:, :total, :]
         vc = self.v_cache[L][:, :total, :]
         s = ext.bmm(qg, kc, trans_b=True, alpha=self.scale, iters=self.iters, mode=ext.MODE_FAST)
-        if T > 1:
-            t = torch.arange(T, device=q.device).repeat(rep).view(rep * T, 1)
-            j = torch.arange(total, device=q.device).view(1, total)
-            s.masked_fill_(j > start + t, float("-inf"))
+        t = torch.arange(T, device=q.device).repeat(rep).view(rep * T, 1)
+        j = torch.arange(total, device=q.device).view(1, total)
+        s.masked_fill_(j > start + t, float("-inf"))
         p = ext.softmax(s.view(nkv * rep * T, total), self.iters).view(nkv, rep * T, total)
         o = ext.bmm(p, vc, iters=self.iters, mode=ext.MODE_FAST)          # [nkv, rep * T, dh]
-        if T == 1:
-            return o.view(1, cfg.d_model)
         return o.view(nkv, rep, T, dh).permute(2, 0, 1, 3).reshape(T, cfg.d_model)
 
-    def _layer(self, L: int, x: torch.Tensor, start: int) -> torch.Tensor:
+    def _prefill_layer(self, L: int, x: torch.Tensor, start: int) -> torch.Tensor:
         cfg, lw = self.cfg, self.layers[L]
         d, dh, nkv = cfg.d_model, cfg.d_head, cfg.n_kv_heads
         T = x.size(0)
-        f32 = lw.f32 or {}
+        w = lw.f32
         h = ext.rmsnorm(x, lw.rms_att, cfg.eps)
-        qkv = self._linear(h, lw.q8_qkv, f32.get("qkv"))                  # [T, d + 2 nkv dh]
-        q = qkv[:, :d]
-        k = qkv[:, d:d + nkv * dh].reshape(T, nkv, dh).transpose(0, 1)
-        v = qkv[:, d + nkv * dh:].reshape(T, nkv, dh).transpose(0, 1)
-        self.k_cache[L][:, start:start + T, :] = k
-        self.v_cache[L][:, start:start + T, :] = v
-        att = self._attention(L, q.contiguous() if T > 1 else q.reshape(1, d), start, T)
-        x = x + self._linear(att, lw.q8_o, f32.get("o"))
+        qkv = self._linear(h, w["qkv"])                                    # [T, d + 2 nkv dh]
+        self.k_cache[L][:, start:start + T, :] = qkv[:, d:d + nkv * dh].reshape(T, nkv, dh).transpose(0, 1)
+        self.v_cache[L][:, start:start + T, :] = qkv[:, d + nkv * dh:].reshape(T, nkv, dh).transpose(0, 1)
+        att = self._prefill_attention(L, qkv[:, :d].contiguous(), start, T)
+        x = x + self._linear(att, w["o"])
         h = ext.rmsnorm(x, lw.rms_ffn, cfg.eps)
-        if T == 1:
-            gu = ext.q8_gemv(h, lw.q8_gu)                                  # [1, 2 d_ff]
-            f = ext.silu(gu[:, :cfg.d_ff], self.iters) * gu[:, cfg.d_ff:]
-        else:
-            f = (ext.fused_linear_forward(h, f32["g"], None, 3, iters=self.iters, mode=ext.MODE_FAST)
-                 * ext.fused_linear_forward(h, f32["u"], None, 0, iters=self.iters, mode=ext.MODE_FAST))
-        return x + self._linear(f, lw.q8_d, f32.get("d"))
+        f = self._linear(h, w["g"], 3) * self._linear(h, w["u"])             # silu(gate) * up
+        return x + self._linear(f, w["d"])
+
+    def _decode_layer(self, L: int, x: torch.Tensor) -> torch.Tensor:
+        cfg, lw = self.cfg, self.layers[L]
+        d = cfg.d_model
+        h = ext.rmsnorm(x, lw.rms_att, cfg.eps)
+        qkv = ext.q8_gemv(h, lw.q8_qkv)                                   # [1, d + 2 nkv dh]
+        ext.kv_append_(qkv[0, d:], self.k_cache[L], self.v_cache[L], self.pos)
+        att = ext.decode_attention(qkv[0, :d], self.k_cache[L], self.v_cache[L], self.pos, cfg.n_heads,
+                                   self.scale, self.iters)
+        x = ext.q8_gemv(att.view(1, d), lw.q8_o, bias=x.view(d))          # x + W_o att
+        h = ext.rmsnorm(x, lw.rms_ffn, cfg.eps)
+        f = ext.swiglu(ext.q8_gemv(h, lw.q8_gu), self.iters)              # silu(gate) * up
+        return ext.q8_gemv(f, lw.q8_d, bias=x.view(d))                    # x + W_d f
+
+    def _decode_step(self, x: torch.Tensor) -> torch.Tensor:
+        for L in range(self.cfg.n_layers):
+            x = self._decode_layer(L, x)
+        ext.position_advance_(self.pos, 1)
+        return x
+
+    @torch.no_grad()
+    def capture(self) -> None:
+        """Records one decode step (every layer and the position's advance)
+        as a HIP graph; step() then replays it.  Runs one eager step first
+        (launcher set-up happens outside the recording) and restores the
+        position, so the cache's visible contents are unchanged."""
+        if self.length >= self.t_max:
+            raise RuntimeError("RAC: KV cache full")
+        dev = self.pos.device
+        x0 = torch.zeros((1, self.cfg.d_model), device=dev)
+        self._decode_step(x0)
+        self.pos.fill_(self.length)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = self._decode_step(x0)
+        torch.cuda.synchronize(dev)
+        self._graph, self._gx, self._gout = graph, x0, out
+
+    def release_graph(self) -> None:
+        self._graph = self._gx = self._gout = None
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -190,8 +232,17 @@ class RACDecoder:
             raise RuntimeError("RAC: prefill needs the fp32 weights (keep_f32=True)")
         start = self.length
         x = x.contiguous()
-        for L in range(self.cfg.n_layers):
-            x = self._layer(L, x, start)
+        if T == 1:
+            if self._graph is not None:
+                self._gx.copy_(x)
+                self._graph.replay()
+                x = self._gout.clone()
+            else:
+                x = self._decode_step(x)
+        else:
+            for L in range(self.cfg.n_layers):
+                x = self._prefill_layer(L, x, start)
+            self.pos.fill_(start + T)
         self.length = start + T
         return x
 

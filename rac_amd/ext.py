@@ -814,6 +814,86 @@ def q8_gemv(x: torch.Tensor, wq: torch.Tensor, bias: Optional[torch.Tensor] = No
     return out.reshape(*lead, N)
 
 
+# ── decode step (bench_rac_transformer.c decoder_forward_kv, T_new = 1) ──
+
+DECODE_MAX_HEAD = 256
+DECODE_MAX_LEN = 8192
+
+
+def _require_pos(pos: torch.Tensor) -> None:
+    _require_gpu(pos, "pos")
+    if pos.dtype != torch.int32 or pos.numel() != 1:
+        raise RuntimeError("RAC: pos must be a one-element int32 device tensor")
+
+
+def _require_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> Tuple[int, int, int]:
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require_f32(t, n)
+        if t.dim() != 3 or not t.is_contiguous():
+            raise RuntimeError(f"RAC: {n} must be a contiguous [n_kv_heads, t_cap, d_head] tensor")
+    if k_cache.shape != v_cache.shape:
+        raise RuntimeError("RAC: k_cache and v_cache must have the same shape")
+    return tuple(k_cache.shape)
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                     n_heads: int, scale: float, iters: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention of one token's queries q [n_heads * d_head] over cache
+    positions 0 .. pos (pos read on the device when the kernel runs); query
+    head h reads key/value head h // (n_heads / n_kv_heads)
+    (bench_rac_transformer.c:508-548).  Returns [n_heads * d_head]."""
+    _require_f32(q, "q")
+    _require_pos(pos)
+    nkv, t_cap, dh = _require_cache(k_cache, v_cache)
+    if q.numel() != n_heads * dh or not q.is_contiguous():
+        raise RuntimeError("RAC: q must be a contiguous n_heads * d_head vector")
+    if out is None:
+        out = torch.empty(n_heads * dh, device=q.device, dtype=torch.float32)
+    elif out.dtype != torch.float32 or out.numel() != n_heads * dh or not out.is_contiguous():
+        raise RuntimeError("RAC: out must be a contiguous fp32 n_heads * d_head vector")
+    check(_lib.load().rac_decode_attention_dev(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                               int(n_heads), nkv, dh, t_cap, pos.data_ptr(), float(scale),
+                                               _resolve_iters(iters), _stream(q)), "rac_decode_attention_dev")
+    return out
+
+
+def kv_append_(kv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor) -> None:
+    """Writes kv = [k | v] (2 * n_kv_heads * d_head values, contiguous) at
+    cache position pos (read on the device)."""
+    _require_f32(kv, "kv")
+    _require_pos(pos)
+    nkv, t_cap, dh = _require_cache(k_cache, v_cache)
+    if kv.numel() != 2 * nkv * dh or not kv.is_contiguous():
+        raise RuntimeError("RAC: kv must hold 2 * n_kv_heads * d_head contiguous values")
+    check(_lib.load().rac_kv_append_dev(kv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), nkv, dh, t_cap,
+                                        pos.data_ptr(), _stream(kv)), "rac_kv_append_dev")
+
+
+def position_advance_(pos: torch.Tensor, by: int = 1) -> None:
+    """pos += by on the stream."""
+    _require_pos(pos)
+    check(_lib.load().rac_position_advance_dev(pos.data_ptr(), int(by), _stream(pos)), "rac_position_advance_dev")
+
+
+def swiglu(gu: torch.Tensor, iters: int = 0) -> torch.Tensor:
+    """silu(gate) * up for gu = [..., 2 n] holding gate then up in its last
+    dim; returns [..., n] (CORDIC SiLU, the bits of silu())."""
+    _require_f32(gu, "gu")
+    if gu.size(-1) % 2:
+        raise RuntimeError("RAC: swiglu expects an even last dim (gate then up)")
+    n = gu.size(-1) // 2
+    gu = gu.contiguous()
+    lead = gu.shape[:-1]
+    rows = gu.numel() // (2 * n) if n else 0
+    out = torch.empty((*lead, n), device=gu.device, dtype=torch.float32)
+    lib = _lib.load()
+    g2, o2 = gu.view(rows, 2 * n), out.view(rows, n)
+    for r in range(rows):
+        check(lib.rac_swiglu_dev(g2[r].data_ptr(), o2[r].data_ptr(), n, _resolve_iters(iters), _stream(gu)),
+              "rac_swiglu_dev")
+    return out
+
+
 # ── RAC-DSP fixed-point engine (sim/rac_dsp_core.h) ──────────────────────
 
 DSP_OPS = {"rotate": 0, "project": 1, "vectoring": 2, "hyperbolic": 3}

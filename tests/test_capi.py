@@ -17,7 +17,7 @@ import raclib as rl
 
 ROOT = rl.ROOT
 HEADERS = [os.path.join(ROOT, "include", h) for h in ("rac.h", "rac_ext.h", "rac_q8_0.h", "rac_dsp.h",
-                                                               "rac_safetensors.h")]
+                                                               "rac_safetensors.h", "rac_decode.h")]
 
 
 def declared_functions():
@@ -56,7 +56,7 @@ def test_python_binding_covers_headers():
 def test_headers_compile_and_link_as_c(tmp_path):
     src = tmp_path / "t.c"
     src.write_text('#include "rac.h"\n#include "rac_ext.h"\n#include "rac_q8_0.h"\n#include "rac_dsp.h"\n'
-                   '#include "rac_safetensors.h"\n'
+                   '#include "rac_safetensors.h"\n#include "rac_decode.h"\n'
                    "int main(void){ rac_set_cordic_iters(8); return rac_get_cordic_iters() == 8 ? 0 : 1; }\n")
     exe = tmp_path / "t"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),

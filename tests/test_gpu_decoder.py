@@ -63,6 +63,25 @@ def _weights(cfg, seed):
 
 # ── the checker composition (bit-exact bar) ──────────────────────────────────
 
+def orc_decode_attention(q, K, V, n, n_heads, scale, iters):
+    """One token's attention over cache positions 0 .. n-1 as the checker's
+    stages: FAST scores (alpha = scale), the lane-order softmax of the row
+    padded with -inf to a multiple of 4, FAST P V."""
+    nkv, _, dh = K.shape
+    rep = n_heads // nkv
+    n4 = 4 * ((n + 3) // 4)
+    out = np.empty(n_heads * dh, F32)
+    for g in range(nkv):
+        qg = np.ascontiguousarray(q.reshape(nkv, rep, dh)[g])
+        s = rl.orc_matmul(qg, np.ascontiguousarray(K[g, :n]), rep, n, dh, iters, 0, tb=1, alpha=float(scale))
+        sp = np.full((rep, n4), -np.inf, F32)
+        sp[:, :n] = s
+        p = np.ascontiguousarray(rl.orc_softmax_lanes(sp, iters)[:, :n])
+        out[g * rep * dh:(g + 1) * rep * dh] = rl.orc_matmul(p, np.ascontiguousarray(V[g, :n]), rep, dh, n,
+                                                             iters, 0).reshape(-1)
+    return out
+
+
 class OrcDecoder:
     def __init__(self, cfg, W, t_max, iters):
         self.cfg, self.W, self.iters = cfg, W, iters
@@ -97,7 +116,9 @@ class OrcDecoder:
             self.V[L][:, start:total] = qkv[:, d + nkv * dh:].reshape(Tn, nkv, dh).transpose(1, 0, 2)
             att = np.empty((Tn, d), F32)
             tq = np.tile(np.arange(Tn), rep)[:, None]
-            for g in range(nkv):
+            if Tn == 1:
+                att[0] = orc_decode_attention(q[0], self.K[L], self.V[L], total, cfg.n_heads, self.scale, n)
+            for g in range(nkv if Tn > 1 else 0):
                 qg = q.reshape(Tn, nkv, rep, dh)[:, g].transpose(1, 0, 2).reshape(rep * Tn, dh)
                 s = rl.orc_matmul(np.ascontiguousarray(qg), np.ascontiguousarray(self.K[L][g, :total]),
                                   rep * Tn, total, dh, n, 0, tb=1, alpha=float(self.scale))
@@ -275,3 +296,113 @@ def test_bmm_on_cache_slices(tb):
                     ref = rl.orc_matmul(np.ascontiguousarray(p[z]), np.ascontiguousarray(cache[z, :total]), 6, dh,
                                         total, iters, mode)
                     assert np.array_equal(got[z], ref), (total, z, mode)
+
+
+# ── the decode-step kernels (rac_decode.h) ───────────────────────────────────
+
+@pytest.mark.parametrize("iters", [24, 16, 8, 12])
+@pytest.mark.parametrize("heads,kv,dh,t_cap", [(8, 2, 16, 40), (4, 4, 64, 300), (6, 1, 7, 33), (32, 4, 64, 1030),
+                                               (2, 2, 256, 9)])
+def test_decode_attention_vs_checker(heads, kv, dh, t_cap, iters):
+    from rac_amd import ext as e
+    K = rl.gen_normal((kv, t_cap, dh), seed=heads + dh)
+    V = rl.gen_normal((kv, t_cap, dh), seed=heads + dh + 1)
+    q = rl.gen_normal((heads * dh,), seed=t_cap)
+    scale = F32(1) / np.sqrt(F32(dh))
+    Kt, Vt, qt = T(K), T(V), T(q)
+    for n in sorted({1, 2, 3, 4, 5, 17, t_cap // 2 + 1, t_cap - 1, t_cap}):
+        if n < 1 or n > t_cap:
+            continue
+        print(f"decode attention heads={heads} kv={kv} dh={dh} t_cap={t_cap} n={n} iters={iters}", flush=True)
+        pos = torch.tensor([n - 1], dtype=torch.int32, device=DEV)
+        got = H(e.decode_attention(qt, Kt, Vt, pos, heads, float(scale), iters))
+        assert np.array_equal(got, orc_decode_attention(q, K, V, n, heads, scale, iters)), n
+
+
+def test_decode_attention_scores_spread():
+    """Large score spread (exps flushing to 0 beside 1) and equal scores."""
+    from rac_amd import ext as e
+    heads, kv, dh, t_cap = 4, 2, 32, 64
+    K = rl.gen_normal((kv, t_cap, dh), seed=1) * F32(30)
+    K[1, :20] = 0.0
+    V = rl.gen_normal((kv, t_cap, dh), seed=2)
+    q = rl.gen_normal((heads * dh,), seed=3) * F32(3)
+    for n in (1, 19, 21, 64):
+        pos = torch.tensor([n - 1], dtype=torch.int32, device=DEV)
+        got = H(e.decode_attention(T(q), T(K.astype(F32)), T(V), pos, heads, 0.125, 16))
+        assert np.array_equal(got, orc_decode_attention(q, K.astype(F32), V, n, heads, F32(0.125), 16)), n
+
+
+def test_decode_attention_position_outside_cache_gives_nan():
+    from rac_amd import ext as e
+    K = T(np.ones((1, 8, 4), F32))
+    for p in (-1, 8, 100):
+        got = H(e.decode_attention(T(np.ones(8, F32)), K, K, torch.tensor([p], dtype=torch.int32, device=DEV), 2, 1.0))
+        assert np.isnan(got).all(), p
+
+
+def test_kv_append_and_advance():
+    from rac_amd import ext as e
+    kv, dh, t_cap = 3, 5, 7
+    Kc = torch.full((kv, t_cap, dh), 7.0, device=DEV)
+    Vc = torch.full((kv, t_cap, dh), 9.0, device=DEV)
+    pos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    want_k, want_v = np.full((kv, t_cap, dh), 7.0, F32), np.full((kv, t_cap, dh), 9.0, F32)
+    for step in range(t_cap + 2):
+        src = rl.gen_normal((2 * kv * dh,), seed=step)
+        e.kv_append_(T(src), Kc, Vc, pos)
+        e.position_advance_(pos, 1)
+        if step < t_cap:        # beyond the cache: nothing written
+            want_k[:, step] = src[:kv * dh].reshape(kv, dh)
+            want_v[:, step] = src[kv * dh:].reshape(kv, dh)
+    assert int(H(pos)[0]) == t_cap + 2
+    assert np.array_equal(H(Kc), want_k) and np.array_equal(H(Vc), want_v)
+    e.position_advance_(pos, -3)
+    assert int(H(pos)[0]) == t_cap - 1
+
+
+@pytest.mark.parametrize("iters", [24, 16, 8, 5])
+def test_swiglu_vs_checker(iters):
+    from rac_amd import ext as e
+    for n in (1, 7, 5632, 70001):
+        gu = rl.gen_normal((1, 2 * n), seed=n) * F32(4)
+        if n >= 4:
+            gu[0, :4] = [0.0, -0.0, 60.0, -60.0]
+        got = H(e.swiglu(T(gu), iters))
+        want = rl.orc_unary("orc_silu", gu[:, :n], iters) * gu[:, n:]
+        assert np.array_equal(got, want), n
+        assert np.array_equal(got, H(e.silu(T(gu[:, :n]), iters) * T(gu[:, n:])))
+
+
+def test_decoder_graph_replays_equal_eager():
+    """The captured decode step replayed per token, with other work and
+    synchronisations between the replays, equals the eager step bit for
+    bit, and the caches agree afterwards."""
+    from rac_amd.decoder import DecoderConfig
+    cfg = DecoderConfig(**CFGS["gqa"])
+    W = _weights(cfg, seed=21)
+    eager, graphed = _decoder(cfg, W, 24, 24), _decoder(cfg, W, 24, 24)
+    x0 = rl.gen_normal((4, cfg.d_model), seed=5)
+    assert np.array_equal(H(eager.forward(T(x0))), H(graphed.forward(T(x0))))
+    graphed.capture()
+    other = torch.ones(1000, device=DEV)
+    for i in range(9):
+        x = rl.gen_normal((1, cfg.d_model), seed=40 + i)
+        want = H(eager.step(T(x)))
+        got = H(graphed.step(T(x)))
+        assert np.array_equal(got, want), i
+        other = (other * 1.5).sum().expand(1000).contiguous()      # unrelated eager work between replays
+        torch.cuda.synchronize()
+    assert eager.length == graphed.length == 13
+    assert int(H(graphed.pos)[0]) == 13
+    for L in range(cfg.n_layers):
+        assert np.array_equal(H(eager.k_cache[L][:, :13]), H(graphed.k_cache[L][:, :13]))
+        assert np.array_equal(H(eager.v_cache[L][:, :13]), H(graphed.v_cache[L][:, :13]))
+    # a prefill chunk after graph replays, then replays again
+    x2 = rl.gen_normal((3, cfg.d_model), seed=77)
+    assert np.array_equal(H(eager.forward(T(x2))), H(graphed.forward(T(x2))))
+    x = rl.gen_normal((1, cfg.d_model), seed=78)
+    assert np.array_equal(H(graphed.step(T(x))), H(eager.step(T(x))))
+    graphed.reset()
+    eager.reset()
+    assert np.array_equal(H(graphed.step(T(x))), H(eager.step(T(x))))
