@@ -41,73 +41,77 @@ __device__ __forceinline__ void dec_exp4(float* v, int iters, float khinv) {
     }
 }
 
-template <int NITER, bool VEC>
+// V tile staged in LDS for the P V chains: kDecTile floats (16 KB)
+constexpr int kDecTile = 4096;
+
+// Scores: lane t computes positions t, t + 256, ... (one fmaf chain each;
+// DH > 0: the row's DH / 4 16-byte loads are issued together).  Softmax:
+// lane l takes the groups l, l + 256, ... as the row kernel.  P V: the
+// value rows pass through LDS a tile at a time (every lane loads, the next
+// tile's loads are in flight during the chains), and lane c < d_head runs
+// output column c's chain over the tile.
+template <int NITER, int DH>
 __global__ __launch_bounds__(kRowThreads) void decode_attention_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
-    float* __restrict__ out, int rep, int dh, long t_cap, const int* __restrict__ pos_dev, float scale,
+    float* __restrict__ out, int rep, int dh_rt, long t_cap, const int* __restrict__ pos_dev, float scale,
     int iters, float khinv)
 {
     __shared__ __attribute__((aligned(16))) float sq[kDecodeMaxHead];
     __shared__ __attribute__((aligned(16))) float sp[kDecodeMaxLen];
+    __shared__ __attribute__((aligned(16))) float sv[kDecTile];
     __shared__ float red[2 * kRowWaves];
+    const int dh = DH > 0 ? DH : dh_rt;
+    const int tid = threadIdx.x;
     const int h = blockIdx.x;
     const long g = h / rep;
     const int pos = *pos_dev;
     float* o = out + (long)h * dh;
     if (pos < 0 || pos >= t_cap || pos >= kDecodeMaxLen) {
         // a position outside the cache: NaN output, nothing read
-        for (int c = threadIdx.x; c < dh; c += kRowThreads) o[c] = __builtin_nanf("");
+        for (int c = tid; c < dh; c += kRowThreads) o[c] = __builtin_nanf("");
         return;
     }
     const int n = pos + 1;                 // positions 0 .. pos, the new token's included
     const int n4 = (n + 3) / 4;
     const float* K = kc + g * t_cap * dh;
     const float* V = vc + g * t_cap * dh;
-    for (int c = threadIdx.x; c < dh; c += kRowThreads) sq[c] = q[(long)h * dh + c];
+    for (int c = tid; c < dh; c += kRowThreads) sq[c] = q[(long)h * dh + c];
     __syncthreads();
 
-    // scores of the lane's groups, kept in LDS; the lane's maximum
-    float m = -__builtin_inff();
-    for (int gi = threadIdx.x; gi < n4; gi += kRowThreads) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int j0 = 4 * gi;
-        const int nr = n - j0 < 4 ? n - j0 : 4;       // rows of this group inside the row
-        if constexpr (VEC) {
-            for (int k = 0; k < dh; k += 4) {
-                const float4 a = *reinterpret_cast<const float4*>(&sq[k]);
+    for (int j = tid; j < n; j += kRowThreads) {
+        const float* kr = K + (long)j * dh;
+        float acc = 0.0f;
+        if constexpr (DH > 0) {
+            float4 kv[DH / 4];
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    if (c < nr) {
-                        const float4 b = *reinterpret_cast<const float4*>(K + (long)(j0 + c) * dh + k);
-                        acc[c] = __builtin_fmaf(a.x, b.x, acc[c]);
-                        acc[c] = __builtin_fmaf(a.y, b.y, acc[c]);
-                        acc[c] = __builtin_fmaf(a.z, b.z, acc[c]);
-                        acc[c] = __builtin_fmaf(a.w, b.w, acc[c]);
-                    }
-                }
+            for (int k = 0; k < DH / 4; k++) kv[k] = reinterpret_cast<const float4*>(kr)[k];
+#pragma unroll
+            for (int k = 0; k < DH / 4; k++) {
+                const float4 a = reinterpret_cast<const float4*>(sq)[k];
+                acc = __builtin_fmaf(a.x, kv[k].x, acc);
+                acc = __builtin_fmaf(a.y, kv[k].y, acc);
+                acc = __builtin_fmaf(a.z, kv[k].z, acc);
+                acc = __builtin_fmaf(a.w, kv[k].w, acc);
             }
         } else {
-            for (int k = 0; k < dh; k++) {
-                const float a = sq[k];
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    if (c < nr) acc[c] = __builtin_fmaf(a, K[(long)(j0 + c) * dh + k], acc[c]);
-            }
+            for (int k = 0; k < dh; k++) acc = __builtin_fmaf(sq[k], kr[k], acc);
         }
+        sp[j] = scale * acc;
+    }
+    if (tid < 4 * n4 - n) sp[n + tid] = -__builtin_inff();       // the row's -inf padding
+    __syncthreads();
+
+    // the lane's maximum, exps and sum over its groups, in group order
+    float m = -__builtin_inff();
+    for (int gi = tid; gi < n4; gi += kRowThreads) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float s = c < nr ? scale * acc[c] : -__builtin_inff();
-            sp[j0 + c] = s;
-            m = fmaxf(m, s);
-        }
+        for (int c = 0; c < 4; c++) m = fmaxf(m, sp[4 * gi + c]);
     }
     m = block_max<false>(m, red);
-
-    // exps, the lane's sum in group order, the row sum
     constexpr bool kLean = NITER > 0;
     float nanp = -__builtin_inff();
     float s = 0.0f;
-    for (int gi = threadIdx.x; gi < n4; gi += kRowThreads) {
+    for (int gi = tid; gi < n4; gi += kRowThreads) {
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -126,38 +130,65 @@ __global__ __launch_bounds__(kRowThreads) void decode_attention_kernel(
     }
     s = block_sum<false>(s, red + kRowWaves);
     const float inv = 1.0f / s;
-    for (int gi = threadIdx.x; gi < n4; gi += kRowThreads) {
+    for (int gi = tid; gi < n4; gi += kRowThreads) {
 #pragma unroll
         for (int c = 0; c < 4; c++) sp[4 * gi + c] = sp[4 * gi + c] * inv;
     }
-    __syncthreads();
 
     // out[c] = sum_j p_j V[j][c], one chain per output column in j order
-    for (int c = threadIdx.x; c < dh; c += kRowThreads) {
-        float acc = 0.0f;
-        int j = 0;
-        for (; j + 8 <= n; j += 8) {
-            float vv[8];
+    const int tj = kDecTile / dh;                        // value rows per tile
+    constexpr int kF4 = kDecTile / 4 / kRowThreads;      // tile float4 per lane
+    const bool vec = DH > 0;
+    float4 pre[kF4];
+    auto fetch = [&](int j0) {                           // rows j0 .. of the tile into registers
+        const int cnt = (n - j0 < tj ? n - j0 : tj) * dh;
+        const float* src = V + (long)j0 * dh;
 #pragma unroll
-            for (int u = 0; u < 8; u++) vv[u] = V[(long)(j + u) * dh + c];
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc = __builtin_fmaf(sp[j + u], vv[u], acc);
+        for (int i = 0; i < kF4; i++) {
+            const int e = (tid + i * kRowThreads) * 4;
+            if (vec) {
+                pre[i] = e < cnt ? *reinterpret_cast<const float4*>(src + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                pre[i].x = e < cnt ? src[e] : 0.0f;
+                pre[i].y = e + 1 < cnt ? src[e + 1] : 0.0f;
+                pre[i].z = e + 2 < cnt ? src[e + 2] : 0.0f;
+                pre[i].w = e + 3 < cnt ? src[e + 3] : 0.0f;
+            }
         }
-        for (; j < n; j++) acc = __builtin_fmaf(sp[j], V[(long)j * dh + c], acc);
-        o[c] = acc;
+    };
+    float acc = 0.0f;
+    fetch(0);
+    for (int j0 = 0; j0 < n; j0 += tj) {
+        __syncthreads();                                 // previous tile's chains done (and sp final)
+#pragma unroll
+        for (int i = 0; i < kF4; i++) reinterpret_cast<float4*>(sv)[tid + i * kRowThreads] = pre[i];
+        __syncthreads();
+        if (j0 + tj < n) fetch(j0 + tj);                 // in flight during the chains
+        const int cnt = n - j0 < tj ? n - j0 : tj;
+        if (tid < dh) {
+            int u = 0;
+            for (; u + 8 <= cnt; u += 8) {
+#pragma unroll
+                for (int w = 0; w < 8; w++) acc = __builtin_fmaf(sp[j0 + u + w], sv[(u + w) * dh + tid], acc);
+            }
+            for (; u < cnt; u++) acc = __builtin_fmaf(sp[j0 + u], sv[u * dh + tid], acc);
+        }
     }
+    if (tid < dh) o[tid] = acc;
 }
 
 template <int NITER>
-static hipError_t decode_attention_vec(bool vec, const float* q, const float* kc, const float* vc, float* out,
-                                       int n_heads, int rep, int dh, long t_cap, const int* pos, float scale,
-                                       int iters, float khinv, hipStream_t s) {
-    if (vec)
-        hipLaunchKernelGGL((decode_attention_kernel<NITER, true>), dim3(n_heads), dim3(kRowThreads), 0, s, q, kc,
-                           vc, out, rep, dh, t_cap, pos, scale, iters, khinv);
-    else
-        hipLaunchKernelGGL((decode_attention_kernel<NITER, false>), dim3(n_heads), dim3(kRowThreads), 0, s, q, kc,
-                           vc, out, rep, dh, t_cap, pos, scale, iters, khinv);
+static hipError_t decode_attention_dh(int dh, bool vec, const float* q, const float* kc, const float* vc,
+                                      float* out, int n_heads, int rep, long t_cap, const int* pos, float scale,
+                                      int iters, float khinv, hipStream_t s) {
+#define RAC_DEC_ATT(D)                                                                                         \
+    hipLaunchKernelGGL((decode_attention_kernel<NITER, D>), dim3(n_heads), dim3(kRowThreads), 0, s, q, kc, vc, \
+                       out, rep, dh, t_cap, pos, scale, iters, khinv)
+    if (vec && dh == 64) RAC_DEC_ATT(64);
+    else if (vec && dh == 128) RAC_DEC_ATT(128);
+    else if (vec && dh == 32) RAC_DEC_ATT(32);
+    else RAC_DEC_ATT(0);
+#undef RAC_DEC_ATT
     return hipGetLastError();
 }
 
@@ -167,13 +198,14 @@ hipError_t decode_attention_launch(const float* q, const float* kc, const float*
     iters = clamp_iters(iters);
     const float khinv = host_consts().exp_khinv[iters];
     const int rep = n_heads / n_kv_heads;
-    // 16-byte key loads: rows of d_head floats on 16-byte boundaries
-    const bool vec = dh % 4 == 0 && (reinterpret_cast<uintptr_t>(kc) & 15) == 0;
+    // 16-byte loads of key and value rows: rows on 16-byte boundaries
+    const bool vec = dh % 4 == 0 && (reinterpret_cast<uintptr_t>(kc) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(vc) & 15) == 0;
     switch (iters) {
-        case 8: return decode_attention_vec<8>(vec, q, kc, vc, out, n_heads, rep, dh, t_cap, pos, scale, iters, khinv, s);
-        case 16: return decode_attention_vec<16>(vec, q, kc, vc, out, n_heads, rep, dh, t_cap, pos, scale, iters, khinv, s);
-        case 24: return decode_attention_vec<24>(vec, q, kc, vc, out, n_heads, rep, dh, t_cap, pos, scale, iters, khinv, s);
-        default: return decode_attention_vec<0>(vec, q, kc, vc, out, n_heads, rep, dh, t_cap, pos, scale, iters, khinv, s);
+        case 8: return decode_attention_dh<8>(dh, vec, q, kc, vc, out, n_heads, rep, t_cap, pos, scale, iters, khinv, s);
+        case 16: return decode_attention_dh<16>(dh, vec, q, kc, vc, out, n_heads, rep, t_cap, pos, scale, iters, khinv, s);
+        case 24: return decode_attention_dh<24>(dh, vec, q, kc, vc, out, n_heads, rep, t_cap, pos, scale, iters, khinv, s);
+        default: return decode_attention_dh<0>(dh, vec, q, kc, vc, out, n_heads, rep, t_cap, pos, scale, iters, khinv, s);
     }
 }
 
