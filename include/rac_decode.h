@@ -54,6 +54,29 @@ int rac_position_advance_dev(int *pos, int by, void *stream);
  * rac_silu_dev. */
 int rac_swiglu_dev(const float *gu, float *out, long n, int iters, void *stream);
 
+/* One-row Q8_0 GEMVs with the RMSNorm fused in: h = rmsnorm(x) *
+ * norm_weight computed as rac_rmsnorm_dev does (same bits), then the GEMV
+ * of rac_q8_0_gemv_dev over h (same bits).  K % 256 == 0, K <= 16384; x,
+ * norm_weight and weight 16-byte aligned.  No counterpart entry point in
+ * the reference, whose decoder_forward_kv calls rmsnorm (:316-332) and
+ * bench_fused_linear_q8 (:301-312) one after the other. */
+int rac_q8_0_gemv_rmsnorm_dev(const float *x, const float *norm_weight, float eps, const void *weight,
+                              const float *bias, float *out, int N, int K, int act, void *stream);
+
+/* The Q, K, V projection of one token (:565-574): weight holds the
+ * (n_heads + 2 n_kv_heads) * d_head rows W_q, W_k, W_v over K = d_model;
+ * queries to q_out [n_heads * d_head], keys and values into the caches at
+ * position *pos (nothing for a position outside [0, t_cap)). */
+int rac_decode_qkv_dev(const float *x, const float *norm_weight, float eps, const void *weight, float *q_out,
+                       float *k_cache, float *v_cache, int n_heads, int n_kv_heads, int d_head, int K,
+                       long t_cap, const int *pos, void *stream);
+
+/* Gate and up of the SwiGLU feed-forward (:605-611): weight holds 2 n_ff
+ * rows interleaved gate_0, up_0, gate_1, up_1, ...; out[i] = silu(gate_i .
+ * h) * (up_i . h), SiLU by the CORDIC exp at `iters` steps. */
+int rac_decode_swiglu_gemv_dev(const float *x, const float *norm_weight, float eps, const void *weight,
+                               float *out, int n_ff, int K, int iters, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,6 +96,9 @@ _SIGNATURES = {
     "rac_kv_append_dev": (_i, [_vp, _vp, _vp, _i, _i, _l, _vp, _vp]),
     "rac_position_advance_dev": (_i, [_vp, _i, _vp]),
     "rac_swiglu_dev": (_i, [_vp, _vp, _l, _i, _vp]),
+    "rac_q8_0_gemv_rmsnorm_dev": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "rac_decode_qkv_dev": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _l, _vp, _vp]),
+    "rac_decode_swiglu_gemv_dev": (_i, [_vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp]),
     "rac_q8_0_gemv_dev": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rac_q8_0_quantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),
     "rac_q8_0_dequantize_dev": (_i, [_vp, _vp, _l, _i, _vp]),

@@ -444,6 +444,66 @@ RAC_EXPORT int rac_kv_append_dev(const float* kv, float* k_cache, float* v_cache
                      "rac_kv_append_dev launch");
 }
 
+// The decode step's fused one-row GEMVs: x is normalised inside the GEMV
+// (rac_rmsnorm_dev's arithmetic and order), so K must take the row kernel's
+// 16-byte form (K % 4 == 0, K <= 16384) and the GEMV its fast layout
+// (K % 256 == 0); x, norm_weight and the weights 16-byte aligned.
+static int check_fused_gemv(const char* who, const float* x, const float* g, const void* w, long rows, int K) {
+    if (!x || !g || !w) return fail(RAC_ERR_NULL_PTR, "%s: null buffer", who);
+    if (rows <= 0 || rows > 2147483647L) return fail(RAC_ERR_INVALID_DIM, "%s: bad row count", who);
+    if (K <= 0 || K % 256 || K > 16384)
+        return fail(RAC_ERR_INVALID_DIM, "%s: K must be a multiple of 256 and at most 16384", who);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(g) |
+                        reinterpret_cast<uintptr_t>(w);
+    if (a & 15) return fail(RAC_ERR_INVALID_DIM, "%s: x, norm_weight and weight must be 16-byte aligned", who);
+    return RAC_OK;
+}
+
+// out = act(W rmsnorm(x) * norm_weight + bias) for one row
+// (bench_rac_transformer.c:566-567 / :605-606, norm then projection).
+RAC_EXPORT int rac_q8_0_gemv_rmsnorm_dev(const float* x, const float* norm_weight, float eps, const void* weight,
+                                         const float* bias, float* out, int N, int K, int act, void* stream) {
+    int rc = check_fused_gemv("rac_q8_0_gemv_rmsnorm_dev", x, norm_weight, weight, N, K);
+    if (rc) return rc;
+    if (!out) return fail(RAC_ERR_NULL_PTR, "rac_q8_0_gemv_rmsnorm_dev: null output");
+    if (act < 0 || act > 3) return fail(RAC_ERR_INVALID_DIM, "rac_q8_0_gemv_rmsnorm_dev: act must be 0..3");
+    return check_hip(q8_rmsnorm_gemv_launch(x, norm_weight, eps, static_cast<const uint8_t*>(weight), bias, out, N,
+                                            K, act, (hipStream_t)stream),
+                     "rac_q8_0_gemv_rmsnorm_dev launch");
+}
+
+// Q, K and V of the new token (:566-574): weight rows (n_heads + 2
+// n_kv_heads) * d_head over K = d_model; the queries to q_out, keys and
+// values into the caches at *pos.
+RAC_EXPORT int rac_decode_qkv_dev(const float* x, const float* norm_weight, float eps, const void* weight,
+                                  float* q_out, float* k_cache, float* v_cache, int n_heads, int n_kv_heads,
+                                  int d_head, int K, long t_cap, const int* pos, void* stream) {
+    if (!q_out || !k_cache || !v_cache || !pos) return fail(RAC_ERR_NULL_PTR, "rac_decode_qkv_dev: null buffer");
+    if (n_heads <= 0 || n_kv_heads <= 0 || d_head <= 0 || t_cap <= 0)
+        return fail(RAC_ERR_INVALID_DIM, "rac_decode_qkv_dev: sizes must be positive");
+    const long rows = (long)(n_heads + 2L * n_kv_heads) * d_head;
+    int rc = check_fused_gemv("rac_decode_qkv_dev", x, norm_weight, weight, rows, K);
+    if (rc) return rc;
+    return check_hip(q8_decode_qkv_launch(x, norm_weight, eps, static_cast<const uint8_t*>(weight), q_out,
+                                          n_heads * d_head, k_cache, v_cache, n_kv_heads * d_head, d_head, t_cap,
+                                          pos, K, (hipStream_t)stream),
+                     "rac_decode_qkv_dev launch");
+}
+
+// Gate and up of the SwiGLU feed-forward (:605-611) in one GEMV: weight
+// rows interleave gate_0, up_0, gate_1, up_1, ...; out[i] = silu(gate_i)
+// * up_i over h = rmsnorm(x) * norm_weight.
+RAC_EXPORT int rac_decode_swiglu_gemv_dev(const float* x, const float* norm_weight, float eps, const void* weight,
+                                          float* out, int n_ff, int K, int iters, void* stream) {
+    if (!out) return fail(RAC_ERR_NULL_PTR, "rac_decode_swiglu_gemv_dev: null output");
+    if (n_ff <= 0 || n_ff > 1073741823) return fail(RAC_ERR_INVALID_DIM, "rac_decode_swiglu_gemv_dev: bad n_ff");
+    int rc = check_fused_gemv("rac_decode_swiglu_gemv_dev", x, norm_weight, weight, 2L * n_ff, K);
+    if (rc) return rc;
+    return check_hip(q8_decode_swiglu_launch(x, norm_weight, eps, static_cast<const uint8_t*>(weight), out, n_ff, K,
+                                             iters, (hipStream_t)stream),
+                     "rac_decode_swiglu_gemv_dev launch");
+}
+
 // *pos += by on the stream (full_model_forward's cur_len += T_new, :624).
 RAC_EXPORT int rac_position_advance_dev(int* pos, int by, void* stream) {
     if (!pos) return fail(RAC_ERR_NULL_PTR, "rac_position_advance_dev: null buffer");

@@ -136,6 +136,19 @@ hipError_t inner_launch(const float2* a, const float2* b, long n, float* out, hi
 hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, float* out, int M, int N,
                           int K, int act, hipStream_t s);
 hipError_t q8_quantize_launch(const float* src, uint8_t* dst, long nblocks, hipStream_t s);
+// One-row GEMVs of the decode step with rmsnorm(x) * gamma as input (the
+// fast layout only: K % 256 == 0, 16-byte aligned weights; else
+// hipErrorInvalidValue): plain (out = act(W h + bias)); Q|K|V (rows below
+// split to q_out, the next kvw rows to the key cache and the kvw after to
+// the value cache at *pos); gate / up pairs (2 n_ff interleaved rows,
+// out[i] = silu(gate_i) * up_i).
+hipError_t q8_rmsnorm_gemv_launch(const float* x, const float* gamma, float eps, const uint8_t* w,
+                                  const float* bias, float* out, int N, int K, int act, hipStream_t s);
+hipError_t q8_decode_qkv_launch(const float* x, const float* gamma, float eps, const uint8_t* w, float* q_out,
+                                int split, float* kc, float* vc, int kvw, int dh, long t_cap, const int* pos,
+                                int K, hipStream_t s);
+hipError_t q8_decode_swiglu_launch(const float* x, const float* gamma, float eps, const uint8_t* w, float* out,
+                                   int n_ff, int K, int iters, hipStream_t s);
 // Decode step of a decoder layer (rac_decode.hip): the token's cache
 // position is read from *pos in device memory.  Attention: one workgroup
 // per query head over positions 0 .. *pos of a cache [n_kv_heads, t_cap,

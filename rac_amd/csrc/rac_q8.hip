@@ -13,8 +13,11 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include "rac_act.hpp"
 #include "rac_internal.hpp"
+#include "rac_math.hpp"
 #include "rac_q8.hpp"
+#include "rac_rowred.hpp"
 
 namespace rac {
 
@@ -69,13 +72,40 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
 // kernel needs 119), several rows for 2.
 constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
 
-template <int MX, int CB, int R>
+// Fusions of a decoder layer's decode step into the one-row GEMV:
+//   NORM   x is replaced by rmsnorm(x) * gamma with the row kernel's
+//          arithmetic and sum order (lane l's float4 groups l, l + 256, ...,
+//          fmaf of the squares in order, the fixed block combination, the
+//          CORDIC rsqrt of mean + eps, then (x * inv) * gamma), computed by
+//          every workgroup while its first chunk's loads are in flight.
+//   EPI 1  rows come in gate / up pairs (2i, 2i + 1): out[i] =
+//          silu(gate) * up, SiLU by the runtime-step CORDIC exp.
+//   EPI 2  rows [split, split + kvw) are the token's keys, [split + kvw,
+//          split + 2 kvw) its values: written into kc / vc [heads, t_cap,
+//          dh] at position *pos (nothing for a position outside the cache);
+//          rows below split go to out.
+// Each output's fold is the plain kernel's, so its bits are unchanged.
+struct Q8Fuse {
+    const float* gamma = nullptr;
+    float eps = 0.0f, rs_khinv = 0.0f;
+    int iters = 0;
+    float khinv = 0.0f;
+    int split = 0, kvw = 0, dh = 1;
+    long t_cap = 0;
+    const int* pos = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+};
+
+template <int MX, int CB, int R, bool NORM = false, int EPI = 0>
 __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const float* __restrict__ x,
                                                       const uint8_t* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ out, int M, int N, int K,
-                                                      int act) {
+                                                      int act, Q8Fuse fz = Q8Fuse()) {
     static_assert(256 % CB == 0 && CB % 8 == 0 && R * CB >= 256 && MX * R <= 256, "chunk shape");
+    static_assert((!NORM && EPI == 0) || MX == 1, "decode fusions take one input row");
+    static_assert(EPI != 1 || R % 2 == 0, "gate / up pairs stay in one workgroup");
     constexpr int kRowLds = CB * kQ8Bytes + 16;                       // row stride in LDS (16-byte multiple)
     constexpr int kVrow = CB * kQ8Bytes / 16;                         // 16-byte vectors per row and chunk
     constexpr int kVPT = (R * kVrow + 255) / 256;                     // weight vectors per lane
@@ -112,6 +142,7 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
     }
     u4 rw[kVPT];
     float4 rx[kXPT];
+    float4 rg[NORM ? kXPT : 1];
     auto chunk_start = [&](int c) { return min(c * CB, nb - CB); };
     auto fetch = [&](int b0) {
         const uint8_t* base = w + j0 * rowB + (long)b0 * kQ8Bytes;
@@ -123,11 +154,27 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
             const int e = min(tid + i * 256, kXF4 - 1) * 4;           // float index in [MX][CB*32]
             const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
             rx[i] = *reinterpret_cast<const float4*>(x + (long)min(m, M - 1) * K + (long)b0 * kQ8Block + q);
+            if constexpr (NORM) rg[i] = *reinterpret_cast<const float4*>(fz.gamma + (long)b0 * kQ8Block + q);
         }
     };
 
     float acc = 0.0f;          // lane tid < MX * R owns output (tid / R, j0 + tid % R)
     fetch(chunk_start(0));
+    float inv = 1.0f;
+    if constexpr (NORM) {
+        __shared__ float red[kRowWaves];
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        float ss = 0.0f;
+        for (int i = tid; i < K / 4; i += 256) {
+            const float4 v = x4[i];
+            ss = __builtin_fmaf(v.x, v.x, ss);
+            ss = __builtin_fmaf(v.y, v.y, ss);
+            ss = __builtin_fmaf(v.z, v.z, ss);
+            ss = __builtin_fmaf(v.w, v.w, ss);
+        }
+        const float ms = block_sum(ss, red) / (float)K;
+        inv = rsqrt_cordic(ms + fz.eps, fz.rs_khinv);
+    }
     for (int c = 0; c < nch; c++) {
         const int b0 = chunk_start(c);
         const int k0 = c * CB - b0;                  // blocks of this chunk already folded
@@ -141,7 +188,12 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
             if (kXF4 % 256 == 0 || e < kXF4 * 4) {
                 const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
                 float* dst = &sx[m][(q / kQ8Block) * kQ8XPad + q % kQ8Block];
-                dst[0] = rx[i].x; dst[1] = rx[i].y; dst[2] = rx[i].z; dst[3] = rx[i].w;
+                if constexpr (NORM) {
+                    dst[0] = rx[i].x * inv * rg[i].x; dst[1] = rx[i].y * inv * rg[i].y;
+                    dst[2] = rx[i].z * inv * rg[i].z; dst[3] = rx[i].w * inv * rg[i].w;
+                } else {
+                    dst[0] = rx[i].x; dst[1] = rx[i].y; dst[2] = rx[i].z; dst[3] = rx[i].w;
+                }
             }
         }
         __syncthreads();
@@ -208,9 +260,31 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
             }
         }
     }
-    if (tid < MX * R) {
-        const int m = tid / R, r = tid % R;
-        if (m < M && r < nrows) out[(long)m * N + j0 + r] = q8_finish(acc, bias, j0 + r, act);
+    if constexpr (EPI == 1) {
+        // lanes 2i and 2i + 1 (wave 0) hold a pair's gate and up
+        const float up = __shfl_down(acc, 1, 64);
+        if (tid < R && tid % 2 == 0 && tid < nrows)
+            out[(j0 + tid) / 2] = elt<kEltSilu, 0>(acc, fz.iters, fz.khinv) * up;
+    } else if constexpr (EPI == 2) {
+        if (tid < R && tid < nrows) {
+            const long j = j0 + tid;
+            const float v = bias ? acc + bias[j] : acc;
+            if (j < fz.split) {
+                out[j] = v;
+            } else {
+                const int p = *fz.pos;
+                const long r = j - fz.split;
+                const bool is_v = r >= fz.kvw;
+                const long rr = is_v ? r - fz.kvw : r;
+                const long hh = rr / fz.dh, c = rr - hh * fz.dh;
+                if (p >= 0 && p < fz.t_cap) (is_v ? fz.vc : fz.kc)[(hh * fz.t_cap + p) * fz.dh + c] = v;
+            }
+        }
+    } else {
+        if (tid < MX * R) {
+            const int m = tid / R, r = tid % R;
+            if (m < M && r < nrows) out[(long)m * N + j0 + r] = q8_finish(acc, bias, j0 + r, act);
+        }
     }
 }
 
@@ -245,10 +319,80 @@ __global__ __launch_bounds__(256) void q8_gemv_generic_kernel(const float* __res
     if (lane == 0) out[m * N + j] = q8_finish(acc, bias, j, act);
 }
 
+// One input row on the fast path: the workgroup shape by the number of
+// rows.  16 rows per workgroup while that still gives two workgroups per
+// CU; below, 4 rows (8 when a row has fewer than 64 blocks) so that small
+// matrices spread over every CU (measured on MI355X with weights streamed
+// from HBM: 2560 x 2048 in 4.6 us instead of 5.2, 2048 x 5632 in 7.1
+// instead of 10.3).  The shape only changes which lane computes what.
+template <bool NORM, int EPI>
+static void q8_launch_row(const float* x, const uint8_t* w, const float* bias, float* out, int N, int K, int act,
+                          const Q8Fuse& fz, hipStream_t s) {
+    const int nb = K / kQ8Block;
+    const long cus = device_cus();
+#define RAC_Q8_ROW(CB, R)                                                                                   \
+    hipLaunchKernelGGL((q8_gemv_kernel<1, CB, R, NORM, EPI>), dim3((unsigned)((N + R - 1) / R)), dim3(256), 0, \
+                       s, x, w, bias, out, 1, N, K, act, fz)
+    if (nb < 32) RAC_Q8_ROW(8, 32);
+    else if ((N + 15) / 16 >= 2 * cus) RAC_Q8_ROW(32, 16);
+    else if (nb >= 64) RAC_Q8_ROW(64, 4);
+    else RAC_Q8_ROW(32, 8);
+#undef RAC_Q8_ROW
+}
+
+static bool q8_fast_ok(const uint8_t* w, int K) {
+    return (K % (8 * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
+}
+
+hipError_t q8_rmsnorm_gemv_launch(const float* x, const float* gamma, float eps, const uint8_t* w,
+                                  const float* bias, float* out, int N, int K, int act, hipStream_t s) {
+    if (!q8_fast_ok(w, K)) return hipErrorInvalidValue;
+    Q8Fuse fz;
+    fz.gamma = gamma;
+    fz.eps = eps;
+    fz.rs_khinv = host_consts().rsqrt_khinv;
+    q8_launch_row<true, 0>(x, w, bias, out, N, K, act, fz, s);
+    return hipGetLastError();
+}
+
+hipError_t q8_decode_qkv_launch(const float* x, const float* gamma, float eps, const uint8_t* w, float* q_out,
+                                int split, float* kc, float* vc, int kvw, int dh, long t_cap, const int* pos,
+                                int K, hipStream_t s) {
+    if (!q8_fast_ok(w, K)) return hipErrorInvalidValue;
+    Q8Fuse fz;
+    fz.gamma = gamma;
+    fz.eps = eps;
+    fz.rs_khinv = host_consts().rsqrt_khinv;
+    fz.split = split;
+    fz.kvw = kvw;
+    fz.dh = dh;
+    fz.t_cap = t_cap;
+    fz.pos = pos;
+    fz.kc = kc;
+    fz.vc = vc;
+    q8_launch_row<true, 2>(x, w, nullptr, q_out, split + 2 * kvw, K, 0, fz, s);
+    return hipGetLastError();
+}
+
+hipError_t q8_decode_swiglu_launch(const float* x, const float* gamma, float eps, const uint8_t* w, float* out,
+                                   int n_ff, int K, int iters, hipStream_t s) {
+    if (!q8_fast_ok(w, K)) return hipErrorInvalidValue;
+    Q8Fuse fz;
+    fz.gamma = gamma;
+    fz.eps = eps;
+    fz.rs_khinv = host_consts().rsqrt_khinv;
+    fz.iters = clamp_iters(iters);
+    fz.khinv = host_consts().exp_khinv[fz.iters];
+    q8_launch_row<true, 1>(x, w, nullptr, out, 2 * n_ff, K, 0, fz, s);
+    return hipGetLastError();
+}
+
 hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, float* out, int M, int N,
                           int K, int act, hipStream_t s) {
-    const bool fast = (K % (8 * kQ8Block) == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
-    if (fast) {
+    const bool fast = q8_fast_ok(w, K);
+    if (fast && M == 1) {
+        q8_launch_row<false, 0>(x, w, bias, out, N, K, act, Q8Fuse(), s);
+    } else if (fast) {
         // chunks of 32 blocks, 16 rows per workgroup; rows of fewer than 32
         // blocks (K < 1024) in chunks of 8 blocks, 32 rows per workgroup
         const int nb = K / kQ8Block;
@@ -259,13 +403,13 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
             float* og = out + (long)m0 * N;
             if (nb < 32) {
                 if (mm > 1)
-                    hipLaunchKernelGGL((q8_gemv_kernel<4, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                    hipLaunchKernelGGL((q8_gemv_kernel<4, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act, Q8Fuse());
                 else
-                    hipLaunchKernelGGL((q8_gemv_kernel<1, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                    hipLaunchKernelGGL((q8_gemv_kernel<1, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act, Q8Fuse());
             } else if (mm > 1) {
-                hipLaunchKernelGGL((q8_gemv_kernel<4, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                hipLaunchKernelGGL((q8_gemv_kernel<4, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act, Q8Fuse());
             } else {
-                hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act);
+                hipLaunchKernelGGL((q8_gemv_kernel<1, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act, Q8Fuse());
             }
         }
     } else {

@@ -83,10 +83,10 @@ class _Layer:
 
     def __init__(self, w: dict, keep_f32: bool):
         wqkv = torch.cat([w["W_q"], w["W_k"], w["W_v"]], 0).contiguous()
-        wgu = torch.cat([w["W_g"], w["W_u"]], 0).contiguous()
         self.q8_qkv = ext.q8_quantize(wqkv)
         self.q8_o = ext.q8_quantize(w["W_o"])
-        self.q8_gu = ext.q8_quantize(wgu)
+        # gate and up rows interleaved: one GEMV, its epilogue pairs them
+        self.q8_gu = ext.q8_quantize(ext.q8_interleave_rows(w["W_g"], w["W_u"]))
         self.q8_d = ext.q8_quantize(w["W_d"])
         self.f32 = None
         if keep_f32:
@@ -131,6 +131,12 @@ class RACDecoder:
         self.length = 0
         self.pos = torch.zeros(1, device=dev, dtype=torch.int32)     # the length, on the device
         self._graph = None
+        # the fused decode GEMVs (norm inside, cache / SwiGLU epilogues) need
+        # d_model % 256 == 0 and 16-byte aligned buffers; other shapes run
+        # the same arithmetic unfused
+        probe = torch.empty((1, cfg.d_model), device=dev)
+        self._fused = all(ext.fused_gemv_ok(probe, g, q) for lw in self.layers
+                          for g, q in ((lw.rms_att, lw.q8_qkv), (lw.rms_ffn, lw.q8_gu)))
         # 1.0f / sqrtf((float)d_head), as attention_head_causal (:515)
         self.scale = float(torch.tensor(1.0) / torch.sqrt(torch.tensor(float(cfg.d_head))))
 
@@ -177,15 +183,23 @@ class RACDecoder:
     def _decode_layer(self, L: int, x: torch.Tensor) -> torch.Tensor:
         cfg, lw = self.cfg, self.layers[L]
         d = cfg.d_model
-        h = ext.rmsnorm(x, lw.rms_att, cfg.eps)
-        qkv = ext.q8_gemv(h, lw.q8_qkv)                                   # [1, d + 2 nkv dh]
-        ext.kv_append_(qkv[0, d:], self.k_cache[L], self.v_cache[L], self.pos)
-        att = ext.decode_attention(qkv[0, :d], self.k_cache[L], self.v_cache[L], self.pos, cfg.n_heads,
-                                   self.scale, self.iters)
-        x = ext.q8_gemv(att.view(1, d), lw.q8_o, bias=x.view(d))          # x + W_o att
-        h = ext.rmsnorm(x, lw.rms_ffn, cfg.eps)
-        f = ext.swiglu(ext.q8_gemv(h, lw.q8_gu), self.iters)              # silu(gate) * up
-        return ext.q8_gemv(f, lw.q8_d, bias=x.view(d))                    # x + W_d f
+        kc, vc = self.k_cache[L], self.v_cache[L]
+        if self._fused:
+            # RMSNorm inside the GEMVs; keys / values straight into the cache;
+            # SiLU(gate) * up in the gate / up GEMV's epilogue
+            q = ext.decode_qkv(x, lw.rms_att, cfg.eps, lw.q8_qkv, kc, vc, cfg.n_heads, self.pos)
+        else:
+            qkv = ext.q8_gemv(ext.rmsnorm(x, lw.rms_att, cfg.eps), lw.q8_qkv)     # [1, d + 2 nkv dh]
+            ext.kv_append_(qkv[0, d:], kc, vc, self.pos)
+            q = qkv[0, :d]
+        att = ext.decode_attention(q, kc, vc, self.pos, cfg.n_heads, self.scale, self.iters)
+        x = ext.q8_gemv(att.view(1, d), lw.q8_o, bias=x.view(d))                  # x + W_o att
+        if self._fused:
+            f = ext.decode_swiglu_gemv(x, lw.rms_ffn, cfg.eps, lw.q8_gu, self.iters)
+        else:
+            gu = ext.q8_gemv(ext.rmsnorm(x, lw.rms_ffn, cfg.eps), lw.q8_gu)       # gate / up pairs
+            f = ext.swiglu(gu.view(-1, 2).t().reshape(1, -1), self.iters)           # silu(gate) * up
+        return ext.q8_gemv(f, lw.q8_d, bias=x.view(d))                            # x + W_d f
 
     def _decode_step(self, x: torch.Tensor) -> torch.Tensor:
         for L in range(self.cfg.n_layers):
@@ -233,6 +247,8 @@ class RACDecoder:
         start = self.length
         x = x.contiguous()
         if T == 1:
+            if x.data_ptr() % 16:
+                x = x.clone()                  # the fused GEMVs read x with 16-byte loads
             if self._graph is not None:
                 self._gx.copy_(x)
                 self._graph.replay()

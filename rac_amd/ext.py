@@ -875,6 +875,85 @@ def position_advance_(pos: torch.Tensor, by: int = 1) -> None:
     check(_lib.load().rac_position_advance_dev(pos.data_ptr(), int(by), _stream(pos)), "rac_position_advance_dev")
 
 
+def _fused_gemv_ok(x: torch.Tensor, norm_weight: torch.Tensor, wq: torch.Tensor) -> bool:
+    K = x.size(-1)
+    return (K % 256 == 0 and K <= 16384 and x.is_contiguous() and norm_weight.is_contiguous()
+            and wq.is_contiguous() and all(t.data_ptr() % 16 == 0 for t in (x, norm_weight, wq)))
+
+
+def _require_q8(wq: torch.Tensor, K: int) -> int:
+    _require_gpu(wq, "wq")
+    if wq.dtype != torch.uint8 or wq.dim() != 3 or wq.size(2) != Q8_BLOCK_BYTES or wq.size(1) * 32 != K:
+        raise RuntimeError("RAC: Q8_0 weights must be a uint8 [N, K/32, 34] tensor matching x")
+    return wq.size(0)
+
+
+def q8_gemv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, wq: torch.Tensor,
+                    bias: Optional[torch.Tensor] = None, act: int = 0) -> torch.Tensor:
+    """q8_gemv(rmsnorm(x, norm_weight, eps), wq, bias, act) for one row x
+    [1, K] in one launch, with the same bits.  Needs K % 256 == 0, K <=
+    16384 and 16-byte aligned contiguous buffers (fused_gemv_ok)."""
+    _require_f32(x, "x")
+    _require_f32(norm_weight, "norm_weight")
+    N = _require_q8(wq, x.size(-1))
+    if x.numel() != x.size(-1) or norm_weight.numel() != x.size(-1):
+        raise RuntimeError("RAC: q8_gemv_rmsnorm takes one row x and a matching norm_weight")
+    b = _bias_f32(bias, N) if bias is not None else None
+    out = torch.empty((1, N), device=x.device, dtype=torch.float32)
+    check(_lib.load().rac_q8_0_gemv_rmsnorm_dev(x.data_ptr(), norm_weight.data_ptr(), float(eps), wq.data_ptr(),
+                                                b.data_ptr() if b is not None else None, out.data_ptr(), N,
+                                                x.size(-1), int(act), _stream(x)), "rac_q8_0_gemv_rmsnorm_dev")
+    return out
+
+
+def fused_gemv_ok(x: torch.Tensor, norm_weight: torch.Tensor, wq: torch.Tensor) -> bool:
+    """Whether the fused-norm decode GEMVs take these buffers."""
+    return _fused_gemv_ok(x, norm_weight, wq)
+
+
+def decode_qkv(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, wq: torch.Tensor, k_cache: torch.Tensor,
+               v_cache: torch.Tensor, n_heads: int, pos: torch.Tensor) -> torch.Tensor:
+    """h = rmsnorm(x); the rows of wq (W_q, W_k, W_v stacked) over h: the
+    queries are returned [n_heads * d_head], keys and values go into the
+    caches at position pos (read on the device)."""
+    _require_f32(x, "x")
+    _require_f32(norm_weight, "norm_weight")
+    _require_pos(pos)
+    nkv, t_cap, dh = _require_cache(k_cache, v_cache)
+    N = _require_q8(wq, x.size(-1))
+    if N != (n_heads + 2 * nkv) * dh:
+        raise RuntimeError("RAC: wq must hold (n_heads + 2 n_kv_heads) * d_head rows")
+    q = torch.empty(n_heads * dh, device=x.device, dtype=torch.float32)
+    check(_lib.load().rac_decode_qkv_dev(x.data_ptr(), norm_weight.data_ptr(), float(eps), wq.data_ptr(),
+                                         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), int(n_heads), nkv,
+                                         dh, x.size(-1), t_cap, pos.data_ptr(), _stream(x)), "rac_decode_qkv_dev")
+    return q
+
+
+def q8_interleave_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Rows a_0, b_0, a_1, b_1, ... (the gate / up layout of
+    decode_swiglu_gemv); works on fp32 rows or Q8_0 block rows alike."""
+    if a.shape != b.shape:
+        raise RuntimeError("RAC: interleaved row sets must have the same shape")
+    return torch.stack([a, b], 1).reshape(2 * a.size(0), *a.shape[1:]).contiguous()
+
+
+def decode_swiglu_gemv(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, wq_pairs: torch.Tensor,
+                       iters: int = 0) -> torch.Tensor:
+    """out[i] = silu(gate_i . h) * (up_i . h), h = rmsnorm(x), for Q8_0
+    weights whose rows interleave gate and up (q8_interleave_rows)."""
+    _require_f32(x, "x")
+    _require_f32(norm_weight, "norm_weight")
+    N = _require_q8(wq_pairs, x.size(-1))
+    if N % 2:
+        raise RuntimeError("RAC: gate / up weights need an even row count")
+    out = torch.empty((1, N // 2), device=x.device, dtype=torch.float32)
+    check(_lib.load().rac_decode_swiglu_gemv_dev(x.data_ptr(), norm_weight.data_ptr(), float(eps),
+                                                 wq_pairs.data_ptr(), out.data_ptr(), N // 2, x.size(-1),
+                                                 _resolve_iters(iters), _stream(x)), "rac_decode_swiglu_gemv_dev")
+    return out
+
+
 def swiglu(gu: torch.Tensor, iters: int = 0) -> torch.Tensor:
     """silu(gate) * up for gu = [..., 2 n] holding gate then up in its last
     dim; returns [..., n] (CORDIC SiLU, the bits of silu())."""

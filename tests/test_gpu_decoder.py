@@ -206,6 +206,8 @@ CFGS = {
     "gqa": dict(d_model=128, n_heads=8, n_kv_heads=2, d_ff=224, n_layers=2),
     "mha": dict(d_model=96, n_heads=3, n_kv_heads=3, d_ff=160, n_layers=2),
     "mqa": dict(d_model=64, n_heads=4, n_kv_heads=1, d_ff=96, n_layers=3),
+    # d_model % 256 == 0: decode runs the fused-norm GEMVs
+    "fused": dict(d_model=256, n_heads=4, n_kv_heads=2, d_ff=352, n_layers=2),
 }
 
 
@@ -217,6 +219,7 @@ def test_decoder_prefill_then_decode(name, iters):
     W = _weights(cfg, seed=11 + iters)
     t_max = 16
     dec, orc, ref = _decoder(cfg, W, t_max, iters), OrcDecoder(cfg, W, t_max, iters), Ref64Decoder(cfg, W, t_max)
+    assert dec._fused == (name == "fused")
     schedule = [5, 1, 1, 3, 1, 1]           # prefill, decode, a second prefill chunk, decode
     for step, Tn in enumerate(schedule):
         print(f"decoder {name} iters={iters} step={step} T_new={Tn}", flush=True)
@@ -374,12 +377,13 @@ def test_swiglu_vs_checker(iters):
         assert np.array_equal(got, H(e.silu(T(gu[:, :n]), iters) * T(gu[:, n:])))
 
 
-def test_decoder_graph_replays_equal_eager():
+@pytest.mark.parametrize("name", ["gqa", "fused"])
+def test_decoder_graph_replays_equal_eager(name):
     """The captured decode step replayed per token, with other work and
     synchronisations between the replays, equals the eager step bit for
     bit, and the caches agree afterwards."""
     from rac_amd.decoder import DecoderConfig
-    cfg = DecoderConfig(**CFGS["gqa"])
+    cfg = DecoderConfig(**CFGS[name])
     W = _weights(cfg, seed=21)
     eager, graphed = _decoder(cfg, W, 24, 24), _decoder(cfg, W, 24, 24)
     x0 = rl.gen_normal((4, cfg.d_model), seed=5)
@@ -406,3 +410,65 @@ def test_decoder_graph_replays_equal_eager():
     graphed.reset()
     eager.reset()
     assert np.array_equal(H(graphed.step(T(x))), H(eager.step(T(x))))
+
+
+# ── the fused-norm decode GEMVs against their unfused forms ──────────────────
+
+@pytest.mark.parametrize("N,K", [(2560, 2048), (2048, 2048), (4, 256), (700, 768), (11264, 2048), (2048, 5632),
+                                 (100, 16384)])
+def test_q8_gemv_rmsnorm_equals_unfused(N, K):
+    from rac_amd import ext as e
+    x = T(rl.gen_normal((1, K), seed=N) * F32(3))
+    g = T((F32(1) + F32(0.2) * rl.gen_normal((K,), seed=K)).astype(F32))
+    wq = e.q8_quantize(T(rl.gen_normal((N, K), seed=N + K) / F32(np.sqrt(K))))
+    b = T(rl.gen_normal((N,), seed=1))
+    for act in (0, 1):
+        for bias in (None, b):
+            got = H(e.q8_gemv_rmsnorm(x, g, 1e-5, wq, bias=bias, act=act))
+            want = H(e.q8_gemv(e.rmsnorm(x, g, 1e-5), wq, bias=bias, act=act))
+            assert np.array_equal(got, want), (N, K, act, bias is None)
+    # against the checker too
+    h = rl.orc_rmsnorm_lanes(H(x), H(g), 1e-5)
+    assert np.array_equal(H(e.q8_gemv_rmsnorm(x, g, 1e-5, wq)), rl.orc_q8_gemv(h, H(wq), None, 0))
+
+
+@pytest.mark.parametrize("heads,kv,dh,K", [(32, 4, 64, 2048), (4, 2, 64, 256), (8, 8, 32, 512), (16, 1, 128, 2048)])
+def test_decode_qkv_equals_unfused(heads, kv, dh, K):
+    from rac_amd import ext as e
+    t_cap = 10
+    x = T(rl.gen_normal((1, K), seed=heads))
+    g = T((F32(1) + F32(0.1) * rl.gen_normal((K,), seed=dh)).astype(F32))
+    wq = e.q8_quantize(T(rl.gen_normal(((heads + 2 * kv) * dh, K), seed=K) / F32(np.sqrt(K))))
+    K1, V1 = torch.zeros((kv, t_cap, dh), device=DEV), torch.zeros((kv, t_cap, dh), device=DEV)
+    K2, V2 = torch.zeros_like(K1), torch.zeros_like(V1)
+    for p in (0, 3, t_cap - 1, t_cap, -1):        # the last two lie outside the cache: no write
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        q = e.decode_qkv(x, g, 1e-5, wq, K1, V1, heads, pos)
+        qkv = e.q8_gemv(e.rmsnorm(x, g, 1e-5), wq)
+        e.kv_append_(qkv[0, heads * dh:], K2, V2, pos)
+        assert np.array_equal(H(q), H(qkv[0, :heads * dh])), p
+        assert np.array_equal(H(K1), H(K2)) and np.array_equal(H(V1), H(V2)), p
+
+
+@pytest.mark.parametrize("iters", [24, 16, 8])
+@pytest.mark.parametrize("n_ff,K", [(5632, 2048), (8, 256), (1000, 512), (96, 4096)])
+def test_decode_swiglu_gemv_equals_unfused(n_ff, K, iters):
+    from rac_amd import ext as e
+    x = T(rl.gen_normal((1, K), seed=n_ff) * F32(2))
+    g = T((F32(1) + F32(0.1) * rl.gen_normal((K,), seed=K)).astype(F32))
+    Wg = T(rl.gen_normal((n_ff, K), seed=1) * F32(3) / F32(np.sqrt(K)))
+    Wu = T(rl.gen_normal((n_ff, K), seed=2) / F32(np.sqrt(K)))
+    got = H(e.decode_swiglu_gemv(x, g, 1e-5, e.q8_quantize(e.q8_interleave_rows(Wg, Wu)), iters))
+    h = e.rmsnorm(x, g, 1e-5)
+    gu = e.q8_gemv(h, e.q8_quantize(torch.cat([Wg, Wu])))
+    assert np.array_equal(got, H(e.swiglu(gu, iters)))
+
+
+def test_fused_gemv_rejects_unsupported_shapes():
+    from rac_amd import ext as e
+    x = T(rl.gen_normal((1, 96), seed=1))
+    g = T(np.ones(96, F32))
+    wq = e.q8_quantize(T(rl.gen_normal((8, 96), seed=2)))
+    assert not e.fused_gemv_ok(x, g, wq)
+    with pytest.raises(RuntimeError, match="multiple of 256"):
+        e.q8_gemv_rmsnorm(x, g, 1e-5, wq)
