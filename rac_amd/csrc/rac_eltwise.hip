@@ -35,10 +35,16 @@ template <int OP, int NITER>
 __global__ __launch_bounds__(kEltThreads) void eltwise_vec_kernel(
     const float4* __restrict__ x, float4* __restrict__ y, long n4, int iters, float khinv)
 {
+    // A new workgroup's address arithmetic and loads issue at raised wave
+    // priority, ahead of the CORDIC chains of older waves on the SIMD, so
+    // its HBM requests leave early and the chains hide their latency
+    // (SiLU 16384 x 11008, n = 16: 260.2 -> 256.6 us median, same bits).
+    __builtin_amdgcn_s_setprio(3);
     const long i = (long)blockIdx.x * kEltGroups + threadIdx.x;
     const long j = i + kEltThreads;
     const float4 a = (i < n4) ? ld4_stream(&x[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const float4 b = (j < n4) ? ld4_stream(&x[j]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    __builtin_amdgcn_s_setprio(0);
     float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     elt_vec<OP, NITER, 8>(v, iters, khinv);
     if (i < n4) st4_stream(&y[i], make_float4(v[0], v[1], v[2], v[3]));
