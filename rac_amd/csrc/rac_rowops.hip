@@ -18,6 +18,8 @@
 // (differences O(1e-7) relative).  That order is fixed, so results do not
 // depend on scheduling and a CPU model of it matches bit for bit.
 #include <hip/hip_runtime.h>
+#include <atomic>
+#include <type_traits>
 #include "rac_math.hpp"
 #include "rac_internal.hpp"
 #include "rac_rowred.hpp"
@@ -87,14 +89,11 @@ __device__ __forceinline__ float softmax_lane_max(float* v, long n4, long t, con
     return m;
 }
 
-// Second stage: row max, exps, row sum, scaling (m: the lane's maximum).
-// red: 2 kRowWaves floats (max and sum partials apart, so neither reduction
-// needs a trailing barrier; a kernel handles one row per workgroup).
+// Exps of the lane's values against the row maximum m, and the lane's sum
+// of them (NaN when the row holds a NaN, unmasked rows).
 template <int VPT, int NITER, bool MASKED>
-__device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters, float khinv,
-                                                   const SoftmaxMask& mk, float* red) {
+__device__ __forceinline__ float softmax_lane_exps(float* v, float m, int iters, float khinv) {
     constexpr int E = 4 * VPT;
-    m = block_max<false>(m, red);
     // Unmasked rows with a compile-time step count: every x - max is <= 0
     // or NaN, and a NaN anywhere (a NaN element, or max = +-inf) makes the
     // reference's row sum NaN and so every output NaN.  The exps then skip
@@ -116,6 +115,18 @@ __device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters,
     if constexpr (kLean) {
         if (nanp != nanp) s = __builtin_nanf("");
     }
+    return s;
+}
+
+// Second stage: row max, exps, row sum, scaling (m: the lane's maximum).
+// red: 2 kRowWaves floats (max and sum partials apart, so neither reduction
+// needs a trailing barrier; a kernel handles one row per workgroup).
+template <int VPT, int NITER, bool MASKED>
+__device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters, float khinv,
+                                                   const SoftmaxMask& mk, float* red) {
+    constexpr int E = 4 * VPT;
+    m = block_max<false>(m, red);
+    float s = softmax_lane_exps<VPT, NITER, MASKED>(v, m, iters, khinv);
     s = block_sum<false>(s, red + kRowWaves);
     const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
 #pragma unroll
@@ -169,6 +180,82 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     store_row_regs<VPT, FULL>(y + row * n, n4, v);
 }
 
+// Unmasked rows of exactly 1024 VPT floats, persistent: workgroup g takes
+// rows g, g + G, g + 2G, ... (G = gridDim.x).  While a row's exps run, the
+// next row is already on its way from HBM into LDS (global_load_lds, which
+// holds no VGPRs), so each workgroup keeps one row of loads in flight
+// through its whole lifetime instead of waiting for its row at start-up.
+// The row reductions use LDS-only barriers (lds_barrier): the previous
+// row's stores stay in flight across them; the barrier of the row sum
+// waits for the prefetch (an LDS write), which has had the exps to land.
+// Same arithmetic as softmax_reg_kernel<VPT, NITER, false, true>, so the
+// same bits.  Used where the exps are short (n = 8): at 16 and 24 steps the
+// one-row-per-workgroup kernel is faster (measured on 4096 x 4096: n = 8
+// 23.6 -> 22.2 us; n = 16 25.0 against 26.3, n = 24 31.1 against 32.2).
+template <int VPT, int NITER>
+__global__ __launch_bounds__(kRowThreads) void softmax_prefetch_kernel(
+    const float* x, float* y, long rows, float khinv)
+{
+    constexpr long n = 1024L * VPT;
+    constexpr int E = 4 * VPT;
+    __shared__ __attribute__((aligned(16))) float row_lds[n];
+    __shared__ float red[2 * kRowWaves];
+    const int t = threadIdx.x, w = t >> 6;
+    const long G = gridDim.x;
+    long row = blockIdx.x;
+    // lane t of wave w copies the float4 groups t + 256 i of row r to the
+    // same group index in row_lds; each instruction fills 1 KB at the
+    // wave's base (64 lanes x 16 bytes)
+    auto prefetch = [&](long r) {
+        const float* src = x + r * n;
+#pragma unroll
+        for (int i = 0; i < VPT; i++)
+            __builtin_amdgcn_global_load_lds(src + 4 * (t + kRowThreads * i),
+                                             (__attribute__((address_space(3))) void*)(row_lds + 4 * (kRowThreads * i + 64 * w)),
+                                             16, 0, 0);
+    };
+    prefetch(row);
+    lds_barrier();
+    for (; row < rows; row += G) {
+        float v[E];
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const float4 q = *reinterpret_cast<const float4*>(row_lds + 4 * (t + kRowThreads * i));
+            v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+        }
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < VPT; i++)
+            m = fmaxf(fmaxf(fmaxf(m, v[4 * i]), fmaxf(v[4 * i + 1], v[4 * i + 2])), v[4 * i + 3]);
+        // every wave has read row_lds (its lane maximum needs the values)
+        // once the barrier inside block_max is passed
+        m = block_max<false, true>(m, red);
+        if (row + G < rows) prefetch(row + G);
+        float s = softmax_lane_exps<VPT, NITER, false>(v, m, 0, khinv);
+        s = block_sum<false, true>(s, red + kRowWaves);
+        const float inv = inv_sum(s, 0);
+#pragma unroll
+        for (int e = 0; e < E; e++) v[e] = v[e] * inv;
+        store_row_regs<VPT, true>(y + row * n, n / 4, v);
+    }
+}
+
+// Workgroups of softmax_prefetch_kernel<VPT, NITER> resident per CU.
+template <int VPT, int NITER>
+static int softmax_prefetch_occupancy() {
+    static std::atomic<int> cached{0};
+    int v = cached.load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, softmax_prefetch_kernel<VPT, NITER>, kRowThreads, 0) !=
+                hipSuccess || v < 1) {
+            (void)hipGetLastError();
+            v = 1;
+        }
+        cached.store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 template <int NITER, bool MASKED>
 __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
     const float* x, float* y, long n, int iters, float khinv,
@@ -217,6 +304,23 @@ static hipError_t softmax_dispatch(const float* x, float* y, long rows, long n, 
                         ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
     const long n4 = n / 4;
     dim3 grid((unsigned)rows), block(kRowThreads);
+    if constexpr (!MASKED && NITER > 0 && NITER <= 8) {
+        // short exps: the persistent prefetching kernel, where every
+        // workgroup gets at least two rows
+        auto prefetch_launch = [&](auto vpt) -> bool {
+            constexpr int VPT = decltype(vpt)::value;
+            if (n != 1024L * VPT) return false;
+            const long g = (long)softmax_prefetch_occupancy<VPT, NITER>() * device_cus();
+            if (rows < 2 * g) return false;
+            hipLaunchKernelGGL((softmax_prefetch_kernel<VPT, NITER>), dim3((unsigned)g), block, 0, s, x, y, rows,
+                               khinv);
+            return true;
+        };
+        if (vec_ok && (prefetch_launch(std::integral_constant<int, 1>{}) ||
+                       prefetch_launch(std::integral_constant<int, 2>{}) ||
+                       prefetch_launch(std::integral_constant<int, 4>{})))
+            return hipGetLastError();
+    }
     if (vec_ok && n4 <= 1 * kRowThreads)
         softmax_reg_launch<1, NITER, MASKED>(grid, s, x, y, n, iters, khinv, mk);
     else if (vec_ok && n4 <= 2 * kRowThreads)

@@ -23,32 +23,50 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also releases
+// global memory, which makes every wave wait for its outstanding global
+// stores; a kernel that keeps stores in flight across its row reductions
+// uses this instead (LDS writes issued by global_load_lds count as LDS
+// writes, so the release still waits for those).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <bool LDS_ONLY>
+__device__ __forceinline__ void red_barrier() {
+    if constexpr (LDS_ONLY) lds_barrier();
+    else __syncthreads();
+}
+
 // Block-wide reductions; `red` holds kRowWaves floats.  The result is the
 // same value in every lane (fixed combination order).  TRAIL: end with a
 // barrier, so that `red` may be rewritten at once; callers that give each
-// reduction of a row its own `red` leave it off.
-template <bool TRAIL = true>
+// reduction of a row its own `red` leave it off.  LDS_ONLY: the barriers
+// order LDS only (lds_barrier).
+template <bool TRAIL = true, bool LDS_ONLY = false>
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int w = threadIdx.x / 64;
     if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
+    red_barrier<LDS_ONLY>();
     float r = red[0];
 #pragma unroll
     for (int i = 1; i < kRowWaves; i++) r += red[i];
-    if constexpr (TRAIL) __syncthreads();
+    if constexpr (TRAIL) red_barrier<LDS_ONLY>();
     return r;
 }
-template <bool TRAIL = true>
+template <bool TRAIL = true, bool LDS_ONLY = false>
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
     const int w = threadIdx.x / 64;
     if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
+    red_barrier<LDS_ONLY>();
     float r = red[0];
 #pragma unroll
     for (int i = 1; i < kRowWaves; i++) r = fmaxf(r, red[i]);
-    if constexpr (TRAIL) __syncthreads();
+    if constexpr (TRAIL) red_barrier<LDS_ONLY>();
     return r;
 }
 

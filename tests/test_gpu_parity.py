@@ -801,3 +801,39 @@ def test_llama_block_matches_oracle_composition():
     err = np.abs(y[0] - ref) / np.maximum(np.abs(ref), 1.0)
     assert err.max() < 1e-4, err.max()
 
+
+
+@pytest.mark.parametrize("cols,rows", [(1024, 16384), (2048, 8192), (4096, 6000)])
+def test_softmax_prefetch_path(cols, rows):
+    """Short exps (n = 8) over enough rows for the persistent kernel that
+    prefetches each workgroup's next row into LDS (every workgroup takes at
+    least two rows; the row count is no multiple of the grid): bit-exact with
+    the lane-order checker.  Special rows (NaN, +-inf, only -inf, huge
+    offsets) sit where workgroups take their first, second and later rows;
+    each gives the same bits, NaN payloads included, as the same row alone
+    (one row: the one-row-per-workgroup kernel)."""
+    x = rl.gen_normal((rows, cols), 31, std=2.0)
+    where = [0, 1, 255, 1279, 1280, 1536, 2047, 2048, 2559, 3071, 4095, rows - 2, rows - 1]
+    for q, r in enumerate(where):
+        kind = q % 6
+        if kind == 0:
+            x[r, 17] = np.nan
+        elif kind == 1:
+            x[r, 3] = np.inf
+        elif kind == 2:
+            x[r, :] = -np.inf
+        elif kind == 3:
+            x[r] -= 200.0
+        elif kind == 4:
+            x[r] = -np.abs(x[r]) * 40.0
+        else:
+            x[r, ::2] = -2e9
+    xt = T(x)
+    got = H(ext().softmax(xt, iters=8))
+    ref = rl.orc_softmax_lanes(x, 8)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(got[fin], ref[fin])
+    for r in where:
+        one = H(ext().softmax(xt[r:r + 1], iters=8))
+        assert np.array_equal(one.view(np.int32), got[r:r + 1].view(np.int32)), r
