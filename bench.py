@@ -17,6 +17,8 @@ Also measured in the same run (fields "ops" and "cpu_baseline"):
     and one training step (forward + backward);
   * the config-5 attention core through RAC ([1,32,2048,128], causal, n=16)
     and the Q8_0 decode GEMV (11008x4096, 32000x4096, 65536x8192; HBM GB/s);
+  * the decoder stack over those kernels (tinyllama shape, 22 layers):
+    prefill of 128 tokens and decode per token, eager and as a HIP graph;
   * softmax 4096x4096 N(0, std 2) at n = 8/16/24, RoPE on Q and K
     [8,32,4096,128], RMSNorm 16384x4096, SiLU 16384x11008 (n=16): HBM GB/s
     of 1 read + 1 write per element, buffers rotated past the 256 MB MALL;
@@ -38,6 +40,7 @@ MI355X FP32 vector 157.3 TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--iters 16]
                        [--no-cpu-baseline] [--matmul-only] [--rowops-only]
+                       [--q8-only] [--decode-only]
 """
 from __future__ import annotations
 
@@ -582,6 +585,53 @@ def bench_q8_ops(torch, ext, dev, g):
     return out
 
 
+def bench_decode_ops(torch, dev):
+    """The decoder stack (rac_amd.decoder, the reference's full-model path of
+    bench_rac_transformer.c) at the tinyllama shape: 22 layers, d_model 2048,
+    32 query / 4 key-value heads, d_ff 5632, synthetic weights; CORDIC SiLU
+    at n = 16.  Prefill of 128 tokens (fp32 weights, fused RAC linears,
+    FAST MAC) and decode of one token (Q8_0 weights) at cache length
+    128..., eager and replayed as one HIP graph per token; ms/token and
+    tok/s as the reference prints them (bench_rac_transformer.c:844-851),
+    and for decode the Q8_0 weight bytes streamed per token over the time."""
+    from rac_amd.decoder import PRESETS, RACDecoder
+    out = {}
+    cfg = PRESETS["tinyllama"]
+    dec = RACDecoder(cfg, RACDecoder.synthetic_weights(cfg, dev, seed=7), t_max=2048, iters=16)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    tp = 128
+    xp = torch.randn((tp, cfg.d_model), device=dev, generator=gen)
+
+    def prefill():
+        dec.reset()
+        dec.forward(xp)
+
+    prefill()
+    torch.cuda.synchronize()
+    t = _events_time(prefill, 2, torch, dist_calls=5)
+    out[f"decoder_tinyllama_prefill_T{tp}"] = {"ms_per_token": round(t * 1e3 / tp, 4),
+                                               "tok_per_s": round(tp / t, 1), **_dist_fields(t, 1e3, "ms")}
+    print(f"# decoder tinyllama prefill T={tp}: {t * 1e3 / tp:.3f} ms/token", file=sys.stderr, flush=True)
+    wbytes = sum(q.numel() * q.element_size() for lw in dec.layers for q in (lw.q8_qkv, lw.q8_o, lw.q8_gu, lw.q8_d))
+    xt = torch.randn((1, cfg.d_model), device=dev, generator=gen)
+    for name, graph in (("eager", False), ("graph", True)):
+        prefill()
+        if graph:
+            dec.capture()
+        t = _events_time(lambda: dec.step(xt), 5, torch, dist_calls=10)
+        at = dec.length
+        dec.release_graph()
+        out[f"decoder_tinyllama_decode_{name}"] = {
+            "ms_per_token": round(t * 1e3, 4), "tok_per_s": round(1.0 / t, 1),
+            "q8_weight_bytes_per_token": wbytes, "weight_GBps": round(wbytes / t / 1e9, 1),
+            "frac_of_hbm_peak": round(wbytes / t / 1e9 / PEAK_HBM_GBPS, 4),
+            "cache_length_at_end": at, **_dist_fields(t, 1e3, "ms")}
+        print(f"# decoder tinyllama decode ({name}): {t * 1e3:.3f} ms/token", file=sys.stderr, flush=True)
+    del dec
+    return out
+
+
 def bench_block_ops(torch, ext, dev, g):
     """Llama block, attention core, Q8_0 GEMV, RAC-DSP and the safetensors loader."""
     lib = ext._lib.load()
@@ -707,6 +757,7 @@ def bench_block_ops(torch, ext, dev, g):
     del qa, ka, va, oa, wsp
 
     out.update(bench_q8_ops(torch, ext, dev, g))
+    out.update(bench_decode_ops(torch, dev))
 
     # RAC-DSP fixed-point engine (Q32.32 / Q0.63 int64): 2^24 evaluations of
     # rotate (x, y, z in and out: 48 B each) and of project (x, z in, x out:
@@ -1003,6 +1054,8 @@ def main():
     ap.add_argument("--rowops-only", action="store_true",
                     help="only time softmax, RoPE, RMSNorm and SiLU and print their figures "
                          "(a short run for rocprofv3 --pmc passes; not the benchmark line)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only time the decoder stack (tinyllama shape: prefill and decode per token)")
     ap.add_argument("--q8-only", action="store_true",
                     help="only time the Q8_0 decode GEMV shapes (a short run for rocprofv3 --pmc passes)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -1029,6 +1082,13 @@ def main():
               "build's hot path is single-GPU (every op would shard by rows or output columns with at most one all-reduce per block).", file=sys.stderr)
         sys.exit(2)
 
+    if args.decode_only:
+        import torch
+        sys.path.insert(0, ROOT)
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        print(json.dumps({"ops": bench_decode_ops(torch, dev)}), flush=True)
+        return
     if args.q8_only:
         import torch
         sys.path.insert(0, ROOT)
