@@ -837,3 +837,8 @@ def test_softmax_prefetch_path(cols, rows):
     for r in where:
         one = H(ext().softmax(xt[r:r + 1], iters=8))
         assert np.array_equal(one.view(np.int32), got[r:r + 1].view(np.int32)), r
+    # in place (y == x): each row is read whole before it is written, and the
+    # prefetched row is one no workgroup has written yet
+    rc = lib().rac_softmax_dev(xt.data_ptr(), xt.data_ptr(), rows, cols, 8, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    assert np.array_equal(H(xt).view(np.int32), got.view(np.int32))
