@@ -232,6 +232,10 @@ __global__ __launch_bounds__(kRowThreads) void softmax_prefetch_kernel(
         m = block_max<false, true>(m, red);
         if (row + G < rows) prefetch(row + G);
         float s = softmax_lane_exps<VPT, NITER, false>(v, m, 0, khinv);
+        // the prefetch has landed before the barrier below (the LDS fence
+        // waits for it too; this states it, and the operand keeps the wait
+        // after the exps)
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(s));
         s = block_sum<false, true>(s, red + kRowWaves);
         const float inv = inv_sum(s, 0);
 #pragma unroll
