@@ -430,18 +430,50 @@ struct CircStep {
     }
 };
 // One 16-step rotation of (K_INV, 0) by theta, with the reference's
-// sequential float wrap of theta into (-pi, pi] (a loop, not a remainder:
-// its rounding drift at large angles is part of the table's values).
-// The reference's wrap loop never terminates for |theta| >= 2^27 or +-inf
-// (theta - 2pi rounds back to theta); such angles return NaN here instead.
-// Below 2^27 every subtraction makes progress, so the loop is bounded.
+// sequential float wrap of theta into (-pi, pi] (rac_cpu.c:92-94: a loop of
+// rounded subtractions, not a remainder: its drift at large angles is part
+// of the table's values).  The reference's wrap loop never terminates for
+// |theta| >= 2^27 or +-inf (theta - 2pi rounds back to theta); such angles
+// return NaN here instead.
 constexpr float kWrapLimit = 134217728.0f;   // 2^27
+
+// The reference's subtractions a <- fl(a - tau) while a >= 16, done a
+// binade at a time (a = |theta|, a in [2^e, 2^(e+1)), 4 <= e <= 26).  On
+// the binade's grid (spacing u = 2^(e-23)) let T be tau rounded to a
+// multiple of u: tau / u never has fractional part 1/2 for these e, so
+// |T - tau| < u / 2, and every step whose exact result a - tau stays >= 2^e
+// rounds to exactly a - T.  Those are the steps i = 1 .. k with
+// k = floor((m - c) / t) + 1 (m the mantissa field of a, t = T / u, c =
+// ceil(tau / u): all in units of u), taken at once by one exact fma; the
+// step that leaves the binade is then taken as the reference takes it.  So
+// the result is the loop's, bit for bit, in at most ~23 passes instead of
+// up to a / 2pi subtractions.
+__device__ __forceinline__ float wrap_binades(float a) {
+    while (a >= 16.0f) {
+        const uint32_t bits = __builtin_bit_cast(uint32_t, a);
+        const int e = (int)(bits >> 23) - 127;
+        const int m = (int)(bits & 0x7FFFFFu);
+        const float u = __builtin_ldexpf(1.0f, e - 23);
+        const float tq = kTau * __builtin_ldexpf(1.0f, 23 - e);    // tau / u, exact
+        const int t = (int)__builtin_rintf(tq), c = (int)__builtin_ceilf(tq);
+        if (m >= c) {
+            const int k = (m - c) / t + 1;
+            a = __builtin_fmaf(-(float)k, (float)t * u, a);          // a - k T, exact
+        }
+        a = a - kTau;
+    }
+    return a;
+}
 
 __device__ __forceinline__ void sincos_cordic(float theta, float& s, float& c) {
     if (!(__builtin_fabsf(theta) < kWrapLimit)) {
         s = c = __builtin_nanf("");
         return;
     }
+    // fl(theta + tau) = -fl(-theta - tau) (round to nearest is odd), so the
+    // negative side runs the same subtractions on |theta|
+    if (theta > kPi) theta = wrap_binades(theta);
+    else if (theta <= -kPi) theta = -wrap_binades(-theta);
     while (theta > kPi) theta -= kTau;
     while (theta <= -kPi) theta += kTau;
     float x = kKInv, y = 0.0f;

@@ -842,3 +842,32 @@ def test_softmax_prefetch_path(cols, rows):
     rc = lib().rac_softmax_dev(xt.data_ptr(), xt.data_ptr(), rows, cols, 8, torch.cuda.current_stream().cuda_stream)
     assert rc == 0, lib().rac_last_error()
     assert np.array_equal(H(xt).view(np.int32), got.view(np.int32))
+
+
+def test_sincos_large_angles_wrap():
+    """The device takes the reference's sequential wrap (rac_cpu.c:92-94) a
+    binade at a time; the checker runs the loop itself.  Angles on both sides
+    of every binade boundary from 2^4 to 2^26 (the last step that stays in a
+    binade and the one that leaves it), spread through each binade, and up
+    to the largest float below 2^27: bit-exact, both signs."""
+    th = []
+    for e in range(4, 27):
+        base = np.float32(2.0 ** e)
+        for k in (0, 1, 2, 3, 7, 1000, 65535):
+            th.append(np.nextafter(base, np.float32(np.inf), dtype=np.float32) if k == 1 else base + np.float32(k) * np.spacing(base))
+            th.append(np.float32(2.0 ** (e + 1)) - np.float32(k + 1) * np.spacing(base))
+        th.extend((base * np.float32(1.0 + f)).astype(np.float32) for f in (0.1234567, 0.5, 0.7777777, 0.9999))
+    th = np.float32(th)
+    th = np.concatenate([th, -th, np.float32([np.nextafter(np.float32(2.0 ** 27), np.float32(0))] * 2) * np.float32([1, -1])])
+    s, c = ext().sincos(T(th))
+    so, co = np.empty_like(th), np.empty_like(th)
+    rl.oracle().orc_sincos_batch(rl.p(th), rl.p(so), rl.p(co), th.size)
+    assert np.array_equal(H(s), so) and np.array_equal(H(c), co)
+
+
+def test_rope_cache_long_context_vs_checker():
+    """A 65536-position table (angles up to 65535 rad: the reference's wrap
+    loop runs up to ~10^4 times per entry) equals the checker bit for bit."""
+    c, s = ext().rope_cache(65536, 64, 10000.0, device=DEV)
+    oc, os_ = rl.orc_rope_cache(65536, 64)
+    assert np.array_equal(H(c), oc) and np.array_equal(H(s), os_)
