@@ -17,19 +17,22 @@ namespace rac {
 
 // ── elementwise ──────────────────────────────────────────────────────────
 
-// One pass, no grid-stride loop: workgroup b (128 lanes) owns float4
-// groups 256 b .. 256 b + 255, lane l the groups 256 b + l and
-// 256 b + 128 + l (both coalesced), so eight CORDIC chains interleave per
-// lane; groups past the end compute on zeros and are not stored.  The
-// grid covers the array once and the hardware dispatcher starts a new
-// workgroup as soon as one retires, which keeps loads in flight better
-// than resident workgroups walking the array (measured on SiLU
-// 16384 x 11008: 216 / 254 / 311 us at n = 8 / 16 / 24 against 258-274 /
-// 277-298 / 331-365 us for a grid-stride loop over a capped grid, and
-// slower still for a grid of resident workgroups, with or without
-// prefetching each next trip into LDS).
-constexpr int kEltThreads = 128;
-constexpr int kEltGroups = 2 * kEltThreads;   // float4 groups per workgroup
+// One pass, no grid-stride loop: workgroup b (64 lanes) owns float4 groups
+// 256 b .. 256 b + 255, lane l the groups 256 b + l + 64 f, f = 0..3 (each
+// coalesced), so sixteen CORDIC chains interleave per lane; groups past the
+// end compute on zeros and are not stored.  The grid covers the array once
+// and the hardware dispatcher starts a new workgroup as soon as one
+// retires, which keeps loads in flight better than resident workgroups
+// walking the array (measured on SiLU 16384 x 11008: 216 / 254 / 311 us at
+// n = 8 / 16 / 24 against 258-274 / 277-298 / 331-365 us for a grid-stride
+// loop over a capped grid, and slower still for a grid of resident
+// workgroups, with or without prefetching each next trip into LDS).  With
+// the loads at raised priority (below), 4 float4 per lane on 64-lane
+// workgroups measured 0.6-1% faster than 2 on 128 (n = 16: 247.7 vs 249.1
+// and 252.6 vs 255.2 us on two boxes; 1 float4 per lane 3-4% slower).
+constexpr int kEltThreads = 64;
+constexpr int kEltF4 = 4;                            // float4 groups per lane
+constexpr int kEltGroups = kEltF4 * kEltThreads;     // float4 groups per workgroup
 
 template <int OP, int NITER>
 __global__ __launch_bounds__(kEltThreads) void eltwise_vec_kernel(
@@ -40,15 +43,25 @@ __global__ __launch_bounds__(kEltThreads) void eltwise_vec_kernel(
     // its HBM requests leave early and the chains hide their latency
     // (SiLU 16384 x 11008, n = 16: 260.2 -> 256.6 us median, same bits).
     __builtin_amdgcn_s_setprio(3);
-    const long i = (long)blockIdx.x * kEltGroups + threadIdx.x;
-    const long j = i + kEltThreads;
-    const float4 a = (i < n4) ? ld4_stream(&x[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const float4 b = (j < n4) ? ld4_stream(&x[j]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const long i0 = (long)blockIdx.x * kEltGroups + threadIdx.x;
+    float4 r[kEltF4];
+#pragma unroll
+    for (int f = 0; f < kEltF4; f++) {
+        const long i = i0 + (long)f * kEltThreads;
+        r[f] = (i < n4) ? ld4_stream(&x[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     __builtin_amdgcn_s_setprio(0);
-    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    elt_vec<OP, NITER, 8>(v, iters, khinv);
-    if (i < n4) st4_stream(&y[i], make_float4(v[0], v[1], v[2], v[3]));
-    if (j < n4) st4_stream(&y[j], make_float4(v[4], v[5], v[6], v[7]));
+    float v[4 * kEltF4];
+#pragma unroll
+    for (int f = 0; f < kEltF4; f++) {
+        v[4 * f] = r[f].x; v[4 * f + 1] = r[f].y; v[4 * f + 2] = r[f].z; v[4 * f + 3] = r[f].w;
+    }
+    elt_vec<OP, NITER, 4 * kEltF4>(v, iters, khinv);
+#pragma unroll
+    for (int f = 0; f < kEltF4; f++) {
+        const long i = i0 + (long)f * kEltThreads;
+        if (i < n4) st4_stream(&y[i], make_float4(v[4 * f], v[4 * f + 1], v[4 * f + 2], v[4 * f + 3]));
+    }
 }
 
 template <int OP, int NITER>
