@@ -39,6 +39,13 @@ int rac_get_cordic_mode(void);
 void rac_set_stream(void *stream);
 void *rac_get_stream(void);
 int rac_version(void);
+/* The synchronous rac.h calls stage host buffers through device buffers
+ * that stay cached per GPU (at most RAC_STAGE_CACHE_MB MiB each, 512 by
+ * default, 0 = no caching).  This frees every cached buffer on every GPU and
+ * returns the bytes released, for processes whose other allocator (torch's)
+ * needs the memory.  No counterpart in the reference, which has no device
+ * staging (rac_hip.cpp:364-379 allocates per call). */
+long rac_release_cached_memory(void);
 /* Host-side queries of the constants the kernels use (no GPU needed):
  * the circular direction sequence of CORDIC-mode matmul (d[i] = +1/-1 for
  * i < iters; returns the clamped count), 1/K_h of the n-step exp, and 1/K_h

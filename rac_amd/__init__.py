@@ -7,7 +7,7 @@ RoPE, CORDIC-vectoring rsqrt norms.
   rac_amd.ext             tensor-level ops (the rac_cuda_ext surface)
   rac_amd.rac_torch       nn.Module surface (RACLinear, RACLlamaBlock, ...)
 """
-from ._lib import LIB_PATH, RACError, load
+from ._lib import LIB_PATH, RACError, load, release_cached_memory
 
 __version__ = "1.0.0"
-__all__ = ["LIB_PATH", "RACError", "load", "__version__"]
+__all__ = ["LIB_PATH", "RACError", "load", "release_cached_memory", "__version__"]

@@ -133,6 +133,7 @@ _SIGNATURES = {
     "rac_fp32_to_fp16": (ctypes.c_uint16, [_f]),
     "rac_last_error": (ctypes.c_char_p, []),
     "rac_clear_error": (None, []),
+    "rac_release_cached_memory": (_l, []),
     "rac_set_cordic_iters": (None, [_i]),
     "rac_get_cordic_iters": (_i, []),
     "rac_set_cordic_mode": (None, [_i]),
@@ -213,6 +214,13 @@ def load(path: str | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+def release_cached_memory() -> int:
+    """Free the device staging buffers the synchronous rac.h calls keep
+    cached (at most RAC_STAGE_CACHE_MB per GPU); returns the bytes freed.
+    Call it when another allocator in the process (torch's) runs short."""
+    return int(load().rac_release_cached_memory())
 
 
 def symbols() -> list[str]:

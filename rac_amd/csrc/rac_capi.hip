@@ -181,8 +181,11 @@ static bool is_device_pointer(const void* p) { return is_device_ptr(p); }
 // pay for up to five of each).  Every synchronous call synchronises its
 // stream before its Staged objects are destroyed, so a buffer is back in the
 // cache only once no work of the call can touch it.  At most
-// kStageCacheBytes stay cached per device; a release beyond that is freed.
-// Buffers cached at process exit are left to the runtime's teardown.
+// stage_cache_cap() bytes stay cached per device (RAC_STAGE_CACHE_MB, 512 by
+// default; 0 disables caching); a release beyond that is freed.
+// rac_release_cached_memory() frees every cached buffer, for processes where
+// another allocator (torch's) needs the memory back.  Buffers cached at
+// process exit are left to the runtime's teardown.
 namespace {
 struct StageCache {
     std::mutex mu;
@@ -190,8 +193,19 @@ struct StageCache {
     size_t cached[64] = {};
 };
 StageCache g_stage_cache;
-constexpr size_t kStageCacheBytes = 512ull << 20;
 constexpr size_t kStageGranule = 64u << 10;
+
+size_t stage_cache_cap() {
+    static const size_t cap = [] {
+        const char* e = getenv("RAC_STAGE_CACHE_MB");
+        if (!e || !*e) return (size_t)512 << 20;
+        char* end = nullptr;
+        const long mb = strtol(e, &end, 10);
+        if (end == e || mb < 0) return (size_t)512 << 20;
+        return (size_t)mb << 20;
+    }();
+    return cap;
+}
 
 void* stage_take(int dev, size_t want, size_t* got) {
     {
@@ -233,7 +247,7 @@ void* stage_take(int dev, size_t want, size_t* got) {
 void stage_give(int dev, void* p, size_t sz) {
     {
         std::lock_guard<std::mutex> lock(g_stage_cache.mu);
-        if (g_stage_cache.cached[dev] + sz <= kStageCacheBytes) {
+        if (g_stage_cache.cached[dev] + sz <= stage_cache_cap()) {
             g_stage_cache.free_list[dev].push_back({p, sz});
             g_stage_cache.cached[dev] += sz;
             return;
@@ -242,6 +256,28 @@ void stage_give(int dev, void* p, size_t sz) {
     (void)hipFree(p);
 }
 }  // namespace
+
+// Frees every staging buffer the synchronous API keeps cached, on every
+// device; returns the bytes released.  Cached buffers are idle by
+// construction (each call synchronises before returning its buffers).
+RAC_EXPORT long rac_release_cached_memory(void) {
+    std::vector<std::pair<void*, size_t>> drop;
+    {
+        std::lock_guard<std::mutex> lock(g_stage_cache.mu);
+        for (int d = 0; d < 64; d++) {
+            for (auto& e : g_stage_cache.free_list[d]) drop.push_back(e);
+            g_stage_cache.free_list[d].clear();
+            g_stage_cache.cached[d] = 0;
+        }
+    }
+    long bytes = 0;
+    for (auto& e : drop) {
+        (void)hipFree(e.first);
+        bytes += (long)e.second;
+    }
+    (void)hipGetLastError();
+    return bytes;
+}
 
 struct Staged {
     void* host = nullptr;     // caller's host pointer (null when device)
@@ -865,19 +901,32 @@ RAC_EXPORT int rac_attention_ws_dev(const float* q, const float* k, const float*
 // (other streams, other host threads) race and must be serialised by the
 // caller.
 // The array's device address is looked up once per device (the host-side
-// name is only a stand-in for it) and used from then on.
+// name is only a stand-in for it) and used from then on.  The lookup is set
+// up outside any stream capture: rac_create_context does it for the current
+// device, and so does the first call of rac_attention_noalloc_dev on a device
+// when its stream is not capturing.  A first call that arrives under
+// capture is refused (-4) instead of querying the runtime there (the lookup
+// may load the library's code object, which allocates the array).
 static constexpr long kScratchBytes = (64L << 20) + 256;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static std::mutex g_scratch_mutex;
 static void* g_scratch_ptr[64];
 
-static int scratch_for_current_device(void** out) {
+static int scratch_for_current_device(hipStream_t stream, void** out) {
     int dev = 0;
     int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
     if (rc) return rc;
     if (dev < 0 || dev >= 64) return fail(RAC_ERR_DEVICE, "device index %d out of range", dev);
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (!g_scratch_ptr[dev]) {
+        if (stream) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            rc = check_hip(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+            if (rc) return rc;
+            if (cs != hipStreamCaptureStatusNone)
+                return fail(RAC_ERR_DEVICE, "rac_attention_noalloc_dev: the first call on device %d is under stream "
+                            "capture; call rac_create_context (or make one call) outside capture first", dev);
+        }
         void* p = nullptr;
         rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "scratch address");
         if (rc) return rc;
@@ -904,7 +953,7 @@ RAC_EXPORT int rac_attention_noalloc_dev(const float* q, const float* k, const f
         return fail(RAC_ERR_INVALID_DIM, "rac_attention_noalloc_dev: batch*n_heads*seq = %ld exceeds the %ld the "
                     "%ld-byte scratch holds", bh * seq, (kScratchBytes - 256) / (long)sizeof(float), kScratchBytes);
     void* ws = nullptr;
-    rc = scratch_for_current_device(&ws);
+    rc = scratch_for_current_device((hipStream_t)stream, &ws);
     if (rc) return rc;
     return attention_launch(q, k, v, mask, is_causal, out, batch, n_heads, seq, head_dim, static_cast<float*>(ws),
                             chunk, clamp_iters(iters), mode, (hipStream_t)stream);
@@ -1635,9 +1684,19 @@ struct rac_context_t {
     int backend;
 };
 
+// The reference's context is a malloc'd stub (rac_hip.cpp:416-435); here it
+// is also the library's set-up call: it resolves the allocation-free
+// attention's scratch address for the current device, outside any capture
+// (a missing device is not an error for the stub).
 RAC_EXPORT rac_context_t* rac_create_context(int backend) {
     rac_context_t* c = (rac_context_t*)malloc(sizeof(rac_context_t));
     if (c) c->backend = backend;
+    int n = 0;
+    if (hipGetDeviceCount(&n) == hipSuccess && n > 0) {
+        void* p = nullptr;
+        (void)scratch_for_current_device(nullptr, &p);
+    }
+    (void)hipGetLastError();
     return c;
 }
 RAC_EXPORT void rac_destroy_context(rac_context_t* ctx) { free(ctx); }

@@ -128,16 +128,17 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
     // Vector placement, fixed for every chunk: byte offset of this lane's
     // vector i from the chunk start (rows past the last re-read row 0: every
     // load is unconditional, so a chunk's loads are all in flight together)
-    // and its LDS offset (-1: nothing to store).  R rows of one chunk span
-    // less than 2^32 bytes (the host checks rows x blocks against 2^31 x 128).
-    unsigned goff[kVPT];
+    // and its LDS offset (-1: nothing to store).  The byte offset is 64-bit:
+    // R rows of a very long K (R rowB >= 2^32 from K ~ 2.5e8 at R = 16)
+    // would wrap a 32-bit one.
+    long goff[kVPT];
     int soff[kVPT];
 #pragma unroll
     for (int i = 0; i < kVPT; i++) {
         const int v = tid + i * 256;
         const bool in = v < R * kVrow;
         const int r = in ? v / kVrow : 0, o = in ? v % kVrow : 0;
-        goff[i] = (unsigned)((r < nrows ? r : 0) * rowB + o * 16);
+        goff[i] = (long)(r < nrows ? r : 0) * rowB + o * 16;
         soff[i] = (in && r < nrows) ? r * kRowLds + o * 16 : -1;
     }
     u4 rw[kVPT];

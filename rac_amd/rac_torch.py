@@ -33,19 +33,25 @@ import torch
 import torch.nn as nn
 from torch.autograd import Function
 
+from . import _probe
 from . import ext as _rac
 from .ext import MODE_CORDIC, MODE_FAST, MODE_SHIFTADD
 
 _FLOAT_TYPES = (torch.float32, torch.float16, torch.bfloat16)
 
+# Start-up probe (rac_torch.py:55-108): library present and loadable, a
+# gfx950 device, one 4x4 CORDIC product correct on it.  Each failure warns
+# with its own diagnosis; without a device nothing is launched and nothing
+# is said (CPU-only imports are legitimate: tests, tooling).
+_PROBE = _probe.probe(run_kernel=os.environ.get('RAC_PROBE', '1') != '0')
+if not _PROBE.ok and _PROBE.stage != 'no-device':
+    warnings.warn(f"RAC start-up probe: {_PROBE.message}", RuntimeWarning, stacklevel=2)
+
 
 def _rac_available() -> bool:
-    """True when the kernel library loads and a ROCm device is present."""
-    try:
-        _rac._lib.load()
-    except Exception:
-        return False
-    return torch.cuda.is_available()
+    """True when the start-up probe passed: the library loads, a gfx950
+    device is present and a RAC product ran correctly on it."""
+    return _PROBE.ok
 
 
 def _rac_has(op: str) -> bool:
@@ -55,6 +61,8 @@ def _rac_has(op: str) -> bool:
 def _need_gpu(t: torch.Tensor, what: str) -> None:
     if not t.is_cuda:
         raise RuntimeError(f"RAC: {what} must be on the ROCm device; the gfx950 kernels have no CPU path")
+    if not _PROBE.ok and _PROBE.stage != 'no-device':
+        raise RuntimeError(f"RAC: {_PROBE.message}")
 
 
 # ── knobs (rac_torch.py:1017-1118) ─────────────────────────────────────────
@@ -456,24 +464,39 @@ class RACFusedQKV(nn.Module):
         [0, d), [d, 2d), [2d, 3d) of the fused weight (and bias) are Q's, K's
         and V's, so chunk(3) in forward hands each projection back."""
         parts = (q_linear, k_linear, v_linear)
-        d_model = q_linear.in_features
-        if any(p.in_features != d_model or p.out_features != d_model for p in parts):
-            raise ValueError("from_qkv_linears: Q, K and V must all map d_model -> d_model")
-        with_bias = q_linear.bias is not None
-        if any((p.bias is not None) != with_bias for p in parts):
-            raise ValueError("from_qkv_linears: Q, K and V must all have a bias or none")
+        d_model, with_bias = _square_projections("from_qkv_linears", parts)
         ref = q_linear.weight
         fused = cls(d_model, bias=with_bias, device=ref.device, dtype=ref.dtype)
-        with torch.no_grad():
-            for slot, p in enumerate(parts):
-                rows = slice(slot * d_model, (slot + 1) * d_model)
-                fused.qkv.weight[rows].copy_(p.weight)
-                if with_bias:
-                    fused.qkv.bias[rows].copy_(p.bias)
+        _load_row_blocks(fused.qkv, parts)
         return fused
 
     def extra_repr(self):
         return f'd_model={self.d_model}, backend=RAC-fused-QKV'
+
+
+def _square_projections(who: str, parts) -> tuple:
+    """(d_model, has_bias) of projections that all map d_model -> d_model and
+    agree on having a bias; ValueError otherwise."""
+    d_model = parts[0].in_features
+    if any(p.in_features != d_model or p.out_features != d_model for p in parts):
+        raise ValueError(f"{who}: every projection must map d_model -> d_model")
+    with_bias = parts[0].bias is not None
+    if any((p.bias is not None) != with_bias for p in parts):
+        raise ValueError(f"{who}: the projections must all have a bias or none")
+    return d_model, with_bias
+
+
+def _load_row_blocks(dst: nn.Module, parts) -> None:
+    """dst.weight (and bias) := the parts' weights (biases) stacked by rows in
+    order, bit for bit: part i fills rows [i*d, (i+1)*d)."""
+    with torch.no_grad():
+        row = 0
+        for p in parts:
+            rows = slice(row, row + p.out_features)
+            dst.weight[rows].copy_(p.weight)
+            if dst.bias is not None:
+                dst.bias[rows].copy_(p.bias)
+            row += p.out_features
 
 
 class RACFusedFFN(nn.Module):
@@ -813,12 +836,39 @@ def rac_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optio
     return RACAttentionFunction.apply(q, k, v, mask, is_causal)
 
 
+def _dropout_inactive(dropout: nn.Module) -> bool:
+    """True when the module between softmax and P V is the identity: an
+    nn.Identity, or an nn.Dropout in eval mode or with p = 0.  Anything else
+    (active dropout, a user module in its place) must be applied."""
+    if type(dropout) is nn.Identity:
+        return True
+    if type(dropout) is nn.Dropout:
+        return not dropout.training or dropout.p == 0
+    return False
+
+
 def _rac_core_ok(mask: Optional[torch.Tensor], T: int, dropout: nn.Module) -> bool:
     """The fused RAC attention core takes a [T, T] additive mask and no
     dropout between softmax and P V; other cases compose the stages."""
-    if isinstance(dropout, nn.Dropout) and dropout.training and dropout.p > 0:
+    if not _dropout_inactive(dropout):
         return False
     return mask is None or (mask.dim() == 2 and tuple(mask.shape) == (T, T) and mask.is_floating_point())
+
+
+def _attention_composed(Q, K, V, scale: float, mask: Optional[torch.Tensor], is_causal: bool,
+                        dropout: nn.Module) -> torch.Tensor:
+    """The stages of rac_torch.py:1327-1337 one by one, every product on the
+    batched RAC matmul: S = (Q K^T) * scale, + causal -inf above the diagonal,
+    + mask (broadcast; a bool mask adds 1.0 where True, as torch's + does),
+    P = dropout(CORDIC softmax(S)), out = P V.  Used where the fused core does
+    not apply (a mask other than [T, T] float, or an active dropout)."""
+    T = Q.shape[-2]
+    scores = rac_bmm(Q, K.transpose(-2, -1)) * scale
+    if is_causal:
+        scores = _causal_scores(scores, T)
+    if mask is not None:
+        scores = scores + mask
+    return rac_bmm(dropout(rac_softmax(scores)), V)
 
 
 class RACAttention(nn.Module):
@@ -845,34 +895,27 @@ class RACAttention(nn.Module):
         if _rac_core_ok(mask, T, self.dropout):
             out = rac_attention(Q, K, V, mask, is_causal)
         else:
-            scores = self._rac_bmm(Q, K.transpose(-2, -1)) * self.scale
-            if is_causal:
-                scores = _causal_scores(scores, T)
-            if mask is not None:
-                scores = scores + mask
-            attn = self.dropout(rac_softmax(scores))
-            out = self._rac_bmm(attn, V)
+            # the reference loops RACMatmulFunction over heads
+            # (rac_torch.py:781-795); one batched launch does the same products
+            out = _attention_composed(Q, K, V, self.scale, mask, is_causal, self.dropout)
         out = out.transpose(1, 2).contiguous().view(B, T, D)
         return self.out_proj(out)
 
-    def _rac_bmm(self, A, B):
-        # the reference loops RACMatmulFunction over heads
-        # (rac_torch.py:781-795); one batched launch does the same products
-        return rac_bmm(A, B)
-
     @classmethod
     def from_attention_layers(cls, q_linear, k_linear, v_linear, out_linear, n_heads, dropout=0.0):
-        d_model = q_linear.in_features
-        has_bias = q_linear.bias is not None
-        attn = cls(d_model, n_heads, bias=has_bias, dropout=dropout,
-                   device=q_linear.weight.device, dtype=q_linear.weight.dtype)
-        with torch.no_grad():
-            attn.qkv.weight.copy_(torch.cat([q_linear.weight, k_linear.weight, v_linear.weight], dim=0))
-            if has_bias:
-                attn.qkv.bias.copy_(torch.cat([q_linear.bias, k_linear.bias, v_linear.bias], dim=0))
-            attn.out_proj.weight.copy_(out_linear.weight)
-            if has_bias:
-                attn.out_proj.bias.copy_(out_linear.bias)
+        """Multi-head attention built from four existing d_model -> d_model
+        projections (rac_torch.py:781-816): Q, K and V become the row blocks
+        of the fused qkv weight in that order, out_linear the output
+        projection; parameters are copied bit for bit.  All four must be
+        square, agree on having a bias, and n_heads must divide d_model."""
+        parts = (q_linear, k_linear, v_linear, out_linear)
+        d_model, with_bias = _square_projections("from_attention_layers", parts)
+        if n_heads <= 0 or d_model % n_heads:
+            raise ValueError(f"from_attention_layers: n_heads ({n_heads}) must divide d_model ({d_model})")
+        ref = q_linear.weight
+        attn = cls(d_model, n_heads, bias=with_bias, dropout=dropout, device=ref.device, dtype=ref.dtype)
+        _load_row_blocks(attn.qkv, parts[:3])
+        _load_row_blocks(attn.out_proj, parts[3:])
         return attn
 
     def extra_repr(self):
@@ -908,8 +951,8 @@ class RACRoPEAttention(nn.Module):
     projections, RoPE kernel on the strided Q/K views, and the attention core
     through RAC (Q K^T and P V on the CORDIC matmul, causal / [T, T] mask and
     CORDIC softmax).  With dropout active or another mask shape, the
-    reference's composition is kept: fp32 torch matmuls around the
-    CORDIC-exp softmax."""
+    reference's stages run one by one, still with every product on the
+    batched RAC matmul and the CORDIC-exp softmax."""
 
     def __init__(self, d_model: int, n_heads: int, max_seq_len: int = 4096, bias: bool = False,
                  dropout: float = 0.0, rope_base: float = 10000.0, device=None, dtype=None):
@@ -937,13 +980,7 @@ class RACRoPEAttention(nn.Module):
         if _rac_core_ok(mask, T, self.dropout):
             out = rac_attention(Q, K, V, mask, is_causal).to(x.dtype)
         else:
-            scores = torch.matmul(Q.float().contiguous(), K.float().transpose(-2, -1).contiguous()) * self.scale
-            if is_causal:
-                scores = _causal_scores(scores, T)
-            if mask is not None:
-                scores = scores + mask
-            attn = self.dropout(rac_softmax(scores))
-            out = torch.matmul(attn, V.float().contiguous()).to(x.dtype)
+            out = _attention_composed(Q, K, V, self.scale, mask, is_causal, self.dropout).to(x.dtype)
         out = out.transpose(1, 2).contiguous().view(B, T, D)
         return self.out_proj(out)
 
@@ -1081,6 +1118,7 @@ def rac_info():
         print(f"  kernel library:        NOT LOADED ({e})")
     if torch.cuda.is_available():
         print(f"  device:                {torch.cuda.get_device_properties(0).name}")
+    print(f"  start-up probe:        {_PROBE.stage}: {_PROBE.message}")
     mode_name = {0: 'fast', 1: 'cordic', 2: 'shiftadd'}.get(_RAC_CORDIC_MODE, '?')
     print(f"  CORDIC iters:          {_RAC_CORDIC_ITERS} (rac_set_precision)")
     print(f"  compute mode:          {mode_name} (rac_set_mode)")

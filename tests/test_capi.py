@@ -540,6 +540,95 @@ def test_patch_helpers_and_qkv_fusion_on_cpu(capsys):
         rt.RACFusedQKV.from_qkv_linears(lq, nn.Linear(16, 16, bias=False), lv)
 
 
+
+def test_attention_from_layers_and_path_choice_on_cpu():
+    """RACAttention.from_attention_layers stacks Q, K, V into the fused
+    projection's row blocks and copies the output projection bit for bit,
+    refusing non-square or bias-mismatched layers and heads that do not
+    divide d_model; the fused attention core is taken only when nothing sits
+    between softmax and P V (identity, or nn.Dropout in eval mode / p = 0)
+    and the mask is None or a float [T, T]."""
+    import torch
+    import torch.nn as nn
+    from rac_amd import rac_torch as rt
+
+    torch.manual_seed(1)
+    lq, lk, lv, lo = (nn.Linear(32, 32) for _ in range(4))
+    attn = rt.RACAttention.from_attention_layers(lq, lk, lv, lo, n_heads=4)
+    w = attn.qkv.weight.detach()
+    assert torch.equal(w[:32], lq.weight) and torch.equal(w[32:64], lk.weight) and torch.equal(w[64:], lv.weight)
+    b = attn.qkv.bias.detach()
+    assert torch.equal(b[:32], lq.bias) and torch.equal(b[32:64], lk.bias) and torch.equal(b[64:], lv.bias)
+    assert torch.equal(attn.out_proj.weight, lo.weight) and torch.equal(attn.out_proj.bias, lo.bias)
+    assert attn.n_heads == 4 and attn.d_head == 8
+    nb = rt.RACAttention.from_attention_layers(*(nn.Linear(32, 32, bias=False) for _ in range(4)), n_heads=2)
+    assert nb.qkv.bias is None and nb.out_proj.bias is None
+    with pytest.raises(ValueError):
+        rt.RACAttention.from_attention_layers(lq, lk, lv, nn.Linear(32, 32, bias=False), n_heads=4)
+    with pytest.raises(ValueError):
+        rt.RACAttention.from_attention_layers(lq, nn.Linear(32, 16), lv, lo, n_heads=4)
+    with pytest.raises(ValueError):
+        rt.RACAttention.from_attention_layers(lq, lk, lv, lo, n_heads=5)
+
+    T = 8
+    drop = nn.Dropout(0.1)
+    assert not rt._rac_core_ok(None, T, drop)
+    drop.eval()
+    assert rt._rac_core_ok(None, T, drop)
+    assert rt._rac_core_ok(None, T, nn.Identity()) and rt._rac_core_ok(None, T, nn.Dropout(0.0))
+
+    class Other(nn.Module):
+        def forward(self, x):
+            return x
+
+    class SubDropout(nn.Dropout):
+        pass
+
+    assert not rt._rac_core_ok(None, T, Other()) and not rt._rac_core_ok(None, T, SubDropout(0.1).eval())
+    assert rt._rac_core_ok(torch.zeros(T, T), T, nn.Identity())
+    assert not rt._rac_core_ok(torch.zeros(1, 1, T, T), T, nn.Identity())
+    assert not rt._rac_core_ok(torch.ones(T, T, dtype=torch.bool), T, nn.Identity())
+
+
+def test_startup_probe_diagnoses_each_stage():
+    """The import-time probe (rac_torch.py:55-108) names its failure: a
+    missing library is "not built" (and rac_torch still imports, with that
+    warning), a non-gfx950 device is "no gfx950 code", no device is
+    reported without a warning; ops then raise with the diagnosis."""
+    import sys
+    import types
+    code = ("import warnings, rac_amd._lib as L\n"
+            "L.LIB_PATH = '/nonexistent/librac_amd.so'\n"
+            "warnings.simplefilter('always')\n"
+            "with warnings.catch_warnings(record=True) as w:\n"
+            "    import rac_amd.rac_torch as rt\n"
+            "print('STAGE', rt._PROBE.stage)\n"
+            "print('WARN', ' | '.join(str(x.message) for x in w))\n")
+    env = dict(os.environ, PYTHONPATH=ROOT)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=ROOT,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert "STAGE no-library" in out.stdout
+    assert "not built" in out.stdout and "/nonexistent/librac_amd.so" in out.stdout
+
+    import torch
+    from rac_amd import _probe
+    real_avail, real_props, real_cur = torch.cuda.is_available, torch.cuda.get_device_properties, \
+        torch.cuda.current_device
+    try:
+        torch.cuda.is_available = lambda: True
+        torch.cuda.current_device = lambda: 0
+        torch.cuda.get_device_properties = lambda d: types.SimpleNamespace(gcnArchName="gfx942:sramecc+:xnack-")
+        r = _probe.probe()
+        assert (r.ok, r.stage) == (False, "arch")
+        assert "no gfx950 code for this device" in r.message and "gfx942" in r.message
+    finally:
+        torch.cuda.is_available, torch.cuda.get_device_properties, torch.cuda.current_device = \
+            real_avail, real_props, real_cur
+    if not torch.cuda.is_available():
+        r = _probe.probe()
+        assert (r.ok, r.stage) == (False, "no-device")
+
 def test_attention_workspace_sizes(lib):
     """The attention workspace holds one chunk of query rows (at most 128 MiB
     of scores, or 64 rows of every head), plus 256 bytes for a flag; the
@@ -555,6 +644,12 @@ def test_attention_workspace_sizes(lib):
     a = ctypes.addressof(buf)
     assert lib.rac_attention_ws_dev(a, a, a, None, 1, a, 1, 2, 16, 4, a, 4 * 2 * 16 + 255, 16, 1, None) == -2
     assert b"below" in lib.rac_last_error()
+    # the allocation-free form: batch*n_heads*seq = 16777216 (one query row
+    # of every head is 64 MiB, past its 64 MiB scratch) is refused before
+    # any device work
+    lib.rac_clear_error()
+    assert lib.rac_attention_noalloc_dev(a, a, a, None, 1, a, 1, 64, 262144, 4, 16, 1, None) == -2
+    assert b"16777215" in lib.rac_last_error()
 
 
 def test_every_device_entry_point_refuses_null_buffers(lib):

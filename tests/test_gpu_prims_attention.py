@@ -378,8 +378,8 @@ def test_rope_attention_module_uses_rac_core():
     m = rt.RACRoPEAttention(256, 4, max_seq_len=64).to(DEV)
     x = torch.randn(2, 40, 256, device=DEV)
     y = m(x, is_causal=True)
-    # the same module with the reference composition (torch matmuls around
-    # the CORDIC softmax): agrees to the CORDIC product error
+    # the same module with the stages composed one by one (batched RAC
+    # products around the CORDIC softmax): agrees to the summation-order bound
     old = rt._rac_core_ok
     rt._rac_core_ok = lambda *a: False
     try:
@@ -390,6 +390,90 @@ def test_rope_attention_module_uses_rac_core():
     y.sum().backward()
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in m.parameters())
 
+
+
+class _FixedDropout(torch.nn.Dropout):
+    """Dropout stand-in whose keep mask (already scaled by 1/(1-p)) is fixed,
+    so the composed attention path can be checked bit for bit."""
+
+    def __init__(self, keep):
+        super().__init__(p=0.5)
+        self.keep = keep
+
+    def forward(self, x):
+        return x * self.keep
+
+
+@pytest.mark.parametrize("case", ["mask4d", "mask_b1", "bool_causal", "dropout"])
+@pytest.mark.parametrize("iters,mode", [(16, 1), (24, 0)])
+def test_rope_attention_composed_path_bit_exact(case, iters, mode):
+    """RACRoPEAttention where the fused core does not apply (a 4-D additive
+    mask, a bool mask, an active dropout): Q K^T and P V on the batched RAC
+    matmul around the CORDIC softmax (rac_torch.py:1327-1337), bit-exact with
+    the checker's composition (orc_matmul, orc_softmax_lanes) on the module's
+    own post-RoPE Q, K and V."""
+    from rac_amd import rac_torch as rt
+    old = (rt.rac_get_precision(), rt.rac_get_mode())
+    rt.rac_set_precision(iters)
+    rt.rac_set_mode(mode)
+    try:
+        torch.manual_seed(7)
+        B, Tn, d, nh = 2, 24, 128, 4
+        hd = d // nh
+        m = rt.RACRoPEAttention(d, nh, max_seq_len=64).to(DEV)
+        x = torch.randn(B, Tn, d, device=DEV)
+        mask, causal, keep = None, False, None
+        if case == "mask4d":
+            mask = torch.randn(B, nh, Tn, Tn, device=DEV) * 0.5
+        elif case == "mask_b1":
+            mask = torch.randn(B, 1, Tn, Tn, device=DEV) * 0.5
+            causal = True
+        elif case == "bool_causal":
+            # torch's + adds 1.0 where the bool mask is True (the reference's
+            # scores + mask, rac_torch.py:1332)
+            mask = torch.tril(torch.ones(Tn, Tn, dtype=torch.bool, device=DEV)).view(1, 1, Tn, Tn)
+            causal = True
+        else:
+            keep = (torch.rand(B, nh, Tn, Tn, device=DEV) >= 0.5).float() * 2.0
+            m.dropout = _FixedDropout(keep)
+            causal = True
+        m.train()
+        assert not rt._rac_core_ok(mask, Tn, m.dropout)
+        seen = {}
+        hooks = [m.rope.register_forward_hook(lambda mod, inp, out: seen.__setitem__("qk", out)),
+                 m.qkv.register_forward_hook(lambda mod, inp, out: seen.__setitem__("qkv", out)),
+                 m.out_proj.register_forward_pre_hook(lambda mod, inp: seen.__setitem__("att", inp[0]))]
+        try:
+            with torch.no_grad():
+                m(x, mask=mask, is_causal=causal)
+        finally:
+            for h in hooks:
+                h.remove()
+        q, k = (np.ascontiguousarray(H(t)) for t in seen["qk"])
+        v = np.ascontiguousarray(H(seen["qkv"].chunk(3, -1)[2].reshape(B, Tn, nh, hd).transpose(1, 2)))
+        got = H(seen["att"])
+        scale = np.float32(hd ** -0.5)
+        maskn = H(mask.float()) if mask is not None else None
+        keepn = H(keep) if keep is not None else None
+        upper = np.triu(np.full((Tn, Tn), -np.inf, np.float32), 1)
+        ref = np.empty((B, nh, Tn, hd), np.float32)
+        for b in range(B):
+            for h in range(nh):
+                s = rl.orc_matmul(q[b, h], np.ascontiguousarray(k[b, h].T), Tn, Tn, hd, iters, mode) * scale
+                if causal:
+                    s = s + upper
+                if maskn is not None:
+                    s = s + maskn[b % maskn.shape[0], h % maskn.shape[1]]
+                pr = rl.orc_softmax_lanes(s, iters)
+                if keepn is not None:
+                    pr = pr * keepn[b, h]
+                ref[b, h] = rl.orc_matmul(pr, v[b, h], Tn, hd, Tn, iters, mode)
+        ref = ref.transpose(0, 2, 1, 3).reshape(B, Tn, d)
+        bad = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+        assert bad.size == 0, f"{bad.size} outputs differ, first {got.ravel()[bad[0]]!r} vs {ref.ravel()[bad[0]]!r}"
+    finally:
+        rt.rac_set_precision(old[0])
+        rt.rac_set_mode(old[1])
 
 def _attention_ws(q, k, v, mask, causal, iters, mode, chunk_rows=None, probs=False):
     """rac_attention_ws_dev with a workspace for `chunk_rows` query rows per

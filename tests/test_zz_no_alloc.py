@@ -1,9 +1,8 @@
 """rac_attention_noalloc_dev, the allocation-free attention entry point,
 against rac_attention_dev (workspace argument): bit-identical outputs on two
-calls in a row, the second with a smaller input, through the C ABI; and
-shapes past its limit refused before any device work."""
-import ctypes
-
+calls in a row, the second with a smaller input, through the C ABI; and the
+same call recorded in a HIP graph and replayed.  (Shapes past its limit are
+refused before any device work: tests/test_capi.py, on the CPU.)"""
 import numpy as np
 import pytest
 
@@ -69,11 +68,34 @@ def test_noalloc_attention_matches_workspace_entry_twice(lib):
     assert np.array_equal(got3, _run(lib, q3, k3, v3, None, True, 24, 0, noalloc=False))
 
 
-def test_noalloc_attention_refuses_beyond_scratch(lib):
-    buf = (ctypes.c_float * 64)()
-    a = ctypes.addressof(buf)
-    # batch*n_heads*seq = 16777216: one query row of every head is 64 MiB,
-    # past the limit; refused before any device work
-    lib.rac_clear_error()
-    assert lib.rac_attention_noalloc_dev(a, a, a, None, 1, a, 1, 64, 262144, 4, 16, 1, None) == -2
-    assert b"16777215" in lib.rac_last_error()
+def test_noalloc_attention_recorded_in_a_graph_replays_bit_identical(lib):
+    """The call recorded under stream capture (torch.cuda.graph) and replayed
+    three times, with eager work (including another no-alloc call, which
+    overwrites the shared scratch) and synchronisation between the replays:
+    every replay equals the eager call bit for bit.  The eager call comes
+    first, so the scratch address is resolved outside the capture."""
+    q, k, v = _qkv((1, 4, 256, 64), seed=830)
+    eager = _run(lib, q, k, v, None, True, 16, 1, noalloc=True)
+    q2, k2, v2 = _qkv((2, 2, 96, 32), seed=840)
+    other = _run(lib, q2, k2, v2, None, False, 8, 1, noalloc=True)
+    qt, kt, vt = (torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in (q, k, v))
+    out = torch.full_like(qt, float("nan"))
+    torch.cuda.synchronize()
+    print("recording rac_attention_noalloc_dev [1, 4, 256, 64] causal n=16 in a graph", flush=True)
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(g):
+        stream = torch.cuda.current_stream().cuda_stream
+        rcs.append(lib.rac_attention_noalloc_dev(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), None, 1,
+                                                 out.data_ptr(), 1, 4, 256, 64, 16, 1, stream))
+    assert rcs == [0], lib.rac_last_error()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"replay {rep}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), f"replay {rep}"
+        assert np.array_equal(_run(lib, q2, k2, v2, None, False, 8, 1, noalloc=True), other)
+    del g
+    torch.cuda.synchronize()
