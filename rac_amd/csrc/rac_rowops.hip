@@ -90,31 +90,87 @@ __device__ __forceinline__ float softmax_lane_max(float* v, long n4, long t, con
 }
 
 // Exps of the lane's values against the row maximum m, and the lane's sum
-// of them (NaN when the row holds a NaN, unmasked rows).
+// of them (masked rows, and rows whose step count is known only at run time).
 template <int VPT, int NITER, bool MASKED>
 __device__ __forceinline__ float softmax_lane_exps(float* v, float m, int iters, float khinv) {
     constexpr int E = 4 * VPT;
-    // Unmasked rows with a compile-time step count: every x - max is <= 0
-    // or NaN, and a NaN anywhere (a NaN element, or max = +-inf) makes the
-    // reference's row sum NaN and so every output NaN.  The exps then skip
-    // their per-element NaN test and sign-dependent rounding bias
-    // (kExpNonPos); NaN is found once per lane with a NaN-propagating
-    // maximum and forced into the row sum instead.
-    constexpr bool kLean = !MASKED && NITER > 0;
-    float nanp = -__builtin_inff();
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-        v[e] = v[e] - m;
-        if constexpr (kLean) nanp = __builtin_elementwise_maximum(nanp, v[e]);
-    }
-    if constexpr (kLean) exp_lane<NITER, E, kExpFlush | kExpNonPos>(v, iters, khinv);
-    else exp_lane<NITER, E>(v, iters, khinv);
+    for (int e = 0; e < E; e++) v[e] = v[e] - m;
+    exp_lane<NITER, E>(v, iters, khinv);
     float s = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; e++) s += v[e];
-    if constexpr (kLean) {
-        if (nanp != nanp) s = __builtin_nanf("");
+    return s;
+}
+
+// Unmasked rows with a compile-time step count.  Every x - max is <= 0 or
+// NaN, and a NaN anywhere, or a maximum of +-inf, makes the reference's row
+// sum NaN and with it every output (rac_cpu.c:258-271).  So:
+//  - the row maximum is the NaN-propagating IEEE maximum (v_maximum3, no
+//    canonicalisation of the loaded values; -0 < +0 as for v_max_f32, so
+//    the maximum and every x - max equal the general path's), and a
+//    non-finite maximum forces the row sum to NaN instead of a per-element
+//    NaN test;
+//  - the exps skip the sign-dependent rounding bias (kExpNonPos);
+//  - when every x - max of the wave is >= -86 (then k >= -124), the exp's
+//    (p / K_h) 2^k is p * (1/K_h 2^k) with the scale built in the exponent
+//    field: one rounding of the same exact product, every intermediate
+//    normal, so the bits of ldexp(p / K_h, k); otherwise ldexp and the
+//    k <= -127 flush.
+// Bit-identical to softmax_lane_exps<VPT, NITER, false> with kExpFlush |
+// kExpNonPos exps and a NaN pass; ~5% fewer VALU instructions per element.
+struct RowExtent {
+    float max;   // row maximum (every lane)
+    float min;   // the lane's minimum
+};
+
+template <int VPT, bool LDS_ONLY>
+__device__ __forceinline__ RowExtent unmasked_row_extent(const float* v, float* red) {
+    constexpr int E = 4 * VPT;
+    float mx = v[0], mn = v[0];
+#pragma unroll
+    for (int e = 1; e < E; e++) {
+        mx = maximum(mx, v[e]);
+        mn = fminf(mn, v[e]);
     }
+    return {block_maximum<false, LDS_ONLY>(mx, red), mn};
+}
+
+template <int N, int G>
+__device__ __forceinline__ void unmasked_exp_group(float* v, float khinv, bool fused) {
+    int k[G];
+    float p[G], z[G];
+#pragma unroll
+    for (int e = 0; e < G; e++) {
+        k[e] = cvt_i32_sat(__builtin_fmaf(v[e], kInvLn2, -0.5f));
+        z[e] = __builtin_fmaf(-(float)k[e], kLn2, v[e]);
+        p[e] = 1.0f;
+    }
+    HypStepV<N, 0, G>::run(p, z);
+    if (fused) {
+#pragma unroll
+        for (int e = 0; e < G; e++) v[e] = p[e] * as_f(as_u(khinv) + ((uint32_t)k[e] << 23));
+    } else {
+#pragma unroll
+        for (int e = 0; e < G; e++) {
+            const float res = __builtin_ldexpf(p[e] * khinv, k[e]);
+            v[e] = (k[e] <= -127) ? 0.0f : res;
+        }
+    }
+}
+
+template <int NITER, int E>
+__device__ __forceinline__ float unmasked_lane_exps(float* v, RowExtent r, float khinv) {
+    const bool fused = __all((r.min - r.max) >= -86.0f);
+#pragma unroll
+    for (int e = 0; e < E; e++) v[e] = v[e] - r.max;
+    constexpr int G = E < 16 ? E : 16;
+#pragma unroll
+    for (int b = 0; b < E; b += G) unmasked_exp_group<NITER, G>(v + b, khinv, fused);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; e++) s += v[e];
+    if (!(__builtin_fabsf(r.max) < __builtin_inff())) s = __builtin_nanf("");
     return s;
 }
 
@@ -136,6 +192,15 @@ __device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters,
 template <int VPT, int NITER, bool MASKED, bool FULL>
 __device__ __forceinline__ void softmax_row_regs(float* v, long n4, long t, int iters, float khinv,
                                                  const SoftmaxMask& mk, float* red) {
+    if constexpr (!MASKED && NITER > 0) {
+        const RowExtent r = unmasked_row_extent<VPT, false>(v, red);
+        float s = unmasked_lane_exps<NITER, 4 * VPT>(v, r, khinv);
+        s = block_sum<false>(s, red + kRowWaves);
+        const float inv = inv_sum(s, 0);
+#pragma unroll
+        for (int e = 0; e < 4 * VPT; e++) v[e] = v[e] * inv;
+        return;
+    }
     const float m = softmax_lane_max<VPT, MASKED, FULL>(v, n4, t, mk);
     softmax_row_finish<VPT, NITER, MASKED>(v, m, iters, khinv, mk, red);
 }
@@ -223,15 +288,11 @@ __global__ __launch_bounds__(kRowThreads) void softmax_prefetch_kernel(
             const float4 q = *reinterpret_cast<const float4*>(row_lds + 4 * (t + kRowThreads * i));
             v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
         }
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int i = 0; i < VPT; i++)
-            m = fmaxf(fmaxf(fmaxf(m, v[4 * i]), fmaxf(v[4 * i + 1], v[4 * i + 2])), v[4 * i + 3]);
         // every wave has read row_lds (its lane maximum needs the values)
-        // once the barrier inside block_max is passed
-        m = block_max<false, true>(m, red);
+        // once the barrier inside block_maximum is passed
+        const RowExtent r = unmasked_row_extent<VPT, true>(v, red);
         if (row + G < rows) prefetch(row + G);
-        float s = softmax_lane_exps<VPT, NITER, false>(v, m, 0, khinv);
+        float s = unmasked_lane_exps<NITER, E>(v, r, khinv);
         // the prefetch has landed before the barrier below (the LDS fence
         // waits for it too; this states it, and the operand keeps the wait
         // after the exps)
@@ -290,14 +351,28 @@ __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
     for (long i = threadIdx.x; i < n; i += kRowThreads) yr[i] = yr[i] * inv;
 }
 
+// Workgroups per CU of the unmasked register kernel with compile-time steps.
+// Its leaner arithmetic needs fewer VGPRs than the general form (59 / 82 /
+// 113 at VPT 4 / 8 / 16 against 74 / 120 / 137), which would raise
+// residency from 6 / 4 / 3 to 8 / 5 / 4 workgroups per CU.  At VPT 4 that
+// was measured slower (softmax 4096 x 4096, n = 16: 8 per CU ran 29.2 µs
+// median against 25.4 at 6 on one box, 0.97x on another; 6 per CU with the
+// lean arithmetic: 0.95-0.99x of the general form), so the launch keeps the
+// general form's residency by requesting unused dynamic LDS: 160 KB / cap
+// minus 1 KB lets exactly `cap` workgroups share a CU's 160 KB.
+constexpr long kCuLdsBytes = 160L * 1024;
+constexpr int unmasked_reg_cap(int vpt) { return vpt <= 2 ? 0 : vpt == 4 ? 6 : vpt == 8 ? 4 : 3; }
+
 template <int VPT, int NITER, bool MASKED>
 static void softmax_reg_launch(dim3 grid, hipStream_t s, const float* x, float* y, long n, int iters,
                                float khinv, const SoftmaxMask& mk) {
+    constexpr int cap = (!MASKED && NITER > 0) ? unmasked_reg_cap(VPT) : 0;
+    constexpr size_t lds = cap ? (size_t)(kCuLdsBytes / cap - 1024) : 0;
     if (n == 4L * VPT * kRowThreads)
-        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, true>), grid, dim3(kRowThreads), 0, s, x, y,
+        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, true>), grid, dim3(kRowThreads), lds, s, x, y,
                            n, iters, khinv, mk);
     else
-        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, false>), grid, dim3(kRowThreads), 0, s, x,
+        hipLaunchKernelGGL((softmax_reg_kernel<VPT, NITER, MASKED, false>), grid, dim3(kRowThreads), lds, s, x,
                            y, n, iters, khinv, mk);
 }
 

@@ -23,6 +23,15 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// IEEE maximum (NaN-propagating; -0 < +0 like v_max_f32): no operand
+// canonicalisation, and a NaN anywhere reaches every lane.
+__device__ __forceinline__ float maximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float wave_maximum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = maximum(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also releases
 // global memory, which makes every wave wait for its outstanding global
 // stores; a kernel that keeps stores in flight across its row reductions
@@ -54,6 +63,19 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     float r = red[0];
 #pragma unroll
     for (int i = 1; i < kRowWaves; i++) r += red[i];
+    if constexpr (TRAIL) red_barrier<LDS_ONLY>();
+    return r;
+}
+// block_max with the NaN-propagating maximum throughout.
+template <bool TRAIL = true, bool LDS_ONLY = false>
+__device__ __forceinline__ float block_maximum(float v, float* red) {
+    v = wave_maximum(v);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    red_barrier<LDS_ONLY>();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; i++) r = maximum(r, red[i]);
     if constexpr (TRAIL) red_barrier<LDS_ONLY>();
     return r;
 }
