@@ -249,6 +249,30 @@ def test_attention_vs_oracle(shape, iters, mode):
         assert np.array_equal(got, rl.orc_attention_lanes(q, k, v, mk, causal, iters, mode))
 
 
+
+@pytest.mark.parametrize("iters", [8, 16, 24])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_peaked_rows_bit_exact(iters, causal):
+    """Peaked softmax rows (Q and K scaled by 8) put many probabilities
+    below 2^-105, where the strength-reduced rotation chain and the
+    reference's literal chain round differently; a few Q entries are tiny,
+    subnormal or zero.  Both attention products take the literal chain for
+    those operands, so the core equals the checker's composition bit for
+    bit, in one chunk and in several."""
+    e = ext()
+    shape = (1, 3, 160, 32)
+    q, k, v = _qkv(shape, seed=4242)
+    q = (q * np.float32(8.0)).astype(np.float32)
+    k = (k * np.float32(8.0)).astype(np.float32)
+    q[0, 0, 3, :4] = np.float32([1e-33, -3e-38, 1e-41, 0.0])
+    q[0, 1, 77, 5] = np.float32(2.0 ** -110)
+    ref = rl.orc_attention_lanes(q, k, v, None, causal, iters, 1)
+    print(f"peaked attention shape={shape} iters={iters} causal={causal}", flush=True)
+    got = H(e.attention(T(q), T(k), T(v), None, causal, iters=iters, mode=1))
+    assert np.array_equal(got, ref)
+    got_chunks = _attention_ws(q, k, v, None, causal, iters, 1, chunk_rows=48)
+    assert np.array_equal(got_chunks, ref)
+
 @pytest.mark.parametrize("shape", [(16, 64, 256, 64), (1, 4, 256, 64)])
 def test_attention_causal_many_heads_sampled(shape):
     """Causal attention over 1024 and 4 heads (the paired-row P V launch at
