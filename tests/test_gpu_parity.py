@@ -183,6 +183,33 @@ def test_rac_h_matmul_1024_config1_host_pointers():
     assert np.array_equal(C.ravel()[idx], ref)
 
 
+
+def test_rac_h_staging_cache_release():
+    """The synchronous rac.h calls stage host buffers through cached device
+    buffers; rac_release_cached_memory frees them (returning the bytes) and
+    later calls stage afresh with the same results."""
+    M, N, K = 256, 192, 320
+    A = rl.gen_uniform((M, K), seed=11)
+    B = rl.gen_uniform((K, N), seed=12)
+    L = lib()
+    L.rac_set_cordic_iters(16)
+    L.rac_set_cordic_mode(1)
+    ref = rl.orc_matmul(A, B, M, N, K, 16, 1)
+    C1 = np.zeros((M, N), np.float32)
+    L.rac_clear_error()
+    L.rac_matmul(rl.p(A), rl.p(B), rl.p(C1), M, N, K)
+    assert L.rac_last_error() == b"", L.rac_last_error()
+    assert np.array_equal(C1, ref)
+    freed = L.rac_release_cached_memory()
+    assert freed >= 4 * (M * K + K * N + M * N), freed
+    assert L.rac_release_cached_memory() == 0
+    C2 = np.zeros((M, N), np.float32)
+    L.rac_matmul(rl.p(A), rl.p(B), rl.p(C2), M, N, K)
+    assert L.rac_last_error() == b"", L.rac_last_error()
+    assert np.array_equal(C2, ref)
+    import rac_amd
+    assert rac_amd.release_cached_memory() >= 4 * (M * K + K * N + M * N)
+
 @pytest.mark.parametrize("iters", [8, 16, 24])
 def test_cordic_matmul_4096_sampled(iters):
     """The metric shape, 4096^3: sampled entries bit-exact vs the checker."""
