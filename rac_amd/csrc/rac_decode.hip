@@ -108,6 +108,17 @@ __global__ __launch_bounds__(kRowThreads) void decode_attention_kernel(
         for (int c = 0; c < 4; c++) m = fmaxf(m, sp[4 * gi + c]);
     }
     m = block_max<false>(m, red);
+    if (m == 0.0f) {
+        // the signed zero the reference's scan ends on (first_zero_max)
+        __shared__ uint32_t zred[kRowWaves];
+        uint32_t key = ~0u;
+        for (int gi = tid; gi < n4 && key == ~0u; gi += kRowThreads) {
+#pragma unroll
+            for (int c = 3; c >= 0; c--)
+                if (sp[4 * gi + c] == 0.0f) key = zero_key<uint32_t>(4 * gi + c, sp[4 * gi + c]);
+        }
+        m = first_zero_max<false>(key, zred);
+    }
     constexpr bool kLean = NITER > 0;
     float nanp = -__builtin_inff();
     float s = 0.0f;

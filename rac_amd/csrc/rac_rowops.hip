@@ -89,6 +89,18 @@ __device__ __forceinline__ float softmax_lane_max(float* v, long n4, long t, con
     return m;
 }
 
+// The lane's first zero (zero_key) in the register layout: group i of lane l
+// is the row's float4 group l + 256 i, so the lane's values run in index
+// order.
+template <int VPT>
+__device__ __forceinline__ uint32_t lane_first_zero(const float* v) {
+    uint32_t key = ~0u;
+#pragma unroll
+    for (int e = 4 * VPT - 1; e >= 0; e--)
+        if (v[e] == 0.0f) key = zero_key<uint32_t>(4 * (threadIdx.x + kRowThreads * (e / 4)) + e % 4, v[e]);
+    return key;
+}
+
 // Exps of the lane's values against the row maximum m, and the lane's sum
 // of them (masked rows, and rows whose step count is known only at run time).
 template <int VPT, int NITER, bool MASKED>
@@ -124,8 +136,12 @@ struct RowExtent {
     float min;   // the lane's minimum
 };
 
+// row_lds: the row in LDS in the same layout (the prefetching kernel), read
+// instead of v for the rare zero-maximum scan, so that scan holds no
+// registers of its own; null: scan v.
 template <int VPT, bool LDS_ONLY>
-__device__ __forceinline__ RowExtent unmasked_row_extent(const float* v, float* red) {
+__device__ __forceinline__ RowExtent unmasked_row_extent(const float* v, float* red, uint32_t* zred,
+                                                         const float* row_lds = nullptr) {
     constexpr int E = 4 * VPT;
     float mx = v[0], mn = v[0];
 #pragma unroll
@@ -133,7 +149,20 @@ __device__ __forceinline__ RowExtent unmasked_row_extent(const float* v, float* 
         mx = maximum(mx, v[e]);
         mn = fminf(mn, v[e]);
     }
-    return {block_maximum<false, LDS_ONLY>(mx, red), mn};
+    mx = block_maximum<false, LDS_ONLY>(mx, red);
+    if (mx == 0.0f) {
+        uint32_t key = ~0u;
+        if (row_lds) {
+            for (int e = 0; e < E && key == ~0u; e++) {
+                const int idx = 4 * (threadIdx.x + kRowThreads * (e / 4)) + e % 4;
+                if (row_lds[idx] == 0.0f) key = zero_key<uint32_t>(idx, row_lds[idx]);
+            }
+        } else {
+            key = lane_first_zero<VPT>(v);
+        }
+        mx = first_zero_max<LDS_ONLY>(key, zred);
+    }
+    return {mx, mn};
 }
 
 template <int N, int G>
@@ -179,9 +208,10 @@ __device__ __forceinline__ float unmasked_lane_exps(float* v, RowExtent r, float
 // needs a trailing barrier; a kernel handles one row per workgroup).
 template <int VPT, int NITER, bool MASKED>
 __device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters, float khinv,
-                                                   const SoftmaxMask& mk, float* red) {
+                                                   const SoftmaxMask& mk, float* red, uint32_t* zred) {
     constexpr int E = 4 * VPT;
     m = block_max<false>(m, red);
+    if (m == 0.0f) m = first_zero_max<false>(lane_first_zero<VPT>(v), zred);
     float s = softmax_lane_exps<VPT, NITER, MASKED>(v, m, iters, khinv);
     s = block_sum<false>(s, red + kRowWaves);
     const float inv = inv_sum(s, MASKED ? mk.zero_guard : 0);
@@ -191,9 +221,9 @@ __device__ __forceinline__ void softmax_row_finish(float* v, float m, int iters,
 
 template <int VPT, int NITER, bool MASKED, bool FULL>
 __device__ __forceinline__ void softmax_row_regs(float* v, long n4, long t, int iters, float khinv,
-                                                 const SoftmaxMask& mk, float* red) {
+                                                 const SoftmaxMask& mk, float* red, uint32_t* zred) {
     if constexpr (!MASKED && NITER > 0) {
-        const RowExtent r = unmasked_row_extent<VPT, false>(v, red);
+        const RowExtent r = unmasked_row_extent<VPT, false>(v, red, zred);
         float s = unmasked_lane_exps<NITER, 4 * VPT>(v, r, khinv);
         s = block_sum<false>(s, red + kRowWaves);
         const float inv = inv_sum(s, 0);
@@ -202,7 +232,7 @@ __device__ __forceinline__ void softmax_row_regs(float* v, long n4, long t, int 
         return;
     }
     const float m = softmax_lane_max<VPT, MASKED, FULL>(v, n4, t, mk);
-    softmax_row_finish<VPT, NITER, MASKED>(v, m, iters, khinv, mk, red);
+    softmax_row_finish<VPT, NITER, MASKED>(v, m, iters, khinv, mk, red, zred);
 }
 
 template <int VPT, bool FULL>
@@ -236,12 +266,13 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
     SoftmaxMask mk)
 {
     __shared__ float red[2 * kRowWaves];
+    __shared__ uint32_t zred[kRowWaves];
     const long row = blockIdx.x;
     const long n4 = n / 4;
     float v[4 * VPT];
     load_row_regs<VPT, FULL>(x + row * n, n4, v);
     softmax_row_regs<VPT, NITER, MASKED, FULL>(v, n4, MASKED ? mk.row0 + row % mk.seq : 0, iters, khinv, mk,
-                                               red);
+                                               red, zred);
     store_row_regs<VPT, FULL>(y + row * n, n4, v);
 }
 
@@ -258,13 +289,14 @@ __global__ __launch_bounds__(kRowThreads) void softmax_reg_kernel(
 // one-row-per-workgroup kernel is faster (measured on 4096 x 4096: n = 8
 // 23.6 -> 22.2 us; n = 16 25.0 against 26.3, n = 24 31.1 against 32.2).
 template <int VPT, int NITER>
-__global__ __launch_bounds__(kRowThreads) void softmax_prefetch_kernel(
+__global__ __launch_bounds__(kRowThreads, 6) void softmax_prefetch_kernel(
     const float* x, float* y, long rows, float khinv)
 {
     constexpr long n = 1024L * VPT;
     constexpr int E = 4 * VPT;
     __shared__ __attribute__((aligned(16))) float row_lds[n];
     __shared__ float red[2 * kRowWaves];
+    __shared__ uint32_t zred[kRowWaves];
     const int t = threadIdx.x, w = t >> 6;
     const long G = gridDim.x;
     long row = blockIdx.x;
@@ -290,7 +322,7 @@ __global__ __launch_bounds__(kRowThreads) void softmax_prefetch_kernel(
         }
         // every wave has read row_lds (its lane maximum needs the values)
         // once the barrier inside block_maximum is passed
-        const RowExtent r = unmasked_row_extent<VPT, true>(v, red);
+        const RowExtent r = unmasked_row_extent<VPT, true>(v, red, zred, row_lds);
         if (row + G < rows) prefetch(row + G);
         float s = unmasked_lane_exps<NITER, E>(v, r, khinv);
         // the prefetch has landed before the barrier below (the LDS fence
@@ -338,6 +370,19 @@ __global__ __launch_bounds__(kRowThreads) void softmax_loop_kernel(
         m = fmaxf(m, v);
     }
     m = block_max(m, red);
+    if (m == 0.0f) {
+        __shared__ uint64_t zred[kRowWaves];
+        uint64_t key = ~0ull;
+        for (long i = threadIdx.x; i < n; i += kRowThreads) {
+            float v = xr[i];
+            if constexpr (MASKED) v = mask_score(v, t, i, mk);
+            if (v == 0.0f) {
+                key = zero_key<uint64_t>(i, v);
+                break;
+            }
+        }
+        m = first_zero_max<false>(key, zred);
+    }
     float s = 0.0f;
     for (long i = threadIdx.x; i < n; i += kRowThreads) {
         float v = xr[i];

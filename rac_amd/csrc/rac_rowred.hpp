@@ -66,6 +66,25 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     if constexpr (TRAIL) red_barrier<LDS_ONLY>();
     return r;
 }
+// The reference's row maximum (rac_cpu.c:258-262: m = x[0], replaced only
+// by a strictly greater x[i]) is the first element, in index order, of
+// those equal to the maximum value.  A parallel maximum finds the value, and
+// can differ from that element only in the sign of a zero maximum (+0 and -0
+// compare equal).  x - max then differs in the sign of zero for the -0
+// entries, which the CORDIC exp's first direction sees (a zero query row in
+// attention gives such rows).  So when the maximum is zero, the row takes
+// the sign of its first zero.  key: the lane's first zero as (element index
+// << 1) | sign bit, all ones if it holds none (K: uint32_t where indices
+// stay below 2^31, else uint64_t).  Returns the signed zero; every lane must
+// call it (it holds barriers); zred: kRowWaves keys of LDS used by nothing
+// else.
+template <class K>
+__device__ __forceinline__ K zero_key(long index, float v) {
+    return ((K)index << 1) | (K)(__float_as_uint(v) >> 31);
+}
+template <bool LDS_ONLY, class K>
+__device__ __forceinline__ float first_zero_max(K key, K* zred);
+
 // block_max with the NaN-propagating maximum throughout.
 template <bool TRAIL = true, bool LDS_ONLY = false>
 __device__ __forceinline__ float block_maximum(float v, float* red) {
@@ -90,6 +109,22 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     for (int i = 1; i < kRowWaves; i++) r = fmaxf(r, red[i]);
     if constexpr (TRAIL) red_barrier<LDS_ONLY>();
     return r;
+}
+
+template <bool LDS_ONLY, class K>
+__device__ __forceinline__ float first_zero_max(K key, K* zred) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const K o = __shfl_xor(key, off, 64);
+        key = o < key ? o : key;
+    }
+    if ((threadIdx.x & 63) == 0) zred[threadIdx.x / 64] = key;
+    red_barrier<LDS_ONLY>();
+    K k = zred[0];
+#pragma unroll
+    for (int i = 1; i < kRowWaves; i++) k = zred[i] < k ? zred[i] : k;
+    red_barrier<LDS_ONLY>();
+    return (k & 1) ? -0.0f : 0.0f;
 }
 
 }  // namespace rac

@@ -556,7 +556,72 @@ def test_softmax_special_rows(iters, cols):
         xm = x[r] - np.max(x[r])                      # float32 subtraction, as the kernel
         e = rl.orc_unary("orc_exp_batch", xm, iters).astype(np.float64)
         assert rl.max_rel(got[r], e / e.sum(), 1e-37) <= 1e-5, r
+    # bit for bit against the checker's lane-order model: the rows whose
+    # x - max falls below -86 (-inf entries, offsets of -200, -1e30, -2e9)
+    # take the ldexp-and-flush scale, the others the exponent-field one, and
+    # NaN or an infinite maximum makes the whole row NaN
+    lanes = rl.orc_softmax_lanes(x, iters)
+    assert np.array_equal(np.isnan(got), np.isnan(lanes))
+    fin = ~np.isnan(lanes)
+    assert np.array_equal(got[fin], lanes[fin])
 
+
+
+def _zero_max_rows(rows, cols, seed):
+    """Rows of negative values whose maximum is a zero of mixed signs:
+    first zero -0 or +0, all -0, a random sign per element (a zero query
+    row's scores), the first zero in another lane's group than a later
+    one; plus rows whose maximum is not zero."""
+    x = -np.abs(rl.gen_normal((rows, cols), seed, std=2.0)) - np.float32(0.001)
+    z = np.float32(0.0)
+    nz = np.float32(-0.0)
+    plant = [
+        lambda r: (r.__setitem__(10, nz), r.__setitem__(cols // 2, z)),
+        lambda r: (r.__setitem__(10, z), r.__setitem__(cols // 2, nz)),
+        lambda r: r.__setitem__(slice(None), nz),
+        lambda r: (r.__setitem__(slice(None), z), r.__setitem__(0, nz)),
+        lambda r: r.__setitem__(slice(None), np.where(rl.gen_uniform((cols,), seed + 1) < 0, nz, z)),
+        lambda r: (r.__setitem__(min(12, cols - 1), z), r.__setitem__(min(1025, cols - 1), nz)),
+        lambda r: (r.__setitem__(min(12, cols - 1), nz), r.__setitem__(min(1025, cols - 1), z)),
+        lambda r: None,
+    ]
+    for i in range(rows):
+        plant[i % len(plant)](x[i])
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("iters", [8, 16, 24, 5])
+@pytest.mark.parametrize("cols", [4096, 1000, 20000])
+def test_softmax_zero_max_takes_first_zero_sign(iters, cols):
+    """A zero row maximum carries the sign of the row's first zero, as the
+    reference's scan leaves it (rac_cpu.c:258-262: m = x[0], replaced only by
+    a strictly greater value); x - max is then +0 or -0 exactly as there,
+    which the CORDIC exp's first direction sees.  Bit-exact with the
+    checker's lane-order model on the register path (4096 columns, the lean
+    unmasked form; 1000, a ragged row), the strided loop (20000) and the
+    run-time step count (n = 5)."""
+    x = _zero_max_rows(16, cols, 57)
+    got = H(ext().softmax(T(x), iters=iters))
+    ref = rl.orc_softmax_lanes(x, iters)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_softmax_zero_max_prefetch_and_masked_paths():
+    """The same rows through the persistent prefetching kernel (n = 8,
+    enough rows for it) and the masked attention softmax (additive mask of
+    -0: x + -0 keeps each zero's sign)."""
+    x = _zero_max_rows(3072, 4096, 61)
+    got = H(ext().softmax(T(x), iters=8))
+    ref = rl.orc_softmax_lanes(x, 8)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    Tn = 256
+    xs = _zero_max_rows(Tn, Tn, 63)
+    mask = np.full((Tn, Tn), -0.0, np.float32)
+    for iters in (8, 16):
+        sc = T(xs)
+        ext().softmax_masked_(sc, T(mask), False, iters=iters)
+        ref = rl.orc_softmax_lanes(xs, iters, mask=mask)
+        assert np.array_equal(H(sc).view(np.uint32), ref.view(np.uint32))
 
 def test_softmax_vs_libm_reference_reported():
     d = np.load(os.path.join(rl.GOLDEN, "softmax.npz"))
