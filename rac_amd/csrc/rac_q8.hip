@@ -115,8 +115,9 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) uint8_t sw[R * kRowLds];
     __shared__ float sx[MX][CB * kQ8XPad];
-    __shared__ float sdot[MX][R][CB + 1];
-    __shared__ float sd[R][CB + 1];
+    constexpr int kTermLd = CB + 4;                                    // 16-byte rows: the fold reads float4
+    __shared__ __attribute__((aligned(16))) float sdot[MX][R][kTermLd];
+    __shared__ __attribute__((aligned(16))) float sd[R][kTermLd];
 
     const int tid = threadIdx.x;
     const long j0 = (long)blockIdx.x * R;
@@ -247,16 +248,23 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
         if (tid < MX * R) {
             const int m = tid / R, r = tid % R;
             if (m < M && r < nrows) {
+                // 16 terms per LDS round trip (float4 reads of both rows)
+                constexpr int kB = CB < 16 ? CB : 16;
 #pragma unroll
-                for (int kk = 0; kk < CB; kk += 8) {
-                    float dv[8], tv[8];
+                for (int kk = 0; kk < CB; kk += kB) {
+                    float4 dv[kB / 4], tv[kB / 4];
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        dv[u] = sd[r][kk + u];
-                        tv[u] = sdot[m][r][kk + u];
+                    for (int u = 0; u < kB / 4; u++) {
+                        dv[u] = *reinterpret_cast<const float4*>(&sd[r][kk + 4 * u]);
+                        tv[u] = *reinterpret_cast<const float4*>(&sdot[m][r][kk + 4 * u]);
                     }
 #pragma unroll
-                    for (int u = 0; u < 8; u++) acc = __builtin_fmaf(dv[u], tv[u], acc);
+                    for (int u = 0; u < kB / 4; u++) {
+                        acc = __builtin_fmaf(dv[u].x, tv[u].x, acc);
+                        acc = __builtin_fmaf(dv[u].y, tv[u].y, acc);
+                        acc = __builtin_fmaf(dv[u].z, tv[u].z, acc);
+                        acc = __builtin_fmaf(dv[u].w, tv[u].w, acc);
+                    }
                 }
             }
         }
