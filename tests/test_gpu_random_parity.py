@@ -1,0 +1,247 @@
+"""Randomized parity sweep: the HIP library against the CPU checker on random
+shapes, layouts, MAC modes, step counts and special values (NaN, +-inf,
+signed zeros, subnormals, tiny and huge operands), with fixed seeds and a
+fixed number of cases per operation.
+
+Each case is bit-exact with the checker (NaN matched by position), except the
+Q8_0 GEMV's GELU and SiLU epilogues, which use the device's erff / expf
+(within 1e-6 relative, as in test_gpu_q8.py).  The case generators draw:
+- matmul: M, N, K in [1, 300), all four layouts, FAST / CORDIC / SHIFTADD,
+  step counts 1..24, alpha and beta (with C accumulated), skinny shapes, and
+  in CORDIC mode A operands outside the strength-reduced chain's range;
+- batched matmul: 1..5 items with transposes and beta;
+- softmax: 1..40 rows of 1..20000 columns (multiples of 4 and not), scales up
+  to 60, special values, zero-maximum rows with signed zeros;
+- softmax over enough rows for the persistent kernel (n <= 8);
+- the masked attention softmax (causal, additive masks with -inf);
+- RMSNorm and LayerNorm with and without gamma / beta;
+- exp, SiLU, sigmoid and tanh on odd lengths and unaligned offsets;
+- RoPE on random [B, H, T, D];
+- the Q8_0 GEMV with 1..8 input rows, every activation, with and without
+  bias;
+- the attention core (three MAC modes, masks, causal, scaled inputs).
+"""
+import numpy as np
+import pytest
+
+import raclib as rl
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+SPECIAL = np.array([0.0, -0.0, np.nan, np.inf, -np.inf, 1e-40, -1e-40, 1e-33, 3e38, -3e38, 1e-38,
+                    2.0 ** -110], np.float32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    import rac_amd
+    rac_amd.load()
+    yield
+    torch.cuda.synchronize()
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def H(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def ext():
+    from rac_amd import ext as e
+    return e
+
+
+def lib():
+    import rac_amd
+    return rac_amd.load()
+
+
+def sprinkle(rng, a, frac):
+    n = max(1, int(a.size * frac))
+    a.reshape(-1)[rng.integers(0, a.size, n)] = rng.choice(SPECIAL, n)
+    return a
+
+
+def same(got, ref):
+    return np.array_equal(got, ref, equal_nan=True)
+
+
+def case_gemm(rng, seed):
+    skinny = rng.random() < 0.3
+    M = int(rng.integers(1, 17)) if skinny and rng.random() < 0.5 else int(rng.integers(1, 300))
+    N = int(rng.integers(1, 17)) if skinny and M > 16 else int(rng.integers(1, 300))
+    K = int(rng.integers(1, 300))
+    ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+    mode = int(rng.integers(0, 3))
+    iters = int(rng.choice([1, 5, 8, 16, 24, int(rng.integers(1, 25))]))
+    alpha = float(np.float32(rng.choice([1.0, rng.normal()])))
+    beta = float(np.float32(rng.choice([0.0, 0.0, rng.normal()])))
+    A = rng.uniform(-2, 2, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-2, 2, (N, K) if tb else (K, N)).astype(np.float32)
+    if mode == 1 and rng.random() < 0.2:
+        sprinkle(rng, A, 0.01)
+    C0 = rng.normal(size=(M, N)).astype(np.float32)
+    print(f"matmul seed={seed} M={M} N={N} K={K} ta={ta} tb={tb} mode={mode} n={iters}", flush=True)
+    Ad, Bd, Cd = T(A), T(B), T(C0)
+    rc = lib().rac_gemm_dev(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, ta, tb, alpha, beta, iters,
+                            mode, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    assert same(H(Cd), rl.orc_matmul(A, B, M, N, K, iters, mode, ta, tb, alpha, beta, C0)), seed
+
+
+def case_bmm(rng, seed):
+    Z = int(rng.integers(1, 6))
+    M, N, K = (int(rng.integers(1, 150)) for _ in range(3))
+    ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    mode = int(rng.integers(0, 3))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    alpha = float(np.float32(rng.normal()))
+    beta = float(np.float32(rng.choice([0.0, rng.normal()])))
+    A = rng.normal(size=(Z, K, M) if ta else (Z, M, K)).astype(np.float32)
+    B = rng.normal(size=(Z, N, K) if tb else (Z, K, N)).astype(np.float32)
+    C0 = rng.normal(size=(Z, M, N)).astype(np.float32)
+    print(f"bmm seed={seed} Z={Z} M={M} N={N} K={K} ta={ta} tb={tb} mode={mode} n={iters}", flush=True)
+    out = T(C0)
+    ext().bmm(T(A), T(B), ta, tb, alpha, iters, mode, out=out, beta=beta)
+    got = H(out)
+    for z in range(Z):
+        assert same(got[z], rl.orc_matmul(A[z], B[z], M, N, K, iters, mode, int(ta), int(tb), alpha, beta,
+                                          C0[z])), (seed, z)
+
+
+def case_softmax(rng, seed):
+    rows = int(rng.integers(1, 40))
+    cols = int(rng.choice([4096, 1024, 2048, 8192, 16384, int(rng.integers(1, 20000)),
+                           int(rng.integers(1, 300)) * 4]))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    x = (rng.normal(size=(rows, cols)) * float(rng.choice([0.5, 2.0, 10.0, 60.0]))).astype(np.float32)
+    if rng.random() < 0.3:
+        sprinkle(rng, x, 0.001)
+    if rng.random() < 0.2:
+        x[0] = -np.abs(x[0])
+        x[0, int(rng.integers(0, cols))] = rng.choice([0.0, -0.0])
+    print(f"softmax seed={seed} rows={rows} cols={cols} n={iters}", flush=True)
+    assert same(H(ext().softmax(T(x), iters=iters)), rl.orc_softmax_lanes(x, iters)), seed
+
+
+def case_softmax_persistent(rng, seed):
+    rows = int(rng.choice([3072, 4000, 5000]))
+    cols = int(rng.choice([1024, 2048, 4096]))
+    iters = int(rng.choice([8, 5, 1]))
+    x = (rng.normal(size=(rows, cols)) * 2).astype(np.float32)
+    if rng.random() < 0.5:
+        sprinkle(rng, x, 0.0001)
+    print(f"softmax persistent seed={seed} rows={rows} cols={cols} n={iters}", flush=True)
+    assert same(H(ext().softmax(T(x), iters=iters)), rl.orc_softmax_lanes(x, iters)), seed
+
+
+def case_masked(rng, seed):
+    Tn, Zb = int(rng.integers(1, 300)), int(rng.integers(1, 4))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    causal, use_mask = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    x = (rng.normal(size=(Zb, Tn, Tn)) * 3).astype(np.float32)
+    mask = None
+    if use_mask:
+        mask = rng.normal(size=(Tn, Tn)).astype(np.float32)
+        if rng.random() < 0.5:
+            mask[rng.random((Tn, Tn)) < 0.3] = -np.inf
+    print(f"masked softmax seed={seed} T={Tn} Z={Zb} causal={causal} mask={use_mask} n={iters}", flush=True)
+    xd = T(x)
+    ext().softmax_masked_(xd, T(mask) if mask is not None else None, causal, iters)
+    ref = rl.orc_softmax_lanes(x.reshape(-1, Tn), iters, causal=causal, mask=mask, zero_guard=True)
+    assert same(H(xd), ref.reshape(x.shape)), seed
+
+
+def case_norms(rng, seed):
+    rows = int(rng.integers(1, 30))
+    d = int(rng.choice([4096, 1024, 11008, int(rng.integers(1, 20000)), int(rng.integers(1, 500)) * 4]))
+    x = (rng.normal(size=(rows, d)) * float(rng.choice([1.0, 1e-3, 1e3]))).astype(np.float32)
+    if rng.random() < 0.2:
+        sprinkle(rng, x, 0.001)
+    g = rng.normal(1, 0.02, d).astype(np.float32) if rng.random() < 0.8 else None
+    b = rng.normal(0, 0.1, d).astype(np.float32) if rng.random() < 0.8 else None
+    eps = float(np.float32(rng.choice([1e-6, 1e-5])))
+    print(f"norms seed={seed} rows={rows} d={d} gamma={g is not None} beta={b is not None}", flush=True)
+    e = ext()
+    assert same(H(e.rmsnorm(T(x), T(g) if g is not None else None, eps)), rl.orc_rmsnorm_lanes(x, g, eps)), seed
+    got = H(e.layernorm(T(x), T(g) if g is not None else None, T(b) if b is not None else None, eps))
+    assert same(got, rl.orc_layernorm_lanes(x, g, b, eps)), seed
+
+
+def case_activations(rng, seed):
+    n = int(rng.choice([int(rng.integers(1, 5000)), int(rng.integers(1, 300000))]))
+    off = int(rng.integers(0, 4))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    x = (rng.normal(size=n + off) * float(rng.choice([1.0, 4.0, 30.0]))).astype(np.float32)
+    if rng.random() < 0.5:
+        sprinkle(rng, x, 0.01)
+    print(f"activations seed={seed} n={n} offset={off} n_iters={iters}", flush=True)
+    xd = T(x)[off:]
+    for name, oname in (("exp", "orc_exp_batch"), ("silu", "orc_silu"), ("sigmoid", "orc_sigmoid"),
+                        ("tanh", "orc_tanh")):
+        assert same(H(getattr(ext(), name)(xd, iters=iters)), rl.orc_unary(oname, x[off:], iters)), (seed, name)
+
+
+def case_rope(rng, seed):
+    B, Hh, Tt = int(rng.integers(1, 4)), int(rng.integers(1, 6)), int(rng.integers(1, 300))
+    D = 2 * int(rng.integers(1, 96))
+    x = rng.normal(size=(B, Hh, Tt, D)).astype(np.float32)
+    print(f"rope seed={seed} B={B} H={Hh} T={Tt} D={D}", flush=True)
+    c, s = rl.orc_rope_cache(Tt, D)
+    xd = T(x)
+    ext().rope_apply_(xd, T(c), T(s))
+    assert same(H(xd), rl.orc_rope_apply(x, c, s)), seed
+
+
+def case_q8(rng, seed):
+    M, N = int(rng.integers(1, 9)), int(rng.integers(1, 3000))
+    K = 32 * int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(1, 40))]))
+    act = int(rng.integers(0, 4))
+    wq = rl.orc_q8_quantize(rng.normal(size=(N, K)).astype(np.float32))
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    bias = rng.normal(size=N).astype(np.float32) if rng.random() < 0.5 else None
+    print(f"q8 gemv seed={seed} M={M} N={N} K={K} act={act} bias={bias is not None}", flush=True)
+    got = H(ext().q8_gemv(T(x), T(wq), T(bias) if bias is not None else None, act))
+    ref = rl.orc_q8_gemv(x, wq, bias, act)
+    if act in (0, 1):
+        assert same(got, ref), seed
+    else:
+        assert np.all(np.abs(got - ref) <= 1e-6 * (np.abs(ref) + 1.0)), seed
+
+
+def case_attention(rng, seed):
+    B, Hh, Tn = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.integers(1, 200))
+    D = int(rng.choice([16, 32, 64, 128, int(rng.integers(1, 129))]))
+    causal = bool(rng.integers(0, 2))
+    iters, mode = int(rng.choice([8, 16, 24])), int(rng.integers(0, 3))
+    scale = float(rng.choice([1.0, 4.0]))
+    q, k, v = ((rng.normal(size=(B, Hh, Tn, D)) * scale).astype(np.float32) for _ in range(3))
+    mask = rng.normal(size=(Tn, Tn)).astype(np.float32) if rng.random() < 0.3 else None
+    print(f"attention seed={seed} B={B} H={Hh} T={Tn} D={D} causal={causal} mask={mask is not None} n={iters} "
+          f"mode={mode} scale={scale}", flush=True)
+    got = H(ext().attention(T(q), T(k), T(v), T(mask) if mask is not None else None, causal, iters, mode))
+    assert same(got, rl.orc_attention_lanes(q, k, v, mask, causal, iters, mode)), seed
+
+
+CASES = {
+    "matmul": (case_gemm, 300), "bmm": (case_bmm, 200), "softmax": (case_softmax, 200),
+    "softmax_persistent": (case_softmax_persistent, 16), "masked_softmax": (case_masked, 300),
+    "norms": (case_norms, 300), "activations": (case_activations, 120), "rope": (case_rope, 300),
+    "q8_gemv": (case_q8, 40), "attention": (case_attention, 200),
+}
+
+
+@pytest.mark.parametrize("op", list(CASES))
+def test_random_parity(op):
+    fn, n = CASES[op]
+    base = 7919 * (list(CASES).index(op) + 1)
+    for i in range(n):
+        seed = base + i
+        fn(np.random.default_rng(seed), seed)
