@@ -19,7 +19,12 @@ Q8_0 GEMV's GELU and SiLU epilogues, which use the device's erff / expf
 - RoPE on random [B, H, T, D];
 - the Q8_0 GEMV with 1..8 input rows, every activation, with and without
   bias;
-- the attention core (three MAC modes, masks, causal, scaled inputs).
+- the attention core (three MAC modes, masks, causal, scaled inputs);
+- the fused linear (bias, the four activations, every MAC mode), whose
+  GELU is bounded as in test_gpu_fused_linear.py;
+- the synchronous rac.h entry points on host buffers (matmul, batched
+  softmax, RMSNorm, LayerNorm, SiLU, RoPE) in a random sequence of sizes,
+  which grows and reuses the cached staging buffers.
 """
 import numpy as np
 import pytest
@@ -230,11 +235,103 @@ def case_attention(rng, seed):
     assert same(got, rl.orc_attention_lanes(q, k, v, mask, causal, iters, mode)), seed
 
 
+def _act_ref(x, act, iters):
+    if act == 0:
+        return x
+    if act == 1:
+        return np.where(x > 0, x, np.float32(0)).astype(np.float32)
+    if act == 2:
+        return rl.orc_unary("orc_gelu", x)
+    return rl.orc_unary("orc_silu", x, iters)
+
+
+def case_fused_linear(rng, seed):
+    M, N, K = int(rng.integers(1, 200)), int(rng.integers(1, 200)), int(rng.integers(1, 200))
+    act, mode = int(rng.integers(0, 4)), int(rng.integers(0, 3))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = (rng.normal(size=(N, K)) * 0.2).astype(np.float32)
+    b = rng.normal(size=N).astype(np.float32) if rng.random() < 0.6 else np.zeros(0, np.float32)
+    print(f"fused linear seed={seed} M={M} N={N} K={K} act={act} mode={mode} n={iters} bias={b.size > 0}",
+          flush=True)
+    out, pre = ext().fused_linear_forward(T(x), T(w), T(b), act, iters=iters, mode=mode, return_pre=True)
+    out, pre = H(out), H(pre)
+    ref_pre = rl.orc_matmul(x, w, M, N, K, iters, mode, tb=1)
+    if b.size:
+        ref_pre = (ref_pre + b[None, :]).astype(np.float32)
+    assert same(pre, ref_pre), seed
+    ref = _act_ref(ref_pre, act, iters)
+    if act == 2:
+        # device erff against glibc's (as test_gpu_fused_linear.py bounds it)
+        assert np.all(np.abs(out - ref) <= 2e-6 * np.abs(ref) + 2.4e-7 * np.abs(ref_pre) + 1e-7), seed
+    else:
+        assert same(out, ref), seed
+
+
+def case_rac_h(rng, seed):
+    """The synchronous rac.h entry points on host buffers, in a random
+    sequence of sizes (the staging buffers are cached, grown and reused)."""
+    L = lib()
+    op = str(rng.choice(["matmul", "softmax", "rmsnorm", "layernorm", "silu", "rope"]))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    L.rac_set_cordic_iters(iters)
+    L.rac_clear_error()
+    if op == "matmul":
+        M, N, K = (int(rng.integers(1, 256)) for _ in range(3))
+        mode = int(rng.integers(0, 3))
+        L.rac_set_cordic_mode(mode)
+        A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        C = np.zeros((M, N), np.float32)
+        print(f"rac.h matmul seed={seed} M={M} N={N} K={K} mode={mode} n={iters}", flush=True)
+        L.rac_matmul(rl.p(A), rl.p(B), rl.p(C), M, N, K)
+        ref = rl.orc_matmul(A, B, M, N, K, iters, mode)
+    elif op == "softmax":
+        rows, n = int(rng.integers(1, 64)), int(rng.integers(1, 5000))
+        x = (rng.normal(size=(rows, n)) * 2).astype(np.float32)
+        C = np.zeros_like(x)
+        print(f"rac.h softmax_batch seed={seed} rows={rows} n={n} iters={iters}", flush=True)
+        L.rac_softmax_batch(rl.p(x), rl.p(C), rows, n)
+        ref = rl.orc_softmax_lanes(x, iters)
+    elif op in ("rmsnorm", "layernorm"):
+        rows, d = int(rng.integers(1, 32)), int(rng.integers(1, 6000))
+        x = rng.normal(size=(rows, d)).astype(np.float32)
+        g = rng.normal(1, 0.02, d).astype(np.float32) if rng.random() < 0.7 else None
+        bt = rng.normal(0, 0.1, d).astype(np.float32) if rng.random() < 0.7 else None
+        C = np.zeros_like(x)
+        print(f"rac.h {op} seed={seed} rows={rows} d={d}", flush=True)
+        gp = rl.p(g) if g is not None else None
+        if op == "rmsnorm":
+            L.rac_rmsnorm(rl.p(x), rl.p(C), gp, 1e-6, rows, d)
+            ref = rl.orc_rmsnorm_lanes(x, g, np.float32(1e-6))
+        else:
+            L.rac_layernorm(rl.p(x), rl.p(C), gp, rl.p(bt) if bt is not None else None, 1e-5, rows, d)
+            ref = rl.orc_layernorm_lanes(x, g, bt, np.float32(1e-5))
+    elif op == "silu":
+        n = int(rng.integers(1, 200000))
+        x = (rng.normal(size=n) * 4).astype(np.float32)
+        C = np.zeros_like(x)
+        print(f"rac.h silu seed={seed} n={n} iters={iters}", flush=True)
+        L.rac_silu(rl.p(x), rl.p(C), n)
+        ref = rl.orc_unary("orc_silu", x, iters)
+    else:
+        B, Hh, Tt, D = int(rng.integers(1, 3)), int(rng.integers(1, 5)), int(rng.integers(1, 130)), \
+            2 * int(rng.integers(1, 64))
+        C = rng.normal(size=(B, Hh, Tt, D)).astype(np.float32)
+        c, s = rl.orc_rope_cache(Tt, D)
+        ref = rl.orc_rope_apply(C, c, s)
+        print(f"rac.h rope_apply seed={seed} B={B} H={Hh} T={Tt} D={D}", flush=True)
+        L.rac_rope_apply(rl.p(C), rl.p(c), rl.p(s), B, Hh, Tt, D)
+    assert L.rac_last_error() == b"", (seed, L.rac_last_error())
+    assert same(C, ref), (seed, op)
+
+
 CASES = {
     "matmul": (case_gemm, 300), "bmm": (case_bmm, 200), "softmax": (case_softmax, 200),
     "softmax_persistent": (case_softmax_persistent, 16), "masked_softmax": (case_masked, 300),
     "norms": (case_norms, 300), "activations": (case_activations, 120), "rope": (case_rope, 300),
     "q8_gemv": (case_q8, 40), "attention": (case_attention, 200),
+    "fused_linear": (case_fused_linear, 150), "rac_h_host_buffers": (case_rac_h, 200),
 }
 
 
@@ -242,6 +339,13 @@ CASES = {
 def test_random_parity(op):
     fn, n = CASES[op]
     base = 7919 * (list(CASES).index(op) + 1)
-    for i in range(n):
-        seed = base + i
-        fn(np.random.default_rng(seed), seed)
+    L = lib()
+    iters, mode = L.rac_get_cordic_iters(), L.rac_get_cordic_mode()
+    try:
+        for i in range(n):
+            seed = base + i
+            fn(np.random.default_rng(seed), seed)
+    finally:
+        # the rac.h cases set the process-wide knobs
+        L.rac_set_cordic_iters(iters)
+        L.rac_set_cordic_mode(mode)
