@@ -22,6 +22,9 @@ Q8_0 GEMV's GELU and SiLU epilogues, which use the device's erff / expf
 - the attention core (three MAC modes, masks, causal, scaled inputs);
 - the fused linear (bias, the four activations, every MAC mode), whose
   GELU is bounded as in test_gpu_fused_linear.py;
+- matmul_backward (each need_grad combination) and linear_backward, the
+  bias gradient (torch's column sum, as the reference takes it) within
+  1e-5 of the float64 sum;
 - the synchronous rac.h entry points on host buffers (matmul, batched
   softmax, RMSNorm, LayerNorm, SiLU, RoPE) in a random sequence of sizes,
   which grows and reuses the cached staging buffers.
@@ -326,12 +329,39 @@ def case_rac_h(rng, seed):
     assert same(C, ref), (seed, op)
 
 
+def case_backward(rng, seed):
+    M, N, K = int(rng.integers(1, 200)), int(rng.integers(1, 200)), int(rng.integers(1, 200))
+    mode = int(rng.integers(0, 3))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    need_a, need_b = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    A = rng.normal(size=(M, K)).astype(np.float32)
+    B = rng.normal(size=(K, N)).astype(np.float32)
+    G = rng.normal(size=(M, N)).astype(np.float32)
+    print(f"backward seed={seed} M={M} N={N} K={K} mode={mode} n={iters} need=({need_a},{need_b})", flush=True)
+    e = ext()
+    gA, gB = e.matmul_backward(T(G), T(A), T(B), need_a, need_b, iters=iters, mode=mode)
+    assert (gA is None) != need_a and (gB is None) != need_b, seed
+    if need_a:
+        assert same(H(gA), rl.orc_matmul(G, B, M, K, N, iters, mode, tb=1)), seed
+    if need_b:
+        assert same(H(gB), rl.orc_matmul(A, G, K, N, M, iters, mode, ta=1)), seed
+    # linear: input [M, K], weight [N, K], grad_output [M, N]
+    W = rng.normal(size=(N, K)).astype(np.float32)
+    gi, gw, gb = e.linear_backward(T(G), T(A), T(W), True, iters=iters, mode=mode)
+    assert same(H(gi), rl.orc_matmul(G, W, M, K, N, iters, mode)), seed
+    assert same(H(gw), rl.orc_matmul(G, A, N, K, M, iters, mode, ta=1)), seed
+    # the bias gradient is torch's column sum, as in the reference
+    ref_b = G.astype(np.float64).sum(0)
+    assert np.all(np.abs(H(gb) - ref_b) <= 1e-5 * np.abs(G).sum(0) + 1e-7), seed
+
+
 CASES = {
     "matmul": (case_gemm, 300), "bmm": (case_bmm, 200), "softmax": (case_softmax, 200),
     "softmax_persistent": (case_softmax_persistent, 16), "masked_softmax": (case_masked, 300),
     "norms": (case_norms, 300), "activations": (case_activations, 120), "rope": (case_rope, 300),
     "q8_gemv": (case_q8, 40), "attention": (case_attention, 200),
     "fused_linear": (case_fused_linear, 150), "rac_h_host_buffers": (case_rac_h, 200),
+    "backward": (case_backward, 150),
 }
 
 
