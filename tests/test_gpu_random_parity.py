@@ -27,7 +27,13 @@ Q8_0 GEMV's GELU and SiLU epilogues, which use the device's erff / expf
   1e-5 of the float64 sum;
 - the synchronous rac.h entry points on host buffers (matmul, batched
   softmax, RMSNorm, LayerNorm, SiLU, RoPE) in a random sequence of sizes,
-  which grows and reuses the cached staging buffers.
+  which grows and reuses the cached staging buffers;
+- RoPE on [B, T, H, D] storage (strided views, in place and out of place),
+  the RoPE table with random bases, sin/cos and rsqrt, the exact vector
+  primitives, attention returning its probabilities;
+- matmuls up to 2048^3 (sampled entries, tile and matrix edges included),
+  rows of 16385..120000 columns (the loop kernels) and Q8_0 GEMVs of up to
+  60 M weights.
 """
 import numpy as np
 import pytest
@@ -355,13 +361,124 @@ def case_backward(rng, seed):
     assert np.all(np.abs(H(gb) - ref_b) <= 1e-5 * np.abs(G).sum(0) + 1e-7), seed
 
 
+def case_rope_strided(rng, seed):
+    B, Hh, Tt = int(rng.integers(1, 4)), int(rng.integers(1, 9)), int(rng.integers(1, 400))
+    D = 2 * int(rng.integers(1, 80))
+    x = rng.normal(size=(B, Hh, Tt, D)).astype(np.float32)
+    print(f"rope strided seed={seed} B={B} H={Hh} T={Tt} D={D}", flush=True)
+    c, s = rl.orc_rope_cache(Tt, D)
+    ref = rl.orc_rope_apply(x, c, s)
+    view = T(np.ascontiguousarray(x.transpose(0, 2, 1, 3))).transpose(1, 2)     # [B, T, H, D] storage
+    assert same(H(ext().rope_apply(view, T(c), T(s))), ref), seed
+    ext().rope_apply_(view, T(c), T(s))
+    assert same(H(view), ref), seed
+
+
+def case_rope_cache(rng, seed):
+    ms, hd = int(rng.integers(1, 5000)), 2 * int(rng.integers(1, 100))
+    base = float(rng.choice([10000.0, 500000.0, 1e4 * rng.random() + 1.5]))
+    print(f"rope cache seed={seed} max_seq={ms} head_dim={hd} base={base}", flush=True)
+    c, s = ext().rope_cache(ms, hd, base, device=DEV)
+    rc, rs = rl.orc_rope_cache(ms, hd, base)
+    assert same(H(c), rc) and same(H(s), rs), seed
+
+
+def case_sincos_rsqrt(rng, seed):
+    n = int(rng.integers(1, 200000))
+    th = (rng.uniform(-1, 1, n) * float(rng.choice([3.2, 100.0, 16000.0]))).astype(np.float32)
+    print(f"sincos / rsqrt seed={seed} n={n}", flush=True)
+    s, c = ext().sincos(T(th))
+    so, co = np.zeros_like(th), np.zeros_like(th)
+    rl.oracle().orc_sincos_batch(rl.p(th), rl.p(so), rl.p(co), th.size)
+    assert same(H(s), so) and same(H(c), co), seed
+    x = (np.abs(rng.normal(size=n)) * float(rng.choice([1e-30, 1.0, 1e30]))).astype(np.float32)
+    ro = np.zeros_like(x)
+    rl.oracle().orc_rsqrt_batch(rl.p(x), rl.p(ro), x.size)
+    assert same(H(ext().rsqrt(T(x))), ro), seed
+
+
+def case_prims(rng, seed):
+    n = int(rng.integers(1, 50000))
+    name = str(rng.choice(["rotate", "rotate_raw", "polar", "complex_mul", "rotate_n"]))
+    a = rng.uniform(-50, 50, (n, 2)).astype(np.float32)
+    b = rng.uniform(-50, 50, (n, 2)).astype(np.float32)
+    th = rng.uniform(-3000, 3000, n).astype(np.float32)
+    _, _, nb, nt = rl.PRIM_OPS[name]
+    iarg = int(rng.integers(1, 31)) if name == "rotate_n" else 0
+    print(f"vector primitive {name} seed={seed} n={n} iters={iarg}", flush=True)
+    op = {"rotate_n": "rotate_precision"}.get(name, name)
+    got = H(ext().vec2(op, T(a), T(b) if nb else None, T(th) if nt else None, iarg))
+    assert same(got, rl.orc_prim(name, a, b if nb else None, th if nt else None, iarg)), seed
+
+
+def case_attention_probs(rng, seed):
+    B, Hh, Tn = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.integers(1, 160))
+    D = int(rng.choice([8, 32, 64, int(rng.integers(1, 100))]))
+    causal, iters, mode = bool(rng.integers(0, 2)), int(rng.choice([8, 16, 24])), int(rng.integers(0, 3))
+    q, k, v = (rng.normal(size=(B, Hh, Tn, D)).astype(np.float32) for _ in range(3))
+    mask = rng.normal(size=(Tn, Tn)).astype(np.float32) if rng.random() < 0.3 else None
+    print(f"attention with probabilities seed={seed} B={B} H={Hh} T={Tn} D={D} causal={causal} n={iters} "
+          f"mode={mode}", flush=True)
+    out, P = ext().attention(T(q), T(k), T(v), T(mask) if mask is not None else None, causal, iters, mode,
+                             return_probs=True)
+    assert same(H(out), rl.orc_attention_lanes(q, k, v, mask, causal, iters, mode)), seed
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    b, h = int(rng.integers(0, B)), int(rng.integers(0, Hh))
+    sc = rl.orc_matmul(q[b, h], k[b, h], Tn, Tn, D, iters, mode, tb=1, alpha=scale)
+    assert same(H(P)[b, h], rl.orc_softmax_lanes(sc, iters, causal=causal, mask=mask, zero_guard=True)), seed
+
+
+def case_big_matmul(rng, seed):
+    M, N, K = (int(rng.integers(256, 2049)) for _ in range(3))
+    ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+    mode, iters = int(rng.integers(0, 3)), int(rng.choice([8, 16, 24, 13]))
+    A = rng.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    print(f"large matmul seed={seed} M={M} N={N} K={K} ta={ta} tb={tb} mode={mode} n={iters}", flush=True)
+    Ad, Bd, Cd = T(A), T(B), torch.zeros((M, N), device=DEV)
+    rc = lib().rac_gemm_dev(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, ta, tb, 1.0, 0.0, iters, mode,
+                            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    rows = rng.integers(0, M, 400).astype(np.int32)
+    cols = rng.integers(0, N, 400).astype(np.int32)
+    rows[:8] = [0, M - 1, 63, 64, 127, 128, M // 2, M - 2]            # tile and matrix edges
+    cols[:8] = [0, N - 1, 63, 64, 127, 128, N // 2, N - 2]
+    assert same(H(Cd)[rows, cols], rl.orc_matmul_entries(A, B, M, N, K, iters, mode, rows, cols, ta, tb)), seed
+
+
+def case_long_rows(rng, seed):
+    rows, cols = int(rng.integers(1, 6)), int(rng.integers(16385, 120000))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    x = (rng.normal(size=(rows, cols)) * 3).astype(np.float32)
+    g = rng.normal(1, 0.02, cols).astype(np.float32)
+    b = rng.normal(0, 0.1, cols).astype(np.float32)
+    print(f"long rows seed={seed} rows={rows} cols={cols} n={iters}", flush=True)
+    e = ext()
+    assert same(H(e.softmax(T(x), iters=iters)), rl.orc_softmax_lanes(x, iters)), seed
+    assert same(H(e.rmsnorm(T(x), T(g), 1e-6)), rl.orc_rmsnorm_lanes(x, g, np.float32(1e-6))), seed
+    assert same(H(e.layernorm(T(x), T(g), T(b), 1e-5)), rl.orc_layernorm_lanes(x, g, b, np.float32(1e-5))), seed
+
+
+def case_big_q8(rng, seed):
+    K = int(rng.choice([2048, 4096, 5632, 8192, 11008]))
+    N = min(int(rng.integers(3000, 40000)), 60_000_000 // K)
+    act = int(rng.integers(0, 2))
+    wq = rl.orc_q8_quantize(rng.standard_normal((N, K), dtype=np.float32))
+    x = rng.normal(size=(1, K)).astype(np.float32)
+    print(f"large q8 gemv seed={seed} N={N} K={K} act={act}", flush=True)
+    assert same(H(ext().q8_gemv(T(x), T(wq), None, act)), rl.orc_q8_gemv(x, wq, None, act)), seed
+
+
 CASES = {
     "matmul": (case_gemm, 300), "bmm": (case_bmm, 200), "softmax": (case_softmax, 200),
     "softmax_persistent": (case_softmax_persistent, 16), "masked_softmax": (case_masked, 300),
     "norms": (case_norms, 300), "activations": (case_activations, 120), "rope": (case_rope, 300),
     "q8_gemv": (case_q8, 40), "attention": (case_attention, 200),
     "fused_linear": (case_fused_linear, 150), "rac_h_host_buffers": (case_rac_h, 200),
-    "backward": (case_backward, 150),
+    "backward": (case_backward, 150), "rope_strided": (case_rope_strided, 100),
+    "rope_cache": (case_rope_cache, 100), "sincos_rsqrt": (case_sincos_rsqrt, 60), "prims": (case_prims, 100),
+    "attention_probs": (case_attention_probs, 100), "large_matmul": (case_big_matmul, 12),
+    "long_rows": (case_long_rows, 12), "large_q8_gemv": (case_big_q8, 3),
 }
 
 
