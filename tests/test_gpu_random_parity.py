@@ -33,7 +33,9 @@ Q8_0 GEMV's GELU and SiLU epilogues, which use the device's erff / expf
   primitives, attention returning its probabilities;
 - matmuls up to 2048^3 (sampled entries, tile and matrix edges included),
   rows of 16385..120000 columns (the loop kernels) and Q8_0 GEMVs of up to
-  60 M weights.
+  60 M weights;
+- the RAC-DSP engine (every op, wide operand ranges) and its systolic
+  product, bit-exact (integer).
 """
 import numpy as np
 import pytest
@@ -469,6 +471,26 @@ def case_big_q8(rng, seed):
     assert same(H(ext().q8_gemv(T(x), T(wq), None, act)), rl.orc_q8_gemv(x, wq, None, act)), seed
 
 
+def case_dsp(rng, seed):
+    n = int(rng.integers(1, 100000))
+    op = int(rng.choice([0, 1, 2, 3, 6]))
+    span = int(rng.choice([20, 40, 62]))
+    x = rng.integers(-2 ** span, 2 ** span, n, dtype=np.int64)
+    y = rng.integers(-2 ** span, 2 ** span, n, dtype=np.int64)
+    z = rng.integers(-2 ** 63, 2 ** 63 - 1, n, dtype=np.int64)
+    print(f"rac-dsp eval seed={seed} op={op} n={n} span=2^{span}", flush=True)
+    got = ext().dsp_eval(op, T(x), T(z), T(y))
+    for a, b in zip(got, rl.orc_dsp_batch(op, x, y, z)):
+        assert np.array_equal(H(a), b), seed
+    N, K = int(rng.integers(1, 200)), int(rng.integers(1, 300))
+    W = rng.integers(-2 ** 63, 2 ** 63 - 1, (N, N), dtype=np.int64)
+    X = rng.integers(-2 ** 40, 2 ** 40, (K, N), dtype=np.int64)
+    ref = np.zeros((K, N), np.int64)
+    rl.oracle().orc_dsp_systolic(N, K, rl.p(W), rl.p(X), rl.p(ref))
+    print(f"rac-dsp systolic seed={seed} N={N} K={K}", flush=True)
+    assert np.array_equal(H(ext().dsp_systolic(T(W), T(X))), ref), seed
+
+
 CASES = {
     "matmul": (case_gemm, 300), "bmm": (case_bmm, 200), "softmax": (case_softmax, 200),
     "softmax_persistent": (case_softmax_persistent, 16), "masked_softmax": (case_masked, 300),
@@ -478,7 +500,7 @@ CASES = {
     "backward": (case_backward, 150), "rope_strided": (case_rope_strided, 100),
     "rope_cache": (case_rope_cache, 100), "sincos_rsqrt": (case_sincos_rsqrt, 60), "prims": (case_prims, 100),
     "attention_probs": (case_attention_probs, 100), "large_matmul": (case_big_matmul, 12),
-    "long_rows": (case_long_rows, 12), "large_q8_gemv": (case_big_q8, 3),
+    "long_rows": (case_long_rows, 12), "large_q8_gemv": (case_big_q8, 3), "rac_dsp": (case_dsp, 60),
 }
 
 
