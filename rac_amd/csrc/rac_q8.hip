@@ -227,9 +227,11 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
                 uint32_t d0[10];
 #pragma unroll
                 for (int t = 0; t < 10; t++) d0[t] = dw[t];
+                // the block's dwords: shifted down 16 bits when it starts 2
+                // bytes into its first dword (a shift of 0 returns d0[t])
                 uint32_t wd[9];
 #pragma unroll
-                for (int t = 0; t < 9; t++) wd[t] = (A & 2) ? __builtin_amdgcn_alignbit(d0[t + 1], d0[t], 16) : d0[t];
+                for (int t = 0; t < 9; t++) wd[t] = __builtin_amdgcn_alignbit(d0[t + 1], d0[t], (A & 2) * 8);
                 float qf[kQ8Block];
 #pragma unroll
                 for (int t = 0; t < kQ8Block; t++) qf[t] = (float)(int8_t)(wd[(2 + t) / 4] >> (8 * ((2 + t) % 4)));
