@@ -69,7 +69,7 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
 // weights.  The shape only decides which lane computes what; every output
 // is the same serial fold, so all shapes give identical bits.
 // One input row asks for 4 workgroups per CU (at most 128 VGPRs; the
-// kernel needs 119), several rows for 2.
+// kernel needs 123), several rows for 2.
 constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
 
 // Fusions of a decoder layer's decode step into the one-row GEMV:
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
                 float qf[kQ8Block];
 #pragma unroll
                 for (int t = 0; t < kQ8Block; t++) qf[t] = (float)(int8_t)(wd[(2 + t) / 4] >> (8 * ((2 + t) % 4)));
-                sd[r][k] = half_bits_to_float(wd[0] & 0xffffu);
+                sd[r][k] = half_bits_to_float_cvt(wd[0] & 0xffffu);
                 if constexpr (MX == 1) {
                     sdot[0][r][k] = q8_block_dot(qf, xr);
                 } else {

@@ -9,6 +9,20 @@ namespace rac {
 constexpr int kQ8Block = 32;
 constexpr int kQ8Bytes = 34;
 
+// The same value by the hardware conversion (v_cvt_f32_f16, fp16
+// denormals preserved): equal to half_bits_to_float for every zero,
+// subnormal, normal and infinite half; a signalling NaN comes back quiet.
+// For a GEMV block scale that difference cannot show, since the scale only
+// enters an fma, whose result is the same quiet NaN either way (the outputs
+// agree bit for bit over all 65536 patterns).  Code that stores the
+// converted value itself keeps half_bits_to_float.
+__device__ __forceinline__ float half_bits_to_float_cvt(uint32_t h) {
+    const uint16_t b = (uint16_t)h;
+    _Float16 v;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+
 // rac_fp16_to_fp32 (rac_q8_0.c:21-45) as bit operations.
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     const uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1fu;

@@ -112,6 +112,17 @@ def test_gemv_every_fp16_scale():
     ref = rl.orc_q8_gemv(x, wq, None, 0)[0]
     got = H(e.q8_gemv(T(x), T(wq), None, 0))
     assert np.array_equal(got, ref, equal_nan=True)
+    # the fast kernel decodes the scale by the hardware conversion, the
+    # generic kernel (weights not 16-byte aligned) by the bit operations of
+    # rac_fp16_to_fp32: their outputs agree bit for bit, NaN payloads included
+    buf = torch.empty(wq.size + 2, dtype=torch.uint8, device=DEV)
+    buf[2:] = T(wq.reshape(-1))
+    wmis = buf[2:].view(wq.shape)
+    assert wmis.data_ptr() % 16 == 2
+    for act in range(4):
+        fast = e.q8_gemv(T(x), T(wq), None, act).view(torch.int32)
+        gen = e.q8_gemv(T(x), wmis, None, act).view(torch.int32)
+        assert torch.equal(fast, gen), act
     K2 = 224                                      # K % 256 != 0: generic kernel
     ref2 = rl.orc_q8_gemv(x[:K2], np.ascontiguousarray(wq[:, :K2 // 32]), None, 0)[0]
     got2 = H(e.q8_gemv(T(x[:K2]), T(np.ascontiguousarray(wq[:, :K2 // 32])), None, 0))
