@@ -70,7 +70,11 @@ __device__ __forceinline__ float q8_finish(float acc, const float* bias, long j,
 // is the same serial fold, so all shapes give identical bits.
 // One input row asks for 4 workgroups per CU (at most 128 VGPRs; the
 // kernel needs 123), several rows for 2.
-constexpr int kQ8XPad = 33;                                 // x floats per block in LDS
+// A block's 32 x floats sit in LDS rows of 36 (16-byte rows): the dot
+// phase reads them with 8 ds_read_b128 at immediate offsets from one
+// address, and a lane's k-stride of 36 dwords keeps every 16-lane pass on
+// distinct banks.
+constexpr int kQ8XPad = 36;                                 // x floats per block in LDS
 
 // Fusions of a decoder layer's decode step into the one-row GEMV:
 //   NORM   x is replaced by rmsnorm(x) * gamma with the row kernel's
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
     constexpr int kRPT = R * CB / 256;                                // rows per lane in the dot phase
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     __shared__ __attribute__((aligned(16))) uint8_t sw[R * kRowLds];
-    __shared__ float sx[MX][CB * kQ8XPad];
+    __shared__ __attribute__((aligned(16))) float sx[MX][CB * kQ8XPad];
     constexpr int kTermLd = CB + 4;                                    // 16-byte rows: the fold reads float4
     __shared__ __attribute__((aligned(16))) float sdot[MX][R][kTermLd];
     __shared__ __attribute__((aligned(16))) float sd[R][kTermLd];
@@ -189,12 +193,14 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
             const int e = (tid + i * 256) * 4;
             if (kXF4 % 256 == 0 || e < kXF4 * 4) {
                 const int m = e / (CB * kQ8Block), q = e % (CB * kQ8Block);
-                float* dst = &sx[m][(q / kQ8Block) * kQ8XPad + q % kQ8Block];
+                // stored component by component: a whole-float4 copy of rx[i]
+                // sends the staging array to scratch memory
+                float4* dst = reinterpret_cast<float4*>(&sx[m][(q / kQ8Block) * kQ8XPad + q % kQ8Block]);
                 if constexpr (NORM) {
-                    dst[0] = rx[i].x * inv * rg[i].x; dst[1] = rx[i].y * inv * rg[i].y;
-                    dst[2] = rx[i].z * inv * rg[i].z; dst[3] = rx[i].w * inv * rg[i].w;
+                    *dst = make_float4(rx[i].x * inv * rg[i].x, rx[i].y * inv * rg[i].y,
+                                       rx[i].z * inv * rg[i].z, rx[i].w * inv * rg[i].w);
                 } else {
-                    dst[0] = rx[i].x; dst[1] = rx[i].y; dst[2] = rx[i].z; dst[3] = rx[i].w;
+                    *dst = make_float4(rx[i].x, rx[i].y, rx[i].z, rx[i].w);
                 }
             }
         }
@@ -217,7 +223,10 @@ __global__ __launch_bounds__(256, MX == 1 ? 4 : 2) void q8_gemv_kernel(const flo
             float xr[kQ8Block];
             if constexpr (MX == 1) {
 #pragma unroll
-                for (int i = 0; i < kQ8Block; i++) xr[i] = sx[0][k * kQ8XPad + i];
+                for (int i = 0; i < kQ8Block / 4; i++) {
+                    const float4 v = *reinterpret_cast<const float4*>(&sx[0][k * kQ8XPad + 4 * i]);
+                    xr[4 * i] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
+                }
             }
 #pragma unroll
             for (int i = 0; i < kRPT; i++) {
