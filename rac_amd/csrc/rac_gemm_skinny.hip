@@ -149,7 +149,7 @@ __device__ __forceinline__ void sk_terms(const float* sA, const float* sB, float
 // The serial fold of output (om, on) over kn k of a tile, in order: the
 // terms from sP row `prow` (SHARED), or computed here from sA row om (own
 // terms; FAST: the A element itself).  Zero k-padding leaves acc as is.
-template <int MODE, int NITER, int ROW, bool SHARED>
+template <int MODE, int NITER, int ROW, bool SHARED, bool RING>
 __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const float* sP, int om, int on,
                                          int prow, int kn, float acc, int iters, float kinv, bool lit) {
     if constexpr (!SHARED && MODE == kModeCordic) {
@@ -169,8 +169,50 @@ __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const
         }
         return acc;
     }
-    // unrolled so the LDS reads of 32 k run ahead of the dependent chain of
-    // FMAs (rolled, each 4-k step waited for its reads; 64 k ran no faster)
+    if constexpr (RING && (SHARED || MODE == kModeFast)) {
+        // Terms (or FAST's A elements) come from LDS, so the chain is fed by
+        // reads alone.  A full tile's fold is unrolled completely and its
+        // reads run D 4-k steps ahead of the FMAs through a ring of D
+        // register pairs: step j folds pair j and reads pair j + D, and a
+        // scheduling barrier after each step keeps that order (left to
+        // itself the scheduler read one step ahead and waited on LDS every
+        // 8 k; a dependent fmaf costs ~4.6 cycles on one wave).  2 D reads
+        // in flight stay within the 15 the LDS counter tracks.  RING is set
+        // where it measured faster (sk_block): FAST blocks of at most 64
+        // outputs in 256-k tiles or on grids of at most two workgroups per
+        // CU (the ring's VGPRs cost a wave per SIMD on wider ones), and the
+        // CORDIC pipeline's 64-output blocks.
+        constexpr int KT = ROW - 4, D = 6;
+        if (kn == KT) {
+            const float* rowb = &sB[on * ROW];
+            const float* rowt = SHARED ? &sP[prow * ROW] : &sA[om * ROW];
+            float4 rb[D], rt[D];
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                rb[j] = *reinterpret_cast<const float4*>(rowb + 4 * j);
+                rt[j] = *reinterpret_cast<const float4*>(rowt + 4 * j);
+            }
+#pragma unroll
+            for (int j = 0; j < KT / 4; j++) {
+                const float b[4] = {rb[j % D].x, rb[j % D].y, rb[j % D].z, rb[j % D].w};
+                const float t[4] = {rt[j % D].x, rt[j % D].y, rt[j % D].z, rt[j % D].w};
+                if (j + D < KT / 4) {
+                    rb[j % D] = *reinterpret_cast<const float4*>(rowb + 4 * (j + D));
+                    rt[j % D] = *reinterpret_cast<const float4*>(rowt + 4 * (j + D));
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if constexpr (MODE == kModeCordic) acc = __builtin_fmaf(t[e], __builtin_fabsf(b[e]), acc);
+                    else if constexpr (MODE == kModeShiftAdd) acc = acc + t[e];
+                    else acc = __builtin_fmaf(t[e], b[e], acc);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return acc;
+        }
+    }
+    // a partial tile (and own SHIFTADD terms): 4-k steps, unrolled so the
+    // LDS reads of 32 k run ahead of the dependent chain of FMAs
 #pragma unroll 8
     for (int kk = 0; kk < kn; kk += 4) {
         const float4 b4 = *reinterpret_cast<const float4*>(&sB[on * ROW + kk]);
@@ -236,7 +278,7 @@ struct SkBlock {
     }
 };
 
-template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool BIGK>
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool BIGK, bool RING>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
@@ -277,7 +319,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
         }
         if (tid == 0) lit[(t + 1) & 1] = 0;            // tile t+1's flag: set after the loop-top barrier
         if (owner)
-            acc = sk_fold<MODE, NITER, ROW, kShared>(sA, sB, sP, om, on, tid, min(KT, blk.kend - k0), acc, iters,
+            acc = sk_fold<MODE, NITER, ROW, kShared, RING>(sA, sB, sP, om, on, tid, min(KT, blk.kend - k0), acc, iters,
                                                      kinv, lit_tile);
     }
     if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
@@ -336,13 +378,14 @@ __global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
                                                             MODE == kModeCordic && lit[nxt] != 0);
         if (tid == 0) lit[cur] = 0;                      // tile t+2's flag (tile t's was read a phase ago)
         if (owner)
-            acc = sk_fold<MODE, NITER, ROW, true>(sA, sB[cur], sP[cur], om, on, tid, min(KT, blk.kend - k0), acc,
+            acc = sk_fold<MODE, NITER, ROW, true, (RB * CB == 64)>(sA, sB[cur], sP[cur], om, on, tid, min(KT, blk.kend - k0), acc,
                                                   iters, kinv, false);
     }
     if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE, bool BIGK = false>
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE, bool BIGK = false,
+          bool RING = (MODE == kModeFast && RB * CB <= 64 && !BIGK)>
 static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
     const unsigned wgs = FEWCOL ? (unsigned)((g.M + RB - 1) / RB) : (unsigned)((g.N + CB - 1) / CB);
     const dim3 grid(wgs, 1, (unsigned)g.batch);
@@ -351,7 +394,7 @@ static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
                            g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
                            g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
     } else {
-        hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, BIGK>), grid, dim3(256), 0, s,
+        hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, BIGK, RING>), grid, dim3(256), 0, s,
                            g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
                            g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
     }
@@ -361,17 +404,26 @@ static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
 // One output block shape (RB x CB): FAST takes 512-k tiles on small grids
 // (<= 64 outputs), CORDIC the pipelined terms (<= 64 outputs); SHIFTADD's
 // terms (a shift-add product each) outweigh its fold and keep all four
-// waves (pipelined on three: 1x4096x4096 213 -> 297 us).
+// waves (pipelined on three: 1x4096x4096 213 -> 297 us).  The read-ahead
+// fold (RING), measured against the looped one, bit-identical: FAST
+// 1x11008x4096 50.7 -> 43.8 us, 8x4096x4096 34.0 -> 32.0, 16x4096x4096
+// 38.6 -> 36.4, 2048x10x4096 55.2 -> 43.2; CORDIC n = 16 4x4096x4096 175.7
+// -> 158.3.  With 2.7 workgroups per CU its VGPRs cost a wave per SIMD
+// (FAST 16x11008x4096 77.7 -> 83.2 us), and one-row CORDIC and SHIFTADD
+// and FAST's 512-k tiles gained nothing (CORDIC 1x4096x4096 54.3 -> 55.1,
+// SHIFTADD 1x11008x4096 271.7 -> 279.7, FAST 1x4096x4096 32.1 -> 32.4 us),
+// so they keep the loop.
 template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
+    const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
     if constexpr (RB * CB <= 64) {
         if constexpr (MODE == kModeFast) {
-            const long cus = device_cus();
-            const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
-            if (wgs <= cus) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
+            if (wgs <= device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
         } else if constexpr (MODE == kModeCordic) {
             return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
         }
+    } else if constexpr (MODE == kModeFast) {
+        if (wgs <= 2 * device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, false, true>(g, s);
     }
     return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false>(g, s);
 }
