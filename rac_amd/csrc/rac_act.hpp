@@ -87,7 +87,9 @@ __device__ __forceinline__ void elt_vec(float* v, int iters, float khinv) {
                 mn = __builtin_fminf(mn, __builtin_fabsf(v[e]));
             }
             if (mx <= 44.0f && mn >= 0x1p-100f) {
-                exp_cordic_vec<NITER, E, kExpNoOvf>(a, khinv);
+#pragma unroll
+                for (int e = 0; e < E; e++) a[e] = v[e];   // exp of -v (kExpNegArg)
+                exp_cordic_vec<NITER, E, kExpNoOvf | kExpNegArg>(a, khinv);
 #pragma unroll
                 for (int e = 0; e < E; e++) v[e] = div_rn_normal(v[e], 1.0f + a[e]);
             } else {

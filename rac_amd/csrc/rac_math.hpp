@@ -331,7 +331,11 @@ struct HypStepV {
 //              k <= 0, so the overflow select (k > 127 -> inf) is dropped.
 //   kExpNoOvf  every argument is below 88 (k <= 127), so the overflow
 //              select is dropped; the rounding bias keeps its sign.
-constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4, kExpNoOvf = 8;
+//   kExpNegArg x holds v and the exp is of -v, with exp_reduce(-v)'s
+//              operands: copysign(0.5, -v) by one v_bitop3 (mask ? 0.5 :
+//              ~v) and -v as source modifiers of the two FMAs, instead of
+//              a v_xor that materialises -v (1 VALU per element fewer).
+constexpr int kExpNan = 1, kExpFlush = 2, kExpNonPos = 4, kExpNoOvf = 8, kExpNegArg = 16;
 constexpr int kExpFull = kExpNan | kExpFlush;
 
 template <int N, int E, int OPT = kExpFull>
@@ -344,6 +348,10 @@ __device__ __forceinline__ void exp_cordic_vec(float* x, float khinv) {
         if constexpr ((OPT & kExpNonPos) != 0) {
             k[e] = cvt_i32_sat(__builtin_fmaf(x[e], kInvLn2, -0.5f));
             z[e] = __builtin_fmaf(-(float)k[e], kLn2, x[e]);
+        } else if constexpr ((OPT & kExpNegArg) != 0) {
+            const float b = as_f(__builtin_amdgcn_bitop3_b32(0x7fffffffu, 0x3f000000u, as_u(x[e]), 0xC5));
+            k[e] = cvt_i32_sat(__builtin_fmaf(-x[e], kInvLn2, b));
+            z[e] = __builtin_fmaf(-(float)k[e], kLn2, -x[e]);
         } else {
             exp_reduce(x[e], k[e], z[e]);
         }
