@@ -33,17 +33,15 @@ namespace rac {
 // per workgroup (one per lane) each lane computes its own MACs' terms and
 // folds them at once ("own"); with fewer, every lane computes terms for the
 // tile into LDS and the lanes owning outputs fold them ("shared").  k per
-// tile keeps the workgroup's LDS under 64 KB.
-// BIGK (FAST, <= 64 outputs): 512-k tiles, taken when the grid has at most
-// one workgroup per CU, whose loads then need twice the bytes in flight
-// (1x4096x4096: 42 -> 31 us); with several workgroups per CU they overlap
-// each other's loads already and the smaller tile is faster (1x11008x4096:
-// 49 against 63 us).
-template <int MODE, int OUTS, bool BIGK = false>
+// tile keeps the workgroup's LDS under 64 KB.  (512-k FAST tiles on grids
+// of one workgroup per CU were faster with the looped fold, 42 -> 31 us at
+// 1x4096x4096; with the read-ahead fold the 256-k tile is: 32.2 -> 29.9 us,
+// 4096x1x4096 31.8 -> 29.3 us, bit-identical.)
+template <int MODE, int OUTS>
 struct SkCfg {
     static constexpr bool kShared = MODE != kModeFast && OUTS < 256;
     static constexpr bool kOwn = MODE != kModeFast && OUTS == 256;
-    static constexpr int kKT = MODE == kModeFast ? (BIGK ? 512 : 256)
+    static constexpr int kKT = MODE == kModeFast ? 256
                                : kOwn ? 128 : (OUTS == 16 ? 256 : (OUTS <= 64 ? 128 : 64));
     static constexpr int kRow = kKT + 4;        // LDS row stride (16 rows cover all banks)
 };
@@ -75,20 +73,23 @@ __device__ __forceinline__ void sk_cordic_terms(const float* a, const float* b, 
 }
 
 // Global -> registers: element (m0 + m, k) of A (row-major M x K) and
-// (k, n0 + n) of op(B) for the K-tile at k0, zero outside the matrices.
-template <int RB, int CB, int KT, bool TB>
+// (k, n0 + n) of op(B) for the K-tile at k0, zero outside the matrices,
+// spread over lanes L0 .. L0 + NL - 1 (the others return: with L0 = 64 the
+// folding wave 0 issues no loads).
+template <int RB, int CB, int KT, bool TB, int L0 = 0, int NL = 256>
 __device__ __forceinline__ void sk_load(const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                                         int K, long m0, long n0, int k0, float* ra, float* rb) {
-    const int tid = threadIdx.x;
+    if ((int)threadIdx.x < L0) return;
+    const int tid = (int)threadIdx.x - L0;
 #pragma unroll
-    for (int r = 0; r < (RB * KT + 255) / 256; r++) {
-        const int idx = tid + r * 256, kk = idx % KT;
+    for (int r = 0; r < (RB * KT + NL - 1) / NL; r++) {
+        const int idx = tid + r * NL, kk = idx % KT;
         const long gm = m0 + idx / KT, gk = (long)k0 + kk;
         ra[r] = (idx < RB * KT && gm < M && gk < K) ? A[gm * K + gk] : 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < (CB * KT + 255) / 256; r++) {
-        const int idx = tid + r * 256;
+    for (int r = 0; r < (CB * KT + NL - 1) / NL; r++) {
+        const int idx = tid + r * NL;
         int nn, kk;
         if constexpr (TB) { nn = idx / KT; kk = idx % KT; }      // W[n][k]: k contiguous
         else { kk = idx / CB; nn = idx % CB; }                   // B[k][n]: n contiguous
@@ -97,21 +98,23 @@ __device__ __forceinline__ void sk_load(const float* __restrict__ A, const float
     }
 }
 
-// Registers -> LDS (A as [RB][ROW], B as [CB][ROW], k contiguous); true when
-// this lane staged a CORDIC input outside the strength-reduced chain's range.
-template <int MODE, int RB, int CB, int KT, int ROW, bool TB>
+// Registers -> LDS (A as [RB][ROW], B as [CB][ROW], k contiguous) by the
+// lanes that loaded them; true when this lane staged a CORDIC input outside
+// the strength-reduced chain's range.
+template <int MODE, int RB, int CB, int KT, int ROW, bool TB, int L0 = 0, int NL = 256>
 __device__ __forceinline__ bool sk_store(float* sA, float* sB, const float* ra, const float* rb) {
-    const int tid = threadIdx.x;
+    if ((int)threadIdx.x < L0) return false;
+    const int tid = (int)threadIdx.x - L0;
     bool special = false;
 #pragma unroll
-    for (int r = 0; r < (RB * KT + 255) / 256; r++) {
-        const int idx = tid + r * 256;
+    for (int r = 0; r < (RB * KT + NL - 1) / NL; r++) {
+        const int idx = tid + r * NL;
         if (idx < RB * KT) sA[(idx / KT) * ROW + idx % KT] = ra[r];
         if constexpr (MODE == kModeCordic) special |= cordic_needs_literal(ra[r]);
     }
 #pragma unroll
-    for (int r = 0; r < (CB * KT + 255) / 256; r++) {
-        const int idx = tid + r * 256;
+    for (int r = 0; r < (CB * KT + NL - 1) / NL; r++) {
+        const int idx = tid + r * NL;
         if (idx < CB * KT) {
             if constexpr (TB) sB[(idx / KT) * ROW + idx % KT] = rb[r];
             else sB[(idx % CB) * ROW + idx / CB] = rb[r];
@@ -179,8 +182,8 @@ __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const
         // 8 k; a dependent fmaf costs ~4.6 cycles on one wave).  2 D reads
         // in flight stay within the 15 the LDS counter tracks.  RING is set
         // where it measured faster (sk_block): FAST blocks of at most 64
-        // outputs in 256-k tiles or on grids of at most two workgroups per
-        // CU (the ring's VGPRs cost a wave per SIMD on wider ones), and the
+        // outputs, and larger ones on grids of at most two workgroups per CU
+        // (the ring's VGPRs cost a wave per SIMD on wider ones), and the
         // CORDIC pipeline's 64-output blocks.
         constexpr int KT = ROW - 4, D = 6;
         if (kn == KT) {
@@ -278,13 +281,13 @@ struct SkBlock {
     }
 };
 
-template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool BIGK, bool RING>
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool RING>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
-    using Cfg = SkCfg<MODE, RB * CB, BIGK>;
+    using Cfg = SkCfg<MODE, RB * CB>;
     constexpr int KT = Cfg::kKT, ROW = Cfg::kRow;
     constexpr bool kShared = Cfg::kShared;
     __shared__ __attribute__((aligned(16))) float sA[RB * ROW];
@@ -304,14 +307,23 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
 
     const int om = tid / CB, on = tid % CB;           // output owned by lanes tid < RB * CB
     const bool owner = tid < RB * CB && om < blk.mv && on < blk.nv;
-    float ra[(RB * KT + 255) / 256], rb[(CB * KT + 255) / 256];
+    // FAST with one row (or column) of 16 outputs: wave 0 only folds, and
+    // waves 1-3 load and stage the tiles, so the next tile's loads are
+    // issued while wave 0 folds this one (per tile at 1x4096x4096 wave 0
+    // spent ~950 of 4300 cycles issuing its share of the loads before its
+    // fold).  Measured, bit-identical: 1x4096x4096 29.9 -> 29.3 us,
+    // 1x4096x11008 72.5 -> 66.6, 4096x1x4096 29.4 -> 28.4; with 4 rows it
+    // lost (30.3 -> 31.8 us), and the CORDIC pipeline, whose waves 1-3
+    // compute the terms, lost too (1x4096x4096 54.3 -> 63.7 us).
+    constexpr int L0 = (MODE == kModeFast && RB * CB <= 16) ? 64 : 0, NL = 256 - L0;
+    float ra[(RB * KT + NL - 1) / NL], rb[(CB * KT + NL - 1) / NL];
     float acc = 0.0f;
-    sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
+    sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
     for (int k0 = 0, t = 0; k0 < blk.kend; k0 += KT, t++) {
         __syncthreads();                                // previous tile's fold done with LDS
-        if (sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB, ra, rb) && exact_specials) lit[t & 1] = 1;
+        if (sk_store<MODE, RB, CB, KT, ROW, TB, L0, NL>(sA, sB, ra, rb) && exact_specials) lit[t & 1] = 1;
         __syncthreads();
-        if (k0 + KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, k0 + KT, ra, rb);
+        if (k0 + KT < blk.kend) sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, k0 + KT, ra, rb);
         const bool lit_tile = MODE == kModeCordic && lit[t & 1] != 0;
         if constexpr (kShared) {
             sk_terms<MODE, NITER, RB, CB, KT, ROW>(sA, sB, sP, blk.mv, blk.nv, iters, kinv, lit_tile);
@@ -384,8 +396,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
     if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
 }
 
-template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE, bool BIGK = false,
-          bool RING = (MODE == kModeFast && RB * CB <= 64 && !BIGK)>
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE,
+          bool RING = (MODE == kModeFast && RB * CB <= 64)>
 static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
     const unsigned wgs = FEWCOL ? (unsigned)((g.M + RB - 1) / RB) : (unsigned)((g.N + CB - 1) / CB);
     const dim3 grid(wgs, 1, (unsigned)g.batch);
@@ -394,15 +406,15 @@ static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
                            g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
                            g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
     } else {
-        hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, BIGK, RING>), grid, dim3(256), 0, s,
+        hipLaunchKernelGGL((gemm_skinny_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, RING>), grid, dim3(256), 0, s,
                            g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
                            g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
     }
     return hipGetLastError();
 }
 
-// One output block shape (RB x CB): FAST takes 512-k tiles on small grids
-// (<= 64 outputs), CORDIC the pipelined terms (<= 64 outputs); SHIFTADD's
+// One output block shape (RB x CB): CORDIC takes the pipelined terms (<= 64
+// outputs); SHIFTADD's
 // terms (a shift-add product each) outweigh its fold and keep all four
 // waves (pipelined on three: 1x4096x4096 213 -> 297 us).  The read-ahead
 // fold (RING), measured against the looped one, bit-identical: FAST
@@ -410,20 +422,15 @@ static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
 // 38.6 -> 36.4, 2048x10x4096 55.2 -> 43.2; CORDIC n = 16 4x4096x4096 175.7
 // -> 158.3.  With 2.7 workgroups per CU its VGPRs cost a wave per SIMD
 // (FAST 16x11008x4096 77.7 -> 83.2 us), and one-row CORDIC and SHIFTADD
-// and FAST's 512-k tiles gained nothing (CORDIC 1x4096x4096 54.3 -> 55.1,
-// SHIFTADD 1x11008x4096 271.7 -> 279.7, FAST 1x4096x4096 32.1 -> 32.4 us),
-// so they keep the loop.
+// gained nothing (CORDIC 1x4096x4096 54.3 -> 55.1, SHIFTADD 1x11008x4096
+// 271.7 -> 279.7 us), so they keep the loop.
 template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
     const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
     if constexpr (RB * CB <= 64) {
-        if constexpr (MODE == kModeFast) {
-            if (wgs <= device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
-        } else if constexpr (MODE == kModeCordic) {
-            return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
-        }
+        if constexpr (MODE == kModeCordic) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
     } else if constexpr (MODE == kModeFast) {
-        if (wgs <= 2 * device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, false, true>(g, s);
+        if (wgs <= 2 * device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
     }
     return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false>(g, s);
 }
