@@ -443,13 +443,20 @@ static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
 // 16x4096x4096 330 -> 225 us, SHIFTADD 1.54 -> 0.85 ms and 2.97 -> 1.69
 // ms, FAST 16 rows 52 -> 37 us; on wider grids (N = 11008) the narrow
 // blocks lost 6-29% (CORDIC, FAST), and FAST lost with 8 rows everywhere.
-// SHIFTADD, bound by its terms, takes them at 9-16 rows on any grid.
+// SHIFTADD, bound by its terms, takes them at 9-16 rows on any grid.  One
+// FAST row (or column) takes 8-wide blocks on such grids too: its fold is
+// one wave per workgroup, so twice the workgroups fold on twice the SIMDs
+// (1x4096x4096 29.1 -> 26.4 us, 1x4096x11008 66.7 -> 62.2; on the wider
+// 1x11008x4096 grid 43.9 -> 51.9, so that keeps 16).
 template <int MODE, int NITER, bool TB, bool FUSED>
 static hipError_t sk_shape(const SkinnyArgs& g, hipStream_t s) {
     const long cus = device_cus();
     if (g.M <= kSkinnyMaxRows) {                         // few rows, the grid over N
         const bool one_per_cu = (long)((g.N + 15) / 16) * g.batch <= cus;
-        if (g.M == 1) return sk_block<MODE, NITER, TB, FUSED, 1, 16, false>(g, s);
+        if (g.M == 1) {
+            if (MODE == kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 1, 8, false>(g, s);
+            return sk_block<MODE, NITER, TB, FUSED, 1, 16, false>(g, s);
+        }
         if (g.M <= 4) return sk_block<MODE, NITER, TB, FUSED, 4, 16, false>(g, s);
         if (g.M <= 8) {
             if (MODE != kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, false>(g, s);
@@ -460,7 +467,10 @@ static hipError_t sk_shape(const SkinnyArgs& g, hipStream_t s) {
     }
     // few columns, the grid over M
     const bool one_per_cu = (long)((g.M + 15) / 16) * g.batch <= cus;
-    if (g.N == 1) return sk_block<MODE, NITER, TB, FUSED, 16, 1, true>(g, s);
+    if (g.N == 1) {
+        if (MODE == kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 1, true>(g, s);
+        return sk_block<MODE, NITER, TB, FUSED, 16, 1, true>(g, s);
+    }
     if (g.N <= 4) return sk_block<MODE, NITER, TB, FUSED, 16, 4, true>(g, s);
     if (g.N <= 8) {
         if (MODE != kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, true>(g, s);
