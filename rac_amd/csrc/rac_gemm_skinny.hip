@@ -343,14 +343,25 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
 // KT dependent operations per output, waited for the terms and the terms
 // for the fold).  Tile t+1's A slice has one buffer: only the terms read it.
 // The prologue's terms of tile 0 use every lane.
-template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
-__global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
+// NT = 512 (grids of at most one workgroup per CU): 7 waves compute the
+// terms and also load and stage the tiles, wave 0 only folds (read-ahead
+// fold); 256-k tiles for 16 outputs, 128-k for 64.  With 256 lanes a tile
+// of 1x4096x4096 took ~4300 cycles, ~3200 of them the three term waves
+// (one wave per SIMD issues slowly), while the fold waited ~1300.
+// Measured, bit-identical, n = 16: 1x4096x4096 54.0 -> 36.4 us,
+// 1x4096x11008 139.4 -> 86.7, 4096x1x4096 56.6 -> 35.5, 4x4096x4096 158.5
+// -> 85.3.
+template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, int NT>
+__global__ __launch_bounds__(NT) void gemm_skinny_pipe_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
     static_assert(RB * CB <= 64, "the fold lanes are wave 0");
-    constexpr int KT = RB * CB == 16 ? 128 : 64, ROW = KT + 4;
+    static_assert(NT == 256 || NT == 512, "block size");
+    constexpr int KT = NT == 512 ? (RB * CB == 16 ? 256 : 128) : (RB * CB == 16 ? 128 : 64), ROW = KT + 4;
+    constexpr int L0 = NT == 512 ? 64 : 0, NL = NT - L0;      // the loading lanes
+    constexpr bool kRing = NT == 512 || RB * CB == 64;
     __shared__ __attribute__((aligned(16))) float sA[RB * ROW];
     __shared__ __attribute__((aligned(16))) float sB[2][CB * ROW];
     __shared__ __attribute__((aligned(16))) float sP[2][RB * CB * ROW];
@@ -368,41 +379,42 @@ __global__ __launch_bounds__(256) void gemm_skinny_pipe_kernel(
 
     const int om = tid / CB, on = tid % CB;
     const bool owner = tid < RB * CB && om < blk.mv && on < blk.nv;
-    float ra[(RB * KT + 255) / 256], rb[(CB * KT + 255) / 256];
+    float ra[(RB * KT + NL - 1) / NL], rb[(CB * KT + NL - 1) / NL];
     float acc = 0.0f;
     // prologue: tile 0 staged and its terms computed, tile 1 in flight
-    sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
+    sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, 0, ra, rb);
     __syncthreads();                                     // flags cleared
-    if (sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB[0], ra, rb) && exact_specials) lit[0] = 1;
+    if (sk_store<MODE, RB, CB, KT, ROW, TB, L0, NL>(sA, sB[0], ra, rb) && exact_specials) lit[0] = 1;
     __syncthreads();
-    if (KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, KT, ra, rb);
-    sk_terms<MODE, NITER, RB, CB, KT, ROW>(sA, sB[0], sP[0], blk.mv, blk.nv, iters, kinv,
-                                           MODE == kModeCordic && lit[0] != 0);
+    if (KT < blk.kend) sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, KT, ra, rb);
+    sk_terms<MODE, NITER, RB, CB, KT, ROW, 0, NT>(sA, sB[0], sP[0], blk.mv, blk.nv, iters, kinv,
+                                                  MODE == kModeCordic && lit[0] != 0);
     for (int k0 = 0, t = 0; k0 < blk.kend; k0 += KT, t++) {
         const int cur = t & 1, nxt = cur ^ 1;
         const bool more = k0 + KT < blk.kend;
         __syncthreads();                                 // tile t's terms written; tile t-1 folded
-        if (more && sk_store<MODE, RB, CB, KT, ROW, TB>(sA, sB[nxt], ra, rb) && exact_specials) lit[nxt] = 1;
+        if (more && sk_store<MODE, RB, CB, KT, ROW, TB, L0, NL>(sA, sB[nxt], ra, rb) && exact_specials) lit[nxt] = 1;
         __syncthreads();                                 // tile t+1 staged
-        if (k0 + 2 * KT < blk.kend) sk_load<RB, CB, KT, TB>(A, B, M, N, K, blk.m0, blk.n0, k0 + 2 * KT, ra, rb);
+        if (k0 + 2 * KT < blk.kend)
+            sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, k0 + 2 * KT, ra, rb);
         if (more)
-            sk_terms<MODE, NITER, RB, CB, KT, ROW, 64, 192>(sA, sB[nxt], sP[nxt], blk.mv, blk.nv, iters, kinv,
-                                                            MODE == kModeCordic && lit[nxt] != 0);
+            sk_terms<MODE, NITER, RB, CB, KT, ROW, 64, NT - 64>(sA, sB[nxt], sP[nxt], blk.mv, blk.nv, iters, kinv,
+                                                                MODE == kModeCordic && lit[nxt] != 0);
         if (tid == 0) lit[cur] = 0;                      // tile t+2's flag (tile t's was read a phase ago)
         if (owner)
-            acc = sk_fold<MODE, NITER, ROW, true, (RB * CB == 64)>(sA, sB[cur], sP[cur], om, on, tid, min(KT, blk.kend - k0), acc,
-                                                  iters, kinv, false);
+            acc = sk_fold<MODE, NITER, ROW, true, kRing>(sA, sB[cur], sP[cur], om, on, tid, min(KT, blk.kend - k0),
+                                                         acc, iters, kinv, false);
     }
     if (owner) sk_epilogue<FUSED>(C, N, blk.m0 + om, blk.n0 + on, acc, alpha, beta, ep, iters);
 }
 
 template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL, bool PIPE,
-          bool RING = (MODE == kModeFast && RB * CB <= 64)>
+          bool RING = (MODE == kModeFast && RB * CB <= 64), int NT = 256>
 static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
     const unsigned wgs = FEWCOL ? (unsigned)((g.M + RB - 1) / RB) : (unsigned)((g.N + CB - 1) / CB);
     const dim3 grid(wgs, 1, (unsigned)g.batch);
     if constexpr (PIPE) {
-        hipLaunchKernelGGL((gemm_skinny_pipe_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL>), grid, dim3(256), 0, s,
+        hipLaunchKernelGGL((gemm_skinny_pipe_kernel<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, NT>), grid, dim3(NT), 0, s,
                            g.A, g.B, g.C, g.M, g.N, g.K, g.alpha, g.beta, g.iters, cordic_kinv(g.iters), g.sa, g.sb,
                            g.sc, g.ep, g.k_causal, g.exact_specials, g.row0);
     } else {
@@ -428,7 +440,10 @@ template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
     const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
     if constexpr (RB * CB <= 64) {
-        if constexpr (MODE == kModeCordic) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
+        if constexpr (MODE == kModeCordic) {
+            if (wgs <= device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true, false, 512>(g, s);
+            return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true>(g, s);
+        }
     } else if constexpr (MODE == kModeFast) {
         if (wgs <= 2 * device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, false, true>(g, s);
     }
