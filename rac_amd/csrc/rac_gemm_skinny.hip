@@ -345,7 +345,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
 // The prologue's terms of tile 0 use every lane.
 // NT = 512 (grids of at most one workgroup per CU): 7 waves compute the
 // terms and also load and stage the tiles, wave 0 only folds (read-ahead
-// fold); 256-k tiles for 16 outputs, 128-k for 64.  With 256 lanes a tile
+// fold); 256-k tiles for 16 outputs, 128-k for 64.  128 outputs (8 x 16
+// blocks) fold on waves 0-1, their terms on waves 2-7, in 64-k tiles
+// (8x4096x4096 175.8 -> 160.4 us against 8 x 8 blocks on 256 lanes,
+// 2048x10x4096 243.6 -> 179.8).  With 256 lanes a tile
 // of 1x4096x4096 took ~4300 cycles, ~3200 of them the three term waves
 // (one wave per SIMD issues slowly), while the fold waited ~1300.
 // Measured, bit-identical, n = 16: 1x4096x4096 54.0 -> 36.4 us,
@@ -357,10 +360,12 @@ __global__ __launch_bounds__(NT) void gemm_skinny_pipe_kernel(
     float alpha, float beta, int iters, float kinv, long sa, long sb, long sc, GemmEpilogue ep,
     const int* k_causal, int exact_specials, int row0)
 {
-    static_assert(RB * CB <= 64, "the fold lanes are wave 0");
     static_assert(NT == 256 || NT == 512, "block size");
-    constexpr int KT = NT == 512 ? (RB * CB == 16 ? 256 : 128) : (RB * CB == 16 ? 128 : 64), ROW = KT + 4;
-    constexpr int L0 = NT == 512 ? 64 : 0, NL = NT - L0;      // the loading lanes
+    static_assert(RB * CB <= (NT == 512 ? 128 : 64), "the fold lanes are wave 0 (and 1)");
+    constexpr int FL = RB * CB <= 64 ? 64 : 128;              // lanes of the folding waves
+    constexpr int KT = NT == 512 ? (RB * CB == 16 ? 256 : (RB * CB == 64 ? 128 : 64)) : (RB * CB == 16 ? 128 : 64);
+    constexpr int ROW = KT + 4;
+    constexpr int L0 = NT == 512 ? FL : 0, NL = NT - L0;      // the loading lanes
     constexpr bool kRing = NT == 512 || RB * CB == 64;
     __shared__ __attribute__((aligned(16))) float sA[RB * ROW];
     __shared__ __attribute__((aligned(16))) float sB[2][CB * ROW];
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(NT) void gemm_skinny_pipe_kernel(
         if (k0 + 2 * KT < blk.kend)
             sk_load<RB, CB, KT, TB, L0, NL>(A, B, M, N, K, blk.m0, blk.n0, k0 + 2 * KT, ra, rb);
         if (more)
-            sk_terms<MODE, NITER, RB, CB, KT, ROW, 64, NT - 64>(sA, sB[nxt], sP[nxt], blk.mv, blk.nv, iters, kinv,
+            sk_terms<MODE, NITER, RB, CB, KT, ROW, FL, NT - FL>(sA, sB[nxt], sP[nxt], blk.mv, blk.nv, iters, kinv,
                                                                 MODE == kModeCordic && lit[nxt] != 0);
         if (tid == 0) lit[cur] = 0;                      // tile t+2's flag (tile t's was read a phase ago)
         if (owner)
@@ -439,6 +444,9 @@ static hipError_t sk_launch(const SkinnyArgs& g, hipStream_t s) {
 template <int MODE, int NITER, bool TB, bool FUSED, int RB, int CB, bool FEWCOL>
 static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
     const long wgs = (FEWCOL ? (long)((g.M + RB - 1) / RB) : (long)((g.N + CB - 1) / CB)) * g.batch;
+    if constexpr (MODE == kModeCordic && RB * CB == 128) {
+        if (wgs <= device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true, false, 512>(g, s);
+    }
     if constexpr (RB * CB <= 64) {
         if constexpr (MODE == kModeCordic) {
             if (wgs <= device_cus()) return sk_launch<MODE, NITER, TB, FUSED, RB, CB, FEWCOL, true, false, 512>(g, s);
@@ -458,7 +466,10 @@ static hipError_t sk_block(const SkinnyArgs& g, hipStream_t s) {
 // 16x4096x4096 330 -> 225 us, SHIFTADD 1.54 -> 0.85 ms and 2.97 -> 1.69
 // ms, FAST 16 rows 52 -> 37 us; on wider grids (N = 11008) the narrow
 // blocks lost 6-29% (CORDIC, FAST), and FAST lost with 8 rows everywhere.
-// SHIFTADD, bound by its terms, takes them at 9-16 rows on any grid.  One
+// SHIFTADD, bound by its terms, takes them at 9-16 rows on any grid.  CORDIC
+// with 5-8 rows (or columns) now keeps 8 x 16 blocks on such grids, which
+// the 512-lane pipeline runs (8 x 8 blocks on 256 lanes: 175.8 us, 8 x 16
+// on 512: 160.4 us at 8x4096x4096 n = 16).  One
 // FAST row (or column) takes 8-wide blocks on such grids too: its fold is
 // one wave per workgroup, so twice the workgroups fold on twice the SIMDs
 // (1x4096x4096 29.1 -> 26.4 us, 1x4096x11008 66.7 -> 62.2; on the wider
@@ -474,7 +485,8 @@ static hipError_t sk_shape(const SkinnyArgs& g, hipStream_t s) {
         }
         if (g.M <= 4) return sk_block<MODE, NITER, TB, FUSED, 4, 16, false>(g, s);
         if (g.M <= 8) {
-            if (MODE != kModeFast && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, false>(g, s);
+            // CORDIC keeps 8 x 16 blocks there: the 512-lane pipeline takes them
+            if (MODE == kModeShiftAdd && one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 8, 8, false>(g, s);
             return sk_block<MODE, NITER, TB, FUSED, 8, 16, false>(g, s);
         }
         if (MODE == kModeShiftAdd || one_per_cu) return sk_block<MODE, NITER, TB, FUSED, 16, 8, false>(g, s);
