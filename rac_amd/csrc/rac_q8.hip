@@ -418,19 +418,24 @@ hipError_t q8_gemv_launch(const float* x, const uint8_t* w, const float* bias, f
         // blocks (K < 1024) in chunks of 8 blocks, 32 rows per workgroup
         const int nb = K / kQ8Block;
         const dim3 g16((unsigned)((N + 15) / 16)), g32((unsigned)((N + 31) / 32));
-        if (M > 4 && M <= 8 && nb >= 32) {
-            // 5-8 rows in one pass over the weights (162 VGPRs, 75 KB of LDS:
-            // 2 workgroups per CU) instead of two 4-row passes; bit-identical,
-            // M = 8: 4096x4096 20.9 -> 16.6 us, 11008x4096 35.0 -> 32.4,
-            // 32000x4096 79.5 -> 71.7
-            hipLaunchKernelGGL((q8_gemv_kernel<8, 32, 16>), g16, dim3(256), 0, s, x, w, bias, out, M, N, K, act,
-                               Q8Fuse());
-            return hipGetLastError();
-        }
-        for (int m0 = 0; m0 < M; m0 += 4) {
-            const int mm = min(4, M - m0);
+        // passes of up to 8 rows where more than 4 remain (K >= 1024): one
+        // pass of the 8-row kernel (162 VGPRs, 75 KB of LDS: 2 workgroups
+        // per CU) reads the weights once for them, against two 4-row passes;
+        // bit-identical, M = 8: 4096x4096 20.9 -> 16.6 us, 11008x4096 35.0
+        // -> 32.4, 32000x4096 79.5 -> 71.7
+        for (int m0 = 0; m0 < M;) {
+            const int left = M - m0;
             const float* xg = x + (long)m0 * K;
             float* og = out + (long)m0 * N;
+            if (left > 4 && nb >= 32) {
+                const int mm = min(8, left);
+                hipLaunchKernelGGL((q8_gemv_kernel<8, 32, 16>), g16, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act,
+                                   Q8Fuse());
+                m0 += mm;
+                continue;
+            }
+            const int mm = min(4, left);
+            m0 += mm;
             if (nb < 32) {
                 if (mm > 1)
                     hipLaunchKernelGGL((q8_gemv_kernel<4, 8, 32>), g32, dim3(256), 0, s, xg, w, bias, og, mm, N, K, act, Q8Fuse());
