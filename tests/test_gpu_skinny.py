@@ -133,12 +133,16 @@ def test_skinny_alpha_beta_and_batch(mode, iters):
         assert np.array_equal(out[z], ref), z
 
 
+@pytest.mark.parametrize("N", [11008, 4096])
 @pytest.mark.parametrize("mode,iters", [(1, 16), (0, 24)])
-def test_skinny_decode_linear(mode, iters):
-    """A decode step's linear layer: x [1, 4096] @ W[11008, 4096]^T + b with
-    SiLU, fused and unfused; pre-activations bit-exact vs the checker."""
+def test_skinny_decode_linear(mode, iters, N):
+    """A decode step's linear layer: x [1, 4096] @ W[N, 4096]^T + b with
+    SiLU, fused and unfused; pre-activations bit-exact vs the checker.
+    N = 4096 is a grid of one workgroup per CU: the 512-lane CORDIC
+    pipeline and FAST's 8-wide blocks, with the fused epilogue."""
     e = ext()
-    M, N, K = 1, 11008, 4096
+    M, K = 1, 4096
+    print(f"decode linear mode={mode} iters={iters} N={N}", flush=True)
     x = rl.gen_normal((M, K), seed=41)
     w = rl.gen_normal((N, K), seed=42, std=0.02)
     b = rl.gen_normal(N, seed=43)
