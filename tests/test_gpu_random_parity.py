@@ -112,6 +112,35 @@ def case_gemm(rng, seed):
     assert same(H(Cd), rl.orc_matmul(A, B, M, N, K, iters, mode, ta, tb, alpha, beta, C0)), seed
 
 
+def case_gemm_fewrow_wide(rng, seed):
+    """Few rows (or columns) on grids of up to one workgroup per CU and
+    wider: the 512-lane CORDIC pipeline (16, 64 and 128 outputs per
+    workgroup), FAST's 8-wide blocks, full and ragged K-tiles, and the
+    literal chain on sprinkled special values."""
+    cols = rng.random() < 0.3
+    small = int(rng.choice([1, 1, 2, 4, int(rng.integers(5, 9)), int(rng.integers(9, 17))]))
+    big = int(rng.integers(256, 4200))
+    M, N = (big, small) if cols else (small, big)
+    K = int(rng.choice([int(rng.integers(1, 1100)), 256 * int(rng.integers(1, 5))]))
+    K = max(1, min(K, int(1.5e7) // (small * big)))
+    mode = int(rng.choice([0, 1, 1, 2])) if small * big * K <= 3_000_000 else int(rng.choice([0, 1, 1]))
+    iters = int(rng.choice([8, 16, 24, int(rng.integers(1, 25))]))
+    tb = int(rng.integers(0, 2))
+    alpha = float(np.float32(rng.choice([1.0, rng.normal()])))
+    beta = float(np.float32(rng.choice([0.0, 0.0, rng.normal()])))
+    A = rng.uniform(-2, 2, (M, K)).astype(np.float32)
+    B = rng.uniform(-2, 2, (N, K) if tb else (K, N)).astype(np.float32)
+    if mode == 1 and rng.random() < 0.3:
+        sprinkle(rng, A, 0.01)
+    C0 = rng.normal(size=(M, N)).astype(np.float32)
+    print(f"matmul few-row wide seed={seed} M={M} N={N} K={K} tb={tb} mode={mode} n={iters}", flush=True)
+    Ad, Bd, Cd = T(A), T(B), T(C0)
+    rc = lib().rac_gemm_dev(Ad.data_ptr(), Bd.data_ptr(), Cd.data_ptr(), M, N, K, 0, tb, alpha, beta, iters,
+                            mode, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib().rac_last_error()
+    assert same(H(Cd), rl.orc_matmul(A, B, M, N, K, iters, mode, 0, tb, alpha, beta, C0)), seed
+
+
 def case_bmm(rng, seed):
     Z = int(rng.integers(1, 6))
     M, N, K = (int(rng.integers(1, 150)) for _ in range(3))
@@ -501,6 +530,7 @@ CASES = {
     "rope_cache": (case_rope_cache, 100), "sincos_rsqrt": (case_sincos_rsqrt, 60), "prims": (case_prims, 100),
     "attention_probs": (case_attention_probs, 100), "large_matmul": (case_big_matmul, 12),
     "long_rows": (case_long_rows, 12), "large_q8_gemv": (case_big_q8, 3), "rac_dsp": (case_dsp, 60),
+    "fewrow_wide_matmul": (case_gemm_fewrow_wide, 60),
 }
 
 
