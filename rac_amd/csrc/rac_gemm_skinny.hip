@@ -184,7 +184,7 @@ __device__ __forceinline__ float sk_fold(const float* sA, const float* sB, const
         // where it measured faster (sk_block): FAST blocks of at most 64
         // outputs, and larger ones on grids of at most two workgroups per CU
         // (the ring's VGPRs cost a wave per SIMD on wider ones), and the
-        // CORDIC pipeline's 64-output blocks.
+        // CORDIC pipeline on 512 lanes or with 64-output blocks.
         constexpr int KT = ROW - 4, D = 6;
         if (kn == KT) {
             const float* rowb = &sB[on * ROW];
