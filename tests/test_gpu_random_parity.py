@@ -246,7 +246,7 @@ def case_rope(rng, seed):
 
 
 def case_q8(rng, seed):
-    M, N = int(rng.integers(1, 9)), int(rng.integers(1, 3000))
+    M, N = int(rng.integers(1, 17)), int(rng.integers(1, 3000))
     K = 32 * int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(1, 40))]))
     act = int(rng.integers(0, 4))
     wq = rl.orc_q8_quantize(rng.normal(size=(N, K)).astype(np.float32))
